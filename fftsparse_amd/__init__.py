@@ -1,0 +1,15 @@
+"""fftsparse_amd -- MI355X-native FFTSparse prefill (FFT-guided block selection
++ block-sparse causal GQA attention) on hand-written gfx950 HIP kernels.
+
+Public API (drop-in for attn_src/fft_attn/my_attn_v7.py and
+attn_src/fix_mask_attn/my_attn.py):
+
+    myattn_prefill(q, k, v, layer_idx, ...)        v7 selection + sparse attention
+    fix_mask.myattn_prefill(q, k, v, layer_idx, ...) fixed sink/recent/local mask
+    select_blocks(q, k, ...)                        stage 1 only (block lists)
+    block_sparse_attention(q, k, v, cnt, idx, ...)  stage 2 only
+"""
+from .attn import BlockSelection, block_sparse_attention, myattn_prefill, select_blocks  # noqa: F401
+from . import fix_mask  # noqa: F401
+
+__all__ = ["myattn_prefill", "select_blocks", "block_sparse_attention", "BlockSelection", "fix_mask"]

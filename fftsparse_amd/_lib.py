@@ -1,0 +1,122 @@
+"""ctypes binding of the C ABI in ``include/fftsparse_amd.h``.
+
+The shared library is built in-tree (``python -m fftsparse_amd.build``).  torch
+is imported first so that the library's HIP runtime dependency resolves to the
+runtime torch already loaded: device pointers and streams are shared.
+Loading fails loudly when the library is missing -- there is no fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+from ctypes import POINTER, c_float, c_int, c_int32, c_int64, c_size_t, c_uint8, c_uint16, c_void_p
+from pathlib import Path
+
+import torch  # noqa: F401  (must precede the library load, see module docstring)
+
+LIB_PATH = Path(__file__).resolve().with_name("libfftsparse_amd.so")
+
+FS_DTYPE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+
+
+class PoolArgs(ctypes.Structure):
+    _fields_ = [("q", c_void_p), ("q_sh", c_int64), ("q_sl", c_int64),
+                ("k", c_void_p), ("k_sh", c_int64), ("k_sl", c_int64),
+                ("dtype", c_int), ("Hq", c_int), ("Hk", c_int), ("L", c_int), ("D", c_int), ("bs", c_int),
+                ("q_b", c_void_p), ("k_b", c_void_p)]
+
+
+class CorrArgs(ctypes.Structure):
+    _fields_ = [("q_b", c_void_p), ("k_b", c_void_p),
+                ("dtype", c_int), ("Hq", c_int), ("Hk", c_int), ("N", c_int), ("D", c_int),
+                ("local_window", c_int), ("keep_sink", c_int), ("remote_start", c_int),
+                ("corr_threshold", c_float),
+                ("work", c_void_p), ("corr", c_void_p), ("corr_sum", c_void_p), ("keep_tau", c_void_p)]
+
+
+class StatsArgs(ctypes.Structure):
+    _fields_ = [("q_b", c_void_p), ("k_b", c_void_p),
+                ("dtype", c_int), ("Hq", c_int), ("Hk", c_int), ("N", c_int), ("D", c_int),
+                ("sample_taus", c_void_p), ("n_samples", c_int),
+                ("col_start", c_int), ("col_end", c_int), ("n_cols", c_int),
+                ("last_k", c_int),
+                ("diag_var", c_void_p), ("col_mean", c_void_p), ("col_sel", c_void_p),
+                ("last_scores", c_void_p), ("last_sel", c_void_p)]
+
+
+class SelectArgs(ctypes.Structure):
+    _fields_ = [("q_b", c_void_p), ("k_b", c_void_p),
+                ("dtype", c_int), ("Hq", c_int), ("Hk", c_int), ("N", c_int), ("Nk", c_int), ("D", c_int),
+                ("mask_causal", c_int),
+                ("keep_sink", c_int), ("keep_recent", c_int), ("local_window", c_int), ("remote_start", c_int),
+                ("dyn_mode", c_int), ("stripe_all_diffuse", c_int),
+                ("diag_var", c_void_p), ("n_samples", c_int), ("stripe_threshold", c_float),
+                ("keep_tau", c_void_p),
+                ("qk_topk_ratio", c_float),
+                ("col_mode", c_int), ("col_sel", c_void_p), ("last_sel", c_void_p),
+                ("mean_var", c_void_p), ("is_stripe", c_void_p),
+                ("blk_cnt", c_void_p), ("blk_idx", c_void_p)]
+
+
+class AttnArgs(ctypes.Structure):
+    _fields_ = [("q", c_void_p), ("q_sb", c_int64), ("q_sh", c_int64), ("q_sl", c_int64),
+                ("k", c_void_p), ("k_sb", c_int64), ("k_sh", c_int64), ("k_sl", c_int64),
+                ("v", c_void_p), ("v_sb", c_int64), ("v_sh", c_int64), ("v_sl", c_int64),
+                ("out", c_void_p), ("o_sb", c_int64), ("o_sh", c_int64), ("o_sl", c_int64),
+                ("dtype", c_int), ("B", c_int), ("Hq", c_int), ("Hk", c_int), ("Lq", c_int), ("Lk", c_int),
+                ("D", c_int), ("bs", c_int),
+                ("is_causal", c_int), ("softmax_scale", c_float),
+                ("blk_cnt", c_void_p), ("blk_idx", c_void_p)]
+
+
+STRUCTS = [PoolArgs, CorrArgs, StatsArgs, SelectArgs, AttnArgs]
+
+ENTRY_POINTS = ["fs_pool", "fs_corr_work_bytes", "fs_corr", "fs_stats", "fs_select", "fs_bsattn",
+                "fs_last_error", "fs_abi_version", "fs_sizeof_args"]
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Load the in-tree library once; raise if it is missing or stale."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(
+            f"fftsparse_amd native library not found at {LIB_PATH}; build it with "
+            "`python -m fftsparse_amd.build` (no CPU fallback exists)")
+    lib = ctypes.CDLL(str(LIB_PATH))
+    lib.fs_last_error.restype = ctypes.c_char_p
+    lib.fs_abi_version.restype = c_int
+    lib.fs_sizeof_args.restype = c_size_t
+    lib.fs_sizeof_args.argtypes = [c_int]
+    lib.fs_corr_work_bytes.restype = c_size_t
+    lib.fs_corr_work_bytes.argtypes = [c_int, c_int, c_int]
+    for name, st in [("fs_pool", PoolArgs), ("fs_corr", CorrArgs), ("fs_stats", StatsArgs),
+                     ("fs_select", SelectArgs), ("fs_bsattn", AttnArgs)]:
+        fn = getattr(lib, name)
+        fn.restype = c_int
+        fn.argtypes = [POINTER(st), c_void_p]
+    if lib.fs_abi_version() != 1:
+        raise RuntimeError("fftsparse_amd: library ABI version mismatch; rebuild it")
+    for i, st in enumerate(STRUCTS):
+        if lib.fs_sizeof_args(i) != ctypes.sizeof(st):
+            raise RuntimeError(f"fftsparse_amd: {st.__name__} layout differs from the library; rebuild it")
+    _lib = lib
+    return lib
+
+
+def call(name: str, args) -> None:
+    """Invoke an entry point on torch's current stream; raise on a non-zero status."""
+    lib = load()
+    stream = torch.cuda.current_stream().cuda_stream
+    rc = getattr(lib, name)(ctypes.byref(args), c_void_p(stream))
+    if rc != 0:
+        msg = lib.fs_last_error().decode(errors="replace")
+        if rc == -1:
+            raise ValueError(msg)
+        raise RuntimeError(msg)
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()

@@ -1,0 +1,283 @@
+"""Drop-in ``myattn_prefill`` (FFTSparse v7 API) on hand-written gfx950 kernels.
+
+Mirrors ``attn_src/fft_attn/my_attn_v7.py:454-792``: same signature, defaults,
+return shape ([bsz, L_q, H*D] in the input dtype) and error types.  The
+computation runs as a fixed sequence of stream-ordered kernel launches with no
+host synchronisation:
+
+    fs_pool    Q/K block means                       (:553-555)
+    fs_corr    FFT lag correlation + lag threshold   (:567-576)
+    fs_stats   diagonal statistics, column scores,
+               last-row scores and their top-n       (:558-560, :581-596, :623-635)
+    fs_select  stripe/diffuse decision, qk top-k,
+               mask composition -> per-row block lists (:600-641)
+    fs_bsattn  block-sparse causal GQA attention     (:775-786)
+
+K/V may carry Hq heads (the reference's repeat_kv'd layout) or Hkv heads with
+Hq % Hkv == 0 (native GQA, no repetition needed).
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from ._lib import AttnArgs, CorrArgs, PoolArgs, SelectArgs, StatsArgs, ptr
+from .params import PrefillParams, derive, f32
+
+_MIN_BLOCKS = 10          # my_attn_v7.py:509
+
+
+@dataclass
+class BlockSelection:
+    """Device-resident result of the mask selection stage."""
+    params: PrefillParams
+    blk_cnt: torch.Tensor            # int32 [Hq, N]
+    blk_idx: torch.Tensor            # uint16 [Hq, N, Nk] (first blk_cnt entries of each row valid)
+    q_b: torch.Tensor | None = None  # [Hq, N, D]
+    k_b: torch.Tensor | None = None  # [Hk, N, D]
+    corr: torch.Tensor | None = None
+    corr_sum: torch.Tensor | None = None
+    keep_tau: torch.Tensor | None = None
+    diag_var: torch.Tensor | None = None
+    col_mean: torch.Tensor | None = None
+    col_sel: torch.Tensor | None = None
+    last_scores: torch.Tensor | None = None
+    last_sel: torch.Tensor | None = None
+    mean_var: torch.Tensor | None = None
+    is_stripe: torch.Tensor | None = None
+
+    def dense_mask(self) -> torch.Tensor:
+        """[Hq, N, Nk] bool mask rebuilt from the block lists (for checks)."""
+        H, N = self.blk_cnt.shape
+        Nk = self.blk_idx.shape[2]
+        idx = self.blk_idx.view(torch.int16).to(torch.int64) & 0xFFFF
+        valid = torch.arange(Nk, device=idx.device)[None, None, :] < self.blk_cnt[:, :, None].to(torch.int64)
+        m = torch.zeros(H, N, Nk + 1, dtype=torch.bool, device=idx.device)
+        m.scatter_(2, torch.where(valid, idx, torch.full_like(idx, Nk)), True)
+        return m[:, :, :Nk]
+
+    def nnz(self) -> int:
+        return int(self.blk_cnt.sum().item())
+
+
+_tau_cache: dict = {}
+
+
+def _sample_taus_device(taus, device):
+    key = (tuple(taus), str(device))
+    t = _tau_cache.get(key)
+    if t is None:
+        t = torch.tensor(list(taus) or [0], dtype=torch.int32).to(device)
+        _tau_cache[key] = t
+    return t
+
+
+def _check_layout(x: torch.Tensor) -> torch.Tensor:
+    if x.dim() != 4:
+        raise ValueError(f"expected a [B, H, L, D] tensor, got shape {tuple(x.shape)}")
+    if x.stride(3) != 1 or x.stride(2) % 8 or x.stride(1) % 8 or x.stride(0) % 8 or x.data_ptr() % 16:
+        x = x.contiguous()
+    return x
+
+
+def select_blocks(query_states: torch.Tensor, key_states: torch.Tensor, *, block_size=128,
+                  sink_ratio=0.1, recent_ratio=0.1, local_span_ratio=0.1,
+                  enable_correlation_mask=True, correlation_selection_mode="threshold",
+                  correlation_topk_ratio=0.2, corr_threshold=0.1,
+                  enable_column_mask=True, column_topk_ratio=0.1,
+                  column_start_exclude_ratio=0.1, column_end_exclude_ratio=0.2,
+                  enable_last_block_mask=True, diag_sample_ratio=0.15, min_diag_samples=5,
+                  max_diag_samples=64, stripe_threshold=0.3, qk_topk_ratio=0.2,
+                  keep_intermediates=False) -> BlockSelection:
+    """Stage 1 of my_attn_v7.myattn_prefill (:533-641): block lists for every
+    (query head, query block).  q [1,Hq,L,D], k [1,Hk,L,D]."""
+    q = _check_layout(query_states)
+    k = _check_layout(key_states)
+    if q.shape[0] != 1 or k.shape[0] != 1:
+        raise ValueError("myattn_prefill supports batch size 1 (my_attn_v7.py:521)")
+    Hq, L_q, D = q.shape[1], q.shape[2], q.shape[3]
+    Hk, L_k = k.shape[1], k.shape[2]
+    if Hq % Hk:
+        raise ValueError(f"query heads {Hq} must be a multiple of key heads {Hk}")
+    if L_q != L_k:
+        raise ValueError(f"prefill expects L_q == L_k, got {L_q} and {L_k}")
+    if q.dtype != k.dtype or q.dtype not in _lib.FS_DTYPE:
+        raise TypeError(f"unsupported dtypes {q.dtype}, {k.dtype}")
+    if correlation_selection_mode not in ("threshold", "topk"):
+        raise ValueError(f"Unknown selection_mode: {correlation_selection_mode}")
+    p = derive(L_q, L_k, block_size, sink_ratio, recent_ratio, local_span_ratio,
+               enable_correlation_mask, correlation_topk_ratio, enable_column_mask,
+               column_topk_ratio, column_start_exclude_ratio, column_end_exclude_ratio,
+               enable_last_block_mask, diag_sample_ratio, min_diag_samples, max_diag_samples)
+    if p.corr_enabled and p.remote_start >= p.N:
+        # my_attn_v7.py:190-191 returns a single tensor there and the six-way
+        # unpacking at :568 raises.
+        raise ValueError("not enough values to unpack (expected 6, got 1)")
+    if p.corr_enabled and correlation_selection_mode == "topk":
+        raise NotImplementedError("correlation_selection_mode='topk' is not implemented on the GPU path yet")
+    dev = q.device
+    dt = _lib.FS_DTYPE[q.dtype]
+    N, Nk = p.N, p.Nk
+    need_pool = enable_last_block_mask or p.corr_enabled or p.col_enabled   # :553
+    sel = BlockSelection(params=p,
+                         blk_cnt=torch.empty(Hq, N, dtype=torch.int32, device=dev),
+                         blk_idx=torch.empty(Hq, N, Nk, dtype=torch.uint16, device=dev))
+    u8 = torch.uint8
+    if need_pool:
+        q_b = torch.empty(Hq, N, D, dtype=q.dtype, device=dev)
+        k_b = torch.empty(Hk, N, D, dtype=q.dtype, device=dev)
+        _lib.call("fs_pool", PoolArgs(q=q.data_ptr(), q_sh=q.stride(1), q_sl=q.stride(2),
+                                      k=k.data_ptr(), k_sh=k.stride(1), k_sl=k.stride(2),
+                                      dtype=dt, Hq=Hq, Hk=Hk, L=L_q, D=D, bs=block_size,
+                                      q_b=q_b.data_ptr(), k_b=k_b.data_ptr()))
+        sel.q_b, sel.k_b = q_b, k_b
+    col_sel = last_sel = None
+    keep = diag_var = None
+    n_samples = 0
+    if p.corr_enabled:
+        lib = _lib.load()
+        work = torch.empty(lib.fs_corr_work_bytes(Hq, N, D), dtype=u8, device=dev)
+        corr = torch.empty(Hq, N, dtype=torch.float32, device=dev)
+        corr_sum = torch.empty(Hq, N, dtype=torch.float32, device=dev)
+        keep = torch.empty(Hq, N, dtype=u8, device=dev)
+        _lib.call("fs_corr", CorrArgs(q_b=ptr(sel.q_b), k_b=ptr(sel.k_b), dtype=dt, Hq=Hq, Hk=Hk, N=N, D=D,
+                                      local_window=p.local_window, keep_sink=p.keep_sink,
+                                      remote_start=p.remote_start, corr_threshold=f32(corr_threshold),
+                                      work=work.data_ptr(), corr=corr.data_ptr(),
+                                      corr_sum=corr_sum.data_ptr(), keep_tau=keep.data_ptr()))
+        sel.corr, sel.corr_sum, sel.keep_tau = corr, corr_sum, keep
+        n_samples = 0 if p.stripe_all_diffuse else len(p.sample_taus)
+    n_cols = p.n_cols if p.col_enabled else 0
+    last_k = p.last_k if enable_last_block_mask else 0
+    if n_samples or n_cols or last_k:
+        diag_var = torch.empty(Hq, max(1, n_samples), dtype=torch.float32, device=dev)
+        col_mean = torch.empty(Hq, N, dtype=torch.float32, device=dev) if n_cols else None
+        col_sel = torch.empty(Hq, N, dtype=u8, device=dev) if n_cols else None
+        last_scores = torch.empty(Hq, N, dtype=torch.float32, device=dev) if last_k else None
+        last_sel = torch.empty(Hq, N, dtype=u8, device=dev) if last_k else None
+        taus = _sample_taus_device(p.sample_taus, dev)
+        _lib.call("fs_stats", StatsArgs(q_b=ptr(sel.q_b), k_b=ptr(sel.k_b), dtype=dt, Hq=Hq, Hk=Hk, N=N, D=D,
+                                        sample_taus=taus.data_ptr(), n_samples=n_samples,
+                                        col_start=p.col_start, col_end=p.col_end, n_cols=n_cols,
+                                        last_k=last_k, diag_var=diag_var.data_ptr(),
+                                        col_mean=ptr(col_mean), col_sel=ptr(col_sel),
+                                        last_scores=ptr(last_scores), last_sel=ptr(last_sel)))
+        sel.diag_var, sel.col_mean, sel.col_sel = diag_var, col_mean, col_sel
+        sel.last_scores, sel.last_sel = last_scores, last_sel
+    if p.corr_enabled:
+        dyn_mode, col_mode = 1, (1 if n_cols else 0)
+        sel.mean_var = torch.empty(Hq, dtype=torch.float32, device=dev)
+        sel.is_stripe = torch.empty(Hq, dtype=u8, device=dev)
+    else:
+        dyn_mode, col_mode = 0, (2 if n_cols else 0)
+    _lib.call("fs_select", SelectArgs(q_b=ptr(sel.q_b), k_b=ptr(sel.k_b), dtype=dt, Hq=Hq, Hk=Hk, N=N, Nk=Nk,
+                                      D=D, mask_causal=1, keep_sink=p.keep_sink, keep_recent=p.keep_recent,
+                                      local_window=p.local_window, remote_start=p.remote_start,
+                                      dyn_mode=dyn_mode, stripe_all_diffuse=int(p.stripe_all_diffuse),
+                                      diag_var=ptr(diag_var), n_samples=n_samples,
+                                      stripe_threshold=f32(stripe_threshold), keep_tau=ptr(keep),
+                                      qk_topk_ratio=f32(qk_topk_ratio), col_mode=col_mode,
+                                      col_sel=ptr(col_sel), last_sel=ptr(last_sel),
+                                      mean_var=ptr(sel.mean_var), is_stripe=ptr(sel.is_stripe),
+                                      blk_cnt=sel.blk_cnt.data_ptr(), blk_idx=sel.blk_idx.data_ptr()))
+    if not keep_intermediates:
+        sel.q_b = sel.k_b = None
+    return sel
+
+
+def block_sparse_attention(query_states, key_states, value_states, blk_cnt=None, blk_idx=None, *,
+                           block_size=128, is_causal=True, softmax_scale=None, out=None) -> torch.Tensor:
+    """Block-sparse (or, with no block lists, dense causal) attention.
+
+    q [B,Hq,Lq,D], k/v [B,Hk,Lk,D] -> out [B, Lq, Hq, D] in the input dtype."""
+    q = _check_layout(query_states)
+    k = _check_layout(key_states)
+    v = _check_layout(value_states)
+    B, Hq, Lq, D = q.shape
+    Hk, Lk = k.shape[1], k.shape[2]
+    if v.shape[1] != Hk or v.shape[2] != Lk or k.shape[0] != B or v.shape[0] != B:
+        raise ValueError("key/value shapes do not match")
+    if q.dtype not in (torch.bfloat16, torch.float16) or k.dtype != q.dtype or v.dtype != q.dtype:
+        # flash-attention kernels accept fp16/bf16 only, as does the reference's
+        # block_sparse_attn_func.
+        raise RuntimeError("FlashAttention only supports fp16 and bf16 data type")
+    if out is None:
+        out = torch.empty(B, Lq, Hq, D, dtype=q.dtype, device=q.device)
+    scale = 1.0 / math.sqrt(D) if softmax_scale is None else float(softmax_scale)
+    _lib.call("fs_bsattn", AttnArgs(
+        q=q.data_ptr(), q_sb=q.stride(0), q_sh=q.stride(1), q_sl=q.stride(2),
+        k=k.data_ptr(), k_sb=k.stride(0), k_sh=k.stride(1), k_sl=k.stride(2),
+        v=v.data_ptr(), v_sb=v.stride(0), v_sh=v.stride(1), v_sl=v.stride(2),
+        out=out.data_ptr(), o_sb=out.stride(0), o_sh=out.stride(2), o_sl=out.stride(1),
+        dtype=_lib.FS_DTYPE[q.dtype], B=B, Hq=Hq, Hk=Hk, Lq=Lq, Lk=Lk, D=D, bs=block_size,
+        is_causal=int(bool(is_causal)), softmax_scale=scale,
+        blk_cnt=ptr(blk_cnt), blk_idx=ptr(blk_idx)))
+    return out
+
+
+def myattn_prefill(
+        query_states,
+        key_states,
+        value_states,
+        layer_idx,
+        block_size=128,
+        is_causal=True,
+        is_visual=False,
+        sink_ratio=0.1,
+        recent_ratio=0.1,
+        local_span_ratio=0.1,
+        enable_correlation_mask=True,
+        correlation_selection_mode: str = "threshold",
+        correlation_topk_ratio: float = 0.2,
+        corr_threshold: float = 0.1,
+        collect_corr_stats: bool = False,
+        enable_column_mask: bool = True,
+        column_topk_ratio: float = 0.1,
+        column_start_exclude_ratio: float = 0.1,
+        column_end_exclude_ratio: float = 0.2,
+        enable_last_block_mask=True,
+        last_block_threshold=0.01,
+        diag_sample_ratio: float = 0.15,
+        min_diag_samples: int = 5,
+        max_diag_samples: int = 64,
+        stripe_threshold: float = 0.3,
+        qk_topk_ratio: float = 0.2,
+        attention_vis_heads=[0],
+        attention_vis_dir=None,
+):
+    """Block-sparse prefill attention, my_attn_v7.py:454-792.
+
+    query_states [bsz,H,L_q,D], key/value_states [bsz,H or Hkv,L_k,D] on the
+    GPU -> [bsz, L_q, H*D].  ``last_block_threshold`` is accepted and unused,
+    as in the reference; ``is_visual`` / ``collect_corr_stats`` (plotting and
+    statistics collection) are accepted and ignored."""
+    assert query_states.is_cuda, "input tensors must be on the GPU"   # :502
+    bsz = query_states.shape[0]
+    L_q = query_states.shape[2]
+    L_k = key_states.shape[2]
+    H = query_states.shape[1]
+    if L_k < block_size * _MIN_BLOCKS:                                 # :509-519
+        o = block_sparse_attention(query_states, key_states, value_states,
+                                   block_size=block_size if block_size in (64, 128) else 128,
+                                   is_causal=True)
+        return o.reshape(bsz, L_q, -1)
+    if query_states.dtype not in (torch.bfloat16, torch.float16):
+        raise RuntimeError("FlashAttention only supports fp16 and bf16 data type")
+    sel = select_blocks(query_states, key_states, block_size=block_size, sink_ratio=sink_ratio,
+                        recent_ratio=recent_ratio, local_span_ratio=local_span_ratio,
+                        enable_correlation_mask=enable_correlation_mask,
+                        correlation_selection_mode=correlation_selection_mode,
+                        correlation_topk_ratio=correlation_topk_ratio, corr_threshold=corr_threshold,
+                        enable_column_mask=enable_column_mask, column_topk_ratio=column_topk_ratio,
+                        column_start_exclude_ratio=column_start_exclude_ratio,
+                        column_end_exclude_ratio=column_end_exclude_ratio,
+                        enable_last_block_mask=enable_last_block_mask,
+                        diag_sample_ratio=diag_sample_ratio, min_diag_samples=min_diag_samples,
+                        max_diag_samples=max_diag_samples, stripe_threshold=stripe_threshold,
+                        qk_topk_ratio=qk_topk_ratio)
+    o = block_sparse_attention(query_states, key_states, value_states, sel.blk_cnt, sel.blk_idx,
+                               block_size=block_size, is_causal=is_causal)
+    return o.reshape(bsz, L_q, H * query_states.shape[3])

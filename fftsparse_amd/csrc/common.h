@@ -1,0 +1,201 @@
+// Shared device helpers for the gfx950 kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "fftsparse_amd.h"
+
+namespace fs {
+
+// ---- element types --------------------------------------------------------
+struct bf16_t { uint16_t u; };
+struct f16_t { uint16_t u; };
+
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(bf16_t x) { return __uint_as_float((uint32_t)x.u << 16); }
+__device__ __forceinline__ float to_f32(f16_t x) {
+  _Float16 h;
+  __builtin_memcpy(&h, &x.u, 2);
+  return (float)h;
+}
+
+// fp32 -> bf16, round to nearest even (nan kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  _Float16 h = (_Float16)f;
+  uint16_t u;
+  __builtin_memcpy(&u, &h, 2);
+  return u;
+}
+
+template <typename T> struct Conv;
+template <> struct Conv<float> {
+  __device__ static float store(float f) { return f; }
+  __device__ static float round(float f) { return f; }
+};
+template <> struct Conv<bf16_t> {
+  __device__ static bf16_t store(float f) { return bf16_t{f32_to_bf16_bits(f)}; }
+  __device__ static float round(float f) { return to_f32(bf16_t{f32_to_bf16_bits(f)}); }
+};
+template <> struct Conv<f16_t> {
+  __device__ static f16_t store(float f) { return f16_t{f32_to_f16_bits(f)}; }
+  __device__ static float round(float f) { return to_f32(f16_t{f32_to_f16_bits(f)}); }
+};
+
+// Order-preserving map float -> uint32 (larger float -> larger key).
+__device__ __forceinline__ uint32_t order_key(float f) {
+  uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// ---- wave helpers (wave64) --------------------------------------------------
+__device__ __forceinline__ int lane_id() { return (int)__lane_id(); }
+
+__device__ __forceinline__ float wave_sum(float v) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ int wave_sum_i(int v) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_min(float v) {
+  for (int o = 32; o > 0; o >>= 1) v = fminf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// Number of set bits of a 64-bit lane mask below this lane.
+__device__ __forceinline__ int rank_below(uint64_t m) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                        __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+// nan-propagating clamp(x, min=lo) (torch.clamp keeps nan).
+__device__ __forceinline__ float clamp_min_nan(float x, float lo) { return x < lo ? lo : x; }
+
+// ---- block reductions (blockDim.x threads, scratch >= 32 floats) ----------
+template <typename F>
+__device__ float block_reduce(float v, float* scratch, F op, float ident) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
+  for (int o = 32; o > 0; o >>= 1) v = op(v, __shfl_xor(v, o, 64));
+  __syncthreads();
+  if (lane == 0) scratch[w] = v;
+  __syncthreads();
+  float r = ident;
+  for (int i = 0; i < nw; ++i) r = op(r, scratch[i]);
+  __syncthreads();
+  return r;
+}
+__device__ __forceinline__ float block_sum(float v, float* s) {
+  return block_reduce(v, s, [](float a, float b) { return a + b; }, 0.0f);
+}
+__device__ __forceinline__ float block_max(float v, float* s) {
+  return block_reduce(v, s, [](float a, float b) { return fmaxf(a, b); }, -INFINITY);
+}
+__device__ __forceinline__ float block_min(float v, float* s) {
+  return block_reduce(v, s, [](float a, float b) { return fminf(a, b); }, INFINITY);
+}
+__device__ __forceinline__ int block_sum_i(int v, int* scratch) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
+  v = wave_sum_i(v);
+  __syncthreads();
+  if (lane == 0) scratch[w] = v;
+  __syncthreads();
+  int r = 0;
+  for (int i = 0; i < nw; ++i) r += scratch[i];
+  __syncthreads();
+  return r;
+}
+
+__device__ __forceinline__ float key_to_f32(uint32_t key) {
+  return __uint_as_float((key & 0x80000000u) ? (key & 0x7fffffffu) : ~key);
+}
+
+// Block-wide top-k over vals[0..n): writes sel[i] = 1 for the k largest
+// values (ties to the lower index) and 0 elsewhere; returns the k-th largest
+// value.  k is clamped to [0, n].  The threshold key is found by a 32-step
+// bisection on the order-preserving uint32 key; equal keys are ranked in
+// index order by wave 0 with ballots.  All threads of the block must call.
+__device__ inline float block_topk_select(const float* vals, int n, int k, uint8_t* sel,
+                                          int* iscratch) {
+  const int tid = threadIdx.x, nt = blockDim.x;
+  if (k > n) k = n;
+  if (k <= 0) {
+    for (int i = tid; i < n; i += nt) sel[i] = 0;
+    __syncthreads();
+    return NAN;
+  }
+  uint32_t prefix = 0;
+  for (int b = 31; b >= 0; --b) {
+    const uint32_t cand = prefix | (1u << b);
+    int c = 0;
+    for (int i = tid; i < n; i += nt) c += order_key(vals[i]) >= cand;
+    c = block_sum_i(c, iscratch);
+    if (c >= k) prefix = cand;
+  }
+  int gt = 0;
+  for (int i = tid; i < n; i += nt) {
+    const bool g = order_key(vals[i]) > prefix;
+    gt += g;
+    sel[i] = g;
+  }
+  gt = block_sum_i(gt, iscratch);
+  const int need = k - gt;
+  if (tid < 64) {
+    int base = 0;
+    for (int c0 = 0; c0 < n && base < need; c0 += 64) {
+      const int i = c0 + tid;
+      const bool eq = i < n && order_key(vals[i]) == prefix;
+      const uint64_t m = __ballot(eq);
+      if (eq && base + rank_below(m) < need) sel[i] = 1;
+      base += __popcll(m);
+    }
+  }
+  __syncthreads();
+  return key_to_f32(prefix);
+}
+
+}  // namespace fs
+
+// host side ----------------------------------------------------------------
+namespace fs_host {
+void set_error(const char* fmt, ...);
+int launch_status(const char* what);
+
+// Allow a kernel more than the default 64 KiB of dynamic LDS (gfx950: 160 KiB).
+template <typename K>
+int allow_dynamic_lds(K kernel, size_t bytes, const char* what) {
+  if (bytes <= 65536) return 0;
+  const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+  if (e != hipSuccess) {
+    set_error("%s: cannot reserve %zu bytes of LDS: %s", what, bytes, hipGetErrorString(e));
+    return FS_ERR_LAUNCH;
+  }
+  return 0;
+}
+}  // namespace fs_host
+
+#define FS_CHECK_ARG(cond, ...)                 \
+  do {                                          \
+    if (!(cond)) {                              \
+      fs_host::set_error(__VA_ARGS__);          \
+      return FS_ERR_ARG;                        \
+    }                                           \
+  } while (0)
+#define FS_CHECK_SUPPORTED(cond, ...)           \
+  do {                                          \
+    if (!(cond)) {                              \
+      fs_host::set_error(__VA_ARGS__);          \
+      return FS_ERR_UNSUPPORTED;                \
+    }                                           \
+  } while (0)

@@ -1,0 +1,195 @@
+// Block-mask composition and per-row block lists
+// (reference: attn_src/fft_attn/my_attn_v7.py:542-550 prior, :558-560 last
+// row, :588-612 stripe/diffuse dynamic mask, :256-294 qk top-k, :623-641
+// columns; attn_src/fix_mask_attn/my_attn.py:39-79 for the fixed mask).
+//
+// One workgroup (4 waves) owns RPW consecutive query-block rows of one head.
+// A diffuse head first computes its score panel S[rows][0..last row] into LDS
+// (fp32 dot products, fixed order).  Each wave then walks one row at a time:
+// for a diffuse row it finds the k_i-th largest score by a 32-step bisection
+// on the ordered float key with wave-wide counts, and in a single ascending
+// pass over the key blocks it evaluates the membership rule 64 blocks at a
+// time, compacting the selected block indices with a ballot + mbcnt prefix.
+#include "common.h"
+
+namespace fs {
+
+constexpr int kSelThreads = 256;
+constexpr int kSelWaves = kSelThreads / 64;
+
+template <typename T>
+__global__ __launch_bounds__(kSelThreads) void select_kernel(fs_select_args a, int rows_per_wave,
+                                                             float inv_sqrt_d) {
+  extern __shared__ float panel[];       // [RPW][N] scores (diffuse heads) then [RPW][D] q rows
+  const int RPW = rows_per_wave * kSelWaves;
+  const int N = a.N, Nk = a.Nk, D = a.D;
+  const int chunks = (N + RPW - 1) / RPW;
+  const int h = blockIdx.x / chunks;
+  const int r0 = (blockIdx.x - h * chunks) * RPW;
+  const int hk = h / (a.Hq / a.Hk);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+  // ---- stripe / diffuse decision (:359-363); identical in every workgroup of the head
+  bool stripe = false;
+  if (a.dyn_mode == 1) {
+    float mv;
+    if (a.stripe_all_diffuse) {
+      mv = INFINITY;
+    } else {
+      float s = 0.f;
+      for (int i = 0; i < a.n_samples; ++i) s += a.diag_var[(int64_t)h * a.n_samples + i];
+      mv = s / (float)a.n_samples;
+      stripe = mv <= a.stripe_threshold;        // false for nan
+    }
+    if (r0 == 0 && tid == 0) {
+      if (a.mean_var) a.mean_var[h] = mv;
+      if (a.is_stripe) a.is_stripe[h] = stripe ? 1 : 0;
+    }
+  }
+  const bool diffuse = a.dyn_mode == 1 && !stripe;
+  const bool use_lags = a.dyn_mode == 1 && stripe;
+  const bool use_cols = a.col_mode == 2 || (a.col_mode == 1 && stripe);
+  const int rend = min(N, r0 + RPW);
+
+  if (diffuse) {
+    // ---- score panel S[i][j] = (q_b[i] . k_b[j]) * (1/sqrt(D)), j <= i (:234-249)
+    const T* qb = static_cast<const T*>(a.q_b) + (int64_t)h * N * D;
+    const T* kb = static_cast<const T*>(a.k_b) + (int64_t)hk * N * D;
+    float* qrows = panel + (size_t)RPW * N;
+    for (int e = tid; e < RPW * D; e += kSelThreads) {
+      const int rr = e / D, d = e - rr * D;
+      qrows[e] = (r0 + rr < N) ? to_f32(qb[(int64_t)(r0 + rr) * D + d]) : 0.f;
+    }
+    __syncthreads();
+    const int jmax = rend;                                   // columns 0 .. rend-1
+    for (int j = tid; j < jmax; j += kSelThreads) {
+      float acc[16];
+#pragma unroll
+      for (int rr = 0; rr < 16; ++rr) acc[rr] = 0.f;
+      const T* kr = kb + (int64_t)j * D;
+      for (int d = 0; d < D; ++d) {
+        const float kv = to_f32(kr[d]);
+#pragma unroll
+        for (int rr = 0; rr < 16; ++rr)
+          if (rr < RPW) acc[rr] += qrows[rr * D + d] * kv;
+      }
+#pragma unroll
+      for (int rr = 0; rr < 16; ++rr)
+        if (rr < RPW) panel[(size_t)rr * N + j] = acc[rr] * inv_sqrt_d;
+    }
+    __syncthreads();
+  }
+
+  const int lw = a.local_window;
+  const uint8_t* keep = a.keep_tau ? a.keep_tau + (int64_t)h * N : nullptr;
+  const uint8_t* cols = a.col_sel ? a.col_sel + (int64_t)h * N : nullptr;
+  const uint8_t* last = a.last_sel ? a.last_sel + (int64_t)h * N : nullptr;
+
+  for (int rr = wave; rr < RPW; rr += kSelWaves) {
+    const int i = r0 + rr;
+    if (i >= N) break;
+    const int jlim = a.mask_causal ? min(i + 1, Nk) : Nk;
+    const float* srow = panel + (size_t)rr * N;
+    // ---- diffuse row: k_i-th largest of S[i][0..i] (:271-276)
+    uint32_t thr = 0;
+    int need = 0;
+    if (diffuse) {
+      int k = (int)((float)(i + 1) * a.qk_topk_ratio);
+      if (k < 1) k = 1;
+      const int n = i + 1;
+      if (k > n) k = n;
+      uint32_t prefix = 0;
+      for (int b = 31; b >= 0; --b) {
+        const uint32_t cand = prefix | (1u << b);
+        int c = 0;
+        for (int j = lane; j < n; j += 64) c += order_key(srow[j]) >= cand;
+        c = wave_sum_i(c);
+        if (c >= k) prefix = cand;
+      }
+      int gt = 0;
+      for (int j = lane; j < n; j += 64) gt += order_key(srow[j]) > prefix;
+      gt = wave_sum_i(gt);
+      thr = prefix;
+      need = k - gt;
+    }
+    // ---- membership + compaction in ascending block order
+    uint16_t* out = a.blk_idx + ((int64_t)h * N + i) * Nk;
+    int cnt = 0, eq_seen = 0;
+    for (int j0 = 0; j0 < jlim; j0 += 64) {
+      const int j = j0 + lane;
+      const bool valid = j < jlim;
+      bool in = false;
+      bool eq = false;
+      if (valid) {
+        // prior (:83-95): sink | recent | local window
+        in = j < a.keep_sink || j >= Nk - a.keep_recent || (lw > 0 && abs(i - j) <= lw);
+        if (last && i == N - 1 && last[j]) in = true;
+        if (use_lags) {
+          const int t = i - j;
+          if (t >= a.remote_start && j >= a.keep_sink && keep[t]) in = true;
+        }
+        if (diffuse && j <= i) {
+          const uint32_t key = order_key(srow[j]);
+          if (key > thr) in = true;
+          eq = key == thr;
+        }
+        if (use_cols && j <= i && cols[j]) in = true;
+      }
+      if (diffuse) {
+        const uint64_t me = __ballot(eq);
+        if (eq && eq_seen + rank_below(me) < need) in = true;
+        eq_seen += __popcll(me);
+      }
+      const uint64_t m = __ballot(in);
+      if (in) out[cnt + rank_below(m)] = (uint16_t)j;
+      cnt += __popcll(m);
+    }
+    if (lane == 0) a.blk_cnt[(int64_t)h * N + i] = cnt;
+  }
+}
+
+template <typename T>
+static int launch_select(const fs_select_args& a, unsigned grid, size_t smem, int rows_per_wave,
+                         float inv_sqrt_d, hipStream_t s) {
+  if (int rc = fs_host::allow_dynamic_lds(select_kernel<T>, smem, "fs_select")) return rc;
+  select_kernel<T><<<grid, kSelThreads, smem, s>>>(a, rows_per_wave, inv_sqrt_d);
+  return 0;
+}
+
+}  // namespace fs
+
+using namespace fs;
+
+extern "C" int fs_select(const fs_select_args* a, void* stream) {
+  FS_CHECK_ARG(a != nullptr, "fs_select: null args");
+  FS_CHECK_ARG(a->blk_cnt && a->blk_idx, "fs_select: null output");
+  FS_CHECK_ARG(a->Hq > 0 && a->Hk > 0 && a->Hq % a->Hk == 0, "fs_select: bad head counts");
+  FS_CHECK_ARG(a->N >= 1 && a->Nk >= 1 && a->Nk <= 65535, "fs_select: bad block counts");
+  FS_CHECK_ARG(a->dyn_mode == 0 || a->dyn_mode == 1, "fs_select: bad dyn_mode");
+  FS_CHECK_ARG(a->col_mode >= 0 && a->col_mode <= 2, "fs_select: bad col_mode");
+  FS_CHECK_ARG(a->dyn_mode == 0 || (a->q_b && a->k_b && a->keep_tau &&
+                                    (a->stripe_all_diffuse || (a->diag_var && a->n_samples > 0))),
+               "fs_select: dynamic mask inputs missing");
+  FS_CHECK_ARG(a->col_mode == 0 || a->col_sel, "fs_select: col_sel missing");
+  FS_CHECK_ARG(a->col_mode != 1 || a->dyn_mode == 1, "fs_select: col_mode 1 needs dyn_mode 1");
+  FS_CHECK_ARG((a->dyn_mode == 0 && a->col_mode == 0 && a->last_sel == nullptr) || a->N == a->Nk,
+               "fs_select: dynamic, column and last-row masks need N == Nk");
+  FS_CHECK_SUPPORTED(a->N <= 4096 && (a->dyn_mode == 0 || a->D <= 256), "fs_select: N=%d too large", a->N);
+  const int rows_per_wave = a->N <= 1024 ? 4 : (a->N <= 2048 ? 2 : 1);
+  const int RPW = rows_per_wave * kSelWaves;
+  const int chunks = (a->N + RPW - 1) / RPW;
+  const float inv_sqrt_d = a->D > 0 ? 1.0f / (float)sqrt((double)a->D) : 1.0f;
+  const size_t smem = a->dyn_mode == 1 ? (size_t)RPW * (a->N + a->D) * sizeof(float) : 0;
+  hipStream_t s = (hipStream_t)stream;
+  const unsigned grid = (unsigned)(a->Hq * chunks);
+  const int dt = a->dyn_mode == 1 ? a->dtype : FS_DTYPE_F32;
+  int rc = 0;
+  switch (dt) {
+    case FS_DTYPE_F32: rc = launch_select<float>(*a, grid, smem, rows_per_wave, inv_sqrt_d, s); break;
+    case FS_DTYPE_BF16: rc = launch_select<bf16_t>(*a, grid, smem, rows_per_wave, inv_sqrt_d, s); break;
+    case FS_DTYPE_F16: rc = launch_select<f16_t>(*a, grid, smem, rows_per_wave, inv_sqrt_d, s); break;
+    default: fs_host::set_error("fs_select: dtype %d unsupported", a->dtype); return FS_ERR_UNSUPPORTED;
+  }
+  if (rc) return rc;
+  return fs_host::launch_status("fs_select");
+}

@@ -1,0 +1,145 @@
+// Per-head statistics on the pooled blocks:
+//   diagonal statistics for the stripe/diffuse test  (my_attn_v7.py:301-363)
+//   column scores and their top-n                     (my_attn_v7.py:390-447)
+//   last-query-row scores and their top-k             (my_attn_v7.py:54-72)
+//
+// Grid (Hq, 2 + n_samples): y == 0 is the column task, y == 1 the last-row
+// task and y >= 2 the diagonal sample y - 2.  All arithmetic is fp32 with a
+// fixed accumulation order.
+#include "common.h"
+
+namespace fs {
+
+constexpr int kStatThreads = 256;
+constexpr int kColChunk = 8;
+
+template <typename T>
+__device__ __forceinline__ float dot_rows(const T* a, const T* b, int D) {
+  float s = 0.f;
+  for (int d = 0; d < D; ++d) s += to_f32(a[d]) * to_f32(b[d]);
+  return s;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kStatThreads) void stats_kernel(fs_stats_args a, float inv_sqrt_d) {
+  extern __shared__ float sm[];          // N floats (+ column scratch)
+  __shared__ float red[32];
+  __shared__ int ired[32];
+  const int h = blockIdx.x, task = blockIdx.y, tid = threadIdx.x;
+  const int N = a.N, D = a.D;
+  const int hk = h / (a.Hq / a.Hk);
+  const T* qb = static_cast<const T*>(a.q_b) + (int64_t)h * N * D;
+  const T* kb = static_cast<const T*>(a.k_b) + (int64_t)hk * N * D;
+
+  if (task == 0) {
+    // ---- column scores (:404-420) and top-n over [col_start, col_end) (:422-438)
+    if (a.n_cols <= 0) return;
+    float* colv = sm;                               // [N]
+    float* prod = sm + N;                           // [kColChunk][D]
+    float* tot = prod + kColChunk * D;              // [D]
+    if (tid < D) {
+      float s = 0.f;
+      for (int i = 0; i <= N - 2; ++i) s += to_f32(qb[(int64_t)i * D + tid]);
+      tot[tid] = s;                                  // cumsum[N-2]
+    }
+    float run = 0.f;                                 // cumsum[j-1]
+    for (int j0 = 0; j0 < N; j0 += kColChunk) {
+      __syncthreads();
+      if (tid < D) {
+        for (int jj = 0; jj < kColChunk; ++jj) {
+          const int j = j0 + jj;
+          if (j >= N) break;
+          const float partial = (j == N - 1) ? 0.f : tot[tid] - run;
+          prod[jj * D + tid] = partial * to_f32(kb[(int64_t)j * D + tid]);
+          run += to_f32(qb[(int64_t)j * D + tid]);
+        }
+      }
+      __syncthreads();
+      const int w = tid >> 6, lane = tid & 63;
+      for (int jj = w; jj < kColChunk; jj += kStatThreads / 64) {
+        const int j = j0 + jj;
+        if (j >= N) break;
+        float v = 0.f;
+        for (int d = lane; d < D; d += 64) v += prod[jj * D + d];
+        v = wave_sum(v);
+        if (lane == 0) colv[j] = (v * inv_sqrt_d) / (float)max(1, N - j - 1);
+      }
+    }
+    __syncthreads();
+    for (int j = tid; j < N; j += kStatThreads) {
+      if (a.col_mean) a.col_mean[(int64_t)h * N + j] = colv[j];
+      if (j < a.col_start || j >= a.col_end) a.col_sel[(int64_t)h * N + j] = 0;
+    }
+    const int cs = a.col_start, nv = a.col_end - a.col_start;
+    block_topk_select(colv + cs, nv, a.n_cols, a.col_sel + (int64_t)h * N + cs, ired);
+    return;
+  }
+  if (task == 1) {
+    // ---- last query row (:61-70): einsum in the input dtype, top-k
+    if (a.last_k <= 0) return;
+    float* lv = sm;
+    const T* ql = qb + (int64_t)(N - 1) * D;
+    for (int j = tid; j < N; j += kStatThreads) {
+      const float s = Conv<T>::round(dot_rows(ql, kb + (int64_t)j * D, D));
+      lv[j] = s;
+      a.last_scores[(int64_t)h * N + j] = s;
+    }
+    __syncthreads();
+    block_topk_select(lv, N, a.last_k, a.last_sel + (int64_t)h * N, ired);
+    return;
+  }
+  // ---- diagonal sample (:342-349)
+  const int si = task - 2;
+  if (si >= a.n_samples) return;
+  const int tau = a.sample_taus[si];
+  float* dv = sm;
+  // diagonal length minus the dropped last element; an out-of-range lag reads nothing
+  const int nd = (tau >= 0 && tau < N) ? N - tau - 1 : 0;
+  for (int j = tid; j < nd; j += kStatThreads)
+    dv[j] = dot_rows(qb + (int64_t)(j + tau) * D, kb + (int64_t)j * D, D) * inv_sqrt_d;
+  __syncthreads();
+  float sabs = 0.f;
+  for (int j = tid; j < nd; j += kStatThreads) sabs += fabsf(dv[j]);
+  const float mean_abs = block_sum(sabs, red) / (float)nd;
+  const int ne = nd - 1;
+  float se = 0.f;
+  for (int j = tid; j < ne; j += kStatThreads) se += dv[j + 1] - dv[j];
+  const float mean_e = block_sum(se, red) / (float)ne;
+  float sq = 0.f;
+  for (int j = tid; j < ne; j += kStatThreads) {
+    const float e = (dv[j + 1] - dv[j]) - mean_e;
+    sq += e * e;
+  }
+  const float var = block_sum(sq, red) / (float)(ne - 1);
+  if (tid == 0) a.diag_var[(int64_t)h * a.n_samples + si] = var / clamp_min_nan(mean_abs, 1e-6f);
+}
+
+}  // namespace fs
+
+using namespace fs;
+
+extern "C" int fs_stats(const fs_stats_args* a, void* stream) {
+  FS_CHECK_ARG(a != nullptr, "fs_stats: null args");
+  FS_CHECK_ARG(a->q_b && a->k_b, "fs_stats: null pooled pointer");
+  FS_CHECK_ARG(a->Hq > 0 && a->Hk > 0 && a->Hq % a->Hk == 0, "fs_stats: bad head counts");
+  FS_CHECK_ARG(a->N >= 1 && a->D >= 1 && a->D <= 256, "fs_stats: bad sizes");
+  FS_CHECK_ARG(a->n_samples >= 0 && (a->n_samples == 0 || (a->sample_taus && a->diag_var)),
+               "fs_stats: sample arrays missing");
+  FS_CHECK_ARG(a->n_cols <= 0 || (a->col_sel && a->col_start >= 0 && a->col_end <= a->N &&
+                                  a->col_end > a->col_start && a->n_cols <= a->col_end - a->col_start),
+               "fs_stats: bad column range");
+  FS_CHECK_ARG(a->last_k <= 0 || (a->last_sel && a->last_scores && a->last_k <= a->N),
+               "fs_stats: bad last-row arguments");
+  FS_CHECK_SUPPORTED(a->N <= 4096, "fs_stats: N=%d > 4096", a->N);
+  const float inv_sqrt_d = 1.0f / (float)sqrt((double)a->D);
+  const size_t smem = (size_t)(a->N + kColChunk * a->D + a->D) * sizeof(float);
+  dim3 grid(a->Hq, 2 + a->n_samples);
+  hipStream_t s = (hipStream_t)stream;
+  switch (a->dtype) {
+    case FS_DTYPE_F32: stats_kernel<float><<<grid, kStatThreads, smem, s>>>(*a, inv_sqrt_d); break;
+    case FS_DTYPE_BF16: stats_kernel<bf16_t><<<grid, kStatThreads, smem, s>>>(*a, inv_sqrt_d); break;
+    case FS_DTYPE_F16: stats_kernel<f16_t><<<grid, kStatThreads, smem, s>>>(*a, inv_sqrt_d); break;
+    default: fs_host::set_error("fs_stats: dtype %d unsupported", a->dtype); return FS_ERR_UNSUPPORTED;
+  }
+  return fs_host::launch_status("fs_stats");
+}

@@ -1,0 +1,169 @@
+/*
+ * fftsparse_amd -- C ABI of the MI355X (gfx950) FFTSparse prefill path.
+ *
+ * Plain pointers, sizes and strides only.  Every pointer named "device" is
+ * device memory owned by the caller; every entry point is stream-ordered on
+ * the given hipStream_t (passed as void*), launches kernels only, allocates
+ * nothing and never synchronises the host.  Return value: FS_OK (0) or a
+ * negative status; fs_last_error() then describes the failure (thread-local).
+ *
+ * Reference interfaces replaced (paths relative to the FFTSparse repository):
+ *   fs_pool      block_mean_pool              attn_src/fft_attn/my_attn_v7.py:105-114 (call :553-555)
+ *   fs_corr      batch_fft_cross_correlation  my_attn_v7.py:117-157
+ *                + threshold lag selection     my_attn_v7.py:190-208 (create_correlation_block_mask)
+ *   fs_stats     compute_stripe_variance      my_attn_v7.py:301-363 (diagonal statistics)
+ *                create_column_block_mask     my_attn_v7.py:390-447 (column scores + top-n)
+ *                create_last_block_query_mask my_attn_v7.py:54-72
+ *   fs_select    mask composition             my_attn_v7.py:542-550, 588-641 (prior | dynamic | column)
+ *                create_qk_topk_block_mask    my_attn_v7.py:256-294 (diffuse heads)
+ *                create_deterministic_block_mask attn_src/fix_mask_attn/my_attn.py:39-79 (fixed role)
+ *                The dense [1,H,N,N] bool mask the reference hands to the
+ *                kernel (my_attn_v7.py:710,780) is replaced by per-row lists
+ *                of selected key blocks.
+ *   fs_bsattn    block_sparse_attn_func call  my_attn_v7.py:775-786, fix_mask_attn/my_attn.py:196-207
+ *                flash_attn_func(causal=True) my_attn_v7.py:509-519 (blk_cnt == NULL: dense causal)
+ */
+#ifndef FFTSPARSE_AMD_H
+#define FFTSPARSE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#if defined(__GNUC__)
+#define FS_API __attribute__((visibility("default")))
+#else
+#define FS_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { FS_DTYPE_F32 = 0, FS_DTYPE_BF16 = 1, FS_DTYPE_F16 = 2 };
+
+enum {
+  FS_OK = 0,
+  FS_ERR_ARG = -1,          /* invalid argument (shape, stride, null pointer) */
+  FS_ERR_UNSUPPORTED = -2,  /* valid but not implemented (dtype, head dim, size) */
+  FS_ERR_LAUNCH = -3        /* the HIP runtime rejected a launch */
+};
+
+/* ---- block pooling (my_attn_v7.py:105-114) ------------------------------
+ * q: [Hq, L, D] view with element strides (q_sh, q_sl), d contiguous.
+ * k: [Hk, L, D] likewise.  Outputs q_b [Hq][N][D], k_b [Hk][N][D] in dtype,
+ * N = ceil(L / bs): mean of each bs-token block, zero padding, divisor bs. */
+typedef struct {
+  const void* q; int64_t q_sh, q_sl;
+  const void* k; int64_t k_sh, k_sl;
+  int dtype, Hq, Hk, L, D, bs;
+  void* q_b;
+  void* k_b;
+} fs_pool_args;
+FS_API int fs_pool(const fs_pool_args* a, void* stream);
+
+/* ---- FFT lag correlation + lag selection (my_attn_v7.py:117-208) --------
+ * For query head h (key head h / (Hq/Hk)):
+ *   corr_sum[h][t] = sum_i <q_b[h][i], k_b[hk][i-t]>  via zero-padded FFTs,
+ *   corr[h][t]     = post-processed value (my_attn_v7.py:134-155),
+ *   keep_tau[h][t] = 1 iff t >= remote_start and
+ *                    corr[h][t] / max(max_{t'>=rs} corr[h][t'], 1e-6) >= corr_threshold.
+ * work: fs_corr_work_bytes(Hq, N, D) bytes of device scratch. */
+typedef struct {
+  const void* q_b; const void* k_b;
+  int dtype, Hq, Hk, N, D;
+  int local_window, keep_sink, remote_start;
+  float corr_threshold;
+  void* work;
+  float* corr;          /* [Hq][N] */
+  float* corr_sum;      /* [Hq][N] */
+  uint8_t* keep_tau;    /* [Hq][N] */
+} fs_corr_args;
+FS_API size_t fs_corr_work_bytes(int Hq, int N, int D);
+FS_API int fs_corr(const fs_corr_args* a, void* stream);
+
+/* ---- per-head statistics (my_attn_v7.py:301-363, 390-447, 54-72) --------
+ * diag_var[h][s]  = var(diff(diag_{tau_s}[:-1])) / clamp(mean|diag_{tau_s}[:-1]|, 1e-6)
+ *                   over S = q_b k_b^T / sqrt(D), unbiased variance;
+ * col_mean[h][j]  = (sum_{i=j}^{N-2} q_b[h][i]) . k_b[hk][j] / sqrt(D) / max(1, N-j-1);
+ * col_sel[h][j]   = 1 for the n_cols largest col_mean in [col_start, col_end);
+ * last_scores[h][j] = <q_b[h][N-1], k_b[hk][j]> rounded to dtype;
+ * last_sel[h][j]  = 1 for the last_k largest last_scores.
+ * Ties in the top-n selections go to the lower index.
+ * sample_taus: device int32[n_samples]; n_samples == 0 skips diag_var;
+ * n_cols == 0 skips the columns; last_k == 0 skips the last row. */
+typedef struct {
+  const void* q_b; const void* k_b;
+  int dtype, Hq, Hk, N, D;
+  const int32_t* sample_taus; int n_samples;
+  int col_start, col_end, n_cols;
+  int last_k;
+  float* diag_var;       /* [Hq][n_samples] */
+  float* col_mean;       /* [Hq][N] */
+  uint8_t* col_sel;      /* [Hq][N] */
+  float* last_scores;    /* [Hq][N] */
+  uint8_t* last_sel;     /* [Hq][N] */
+} fs_stats_args;
+FS_API int fs_stats(const fs_stats_args* a, void* stream);
+
+/* ---- mask composition -> per-row block lists ----------------------------
+ * Row i of head h selects key block j (0 <= j < Nk, and j <= i if mask_causal) iff
+ *   prior:  j < keep_sink || j >= Nk - keep_recent || (local_window > 0 && |i-j| <= local_window)
+ *   last:   last_sel && i == N-1 && last_sel[h][j]
+ *   dyn_mode 1, stripe head:  t = i-j >= remote_start && j >= keep_sink && keep_tau[h][t]
+ *   dyn_mode 1, diffuse head: S[h][i][j] among the top k_i of S[h][i][0..i],
+ *                             k_i = max(1, trunc(float(i+1) * qk_topk_ratio)), ties -> lower j
+ *   column: col_mode 2, or col_mode 1 and stripe head: col_sel[h][j] && j <= i
+ * with is_stripe[h] = mean_s(diag_var[h][s]) <= stripe_threshold (false when
+ * stripe_all_diffuse or the mean is nan).  Output: blk_cnt[h][i] and the
+ * selected j in ascending order at blk_idx[(h*N + i) * Nk ...]. */
+typedef struct {
+  const void* q_b; const void* k_b;
+  int dtype, Hq, Hk, N, Nk, D;
+  int mask_causal;
+  int keep_sink, keep_recent, local_window, remote_start;
+  int dyn_mode;                 /* 0: none, 1: stripe -> lags, diffuse -> qk top-k */
+  int stripe_all_diffuse;
+  const float* diag_var; int n_samples; float stripe_threshold;
+  const uint8_t* keep_tau;
+  float qk_topk_ratio;
+  int col_mode;                 /* 0: none, 1: stripe heads, 2: all heads */
+  const uint8_t* col_sel;
+  const uint8_t* last_sel;      /* NULL: no last-row mask */
+  float* mean_var;              /* [Hq] out (may be NULL) */
+  uint8_t* is_stripe;           /* [Hq] out (may be NULL) */
+  int32_t* blk_cnt;             /* [Hq][N] */
+  uint16_t* blk_idx;            /* [Hq][N][Nk] */
+} fs_select_args;
+FS_API int fs_select(const fs_select_args* a, void* stream);
+
+/* ---- block-sparse attention prefill --------------------------------------
+ * out[b][t][h] = softmax(q[b][h][t] . k[b][hk][s] * scale) v[b][hk][s] over the
+ * key tokens s of the selected key blocks of query block t / bs (and s <= t +
+ * Lk - Lq when is_causal).  blk_cnt == NULL selects every key block up to the
+ * causal limit (dense causal attention).  Supported: dtype bf16/f16, D == 128,
+ * bs in {64, 128}.  All tensors are strided views with d contiguous. */
+typedef struct {
+  const void* q; int64_t q_sb, q_sh, q_sl;
+  const void* k; int64_t k_sb, k_sh, k_sl;
+  const void* v; int64_t v_sb, v_sh, v_sl;
+  void* out; int64_t o_sb, o_sh, o_sl;
+  int dtype, B, Hq, Hk, Lq, Lk, D, bs;
+  int is_causal;
+  float softmax_scale;
+  const int32_t* blk_cnt;       /* [Hq][Nq] or NULL (B must be 1 when non-NULL) */
+  const uint16_t* blk_idx;      /* [Hq][Nq][Nk] */
+} fs_attn_args;
+FS_API int fs_bsattn(const fs_attn_args* a, void* stream);
+
+/* Description of the last failure on this thread ("" if none). */
+FS_API const char* fs_last_error(void);
+/* sizeof the argument struct: 0 pool, 1 corr, 2 stats, 3 select, 4 attn
+ * (lets a foreign-function binding check its struct layout). */
+FS_API size_t fs_sizeof_args(int which);
+/* ABI version of this library (increments on any struct change). */
+FS_API int fs_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FFTSPARSE_AMD_H */

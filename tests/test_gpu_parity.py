@@ -1,0 +1,295 @@
+"""GPU parity: the HIP path (through the C ABI) against the CPU oracle.
+
+Bars: block decisions exact except those within 1e-3
+relative of their selection threshold, >= 99.9% of all causal decisions;
+attention under the reference mask within max-abs 2e-2 and mean-abs 1e-3 of
+fp32 attention; integer outputs (block lists) bit-exact and deterministic.
+"""
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from fftsparse_amd import block_sparse_attention, fix_mask, myattn_prefill, select_blocks
+from fftsparse_amd.synth import make_qkv, make_config
+from oracle import v7
+from tests.helpers import BAND, MATCH_MIN, PROD, block_match, lists_from_mask
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+def _gpu(*ts):
+    return [t.to(DEV) for t in ts]
+
+
+def _orig_layout(xb, Hq):
+    """GPU pooled [H,N,D] -> oracle layout [N,Hq,D] (key heads repeated)."""
+    H = xb.shape[0]
+    x = xb.permute(1, 0, 2).cpu()
+    return x.repeat_interleave(Hq // H, dim=1) if H != Hq else x
+
+
+def _print_case(case, **kw):
+    print(f"[case] {case} " + " ".join(f"{k}={v}" for k, v in kw.items()), flush=True)
+
+
+# --------------------------------------------------------------------------- pooling
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("L,bs", [(8192, 128), (5000, 128), (4096, 64)])
+def test_pool_parity(dtype, L, bs):
+    _print_case("pool", dtype=dtype, L=L, bs=bs)
+    q, k, _ = make_qkv(L, 4, 2, dtype=dtype, seed=1)
+    sel = select_blocks(*_gpu(q, k), **{**PROD, "block_size": bs}, keep_intermediates=True)
+    torch.cuda.synchronize()
+    ref_q = v7.block_mean_pool(v7.to_lhd(q), bs)
+    ref_k = v7.block_mean_pool(v7.to_lhd(k), bs)
+    for got, ref in ((sel.q_b, ref_q), (sel.k_b, ref_k)):
+        got = got.permute(1, 0, 2).cpu()
+        if dtype == torch.float32:
+            torch.testing.assert_close(got, ref, rtol=2e-6, atol=1e-7)
+        else:
+            # one rounding of an fp32 sum: at most one ulp apart, almost always equal
+            gi = got.view(torch.int16).to(torch.int32)
+            ri = ref.view(torch.int16).to(torch.int32)
+            assert (gi - ri).abs().max().item() <= 1
+            assert (gi == ri).float().mean().item() >= 0.999
+
+
+# --------------------------------------------------------------------------- FFT correlation
+@pytest.mark.parametrize("dtype,L,Hq,Hk", [(torch.float32, 8192, 4, 1), (torch.bfloat16, 32768, 8, 2),
+                                         (torch.bfloat16, 20000, 4, 4)])
+def test_corr_parity(dtype, L, Hq, Hk):
+    _print_case("corr", dtype=dtype, L=L, Hq=Hq, Hk=Hk)
+    q, k, _ = make_qkv(L, Hq, Hk, dtype=dtype, seed=2)
+    sel = select_blocks(*_gpu(q, k), **PROD, keep_intermediates=True)
+    torch.cuda.synchronize()
+    p = sel.params
+    Qb, Kb = _orig_layout(sel.q_b, Hq), _orig_layout(sel.k_b, Hq)
+    corr_ref, corr_sum_ref = v7.fft_lag_correlation(Qb, Kb, p.local_window, p.keep_sink)
+    # closed form: the lag sums are the diagonal sums of Q_b K_b^T
+    S = torch.einsum("ihd,jhd->hij", Qb.double(), Kb.double())
+    diag = torch.stack([torch.diagonal(S, offset=-t, dim1=1, dim2=2).sum(-1) for t in range(p.N)], -1)
+    scale = diag.abs().max().item()
+    assert (sel.corr_sum.cpu().double() - diag).abs().max().item() <= 2e-5 * scale
+    assert (corr_sum_ref.double() - diag).abs().max().item() <= 2e-5 * scale
+    keep_ref, norm_ref = v7.correlation_keep(corr_ref, p.remote_start, PROD["corr_threshold"])
+    keep = sel.keep_tau.cpu().bool()
+    diff = keep != keep_ref
+    near = ((norm_ref - PROD["corr_threshold"]).abs() <= BAND * PROD["corr_threshold"])
+    assert not (diff & ~near).any(), f"lag decisions differ outside the band: {torch.nonzero(diff & ~near)}"
+    cmax = corr_ref[:, p.remote_start:].abs().max()
+    torch.testing.assert_close(sel.corr.cpu(), corr_ref, rtol=0, atol=float(2e-4 * cmax))
+
+
+# --------------------------------------------------------------------------- statistics
+@pytest.mark.parametrize("dtype,L,Hq,Hk", [(torch.float32, 8192, 4, 1), (torch.bfloat16, 32768, 8, 2)])
+def test_stats_parity(dtype, L, Hq, Hk):
+    _print_case("stats", dtype=dtype, L=L)
+    q, k, _ = make_qkv(L, Hq, Hk, dtype=dtype, seed=3)
+    sel = select_blocks(*_gpu(q, k), **PROD, keep_intermediates=True)
+    torch.cuda.synchronize()
+    p = sel.params
+    Qb, Kb = _orig_layout(sel.q_b, Hq), _orig_layout(sel.k_b, Hq)
+    S = v7.block_scores(Qb, Kb)
+    # per-sample normalised diagonal variance
+    for si, tau in enumerate(p.sample_taus):
+        dv = torch.diagonal(S, offset=-tau, dim1=1, dim2=2)[:, :-1].double()
+        ref = dv.diff(dim=-1).var(dim=-1) / dv.abs().mean(-1).clamp(min=1e-6)
+        torch.testing.assert_close(sel.diag_var[:, si].cpu().double(), ref, rtol=2e-4, atol=1e-9)
+    mv_ref, st_ref = v7.stripe_variance(S, p.remote_start, p.sample_taus, PROD["stripe_threshold"],
+                                        p.stripe_all_diffuse)
+    torch.testing.assert_close(sel.mean_var.cpu(), mv_ref, rtol=2e-4, atol=1e-9)
+    # column scores + top-n
+    cm_ref = v7.column_scores(Qb, Kb)
+    scale = cm_ref.abs().max().item()
+    torch.testing.assert_close(sel.col_mean.cpu(), cm_ref, rtol=0, atol=2e-5 * scale)
+    cs_ref, kth = v7.column_select(cm_ref, p)
+    diff = sel.col_sel.cpu().bool() != cs_ref
+    near = (cm_ref - kth[:, None]).abs() <= BAND * kth.abs()[:, None]
+    assert not (diff & ~near).any()
+    # last row: scores rounded to the input dtype (one rounding apart at most)
+    ls_ref = v7.last_row_scores(Qb, Kb).float()
+    gs = sel.last_scores.cpu()
+    torch.testing.assert_close(gs, ls_ref, rtol=8e-3 if dtype != torch.float32 else 1e-5, atol=1e-6)
+    sel_ref, _, kth = v7.last_row_topk(Qb, Kb, p.last_k)
+    diff = sel.last_sel.cpu().bool() != sel_ref
+    near = ((ls_ref - kth[:, None]).abs() <= BAND * kth.abs()[:, None]) | (gs != ls_ref)
+    assert not (diff & ~near).any()
+
+
+# --------------------------------------------------------------------------- full selection
+SEL_CASES = [
+    ("c0", dict()),
+    ("c0-diffuse", dict(stripe_threshold=0.0)),
+    ("c0-nocorr", dict(enable_correlation_mask=False)),
+    ("c0-nocol-nolast", dict(enable_column_mask=False, enable_last_block_mask=False)),
+    ("c0-defaults", "defaults"),
+    ("c0-T0.95", dict(corr_threshold=0.95)),
+]
+
+
+@pytest.mark.parametrize("name,over", SEL_CASES)
+def test_selection_parity_c0(name, over):
+    _print_case("selection", name=name)
+    q, k, _ = make_config("c0")
+    kw = {} if over == "defaults" else {**PROD, **over}
+    sel = select_blocks(*_gpu(q, k), **kw)
+    ref = v7.select_mask(q, k, **kw)
+    frac, exact, unexc = block_match(sel.dense_mask(), ref.mask, ref.excusable)
+    print(f"  match={frac:.6f} exact={exact:.6f} unexcused={unexc}")
+    assert frac >= MATCH_MIN
+    if ref.is_stripe is not None:
+        gs = sel.is_stripe.cpu().bool()
+        near = (ref.mean_var - PROD["stripe_threshold"]).abs() <= BAND * PROD["stripe_threshold"]
+        assert not ((gs != ref.is_stripe) & ~near).any()
+
+
+@pytest.mark.parametrize("L,Hq,Hk,bs,dtype,over", [
+    (32768, 32, 8, 128, torch.bfloat16, {}),                     # config 1 shape
+    (32768, 8, 2, 128, torch.bfloat16, dict(stripe_threshold=0.0)),
+    (24000, 7, 1, 64, torch.bfloat16, {}),                       # ragged L, bs 64, GQA 7
+    (16384, 4, 4, 128, torch.float16, dict(corr_threshold=0.5)),
+])
+def test_selection_parity_bf16(L, Hq, Hk, bs, dtype, over):
+    _print_case("selection", L=L, Hq=Hq, Hk=Hk, bs=bs, dtype=dtype, over=over)
+    q, k, _ = make_qkv(L, Hq, Hk, dtype=dtype, seed=4)
+    kw = {**PROD, "block_size": bs, **over}
+    sel = select_blocks(*_gpu(q, k), **kw)
+    ref = v7.select_mask(q, k, **kw)
+    frac, exact, unexc = block_match(sel.dense_mask(), ref.mask, ref.excusable)
+    print(f"  match={frac:.6f} exact={exact:.6f} unexcused={unexc}")
+    assert frac >= MATCH_MIN
+
+
+def test_block_lists_are_ascending_and_deterministic():
+    q, k, _ = make_qkv(32768, 8, 2, seed=5)
+    qg, kg = _gpu(q, k)
+    a = select_blocks(qg, kg, **PROD)
+    b = select_blocks(qg, kg, **PROD)
+    assert torch.equal(a.blk_cnt, b.blk_cnt)
+    assert torch.equal(a.blk_idx.view(torch.int16), b.blk_idx.view(torch.int16))
+    N = a.params.N
+    cnt = a.blk_cnt.cpu()
+    idx = a.blk_idx.view(torch.int16).cpu().to(torch.int64)
+    for h in range(cnt.shape[0]):
+        for i in range(0, N, 17):
+            row = idx[h, i, : cnt[h, i]]
+            assert bool((row[1:] > row[:-1]).all()) and int(row[-1]) == i and int(row[0]) == 0
+
+
+# --------------------------------------------------------------------------- attention
+def _attn_check(out, ref, rows=None):
+    o = out.float().cpu()
+    if rows is not None:
+        o, ref = o[rows], ref[rows]
+    err = (o - ref).abs()
+    print(f"  max_abs={err.max().item():.3e} mean_abs={err.mean().item():.3e}")
+    assert err.max().item() <= 2e-2
+    assert err.mean().item() <= 1e-3
+
+
+@pytest.mark.parametrize("L,Hq,Hk,bs,dtype", [
+    (8192, 4, 1, 128, torch.bfloat16),
+    (6000, 4, 2, 128, torch.bfloat16),
+    (4096, 4, 1, 64, torch.bfloat16),
+    (8192, 4, 4, 128, torch.float16),
+])
+def test_attention_parity_reference_mask(L, Hq, Hk, bs, dtype):
+    """Stage 2 alone, under the oracle's mask."""
+    _print_case("attention", L=L, Hq=Hq, Hk=Hk, bs=bs, dtype=dtype)
+    q, k, v = make_qkv(L, Hq, Hk, dtype=dtype, seed=6)
+    ref_sel = v7.select_mask(q, k, **{**PROD, "block_size": bs})
+    cnt, idx = lists_from_mask(ref_sel.mask, DEV)
+    out = block_sparse_attention(*_gpu(q, k, v), cnt, idx, block_size=bs)
+    torch.cuda.synchronize()
+    ref = v7.block_sparse_attention(q, k, v, ref_sel.mask, bs)
+    _attn_check(out[0], ref)
+
+
+def test_attention_noncausal_and_dense():
+    q, k, v = make_qkv(2048, 4, 2, seed=7)
+    N = 16
+    mask = torch.rand(4, N, N, generator=torch.Generator().manual_seed(0)) < 0.3
+    mask |= torch.eye(N, dtype=torch.bool)
+    cnt, idx = lists_from_mask(mask, DEV)
+    out = block_sparse_attention(*_gpu(q, k, v), cnt, idx, block_size=128, is_causal=False)
+    ref = v7.block_sparse_attention(q, k, v, mask, 128, is_causal=False)
+    _attn_check(out[0], ref)
+    out = block_sparse_attention(*_gpu(q, k, v), block_size=128, is_causal=True)
+    ref = v7.dense_causal_attention(q, k, v)[0]
+    _attn_check(out[0], ref)
+
+
+def test_myattn_prefill_end_to_end_c1_shape():
+    """myattn_prefill on config 1's shape: output vs fp32 attention under the
+    oracle mask on a sample of query blocks of every head."""
+    _print_case("myattn_prefill", config="c1")
+    q, k, v = make_config("c1")
+    qg, kg, vg = _gpu(q, k, v)
+    out = myattn_prefill(qg, kg, vg, layer_idx=0, **PROD)
+    torch.cuda.synchronize()
+    assert out.shape == (1, q.shape[2], q.shape[1] * q.shape[3]) and out.dtype == q.dtype
+    ref_sel = v7.select_mask(q, k, **PROD)
+    sel = select_blocks(qg, kg, **PROD)
+    frac, exact, unexc = block_match(sel.dense_mask(), ref_sel.mask, ref_sel.excusable)
+    print(f"  match={frac:.6f} exact={exact:.6f}")
+    assert frac >= MATCH_MIN
+    qblocks = [0, 1, 37, 128, 200, 255]
+    ref = v7.block_sparse_attention(q, k, v, sel.dense_mask().cpu(), 128, qblocks=qblocks)
+    rows = torch.cat([torch.arange(i * 128, (i + 1) * 128) for i in qblocks])
+    _attn_check(out.view(q.shape[2], q.shape[1], q.shape[3]), ref, rows)
+
+
+def test_short_sequence_fallback_is_dense_causal():
+    q, k, v = make_qkv(1000, 4, 2, seed=8)                      # L < 10 * bs
+    out = myattn_prefill(*_gpu(q, k, v), layer_idx=0, **PROD)
+    assert out.shape == (1, 1000, 4 * 128)
+    ref = v7.dense_causal_attention(q, k, v)[0]
+    _attn_check(out.view(1000, 4, 128), ref)
+
+
+def test_fix_mask_role():
+    q, k, v = make_qkv(8192, 4, 4, seed=9)
+    out = fix_mask.myattn_prefill(*_gpu(q, k, v), layer_idx=0, sink_ratio=0.05, recent_ratio=0.05,
+                                  local_span_ratio=0.1)
+    N = 64
+    ks, kr, lw = max(1, int(N * 0.05)), max(1, int(N * 0.05)), max(2, int(N * 0.1)) // 2
+    mask = v7.fixed_mask(N, N, 4, ks, kr, lw)
+    ref = v7.block_sparse_attention(q, k, v, mask, 128, is_causal=True)
+    _attn_check(out.view(8192, 4, 128), ref)
+
+
+def test_fp32_attention_rejected_like_flash_attn():
+    q, k, v = make_config("c0", L=2048)
+    with pytest.raises(RuntimeError, match="fp16 and bf16"):
+        myattn_prefill(*_gpu(q, k, v), layer_idx=0, **PROD)
+
+
+def test_full_length_c2_properties():
+    """Config 2 length (128K) on device-generated data: pooled blocks against
+    the oracle's downstream stages, plus invariants of the block lists."""
+    _print_case("c2-properties")
+    g = torch.Generator(device=DEV).manual_seed(11)
+    L, Hq, Hk = 131072, 32, 8
+    q = torch.randn(1, Hq, L, 128, device=DEV, generator=g, dtype=torch.bfloat16)
+    k = torch.randn(1, Hk, L, 128, device=DEV, generator=g, dtype=torch.bfloat16)
+    k[:, :, :4] *= 6
+    sel = select_blocks(q, k, **PROD, keep_intermediates=True)
+    torch.cuda.synchronize()
+    p = sel.params
+    assert p.N == 1024
+    Qb, Kb = _orig_layout(sel.q_b, Hq), _orig_layout(sel.k_b, Hq)
+    corr_ref, _ = v7.fft_lag_correlation(Qb, Kb, p.local_window, p.keep_sink)
+    keep_ref, norm_ref = v7.correlation_keep(corr_ref, p.remote_start, PROD["corr_threshold"])
+    near = (norm_ref - PROD["corr_threshold"]).abs() <= BAND * PROD["corr_threshold"]
+    assert not ((sel.keep_tau.cpu().bool() != keep_ref) & ~near).any()
+    cnt = sel.blk_cnt.cpu()
+    assert int(cnt.min()) >= 1 and bool((cnt <= torch.arange(1, p.N + 1)[None, :]).all())
+    idx = sel.blk_idx.view(torch.int16).cpu().to(torch.int64)
+    for h in (0, 13, 31):
+        for i in (0, 511, 1023):
+            row = idx[h, i, : cnt[h, i]]
+            assert int(row[0]) == 0 and int(row[-1]) == i and bool((row[1:] > row[:-1]).all())

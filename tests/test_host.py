@@ -1,0 +1,97 @@
+"""CPU tests of the host side: the C ABI library loads and exports what the
+header declares, struct layouts agree, parameter derivation agrees with the
+oracle, and the Python API raises the reference's error types."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+import fftsparse_amd
+from fftsparse_amd import _lib, params
+from fftsparse_amd.synth import CONFIGS, make_qkv, sha256_of
+from oracle import v7
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "fftsparse_amd.h"
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    declared = re.findall(r"FS_API\s+[\w\s\*]+?\b(fs_\w+)\s*\(", HEADER.read_text())
+    assert set(declared) == set(_lib.ENTRY_POINTS)
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert lib.fs_abi_version() == 1
+
+
+def test_struct_layouts_match_library():
+    lib = _lib.load()
+    for i, st in enumerate(_lib.STRUCTS):
+        assert lib.fs_sizeof_args(i) == ctypes.sizeof(st), st.__name__
+
+
+def test_null_args_rejected_without_gpu():
+    lib = _lib.load()
+    for name in ("fs_pool", "fs_corr", "fs_stats", "fs_select", "fs_bsattn"):
+        rc = getattr(lib, name)(None, None)
+        assert rc == -1
+        assert b"null args" in lib.fs_last_error()
+
+
+def test_bad_shapes_rejected_without_gpu():
+    lib = _lib.load()
+    a = _lib.AttnArgs(q=16, k=16, v=16, out=16, dtype=1, B=1, Hq=3, Hk=2, Lq=10, Lk=10, D=128, bs=128)
+    assert lib.fs_bsattn(ctypes.byref(a), None) == -1
+    a = _lib.AttnArgs(q=16, k=16, v=16, out=16, dtype=1, B=1, Hq=4, Hk=2, Lq=10, Lk=10, D=96, bs=128)
+    assert lib.fs_bsattn(ctypes.byref(a), None) == -2
+    assert b"head_dim" in lib.fs_last_error()
+
+
+@pytest.mark.parametrize("L", [1280, 8192, 10000, 32768, 65536, 131072, 262144])
+@pytest.mark.parametrize("bs", [64, 128])
+@pytest.mark.parametrize("ratios", [(0.01, 0.0, 0.02, 0.2), (0.1, 0.1, 0.1, 0.1), (0.3, 0.05, 0.5, 0.05)])
+def test_params_agree_with_oracle(L, bs, ratios):
+    sink, recent, local, col = ratios
+    kw = dict(sink_ratio=sink, recent_ratio=recent, local_span_ratio=local, column_topk_ratio=col)
+    a = params.derive(L, L, bs, **kw)
+    b = v7.derive_params(L, L, bs, **kw)
+    for f in ("N", "Nk", "keep_sink", "keep_recent", "local_window", "corr_enabled", "remote_start",
+              "sample_taus", "stripe_all_diffuse", "col_enabled", "col_start", "col_end", "n_cols", "last_k"):
+        assert getattr(a, f) == getattr(b, f), f
+
+
+def test_api_asserts_gpu_tensors_like_reference():
+    q = torch.zeros(1, 4, 2048, 128, dtype=torch.bfloat16)
+    with pytest.raises(AssertionError):
+        fftsparse_amd.myattn_prefill(q, q, q, layer_idx=0)
+    with pytest.raises(AssertionError):
+        fftsparse_amd.fix_mask.myattn_prefill(q, q, q, layer_idx=0)
+
+
+def test_signature_matches_reference_v7():
+    import inspect
+    sig = inspect.signature(fftsparse_amd.myattn_prefill)
+    expected = ["query_states", "key_states", "value_states", "layer_idx", "block_size", "is_causal",
+                "is_visual", "sink_ratio", "recent_ratio", "local_span_ratio", "enable_correlation_mask",
+                "correlation_selection_mode", "correlation_topk_ratio", "corr_threshold",
+                "collect_corr_stats", "enable_column_mask", "column_topk_ratio",
+                "column_start_exclude_ratio", "column_end_exclude_ratio", "enable_last_block_mask",
+                "last_block_threshold", "diag_sample_ratio", "min_diag_samples", "max_diag_samples",
+                "stripe_threshold", "qk_topk_ratio", "attention_vis_heads", "attention_vis_dir"]
+    assert list(sig.parameters) == expected
+    d = {k: p.default for k, p in sig.parameters.items()}
+    assert (d["block_size"], d["sink_ratio"], d["corr_threshold"], d["qk_topk_ratio"],
+            d["stripe_threshold"], d["max_diag_samples"]) == (128, 0.1, 0.1, 0.2, 0.3, 64)
+
+
+def test_synthetic_inputs_are_pinned():
+    golden = Path(__file__).resolve().parent / "golden" / "synth_sha256.txt"
+    want = dict(line.split() for line in golden.read_text().splitlines() if line.strip())
+    q, k, v = make_qkv(2048, 4, 1, dtype=torch.float32, seed=0)
+    assert sha256_of(q, k, v) == want["small_f32_seed0"]
+    q, k, v = make_qkv(2048, 4, 2, dtype=torch.bfloat16, seed=0, stripe_density=0.005, period=512)
+    assert sha256_of(q, k, v) == want["small_bf16_seed0"]
+    assert CONFIGS["c2"].period == 512 and CONFIGS["c3a"].theta == 1000000.0
