@@ -16,6 +16,7 @@ import torch  # noqa: F401  (must precede the library load, see module docstring
 LIB_PATH = Path(__file__).resolve().with_name("libfftsparse_amd.so")
 
 FS_DTYPE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+ABI_VERSION = 2
 
 
 class PoolArgs(ctypes.Structure):
@@ -65,12 +66,13 @@ class AttnArgs(ctypes.Structure):
                 ("dtype", c_int), ("B", c_int), ("Hq", c_int), ("Hk", c_int), ("Lq", c_int), ("Lk", c_int),
                 ("D", c_int), ("bs", c_int),
                 ("is_causal", c_int), ("softmax_scale", c_float),
-                ("blk_cnt", c_void_p), ("blk_idx", c_void_p)]
+                ("blk_cnt", c_void_p), ("blk_idx", c_void_p), ("work", c_void_p)]
 
 
 STRUCTS = [PoolArgs, CorrArgs, StatsArgs, SelectArgs, AttnArgs]
 
-ENTRY_POINTS = ["fs_pool", "fs_corr_work_bytes", "fs_corr", "fs_stats", "fs_select", "fs_bsattn",
+ENTRY_POINTS = ["fs_pool", "fs_corr_work_bytes", "fs_corr", "fs_stats", "fs_select", "fs_bsattn_work_bytes",
+                "fs_bsattn",
                 "fs_last_error", "fs_abi_version", "fs_sizeof_args"]
 
 _lib = None
@@ -92,12 +94,14 @@ def load() -> ctypes.CDLL:
     lib.fs_sizeof_args.argtypes = [c_int]
     lib.fs_corr_work_bytes.restype = c_size_t
     lib.fs_corr_work_bytes.argtypes = [c_int, c_int, c_int]
+    lib.fs_bsattn_work_bytes.restype = c_size_t
+    lib.fs_bsattn_work_bytes.argtypes = [c_int, c_int, c_int, c_int, c_int]
     for name, st in [("fs_pool", PoolArgs), ("fs_corr", CorrArgs), ("fs_stats", StatsArgs),
                      ("fs_select", SelectArgs), ("fs_bsattn", AttnArgs)]:
         fn = getattr(lib, name)
         fn.restype = c_int
         fn.argtypes = [POINTER(st), c_void_p]
-    if lib.fs_abi_version() != 1:
+    if lib.fs_abi_version() != ABI_VERSION:
         raise RuntimeError("fftsparse_amd: library ABI version mismatch; rebuild it")
     for i, st in enumerate(STRUCTS):
         if lib.fs_sizeof_args(i) != ctypes.sizeof(st):

@@ -24,7 +24,7 @@ def test_library_exports_every_declared_symbol():
     assert set(declared) == set(_lib.ENTRY_POINTS)
     for name in declared:
         assert hasattr(lib, name), name
-    assert lib.fs_abi_version() == 1
+    assert lib.fs_abi_version() == _lib.ABI_VERSION
 
 
 def test_struct_layouts_match_library():
