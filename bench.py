@@ -45,6 +45,9 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-qblocks", type=int, default=24,
                     help="query blocks of head 0 timed for the CPU attention sample")
+    ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB (5 times) to calibrate "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE, then exit")
     return ap.parse_args()
 
 
@@ -103,7 +106,16 @@ def main():
                                    "note (DESIGN.md), not a code path", "n_gpus": args.gpus}))
         sys.exit(2)
     import torch
-    import fftsparse_amd
+    if args.copy_calib:
+        n = args.copy_calib * (1 << 20)
+        x = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+        y = torch.empty_like(x)
+        for _ in range(5):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calib_bytes": n, "launches": 5}))
+        return
+    import fftsparse_amd  # noqa: F401
     from fftsparse_amd import block_sparse_attention, select_blocks
     from fftsparse_amd.synth import CONFIGS, make_config
 

@@ -23,9 +23,9 @@
 // LDS rows are 256 B with the 16-byte chunk c of row r stored at c ^ (r & 15)
 // so the 8 lanes of a ds_read_b128 phase hit distinct banks.
 //
-// Scheduling: items are mapped XCD-major (workgroup w runs on XCD w % 8) so
-// that one XCD walks a contiguous range of (kv head, query block, head in
-// group); query blocks are visited last-first so the longest rows start first.
+// Scheduling: workgroup w runs on XCD w % 8; XCD x owns every 8th
+// query-block row (last rows first) of every head, which balances the work
+// of unevenly sparse heads across XCDs.
 #include "common.h"
 
 namespace fs {
@@ -144,18 +144,22 @@ __global__ __launch_bounds__(AttnCfg<BS>::NT) void bsattn_kernel(fs_attn_args a,
   // double-buffered [K | V^T] tiles; 256-byte rows with swizzled 16-byte chunks
   __shared__ __attribute__((aligned(1024))) uint16_t lds[2][2][C::TILE];
 
+  // Workgroup wg runs on XCD wg % 8.  XCD x takes the query-block rows
+  // r = x, x + 8, x + 16, ... (counted from the last query block, so long
+  // rows start first) of every head: each XCD gets an even share of every
+  // head's work, and the heads of one GQA group at one query block run back
+  // to back on the same XCD (shared K/V tiles in its L2).
   const int wg = blockIdx.x;
-  const int li = (wg & 7) * per_xcd + (wg >> 3);
-  if (li >= total) return;
+  const int x = wg & 7, slot = wg >> 3;
+  const int per_row = a.Hq;                       // items per row: (hk, head in group)
+  const int r = x + 8 * (slot / per_row);
+  if (r >= total) return;                         // total = B * Nq rows
   const int g = a.Hq / a.Hk;
-  const int per_b = a.Hk * Nq * g;
-  const int b = li / per_b;
-  int rem = li - b * per_b;
-  const int hk = rem / (Nq * g);
-  rem -= hk * (Nq * g);
-  const int qi = rem / g;
-  const int h = hk * g + (rem - qi * g);
-  const int qb = Nq - 1 - qi;
+  const int hsel = slot % per_row;
+  const int hk = hsel / g;
+  const int h = hsel;                             // heads of group hk are hk*g .. hk*g+g-1
+  const int b = r / Nq;
+  const int qb = Nq - 1 - (r - b * Nq);
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int l32 = lane & 31, hi = lane >> 5;
@@ -250,21 +254,45 @@ __global__ __launch_bounds__(AttnCfg<BS>::NT) void bsattn_kernel(fs_attn_args a,
   // guards their first use inside the loop with a vmcnt(0) on every iteration,
   // which would also wait for the tile copy in flight.
   __builtin_amdgcn_s_waitcnt(0);
+  // Pipeline per iteration t: wait for the copy of tile t, one barrier (tile t
+  // visible; every wave is past tile t-1, so its buffer may be refilled),
+  // start the copy of tile t+1, touch tile t+2 into L2 (one dword per
+  // 128-byte line and thread), compute tile t.  The touch loads land in a
+  // register that stays live until a later wait has retired them.
+  auto touch = [&](int kb) -> uint32_t {
+    kb = min(kb, Nk - 1);
+    const int k0 = kb * BS;
+    const uint16_t* p;
+    if (tid < BS * 2) {                            // K: two 128-byte lines per 256-byte row
+      const int key = min(k0 + (tid >> 1), a.Lk - 1);
+      p = kp + (int64_t)key * a.k_sl + (tid & 1) * 64;
+    } else {                                       // V^T: BS/64 lines per d row
+      const int v = tid - BS * 2;
+      p = vtp + (int64_t)(v / (BS / 64)) * Lp + k0 + (v % (BS / 64)) * 64;
+    }
+    uint32_t x;
+    asm volatile("global_load_dword %0, %1, off" : "=v"(x) : "v"(p) : "memory");
+    return x;
+  };
+  static_assert(AttnCfg<BS>::NT == BS * 2 + kD * (BS / 64), "one touch line per thread");
+  uint32_t pf_prev = 0, pf_cur = 0;
   int kb_cur = cnt > 0 ? block_at(0) : 0;
   if (cnt > 0) issue(kb_cur, 0);
+  if (cnt > 1) pf_cur = touch(block_at(1));
   for (int t = 0; t < cnt; ++t) {
     const int buf = t & 1;
     const bool more = t + 1 < cnt;
-    const int kb_next = more ? block_at(t + 1) : 0;
-    if (more) {
-      issue(kb_next, buf ^ 1);
-      asm volatile("s_waitcnt vmcnt(%0)" :: "n"(C::DMA_PER_WAVE) : "memory");
-    } else {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    }
-    __builtin_amdgcn_s_barrier();                 // tile t is in LDS for every wave
+    if (more) asm volatile("s_waitcnt vmcnt(1)" ::: "memory");   // the touch of t+1 may stay in flight
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    asm volatile("" :: "v"(pf_prev));             // touch of tile t retired: release its register
+    pf_prev = pf_cur;
+    __builtin_amdgcn_s_barrier();
     const int kb = kb_cur;
-    kb_cur = kb_next;
+    if (more) {
+      kb_cur = block_at(t + 1);
+      issue(kb_cur, buf ^ 1);
+    }
+    if (t + 2 < cnt) pf_cur = touch(block_at(t + 2));
     const int k0 = kb * BS;
     const int kw0 = k0 + kbase;                   // first key of this wave
     const bool active = kb < Nk && kw0 < a.Lk && !(a.is_causal && kw0 > qw0 + 31 + off);
@@ -338,8 +366,8 @@ __global__ __launch_bounds__(AttnCfg<BS>::NT) void bsattn_kernel(fs_attn_args a,
         }
       }
     }
-    __builtin_amdgcn_s_barrier();                 // every wave is done with buffer t & 1
   }
+  asm volatile("s_waitcnt vmcnt(0)" :: "v"(pf_prev), "v"(pf_cur) : "memory");
   __syncthreads();
 
   // ---- merge the two key halves through LDS, normalise, store
@@ -392,9 +420,9 @@ static int launch_attn(const fs_attn_args& a, int Nq, int Nk, hipStream_t s) {
   vt_kernel<<<a.B * a.Hk * slabs, 256, 0, s>>>(static_cast<const uint16_t*>(a.v), a.v_sb, a.v_sh, a.v_sl, vt,
                                                a.Hk, a.Lk, Lp);
   if (int rc = fs_host::launch_status("fs_bsattn (V^T)")) return rc;
-  const int total = a.B * a.Hq * Nq;
-  const int per_xcd = (total + 7) / 8;
-  bsattn_kernel<BS, T><<<per_xcd * 8, AttnCfg<BS>::NT, 0, s>>>(a, vt, Nq, Nk, Lp, total, per_xcd);
+  const int rows = a.B * Nq;
+  const int per_xcd = (rows + 7) / 8 * a.Hq;
+  bsattn_kernel<BS, T><<<per_xcd * 8, AttnCfg<BS>::NT, 0, s>>>(a, vt, Nq, Nk, Lp, rows, per_xcd);
   return fs_host::launch_status("fs_bsattn");
 }
 

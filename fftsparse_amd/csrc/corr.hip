@@ -10,8 +10,9 @@
 // LDS.  X = (Z[f] + conj Z[M-f]) / 2 and Y = (Z[f] - conj Z[M-f]) / 2i give
 // the cross spectrum X conj(Y), summed over d in registers.
 //
-// Kernel 1 (grid Hq x ceil(D/8)): each workgroup transforms 8 dims of one
-// head and writes its partial cross spectrum (M/2+1 bins) to the work buffer.
+// Kernel 1 (grid Hq x ceil(D/dpg)): each workgroup stages dpg dims of one
+// head (8, 4 or 2 by N) from the pooled rows into LDS, transforms them one by
+// one and writes its partial cross spectrum (M/2+1 bins) to the work buffer.
 // Kernel 2 (grid Hq): sums the partials, inverts with one FFT per head, and
 // applies the reference's post-processing and threshold in the same kernel.
 #include "common.h"
@@ -19,7 +20,6 @@
 namespace fs {
 
 constexpr int kFftThreads = 256;
-constexpr int kDimsPerGroup = 8;
 constexpr int kMaxLogM = 13;                              // M <= 8192, N <= 4096
 constexpr int kMaxBins = ((1 << kMaxLogM) / 2 + 1 + kFftThreads - 1) / kFftThreads;
 
@@ -29,12 +29,12 @@ __device__ __forceinline__ float2 cmul(float2 a, float2 b) {
   return make_float2(a.x * b.x - a.y * b.y, a.x * b.y + a.y * b.x);
 }
 
-// tw[k] = exp(-2 pi i k / M), k < M/2, from double-precision sincospi.
+// tw[k] = exp(-2 pi i k / M), k < M/2 (single-precision sincospi, exact argument).
 __device__ void fill_twiddles(float2* tw, int M) {
   for (int k = threadIdx.x; k < M / 2; k += blockDim.x) {
-    double s, c;
-    sincospi(-2.0 * (double)k / (double)M, &s, &c);
-    tw[k] = make_float2((float)c, (float)s);
+    float s, c;
+    sincospif(-2.0f * (float)k / (float)M, &s, &c);
+    tw[k] = make_float2(c, s);
   }
 }
 
@@ -57,33 +57,33 @@ __device__ void fft_dit(float2* buf, const float2* tw, int M, int logM) {
 }
 
 template <typename T>
-__global__ __launch_bounds__(kFftThreads) void corr_partial_kernel(fs_corr_args a, int M, int logM,
+__global__ __launch_bounds__(kFftThreads) void corr_partial_kernel(fs_corr_args a, int M, int logM, int dpg,
                                                                    float2* part) {
   extern __shared__ float2 smem[];
   float2* buf = smem;
   float2* tw = smem + M;
+  float2* stage = smem + M + M / 2;                 // [dpg][N] (q, k) pairs of this group's dims
   const int h = blockIdx.x, g = blockIdx.y, G = gridDim.y;
   const int hk = h / (a.Hq / a.Hk);
   const int N = a.N, D = a.D, tid = threadIdx.x;
   const T* qb = static_cast<const T*>(a.q_b) + (int64_t)h * N * D;
   const T* kb = static_cast<const T*>(a.k_b) + (int64_t)hk * N * D;
   fill_twiddles(tw, M);
+  // stage the group's dims of every row once (independent loads, row-contiguous)
+  const int d0 = g * dpg;
+  const int nd = min(dpg, D - d0);
+  for (int n = tid; n < N; n += kFftThreads) {
+    for (int e = 0; e < nd; ++e)
+      stage[e * N + n] = make_float2(to_f32(qb[(int64_t)n * D + d0 + e]), to_f32(kb[(int64_t)n * D + d0 + e]));
+  }
   const int nb = M / 2 + 1;
   float2 acc[kMaxBins];
 #pragma unroll
   for (int r = 0; r < kMaxBins; ++r) acc[r] = make_float2(0.f, 0.f);
   __syncthreads();
-  for (int dd = 0; dd < kDimsPerGroup; ++dd) {
-    const int d = g * kDimsPerGroup + dd;
-    if (d >= D) break;
-    for (int n = tid; n < M; n += kFftThreads) {
-      float x = 0.f, y = 0.f;
-      if (n < N) {
-        x = to_f32(qb[(int64_t)n * D + d]);
-        y = to_f32(kb[(int64_t)n * D + d]);
-      }
-      buf[bitrev(n, logM)] = make_float2(x, y);
-    }
+  for (int dd = 0; dd < nd; ++dd) {
+    for (int n = tid; n < M; n += kFftThreads)
+      buf[bitrev(n, logM)] = n < N ? stage[dd * N + n] : make_float2(0.f, 0.f);
     __syncthreads();
     fft_dit(buf, tw, M, logM);
 #pragma unroll
@@ -172,12 +172,15 @@ __global__ __launch_bounds__(kFftThreads) void corr_final_kernel(fs_corr_args a,
 }
 
 template <typename T>
-static int launch_partial(const fs_corr_args& a, dim3 grid, size_t smem, int M, int logM, float2* part,
-                          hipStream_t s) {
+static int launch_partial(const fs_corr_args& a, dim3 grid, size_t smem, int M, int logM, int dpg,
+                          float2* part, hipStream_t s) {
   if (int rc = fs_host::allow_dynamic_lds(corr_partial_kernel<T>, smem, "fs_corr")) return rc;
-  corr_partial_kernel<T><<<grid, kFftThreads, smem, s>>>(a, M, logM, part);
+  corr_partial_kernel<T><<<grid, kFftThreads, smem, s>>>(a, M, logM, dpg, part);
   return 0;
 }
+
+// dims per workgroup: keeps the staged rows at 2 * dpg * N * 8 bytes <= 64 KiB
+static int dims_per_group(int N) { return N <= 1024 ? 8 : (N <= 2048 ? 4 : 2); }
 
 static int corr_logM(int N) {
   int logM = 1;
@@ -192,7 +195,8 @@ using namespace fs;
 extern "C" size_t fs_corr_work_bytes(int Hq, int N, int D) {
   if (Hq <= 0 || N <= 0 || D <= 0) return 0;
   const int M = 1 << corr_logM(N);
-  const int G = (D + kDimsPerGroup - 1) / kDimsPerGroup;
+  const int dpg = dims_per_group(N);
+  const int G = (D + dpg - 1) / dpg;
   return (size_t)Hq * G * (M / 2 + 1) * sizeof(float2);
 }
 
@@ -207,22 +211,24 @@ extern "C" int fs_corr(const fs_corr_args* a, void* stream) {
   FS_CHECK_SUPPORTED(logM <= kMaxLogM, "fs_corr: N=%d exceeds the LDS FFT limit (N <= %d)", a->N,
                      1 << (kMaxLogM - 1));
   const int M = 1 << logM;
-  const int G = (a->D + kDimsPerGroup - 1) / kDimsPerGroup;
+  const int dpg = dims_per_group(a->N);
+  const int G = (a->D + dpg - 1) / dpg;
   hipStream_t s = (hipStream_t)stream;
   float2* part = static_cast<float2*>(a->work);
-  const size_t sm1 = (size_t)(M + M / 2) * sizeof(float2);
+  const size_t sm_fft = (size_t)(M + M / 2) * sizeof(float2);
+  const size_t sm1 = sm_fft + (size_t)dpg * a->N * sizeof(float2);
   dim3 g1(a->Hq, G);
   int rc = 0;
   switch (a->dtype) {
-    case FS_DTYPE_F32: rc = launch_partial<float>(*a, g1, sm1, M, logM, part, s); break;
-    case FS_DTYPE_BF16: rc = launch_partial<bf16_t>(*a, g1, sm1, M, logM, part, s); break;
-    case FS_DTYPE_F16: rc = launch_partial<f16_t>(*a, g1, sm1, M, logM, part, s); break;
+    case FS_DTYPE_F32: rc = launch_partial<float>(*a, g1, sm1, M, logM, dpg, part, s); break;
+    case FS_DTYPE_BF16: rc = launch_partial<bf16_t>(*a, g1, sm1, M, logM, dpg, part, s); break;
+    case FS_DTYPE_F16: rc = launch_partial<f16_t>(*a, g1, sm1, M, logM, dpg, part, s); break;
     default: fs_host::set_error("fs_corr: dtype %d unsupported", a->dtype); return FS_ERR_UNSUPPORTED;
   }
   if (rc) return rc;
   rc = fs_host::launch_status("fs_corr partial");
   if (rc) return rc;
-  const size_t sm2 = sm1 + (size_t)a->N * sizeof(float);
+  const size_t sm2 = sm_fft + (size_t)a->N * sizeof(float);
   if ((rc = fs_host::allow_dynamic_lds(corr_final_kernel, sm2, "fs_corr"))) return rc;
   corr_final_kernel<<<a->Hq, kFftThreads, sm2, s>>>(*a, M, logM, G, part);
   return fs_host::launch_status("fs_corr final");

@@ -81,9 +81,17 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(fs_select_args a, i
   }
 
   const int lw = a.local_window;
-  const uint8_t* keep = a.keep_tau ? a.keep_tau + (int64_t)h * N : nullptr;
-  const uint8_t* cols = a.col_sel ? a.col_sel + (int64_t)h * N : nullptr;
-  const uint8_t* last = a.last_sel ? a.last_sel + (int64_t)h * N : nullptr;
+  // per-head lag / column / last-row flags, staged in LDS (bit 0 lag, 1 column, 2 last row)
+  __shared__ uint8_t flags[4096];
+  for (int j = tid; j < N; j += kSelThreads) {
+    uint8_t f = 0;
+    if (a.keep_tau && a.keep_tau[(int64_t)h * N + j]) f |= 1;
+    if (a.col_sel && a.col_sel[(int64_t)h * N + j]) f |= 2;
+    if (a.last_sel && a.last_sel[(int64_t)h * N + j]) f |= 4;
+    flags[j] = f;
+  }
+  __syncthreads();
+  const bool has_last = a.last_sel != nullptr;
 
   for (int rr = wave; rr < RPW; rr += kSelWaves) {
     const int i = r0 + rr;
@@ -123,17 +131,18 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(fs_select_args a, i
       if (valid) {
         // prior (:83-95): sink | recent | local window
         in = j < a.keep_sink || j >= Nk - a.keep_recent || (lw > 0 && abs(i - j) <= lw);
-        if (last && i == N - 1 && last[j]) in = true;
+        const uint8_t fj = j < N ? flags[j] : 0;
+        if (has_last && i == N - 1 && (fj & 4)) in = true;
         if (use_lags) {
           const int t = i - j;
-          if (t >= a.remote_start && j >= a.keep_sink && keep[t]) in = true;
+          if (t >= a.remote_start && j >= a.keep_sink && (flags[t] & 1)) in = true;
         }
         if (diffuse && j <= i) {
           const uint32_t key = order_key(srow[j]);
           if (key > thr) in = true;
           eq = key == thr;
         }
-        if (use_cols && j <= i && cols[j]) in = true;
+        if (use_cols && j <= i && (fj & 2)) in = true;
       }
       if (diffuse) {
         const uint64_t me = __ballot(eq);

@@ -3,67 +3,91 @@
 //   column scores and their top-n                     (my_attn_v7.py:390-447)
 //   last-query-row scores and their top-k             (my_attn_v7.py:54-72)
 //
-// Grid (Hq, 2 + n_samples): y == 0 is the column task, y == 1 the last-row
-// task and y >= 2 the diagonal sample y - 2.  All arithmetic is fp32 with a
-// fixed accumulation order.
+// Grid (Hq, 2 + n_samples), 1024 threads: y == 0 is the column task, y == 1
+// the last-row task and y >= 2 the diagonal sample y - 2.  Row dot products
+// use 16-byte loads; all arithmetic is fp32 with a fixed accumulation order.
 #include "common.h"
 
 namespace fs {
 
-constexpr int kStatThreads = 256;
-constexpr int kColChunk = 8;
+constexpr int kStatThreads = 1024;
+constexpr int kStatWaves = kStatThreads / 64;
 
+// fp32 dot product of two rows of D elements (D % 8 == 0), 16-byte loads,
+// sequential accumulation in d order.
 template <typename T>
 __device__ __forceinline__ float dot_rows(const T* a, const T* b, int D) {
+  constexpr int V = 16 / sizeof(T);
   float s = 0.f;
-  for (int d = 0; d < D; ++d) s += to_f32(a[d]) * to_f32(b[d]);
+  for (int d0 = 0; d0 < D; d0 += V) {
+    const uint4 ra = *reinterpret_cast<const uint4*>(a + d0);
+    const uint4 rb = *reinterpret_cast<const uint4*>(b + d0);
+    const T* ea = reinterpret_cast<const T*>(&ra);
+    const T* eb = reinterpret_cast<const T*>(&rb);
+#pragma unroll
+    for (int e = 0; e < V; ++e) s += to_f32(ea[e]) * to_f32(eb[e]);
+  }
   return s;
 }
 
 template <typename T>
 __global__ __launch_bounds__(kStatThreads) void stats_kernel(fs_stats_args a, float inv_sqrt_d) {
-  extern __shared__ float sm[];          // N floats (+ column scratch)
+  extern __shared__ float sm[];          // [N] values, then [kStatWaves][D] run sums
   __shared__ float red[32];
   __shared__ int ired[32];
   const int h = blockIdx.x, task = blockIdx.y, tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
   const int N = a.N, D = a.D;
   const int hk = h / (a.Hq / a.Hk);
   const T* qb = static_cast<const T*>(a.q_b) + (int64_t)h * N * D;
   const T* kb = static_cast<const T*>(a.k_b) + (int64_t)hk * N * D;
 
   if (task == 0) {
-    // ---- column scores (:404-420) and top-n over [col_start, col_end) (:422-438)
+    // ---- column scores (:404-420):
+    //   col[j] = (total - cumsum[j-1]) . k_b[j] / sqrt(D) / max(1, N-j-1),  total = cumsum[N-2],
+    // the difference being 0 for j = N-1 (:414).  Wave w owns rows [w R, (w+1) R),
+    // lane l owns dims l, l+64, ... (D <= 256).
     if (a.n_cols <= 0) return;
     float* colv = sm;                               // [N]
-    float* prod = sm + N;                           // [kColChunk][D]
-    float* tot = prod + kColChunk * D;              // [D]
-    if (tid < D) {
+    float* runs = sm + N;                           // [kStatWaves][D]
+    const int R = (N + kStatWaves - 1) / kStatWaves;
+    const int r0 = min(N, wave * R), r1 = min(N, r0 + R);
+    const int nd = (D + 63) / 64;
+    for (int k = 0; k < nd; ++k) {
+      const int d = lane + 64 * k;
+      if (d >= D) break;
       float s = 0.f;
-      for (int i = 0; i <= N - 2; ++i) s += to_f32(qb[(int64_t)i * D + tid]);
-      tot[tid] = s;                                  // cumsum[N-2]
+      for (int i = r0; i < min(r1, N - 1); ++i) s += to_f32(qb[(int64_t)i * D + d]);
+      runs[wave * D + d] = s;
     }
-    float run = 0.f;                                 // cumsum[j-1]
-    for (int j0 = 0; j0 < N; j0 += kColChunk) {
-      __syncthreads();
-      if (tid < D) {
-        for (int jj = 0; jj < kColChunk; ++jj) {
-          const int j = j0 + jj;
-          if (j >= N) break;
-          const float partial = (j == N - 1) ? 0.f : tot[tid] - run;
-          prod[jj * D + tid] = partial * to_f32(kb[(int64_t)j * D + tid]);
-          run += to_f32(qb[(int64_t)j * D + tid]);
+    __syncthreads();
+    float run[4], tot[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      run[k] = 0.f;
+      tot[k] = 0.f;
+      const int d = lane + 64 * k;
+      if (k < nd && d < D) {
+        for (int w = 0; w < kStatWaves; ++w) {
+          const float v = runs[w * D + d];
+          if (w < wave) run[k] += v;
+          tot[k] += v;
         }
       }
-      __syncthreads();
-      const int w = tid >> 6, lane = tid & 63;
-      for (int jj = w; jj < kColChunk; jj += kStatThreads / 64) {
-        const int j = j0 + jj;
-        if (j >= N) break;
-        float v = 0.f;
-        for (int d = lane; d < D; d += 64) v += prod[jj * D + d];
-        v = wave_sum(v);
-        if (lane == 0) colv[j] = (v * inv_sqrt_d) / (float)max(1, N - j - 1);
+    }
+    for (int j = r0; j < r1; ++j) {
+      float dot = 0.f;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int d = lane + 64 * k;
+        if (k < nd && d < D) {
+          const float partial = (j == N - 1) ? 0.f : tot[k] - run[k];
+          dot += partial * to_f32(kb[(int64_t)j * D + d]);
+          run[k] += to_f32(qb[(int64_t)j * D + d]);
+        }
       }
+      dot = wave_sum(dot);
+      if (lane == 0) colv[j] = (dot * inv_sqrt_d) / (float)max(1, N - j - 1);
     }
     __syncthreads();
     for (int j = tid; j < N; j += kStatThreads) {
@@ -114,6 +138,13 @@ __global__ __launch_bounds__(kStatThreads) void stats_kernel(fs_stats_args a, fl
   if (tid == 0) a.diag_var[(int64_t)h * a.n_samples + si] = var / clamp_min_nan(mean_abs, 1e-6f);
 }
 
+template <typename T>
+static int launch_stats(const fs_stats_args& a, dim3 grid, size_t smem, float inv_sqrt_d, hipStream_t s) {
+  if (int rc = fs_host::allow_dynamic_lds(stats_kernel<T>, smem, "fs_stats")) return rc;
+  stats_kernel<T><<<grid, kStatThreads, smem, s>>>(a, inv_sqrt_d);
+  return 0;
+}
+
 }  // namespace fs
 
 using namespace fs;
@@ -122,7 +153,8 @@ extern "C" int fs_stats(const fs_stats_args* a, void* stream) {
   FS_CHECK_ARG(a != nullptr, "fs_stats: null args");
   FS_CHECK_ARG(a->q_b && a->k_b, "fs_stats: null pooled pointer");
   FS_CHECK_ARG(a->Hq > 0 && a->Hk > 0 && a->Hq % a->Hk == 0, "fs_stats: bad head counts");
-  FS_CHECK_ARG(a->N >= 1 && a->D >= 1 && a->D <= 256, "fs_stats: bad sizes");
+  FS_CHECK_ARG(a->N >= 1 && a->D >= 8 && a->D <= 256 && a->D % 8 == 0, "fs_stats: bad sizes");
+  FS_CHECK_ARG(((uintptr_t)a->q_b % 16) == 0 && ((uintptr_t)a->k_b % 16) == 0, "fs_stats: unaligned pooled tensors");
   FS_CHECK_ARG(a->n_samples >= 0 && (a->n_samples == 0 || (a->sample_taus && a->diag_var)),
                "fs_stats: sample arrays missing");
   FS_CHECK_ARG(a->n_cols <= 0 || (a->col_sel && a->col_start >= 0 && a->col_end <= a->N &&
@@ -132,14 +164,16 @@ extern "C" int fs_stats(const fs_stats_args* a, void* stream) {
                "fs_stats: bad last-row arguments");
   FS_CHECK_SUPPORTED(a->N <= 4096, "fs_stats: N=%d > 4096", a->N);
   const float inv_sqrt_d = 1.0f / (float)sqrt((double)a->D);
-  const size_t smem = (size_t)(a->N + kColChunk * a->D + a->D) * sizeof(float);
+  const size_t smem = (size_t)(a->N + kStatWaves * a->D) * sizeof(float);
   dim3 grid(a->Hq, 2 + a->n_samples);
   hipStream_t s = (hipStream_t)stream;
+  int rc = 0;
   switch (a->dtype) {
-    case FS_DTYPE_F32: stats_kernel<float><<<grid, kStatThreads, smem, s>>>(*a, inv_sqrt_d); break;
-    case FS_DTYPE_BF16: stats_kernel<bf16_t><<<grid, kStatThreads, smem, s>>>(*a, inv_sqrt_d); break;
-    case FS_DTYPE_F16: stats_kernel<f16_t><<<grid, kStatThreads, smem, s>>>(*a, inv_sqrt_d); break;
+    case FS_DTYPE_F32: rc = launch_stats<float>(*a, grid, smem, inv_sqrt_d, s); break;
+    case FS_DTYPE_BF16: rc = launch_stats<bf16_t>(*a, grid, smem, inv_sqrt_d, s); break;
+    case FS_DTYPE_F16: rc = launch_stats<f16_t>(*a, grid, smem, inv_sqrt_d, s); break;
     default: fs_host::set_error("fs_stats: dtype %d unsupported", a->dtype); return FS_ERR_UNSUPPORTED;
   }
+  if (rc) return rc;
   return fs_host::launch_status("fs_stats");
 }
