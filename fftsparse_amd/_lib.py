@@ -8,15 +8,18 @@ Loading fails loudly when the library is missing -- there is no fallback.
 from __future__ import annotations
 
 import ctypes
+import os
 from ctypes import POINTER, c_float, c_int, c_int32, c_int64, c_size_t, c_uint8, c_uint16, c_void_p
 from pathlib import Path
 
 import torch  # noqa: F401  (must precede the library load, see module docstring)
 
-LIB_PATH = Path(__file__).resolve().with_name("libfftsparse_amd.so")
+# FFTSPARSE_AMD_LIB may name another build of the same library (e.g. one built
+# with different compile-time options); by default the in-tree build is used.
+LIB_PATH = Path(os.environ.get("FFTSPARSE_AMD_LIB") or Path(__file__).resolve().with_name("libfftsparse_amd.so"))
 
 FS_DTYPE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 class PoolArgs(ctypes.Structure):
@@ -95,7 +98,7 @@ def load() -> ctypes.CDLL:
     lib.fs_corr_work_bytes.restype = c_size_t
     lib.fs_corr_work_bytes.argtypes = [c_int, c_int, c_int]
     lib.fs_bsattn_work_bytes.restype = c_size_t
-    lib.fs_bsattn_work_bytes.argtypes = [c_int, c_int, c_int, c_int, c_int]
+    lib.fs_bsattn_work_bytes.argtypes = [POINTER(AttnArgs)]
     for name, st in [("fs_pool", PoolArgs), ("fs_corr", CorrArgs), ("fs_stats", StatsArgs),
                      ("fs_select", SelectArgs), ("fs_bsattn", AttnArgs)]:
         fn = getattr(lib, name)

@@ -18,6 +18,7 @@ Hq % Hkv == 0 (native GQA, no repetition needed).
 """
 from __future__ import annotations
 
+import ctypes
 import math
 from dataclasses import dataclass
 
@@ -207,16 +208,17 @@ def block_sparse_attention(query_states, key_states, value_states, blk_cnt=None,
     if out is None:
         out = torch.empty(B, Lq, Hq, D, dtype=q.dtype, device=q.device)
     scale = 1.0 / math.sqrt(D) if softmax_scale is None else float(softmax_scale)
-    work = torch.empty(_lib.load().fs_bsattn_work_bytes(B, Hk, Lk, D, block_size), dtype=torch.uint8,
-                       device=q.device)
-    _lib.call("fs_bsattn", AttnArgs(
+    args = AttnArgs(
         q=q.data_ptr(), q_sb=q.stride(0), q_sh=q.stride(1), q_sl=q.stride(2),
         k=k.data_ptr(), k_sb=k.stride(0), k_sh=k.stride(1), k_sl=k.stride(2),
         v=v.data_ptr(), v_sb=v.stride(0), v_sh=v.stride(1), v_sl=v.stride(2),
         out=out.data_ptr(), o_sb=out.stride(0), o_sh=out.stride(2), o_sl=out.stride(1),
         dtype=_lib.FS_DTYPE[q.dtype], B=B, Hq=Hq, Hk=Hk, Lq=Lq, Lk=Lk, D=D, bs=block_size,
         is_causal=int(bool(is_causal)), softmax_scale=scale,
-        blk_cnt=ptr(blk_cnt), blk_idx=ptr(blk_idx), work=work.data_ptr()))
+        blk_cnt=ptr(blk_cnt), blk_idx=ptr(blk_idx))
+    work = torch.empty(_lib.load().fs_bsattn_work_bytes(ctypes.byref(args)), dtype=torch.uint8, device=q.device)
+    args.work = work.data_ptr()
+    _lib.call("fs_bsattn", args)
     return out
 
 

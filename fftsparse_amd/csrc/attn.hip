@@ -23,9 +23,10 @@
 // LDS rows are 256 B with the 16-byte chunk c of row r stored at c ^ (r & 15)
 // so the 8 lanes of a ds_read_b128 phase hit distinct banks.
 //
-// Scheduling: workgroup w runs on XCD w % 8; XCD x owns every 8th
-// query-block row (last rows first) of every head, which balances the work
-// of unevenly sparse heads across XCDs.
+// Scheduling: workgroup w runs on XCD w % 8.  With block lists, a counting
+// sort (order_kernel) ranks the (head, query block) items by tile count and
+// the items are dealt round-robin to the XCDs, longest first; the dense path
+// gives XCD x every 8th query-block row (last rows first) of every head.
 #include "common.h"
 
 namespace fs {
@@ -50,6 +51,14 @@ template <> struct MfmaOps<bf16_t> {
     __bf16 b = (__bf16)x;
     return __builtin_bit_cast(uint16_t, b);
   }
+  // acc + sum of the 8 elements (v_dot2_f32_bf16 against ones)
+  static __device__ __forceinline__ float sum8(V8 p, float acc) {
+    typedef __bf16 x2 __attribute__((ext_vector_type(2)));
+    const x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc = __builtin_amdgcn_fdot2_f32_bf16(x2{p[2 * i], p[2 * i + 1]}, one, acc, false);
+    return acc;
+  }
 };
 template <> struct MfmaOps<f16_t> {
   using V8 = f16x8_t;
@@ -65,6 +74,13 @@ template <> struct MfmaOps<f16_t> {
   static __device__ __forceinline__ uint16_t bits(float x) {
     _Float16 b = (_Float16)x;
     return __builtin_bit_cast(uint16_t, b);
+  }
+  static __device__ __forceinline__ float sum8(V8 p, float acc) {
+    typedef _Float16 x2 __attribute__((ext_vector_type(2)));
+    const x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc = __builtin_amdgcn_fdot2(x2{p[2 * i], p[2 * i + 1]}, one, acc, false);
+    return acc;
   }
 };
 
@@ -134,40 +150,76 @@ __device__ __forceinline__ void dma16(uint32_t lds_base, const void* gptr) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
                :: "s"(lds_base), "v"(gptr) : "memory");
 }
+// Same, addressed as a wave-uniform base (scalar registers) plus a 32-bit lane offset.
+__device__ __forceinline__ void dma16s(uint32_t lds_base, const void* sbase, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :: "s"(lds_base), "v"(voff), "s"(sbase) : "memory");
+}
+
+// Arguments of the main kernel: the subset of fs_attn_args it reads, with the
+// per-row strides narrowed to 32 bits (checked on the host).
+struct AttnKArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* vt;
+  uint16_t* out;
+  const int32_t* blk_cnt;
+  const uint16_t* blk_idx;
+  const int32_t* order;
+  int64_t q_sb, q_sh, k_sb, k_sh, o_sb, o_sh;
+  int q_sl, k_sl, o_sl;
+  int Hq, Hk, Lq, Lk, Nq, Nk, Lp, total, is_causal;
+  float scale;
+};
+
+// 16-byte LDS operand at byte offset off of base
+__device__ __forceinline__ uint4 lds16(const char* base, uint32_t off) {
+  return *reinterpret_cast<const uint4*>(base + off);
+}
 
 template <int BS, typename T>
-__global__ __launch_bounds__(AttnCfg<BS>::NT) void bsattn_kernel(fs_attn_args a, const uint16_t* __restrict__ vt,
-                                                                 int Nq, int Nk, int Lp, int total, int per_xcd) {
+__global__ __launch_bounds__(AttnCfg<BS>::NT) void bsattn_kernel(AttnKArgs a) {
   using C = AttnCfg<BS>;
   using Ops = MfmaOps<T>;
   using V8 = typename Ops::V8;
-  // double-buffered [K | V^T] tiles; 256-byte rows with swizzled 16-byte chunks
+  // [K | V^T][buffer] tiles; 256-byte rows with swizzled 16-byte chunks
   __shared__ __attribute__((aligned(1024))) uint16_t lds[2][2][C::TILE];
 
-  // Workgroup wg runs on XCD wg % 8.  XCD x takes the query-block rows
-  // r = x, x + 8, x + 16, ... (counted from the last query block, so long
-  // rows start first) of every head: each XCD gets an even share of every
-  // head's work, and the heads of one GQA group at one query block run back
-  // to back on the same XCD (shared K/V tiles in its L2).
+  // Workgroup wg runs on XCD wg % 8.
+  typedef const __attribute__((address_space(4))) uint32_t* cptr32;
   const int wg = blockIdx.x;
   const int x = wg & 7, slot = wg >> 3;
-  const int per_row = a.Hq;                       // items per row: (hk, head in group)
-  const int r = x + 8 * (slot / per_row);
-  if (r >= total) return;                         // total = B * Nq rows
   const int g = a.Hq / a.Hk;
-  const int hsel = slot % per_row;
-  const int hk = hsel / g;
-  const int h = hsel;                             // heads of group hk are hk*g .. hk*g+g-1
-  const int b = r / Nq;
-  const int qb = Nq - 1 - (r - b * Nq);
+  int b, h, qb;
+  if (a.order != nullptr) {
+    // block lists: items in decreasing tile count, dealt round-robin to the XCDs
+    const int p = slot * 8 + x;
+    if (p >= a.total) return;                     // total = Hq * Nq items
+    const int item = (int)((cptr32)(uintptr_t)a.order)[p];
+    b = 0;
+    h = item / a.Nq;
+    qb = item - h * a.Nq;
+  } else {
+    // dense: XCD x takes the query-block rows r = x, x + 8, ... (counted from
+    // the last query block, so long rows start first) of every head; the heads
+    // of one GQA group at one query block run back to back on one XCD and
+    // share their K/V tiles in its L2
+    const int r = x + 8 * (slot / a.Hq);
+    if (r >= a.total) return;                     // total = B * Nq rows
+    h = slot % a.Hq;
+    b = r / a.Nq;
+    qb = a.Nq - 1 - (r - b * a.Nq);
+  }
+  const int hk = h / g;
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (scalar register)
   const int l32 = lane & 31, hi = lane >> 5;
   const int qq = wave % C::QW, kh = wave / C::QW;
   const int kbase = kh * C::KH;
-  const uint16_t* qp = static_cast<const uint16_t*>(a.q) + b * a.q_sb + h * a.q_sh;
-  const uint16_t* kp = static_cast<const uint16_t*>(a.k) + b * a.k_sb + hk * a.k_sh;
-  const uint16_t* vtp = vt + (int64_t)(b * a.Hk + hk) * kD * Lp;
+  const uint16_t* qp = a.q + b * a.q_sb + h * a.q_sh;
+  const uint16_t* kp = a.k + b * a.k_sb + hk * a.k_sh;
+  const uint16_t* vtp = a.vt + (int64_t)(b * a.Hk + hk) * kD * a.Lp;
   const int q0 = qb * BS;
   const int off = a.Lk - a.Lq;
   const int qw0 = q0 + qq * 32;                 // first query of this wave
@@ -185,13 +237,12 @@ __global__ __launch_bounds__(AttnCfg<BS>::NT) void bsattn_kernel(fs_attn_args a,
   // Block lists are read through the scalar unit (constant address space):
   // their completion is tracked by lgkmcnt, so reading the next index never
   // waits on the tile copies in flight (vmcnt).
-  typedef const __attribute__((address_space(4))) uint32_t* cptr32;
   int cnt;
   const bool listed = a.blk_cnt != nullptr;
   int64_t lbase = 0;
   if (listed) {
-    cnt = (int)((cptr32)(uintptr_t)a.blk_cnt)[(int64_t)h * Nq + qb];
-    lbase = ((int64_t)h * Nq + qb) * Nk;
+    cnt = (int)((cptr32)(uintptr_t)a.blk_cnt)[(int64_t)h * a.Nq + qb];
+    lbase = ((int64_t)h * a.Nq + qb) * a.Nk;
   } else {
     const int last_key = a.is_causal ? min(a.Lk - 1, q0 + BS - 1 + off) : a.Lk - 1;
     cnt = last_key < 0 ? 0 : last_key / BS + 1;
@@ -207,41 +258,70 @@ __global__ __launch_bounds__(AttnCfg<BS>::NT) void bsattn_kernel(fs_attn_args a,
     while (cnt > 0 && block_at(cnt - 1) * BS > q0 + BS - 1 + off) --cnt;
   }
 
-  // ---- tile DMA: wave w copies regions w*DPW/2 .. of the K tile and of the V^T tile
-  const uint32_t lds0 = (uint32_t)(uintptr_t)&lds[0][0][0];
-  auto issue = [&](int kb, int buf) {
-    kb = min(kb, Nk - 1);                          // out-of-range entries are skipped at compute
-    const int k0 = kb * BS;
-    const int row = lane >> 4, slot = lane & 15;
+  // ---- tile DMA: wave w copies 1 KiB regions w*NR .. w*NR+NR-1 of the K tile
+  // and of the V^T tile.  koff / voff are this lane's byte offsets inside a
+  // K / V^T tile in global memory (fixed for the loop); each copy adds them to
+  // a wave-uniform tile origin held in scalar registers.
+  constexpr int NR = C::DMA_PER_WAVE / 2;
+  uint32_t koff[NR], voff[NR];
 #pragma unroll
-    for (int i = 0; i < C::DMA_PER_WAVE / 2; ++i) {
-      const int R = wave * (C::DMA_PER_WAVE / 2) + i;          // region: LDS rows 4R .. 4R+3
-      const int r = 4 * R + row;
-      const int c = slot ^ (r & 15);
-      // K rows past Lk are clamped to the last row (their scores are masked)
-      const int key = min(k0 + r, a.Lk - 1);
-      dma16(__builtin_amdgcn_readfirstlane(lds0 + (uint32_t)(((buf * 2 + 0) * C::TILE + R * 512) * 2)),
-            kp + (int64_t)key * a.k_sl + c * 8);
-      int d, kc;
-      if (BS == 128) {
-        d = r;
-        kc = c;
-      } else {                                     // two 64-key d rows per 256-byte LDS row
-        d = 2 * r + (c >> 3);
-        kc = c & 7;
+  for (int i = 0; i < NR; ++i) {
+    const int R = wave * NR + i;                   // region: LDS rows 4R .. 4R+3
+    const int r = 4 * R + (lane >> 4);
+    const int c = (lane & 15) ^ (r & 15);
+    koff[i] = (uint32_t)(r * a.k_sl + c * 8) * 2u;
+    voff[i] = (BS == 128 ? (uint32_t)(r * a.Lp + c * 8)                          // d = r
+                         : (uint32_t)((2 * r + (c >> 3)) * a.Lp + (c & 7) * 8))  // two d rows per LDS row
+              * 2u;
+  }
+  const int Nk = a.Nk;
+  const int k0_last = (Nk - 1) * BS;
+  const bool last_partial = k0_last + BS > a.Lk;
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&lds[0][0][0]);
+  auto issue_k = [&](int kb, int buf) {
+    kb = min(kb, Nk - 1);                          // out-of-range entries are skipped at compute
+    const uint16_t* base = kp + (int64_t)(kb * BS) * a.k_sl;
+    const uint32_t lk = lds0 + (uint32_t)(buf * C::TILE * 2 + wave * NR * 1024);
+    if (last_partial && kb == Nk - 1) {
+      // the last, partial block: K rows past Lk read the last row instead (their scores are masked)
+      int ln = lane;
+      asm volatile("" : "+v"(ln));                 // keep this rare path's offsets out of the loop preheader
+#pragma unroll
+      for (int i = 0; i < NR; ++i) {
+        const int r = 4 * (wave * NR + i) + (ln >> 4);
+        const int c = (ln & 15) ^ (r & 15);
+        dma16s(lk + i * 1024, base, (uint32_t)(min(r, a.Lk - 1 - k0_last) * a.k_sl + c * 8) * 2u);
       }
-      dma16(__builtin_amdgcn_readfirstlane(lds0 + (uint32_t)(((buf * 2 + 1) * C::TILE + R * 512) * 2)),
-            vtp + (int64_t)d * Lp + k0 + kc * 8);
+    } else {
+#pragma unroll
+      for (int i = 0; i < NR; ++i) dma16s(lk + i * 1024, base, koff[i]);
     }
   };
-  auto vt_slot = [](int d, int chunk) {
-    return BS == 128 ? swz(d, chunk) : swz(d >> 1, (d & 1) * 8 + chunk);
+  auto issue_v = [&](int kb, int buf) {
+    const uint16_t* base = vtp + min(kb, Nk - 1) * BS;
+    const uint32_t lv = lds0 + (uint32_t)((2 + buf) * C::TILE * 2 + wave * NR * 1024);
+#pragma unroll
+    for (int i = 0; i < NR; ++i) dma16s(lv + i * 1024, base, voff[i]);
   };
+
+  // MFMA operand addressing.  A lane reads row l32 of a group of 32 rows and
+  // chunk hi of a pair of 16-byte chunks.  The swizzle XORs the chunk with
+  // (row & 15); the group origin R0 is a multiple of 16 and the pair origin C0
+  // is even, so the operand at (R0, C0) of a tile is at byte
+  //   tile + R0 * 256 + (lane_off ^ (C0 << 4)),   lane_off = l32 * 256 + ((hi ^ (l32 & 15)) << 4).
+  // For V^T at BS = 64 an LDS row holds two d rows (d = 2 r + (chunk >> 3)):
+  // the lane's d row dt * 32 + l32 sits in LDS row dt * 16 + (l32 >> 1), chunk
+  // (l32 & 1) * 8 + C0 + hi.
+  const uint32_t lane_off = (uint32_t)(l32 * 256 + ((hi ^ (l32 & 15)) << 4));
+  const uint32_t lane_off_v =
+      BS == 128 ? lane_off
+                : (uint32_t)((l32 >> 1) * 256 + (((((l32 & 1) << 3) | hi) ^ (l32 >> 1)) << 4));
+  constexpr int VROW = BS == 128 ? 32 * 256 : 16 * 256;   // bytes per 32 d rows of V^T
 
   // Running max is kept in the exp2 domain of raw scores times sc; it is only
   // raised (and O rescaled) when a new score exceeds it by more than 2^8, so
   // p = 2^(s*sc - m) <= 256 and most tiles skip the rescale.
-  const float sc = a.softmax_scale * 1.44269504088896340736f;
+  const float sc = a.scale * 1.44269504088896340736f;
   constexpr float kSlack = 8.0f;
   float m_run = -INFINITY, l_run = 0.f;
   f32x16_t o[kD / 32];
@@ -250,124 +330,124 @@ __global__ __launch_bounds__(AttnCfg<BS>::NT) void bsattn_kernel(fs_attn_args a,
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[dt][r] = 0.f;
 
-  // Retire the Q loads here, through a wait the compiler sees: otherwise it
-  // guards their first use inside the loop with a vmcnt(0) on every iteration,
-  // which would also wait for the tile copy in flight.
-  __builtin_amdgcn_s_waitcnt(0);
-  // Pipeline per iteration t: wait for the copy of tile t, one barrier (tile t
-  // visible; every wave is past tile t-1, so its buffer may be refilled),
-  // start the copy of tile t+1, touch tile t+2 into L2 (one dword per
-  // 128-byte line and thread), compute tile t.  The touch loads land in a
-  // register that stays live until a later wait has retired them.
-  auto touch = [&](int kb) -> uint32_t {
-    kb = min(kb, Nk - 1);
-    const int k0 = kb * BS;
-    const uint16_t* p;
-    if (tid < BS * 2) {                            // K: two 128-byte lines per 256-byte row
-      const int key = min(k0 + (tid >> 1), a.Lk - 1);
-      p = kp + (int64_t)key * a.k_sl + (tid & 1) * 64;
-    } else {                                       // V^T: BS/64 lines per d row
-      const int v = tid - BS * 2;
-      p = vtp + (int64_t)(v / (BS / 64)) * Lp + k0 + (v % (BS / 64)) * 64;
+  // S^T = K Q^T for this wave's keys of the K tile in buffer kbuf
+  auto compute_s = [&](int kbuf, f32x16_t* s) {
+    const char* kt_base = reinterpret_cast<const char*>(lds[0][kbuf]) + kbase * 256;
+#pragma unroll
+    for (int kt = 0; kt < C::KT; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[kt][r] = 0.f;
+#pragma unroll
+    for (int st = 0; st < kD / 16; ++st) {
+      const uint32_t lo = lane_off ^ (uint32_t)(st << 5);
+#pragma unroll
+      for (int kt = 0; kt < C::KT; ++kt) {
+        const V8 ka = __builtin_bit_cast(V8, lds16(kt_base + kt * 32 * 256, lo));
+        s[kt] = Ops::mma(ka, qf[st], s[kt]);
+      }
     }
-    uint32_t x;
-    asm volatile("global_load_dword %0, %1, off" : "=v"(x) : "v"(p) : "memory");
-    return x;
   };
-  static_assert(AttnCfg<BS>::NT == BS * 2 + kD * (BS / 64), "one touch line per thread");
-  uint32_t pf_prev = 0, pf_cur = 0;
-  int kb_cur = cnt > 0 ? block_at(0) : 0;
-  if (cnt > 0) issue(kb_cur, 0);
-  if (cnt > 1) pf_cur = touch(block_at(1));
-  for (int t = 0; t < cnt; ++t) {
-    const int buf = t & 1;
-    const bool more = t + 1 < cnt;
-    if (more) asm volatile("s_waitcnt vmcnt(1)" ::: "memory");   // the touch of t+1 may stay in flight
-    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    asm volatile("" :: "v"(pf_prev));             // touch of tile t retired: release its register
-    pf_prev = pf_cur;
-    __builtin_amdgcn_s_barrier();
-    const int kb = kb_cur;
-    if (more) {
-      kb_cur = block_at(t + 1);
-      issue(kb_cur, buf ^ 1);
-    }
-    if (t + 2 < cnt) pf_cur = touch(block_at(t + 2));
-    const int k0 = kb * BS;
-    const int kw0 = k0 + kbase;                   // first key of this wave
-    const bool active = kb < Nk && kw0 < a.Lk && !(a.is_causal && kw0 > qw0 + 31 + off);
-    if (active) {
-      const uint16_t* Kt = lds[buf][0];
-      const uint16_t* Vt = lds[buf][1];
-      // ---- S^T = K Q^T  (this wave's KH keys x 32 queries)
-      f32x16_t s[C::KT];
-#pragma unroll
-      for (int kt = 0; kt < C::KT; ++kt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s[kt][r] = 0.f;
-#pragma unroll
-      for (int st = 0; st < kD / 16; ++st)
-#pragma unroll
-        for (int kt = 0; kt < C::KT; ++kt) {
-          const int row = kbase + kt * 32 + l32;
-          const V8 ka = __builtin_bit_cast(V8, *reinterpret_cast<const uint4*>(&Kt[swz(row, st * 2 + hi)]));
-          s[kt] = Ops::mma(ka, qf[st], s[kt]);
-        }
-      // ---- mask, online softmax (exp2 domain)
-      if ((kw0 + C::KH > a.Lk) || (a.is_causal && kw0 + C::KH - 1 > qw0 + off)) {
-#pragma unroll
-        for (int kt = 0; kt < C::KT; ++kt)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = kw0 + kt * 32 + (r >> 2) * 8 + hi * 4 + (r & 3);
-            if (key >= a.Lk || (a.is_causal && key > qrow + off)) s[kt][r] = -INFINITY;
-          }
-      }
-      float mx = -INFINITY;
-#pragma unroll
-      for (int kt = 0; kt < C::KT; ++kt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kt][r]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * sc;
-      if (__builtin_amdgcn_ballot_w64(mx > m_run + kSlack) != 0) {
-        const float m_new = fmaxf(m_run, mx);
-        const float alpha = __builtin_amdgcn_exp2f(m_run - (m_new == -INFINITY ? 0.f : m_new));
-        l_run *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < kD / 32; ++dt)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
-        m_run = m_new;
-      }
-      const float m_use = m_run == -INFINITY ? 0.f : m_run;
-      float rs = 0.f;
+  // Masking (diagonal / partial tiles only), online softmax and
+  // O^T += V^T P^T for the tile kb whose scores are in s (V^T in buffer vbuf).
+  // The O rescale is rare (see kSlack).
+  auto softmax_pv = [&](int kb, int vbuf, f32x16_t* s) {
+    const int kw0 = kb * BS + kbase;                // first key of this wave
+    if ((kw0 + C::KH > a.Lk) || (a.is_causal && kw0 + C::KH - 1 > qw0 + off)) {
 #pragma unroll
       for (int kt = 0; kt < C::KT; ++kt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][r], sc, -m_use));
-          s[kt][r] = p;
-          rs += p;
+          const int key = kw0 + kt * 32 + (r >> 2) * 8 + hi * 4 + (r & 3);
+          if (key >= a.Lk || (a.is_causal && key > qrow + off)) s[kt][r] = -INFINITY;
         }
-      l_run += rs + __shfl_xor(rs, 32, 64);
-      // ---- O^T += V^T P^T over this wave's keys
+    }
+    float mx = -INFINITY;
 #pragma unroll
-      for (int kk = 0; kk < C::KH / 16; ++kk) {
-        const int kt = kk >> 1, half = kk & 1;
-        float pv[8];
+    for (int kt = 0; kt < C::KT; ++kt)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) pv[j] = s[kt][8 * half + j];
-        const V8 pb = Ops::pack(pv);
-        const int ch = ((kbase + kk * 16) >> 3) + hi;    // 16-byte chunk of this lane's 8 keys
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kt][r]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * sc;
+    if (__builtin_amdgcn_ballot_w64(mx > m_run + kSlack) != 0) {
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - (m_new == -INFINITY ? 0.f : m_new));
+      l_run *= alpha;
 #pragma unroll
-        for (int dt = 0; dt < kD / 32; ++dt) {
-          const V8 va = __builtin_bit_cast(V8, *reinterpret_cast<const uint4*>(&Vt[vt_slot(dt * 32 + l32, ch)]));
-          o[dt] = Ops::mma(va, pb, o[dt]);
-        }
+      for (int dt = 0; dt < kD / 32; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+      m_run = m_new;
+    }
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+    const char* vt_base = reinterpret_cast<const char*>(lds[1][vbuf]);
+    float rs = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < C::KH / 16; ++kk) {
+      const int kt = kk >> 1, half = kk & 1;
+      float pv[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) pv[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][8 * half + j], sc, -m_use));
+      const V8 pb = Ops::pack(pv);
+      rs = Ops::sum8(pb, rs);                       // row sum of the rounded P actually multiplied
+      const uint32_t lo = lane_off_v ^ (uint32_t)(((kbase >> 3) + 2 * kk) << 4);
+#pragma unroll
+      for (int dt = 0; dt < kD / 32; ++dt) {
+        const V8 va = __builtin_bit_cast(V8, lds16(vt_base + dt * VROW, lo));
+        o[dt] = Ops::mma(va, pb, o[dt]);
       }
     }
+    l_run += rs + __shfl_xor(rs, 32, 64);
+  };
+  // whether any key of this wave's half of tile kb is visible to its queries
+  auto active_for = [&](int kb) {
+    const int kw0 = kb * BS + kbase;
+    return kb < Nk && kw0 < a.Lk && !(a.is_causal && kw0 > qw0 + 31 + off);
+  };
+
+  // Retire the Q loads here, through a wait the compiler sees: otherwise it
+  // guards their first use inside the loop with a vmcnt(0) on every iteration,
+  // which would also wait for the tile copies in flight.
+  __builtin_amdgcn_s_waitcnt(0);
+  // Pipeline: K runs one tile ahead of V.  At the top of iteration t the
+  // copies of K(t+1) and V(t) have landed; after one barrier the copies of
+  // K(t+2) (into the buffer of K(t)) and V(t+1) (into the buffer of V(t-1))
+  // start, the MFMAs of S(t+1) are issued, and the softmax of tile t runs on
+  // the VALU while they execute, followed by the P V MFMAs of tile t.
+  f32x16_t sa[C::KT], sb[C::KT];
+  int kb0 = 0, kb1 = 0, kb2 = 0;
+  if (cnt > 0) {
+    kb0 = block_at(0);
+    issue_k(kb0, 0);
+    issue_v(kb0, 0);
+    if (cnt > 1) {
+      kb1 = block_at(1);
+      issue_k(kb1, 1);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    if (active_for(kb0)) compute_s(0, sa);
   }
-  asm volatile("s_waitcnt vmcnt(0)" :: "v"(pf_prev), "v"(pf_cur) : "memory");
+  auto step = [&](int t, f32x16_t* s_cur, f32x16_t* s_next) {
+    // K(t+1), V(t) landed; every wave is past iteration t-1 and its LDS reads
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    if (t + 2 < cnt) {
+      kb2 = block_at(t + 2);
+      issue_k(kb2, t & 1);
+    }
+    if (t + 1 < cnt) {
+      issue_v(kb1, (t + 1) & 1);
+      if (active_for(kb1)) compute_s((t + 1) & 1, s_next);
+    }
+    if (active_for(kb0)) softmax_pv(kb0, t & 1, s_cur);
+    kb0 = kb1;
+    kb1 = kb2;
+  };
+  int t = 0;
+  for (; t + 1 < cnt; t += 2) {
+    step(t, sa, sb);
+    step(t + 1, sb, sa);
+  }
+  if (t < cnt) step(t, sa, sb);
   __syncthreads();
 
   // ---- merge the two key halves through LDS, normalise, store
@@ -393,7 +473,7 @@ __global__ __launch_bounds__(AttnCfg<BS>::NT) void bsattn_kernel(fs_attn_args a,
   const float f1 = __builtin_amdgcn_exp2f(m1 - mu);
   const float l = l_run * f0 + l1 * f1;
   const float inv = l > 0.f ? 1.0f / l : 0.f;
-  uint16_t* op = static_cast<uint16_t*>(a.out) + b * a.o_sb + h * a.o_sh + (int64_t)qrow * a.o_sl;
+  uint16_t* op = a.out + b * a.o_sb + h * a.o_sh + (int64_t)qrow * a.o_sl;
 #pragma unroll
   for (int dt = 0; dt < kD / 32; ++dt)
 #pragma unroll
@@ -412,6 +492,56 @@ __global__ __launch_bounds__(AttnCfg<BS>::NT) void bsattn_kernel(fs_attn_args a,
     }
 }
 
+// ---- longest-first order of (head, query block) items: counting sort by tile count
+constexpr int kOrderThreads = 1024;
+constexpr int kOrderMaxBins = 8192;
+__global__ __launch_bounds__(kOrderThreads) void order_kernel(const int32_t* __restrict__ cnt, int items, int maxc,
+                                                              int32_t* __restrict__ order) {
+  __shared__ int hist[kOrderMaxBins];
+  __shared__ int part[kOrderThreads];
+  const int tid = threadIdx.x;
+  const int nb = maxc + 1;                         // bins 0 .. maxc
+  for (int i = tid; i < nb; i += kOrderThreads) hist[i] = 0;
+  __syncthreads();
+  for (int r = tid; r < items; r += kOrderThreads) atomicAdd(&hist[min(max(cnt[r], 0), maxc)], 1);
+  __syncthreads();
+  // start[c] = number of items with a larger count: scan bins from maxc down
+  const int per = (nb + kOrderThreads - 1) / kOrderThreads;
+  const int c_hi = nb - 1 - tid * per;             // this thread scans bins c_hi, c_hi-1, ...
+  int local = 0;
+  for (int k = 0; k < per; ++k) {
+    const int c = c_hi - k;
+    if (c >= 0) local += hist[c];
+  }
+  part[tid] = local;
+  __syncthreads();
+  for (int off = 1; off < kOrderThreads; off <<= 1) {   // inclusive scan of chunk sums
+    const int v = tid >= off ? part[tid - off] : 0;
+    __syncthreads();
+    part[tid] += v;
+    __syncthreads();
+  }
+  int run = part[tid] - local;                     // exclusive prefix of this chunk
+  for (int k = 0; k < per; ++k) {
+    const int c = c_hi - k;
+    if (c >= 0) {
+      const int h = hist[c];
+      hist[c] = run;
+      run += h;
+    }
+  }
+  __syncthreads();
+  for (int r = tid; r < items; r += kOrderThreads) {
+    const int pos = atomicAdd(&hist[min(max(cnt[r], 0), maxc)], 1);
+    order[pos] = r;
+  }
+}
+
+static size_t vt_bytes(const fs_attn_args& a) {
+  const int64_t Nk = (a.Lk + a.bs - 1) / a.bs;
+  return ((size_t)a.B * a.Hk * a.D * Nk * a.bs * 2 + 255) & ~(size_t)255;
+}
+
 template <int BS, typename T>
 static int launch_attn(const fs_attn_args& a, int Nq, int Nk, hipStream_t s) {
   const int Lp = Nk * BS;
@@ -420,9 +550,33 @@ static int launch_attn(const fs_attn_args& a, int Nq, int Nk, hipStream_t s) {
   vt_kernel<<<a.B * a.Hk * slabs, 256, 0, s>>>(static_cast<const uint16_t*>(a.v), a.v_sb, a.v_sh, a.v_sl, vt,
                                                a.Hk, a.Lk, Lp);
   if (int rc = fs_host::launch_status("fs_bsattn (V^T)")) return rc;
-  const int rows = a.B * Nq;
-  const int per_xcd = (rows + 7) / 8 * a.Hq;
-  bsattn_kernel<BS, T><<<per_xcd * 8, AttnCfg<BS>::NT, 0, s>>>(a, vt, Nq, Nk, Lp, rows, per_xcd);
+  int32_t* order = nullptr;
+  int total;
+  unsigned grid;
+  if (a.blk_cnt && Nk < kOrderMaxBins) {
+    order = reinterpret_cast<int32_t*>(static_cast<char*>(a.work) + vt_bytes(a));
+    total = a.Hq * Nq;
+    order_kernel<<<1, kOrderThreads, 0, s>>>(a.blk_cnt, total, Nk, order);
+    if (int rc = fs_host::launch_status("fs_bsattn (order)")) return rc;
+    grid = (unsigned)((total + 7) / 8 * 8);
+  } else {
+    total = a.B * Nq;
+    grid = (unsigned)((total + 7) / 8 * a.Hq * 8);
+  }
+  AttnKArgs k;
+  k.q = static_cast<const uint16_t*>(a.q);
+  k.k = static_cast<const uint16_t*>(a.k);
+  k.vt = vt;
+  k.out = static_cast<uint16_t*>(a.out);
+  k.blk_cnt = a.blk_cnt;
+  k.blk_idx = a.blk_idx;
+  k.order = order;
+  k.q_sb = a.q_sb; k.q_sh = a.q_sh; k.k_sb = a.k_sb; k.k_sh = a.k_sh; k.o_sb = a.o_sb; k.o_sh = a.o_sh;
+  k.q_sl = (int)a.q_sl; k.k_sl = (int)a.k_sl; k.o_sl = (int)a.o_sl;
+  k.Hq = a.Hq; k.Hk = a.Hk; k.Lq = a.Lq; k.Lk = a.Lk;
+  k.Nq = Nq; k.Nk = Nk; k.Lp = Lp; k.total = total; k.is_causal = a.is_causal;
+  k.scale = a.softmax_scale;
+  bsattn_kernel<BS, T><<<grid, AttnCfg<BS>::NT, 0, s>>>(k);
   return fs_host::launch_status("fs_bsattn");
 }
 
@@ -430,10 +584,10 @@ static int launch_attn(const fs_attn_args& a, int Nq, int Nk, hipStream_t s) {
 
 using namespace fs;
 
-extern "C" size_t fs_bsattn_work_bytes(int B, int Hk, int Lk, int D, int bs) {
-  if (B <= 0 || Hk <= 0 || Lk <= 0 || D <= 0 || bs <= 0) return 0;
-  const int64_t Nk = (Lk + bs - 1) / bs;
-  return (size_t)B * Hk * D * Nk * bs * 2;
+extern "C" size_t fs_bsattn_work_bytes(const fs_attn_args* a) {
+  if (!a || a->B <= 0 || a->Hq <= 0 || a->Hk <= 0 || a->Lq <= 0 || a->Lk <= 0 || a->D <= 0 || a->bs <= 0) return 0;
+  const int64_t Nq = (a->Lq + a->bs - 1) / a->bs;
+  return vt_bytes(*a) + (size_t)a->Hq * Nq * sizeof(int32_t);
 }
 
 extern "C" int fs_bsattn(const fs_attn_args* a, void* stream) {
@@ -458,6 +612,10 @@ extern "C" int fs_bsattn(const fs_attn_args* a, void* stream) {
   const int Nk = (a->Lk + a->bs - 1) / a->bs;
   FS_CHECK_SUPPORTED((int64_t)a->B * a->Hq * Nq < (1ll << 30) && (int64_t)a->B * a->Hk * Nk * a->bs / 64 < (1ll << 31),
                      "fs_bsattn: grid too large");
+  // per-lane tile-copy offsets are 32-bit byte offsets: 128 rows of a row stride, 128 d rows of V^T
+  FS_CHECK_SUPPORTED(a->q_sl < (1 << 23) && a->k_sl < (1 << 23) && a->o_sl < (1 << 23) &&
+                         (int64_t)Nk * a->bs < (1 << 23),
+                     "fs_bsattn: row stride or sequence too large");
   hipStream_t s = (hipStream_t)stream;
   if (a->bs == 128) {
     return a->dtype == FS_DTYPE_BF16 ? launch_attn<128, bf16_t>(*a, Nq, Nk, s) : launch_attn<128, f16_t>(*a, Nq, Nk, s);

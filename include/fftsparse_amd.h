@@ -142,8 +142,9 @@ FS_API int fs_select(const fs_select_args* a, void* stream);
  * Lk - Lq when is_causal).  blk_cnt == NULL selects every key block up to the
  * causal limit (dense causal attention).  Supported: dtype bf16/f16, D == 128,
  * bs in {64, 128}.  All tensors are strided views with d contiguous.
- * work: fs_bsattn_work_bytes(B, Hk, Lk, D, bs) bytes of device scratch (V is
- * staged there transposed before the attention kernel runs). */
+ * work: fs_bsattn_work_bytes(a) bytes of device scratch (V is staged there
+ * transposed, and the work items' longest-first order is computed there,
+ * before the attention kernel runs). */
 typedef struct {
   const void* q; int64_t q_sb, q_sh, q_sl;
   const void* k; int64_t k_sb, k_sh, k_sl;
@@ -156,7 +157,7 @@ typedef struct {
   const uint16_t* blk_idx;      /* [Hq][Nq][Nk] */
   void* work;
 } fs_attn_args;
-FS_API size_t fs_bsattn_work_bytes(int B, int Hk, int Lk, int D, int bs);
+FS_API size_t fs_bsattn_work_bytes(const fs_attn_args* a);
 FS_API int fs_bsattn(const fs_attn_args* a, void* stream);
 
 /* Description of the last failure on this thread ("" if none). */

@@ -45,7 +45,7 @@ def test_bad_shapes_rejected_without_gpu():
     lib = _lib.load()
     a = _lib.AttnArgs(q=16, k=16, v=16, out=16, dtype=1, B=1, Hq=3, Hk=2, Lq=10, Lk=10, D=128, bs=128)
     assert lib.fs_bsattn(ctypes.byref(a), None) == -1
-    a = _lib.AttnArgs(q=16, k=16, v=16, out=16, dtype=1, B=1, Hq=4, Hk=2, Lq=10, Lk=10, D=96, bs=128)
+    a = _lib.AttnArgs(q=16, k=16, v=16, out=16, work=16, dtype=1, B=1, Hq=4, Hk=2, Lq=10, Lk=10, D=96, bs=128)
     assert lib.fs_bsattn(ctypes.byref(a), None) == -2
     assert b"head_dim" in lib.fs_last_error()
 
