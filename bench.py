@@ -43,8 +43,8 @@ def parse():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-dense", action="store_true", help="skip the dense comparators")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-qblocks", type=int, default=24,
-                    help="query blocks of head 0 timed for the CPU attention sample")
+    ap.add_argument("--cpu-heads", type=int, default=2,
+                    help="query heads (all their query blocks) timed for the CPU attention sample")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (5 times) to calibrate "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE, then exit")
@@ -56,10 +56,11 @@ def _ev():
     return torch.cuda.Event(enable_timing=True)
 
 
-def cpu_baseline(q, k, v, kw, bs, nnz_total, sample_qblocks):
+def cpu_baseline(q, k, v, kw, bs, nnz_total, sample_heads):
     """Oracle restatement of the reference path on this host's cores: full
-    selection, and fp32 block-sparse attention over a sample of query blocks
-    of one head, scaled to the whole layer by the selected-tile count."""
+    selection, and fp32 block-sparse attention over every query block of the
+    first sample_heads query heads, scaled to the whole layer by the
+    selected-tile count (heads are independent)."""
     import torch
     from oracle import v7
     threads = torch.get_num_threads()
@@ -67,11 +68,10 @@ def cpu_baseline(q, k, v, kw, bs, nnz_total, sample_qblocks):
     t0 = time.perf_counter()
     ref = v7.select_mask(qc, kc, **kw)
     t_sel = time.perf_counter() - t0
-    N = ref.params.N
-    qbl = sorted({int(round(x)) for x in torch.linspace(0, N - 1, sample_qblocks).tolist()})
-    tiles = int(ref.mask[0, qbl].sum())
+    heads = list(range(min(sample_heads, q.shape[1])))
+    tiles = int(ref.mask[heads].sum())
     t0 = time.perf_counter()
-    v7.block_sparse_attention(qc, kc, vc, ref.mask, bs, heads=[0], qblocks=qbl)
+    v7.block_sparse_attention(qc, kc, vc, ref.mask, bs, heads=heads)
     t_att_sample = time.perf_counter() - t0
     t_att = t_att_sample * nnz_total / max(1, tiles)
     return {
@@ -79,14 +79,30 @@ def cpu_baseline(q, k, v, kw, bs, nnz_total, sample_qblocks):
         "unit": "ms",
         "cores": threads,
         "kind": "port",
-        "sample": (f"oracle/v7.py on this host: full v7 selection ({t_sel:.1f} s) + fp32 block-sparse "
-                   f"attention over {len(qbl)} query blocks of head 0 ({tiles} tiles, {t_att_sample:.1f} s) "
-                   f"scaled x{nnz_total / max(1, tiles):.0f} to the layer's {nnz_total} selected tiles"),
+        "sample": (f"oracle/v7.py on this host ({threads} torch threads): full v7 selection ({t_sel:.1f} s) + "
+                   f"fp32 block-sparse attention over all query blocks of heads {heads} ({tiles} tiles, "
+                   f"{t_att_sample:.1f} s) scaled x{nnz_total / max(1, tiles):.1f} to the layer's {nnz_total} "
+                   f"selected tiles"),
         "select_ms": round(t_sel * 1e3, 1),
         "attn_ms_scaled": round(t_att * 1e3, 1),
         "cpu_model": _cpu_model(),
         "os_cpu_count": os.cpu_count(),
     }
+
+
+def pmc_traffic(kernel, config):
+    """HBM bytes per launch of a kernel from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE and WRITE_SIZE, calibrated against a plain copy), or
+    None when that kernel/config was not profiled."""
+    path = os.path.join(ROOT, "profiles", "traffic.txt")
+    try:
+        for line in open(path):
+            f = line.split()
+            if len(f) >= 4 and not line.startswith("#") and f[0] == kernel and f[1] == config:
+                return int(float(f[2]) + float(f[3]))
+    except OSError:
+        pass
+    return None
 
 
 def _cpu_model():
@@ -116,7 +132,7 @@ def main():
         print(json.dumps({"copy_calib_bytes": n, "launches": 5}))
         return
     import fftsparse_amd  # noqa: F401
-    from fftsparse_amd import block_sparse_attention, select_blocks
+    from fftsparse_amd import AttentionCall, block_sparse_attention, select_blocks
     from fftsparse_amd.synth import CONFIGS, make_config
 
     cfg = CONFIGS[args.config]
@@ -131,29 +147,38 @@ def main():
     Hq, L, D = q.shape[1], q.shape[2], q.shape[3]
     Hk = k.shape[1]
 
+    # One step = selection (pool, corr, stats, select) + attention (V^T
+    # pre-pass, then order + attention kernel), all on torch's current stream,
+    # which is the stream the events below are recorded on.
     def step(ev=None):
         if ev:
             ev[0].record()
         sel = select_blocks(q, k, **kw)
         if ev:
             ev[1].record()
-        out = block_sparse_attention(q, k, v, sel.blk_cnt, sel.blk_idx, block_size=bs)
+        call = AttentionCall(q, k, v, sel.blk_cnt, sel.blk_idx, block_size=bs)
+        call.prepare()
         if ev:
             ev[2].record()
+        out = call.run()
+        if ev:
+            ev[3].record()
         return sel, out
 
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    events = [(_ev(), _ev(), _ev()) for _ in range(args.steps)]
+    events = [(_ev(), _ev(), _ev(), _ev()) for _ in range(args.steps)]
+    torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
         sel, _ = step(events[i])
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) * 1e3 / args.steps
-    sel_ms = [a.elapsed_time(b) for a, b, c in events]
-    att_ms = [b.elapsed_time(c) for a, b, c in events]
-    tot_ms = [a.elapsed_time(c) for a, b, c in events]
+    sel_ms = [e[0].elapsed_time(e[1]) for e in events]
+    att_ms = [e[1].elapsed_time(e[3]) for e in events]
+    run_ms = [e[2].elapsed_time(e[3]) for e in events]
+    tot_ms = [e[0].elapsed_time(e[3]) for e in events]
     ms = statistics.mean(tot_ms)
 
     nnz = sel.nnz()
@@ -161,7 +186,8 @@ def main():
     density = nnz / (Hq * N * (N + 1) / 2)
     attn_flops = 4.0 * D * bs * bs * nnz
     t_att = statistics.mean(att_ms)
-    achieved = attn_flops / (t_att * 1e-3) / 1e12
+    t_run = statistics.mean(run_ms)
+    achieved = attn_flops / (t_run * 1e-3) / 1e12
     esz = q.element_size()
     sel_bytes = L * Hq * D * esz + L * Hk * D * esz
     t_sel = statistics.mean(sel_ms)
@@ -200,7 +226,7 @@ def main():
     cpu = None
     if not args.no_cpu:
         torch.cuda.synchronize()
-        cpu = cpu_baseline(q, k, v, kw, bs, nnz, args.cpu_qblocks)
+        cpu = cpu_baseline(q, k, v, kw, bs, nnz, args.cpu_heads)
 
     line = {
         "metric": METRIC,
@@ -225,18 +251,23 @@ def main():
         "attn_ms": round(t_att, 4),
         "select_ms_median": round(statistics.median(sel_ms), 4),
         "attn_ms_median": round(statistics.median(att_ms), 4),
+        "attn_kernel_ms": round(t_run, 4),
         "host_wall_ms_per_step": round(wall, 4),
         "density": round(density, 5),
         "selected_tiles": nnz,
         "stripe_heads": stripe,
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
-                     "kernel": "fs::bsattn_kernel<128,bf16>",
-                     "work": "4*D*bs^2 flop per selected (query block, key block) tile"},
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": pmc_traffic("bsattn", cfg.name),
+                     "kernel": f"fs::bsattn_kernel<{bs},{'bf16' if q.dtype == torch.bfloat16 else 'f16'}>",
+                     "work": f"4*D*bs^2 flop per selected (query block, key block) tile x {nnz} tiles",
+                     "timed": "fs_bsattn_run (order pass + attention kernel), HIP events on the launch stream"},
         "roofline_select": {"bound": "hbm", "achieved": round(sel_bytes / (t_sel * 1e-3) / 1e9, 1),
                             "peak": PEAK_HBM_GBS, "unit": "GB/s",
                             "frac": round(sel_bytes / (t_sel * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-                            "traffic": None, "work": "Q and K read once (L*(Hq+Hkv)*D*2 bytes)"},
+                            "traffic": pmc_traffic("select", cfg.name),
+                            "work": "Q and K read once (L*(Hq+Hkv)*D*2 bytes)",
+                            "timed": "the four selection launches (pool, corr x2, stats, select)"},
         "cpu_baseline": cpu,
         "input_gen_s": round(t_gen, 1),
     }

@@ -9,7 +9,8 @@ attn_src/fix_mask_attn/my_attn.py):
     select_blocks(q, k, ...)                        stage 1 only (block lists)
     block_sparse_attention(q, k, v, cnt, idx, ...)  stage 2 only
 """
-from .attn import BlockSelection, block_sparse_attention, myattn_prefill, select_blocks  # noqa: F401
+from .attn import AttentionCall, BlockSelection, block_sparse_attention, myattn_prefill, select_blocks  # noqa: F401
 from . import fix_mask  # noqa: F401
 
-__all__ = ["myattn_prefill", "select_blocks", "block_sparse_attention", "BlockSelection", "fix_mask"]
+__all__ = ["myattn_prefill", "select_blocks", "block_sparse_attention", "AttentionCall", "BlockSelection",
+           "fix_mask"]

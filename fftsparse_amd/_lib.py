@@ -75,7 +75,7 @@ class AttnArgs(ctypes.Structure):
 STRUCTS = [PoolArgs, CorrArgs, StatsArgs, SelectArgs, AttnArgs]
 
 ENTRY_POINTS = ["fs_pool", "fs_corr_work_bytes", "fs_corr", "fs_stats", "fs_select", "fs_bsattn_work_bytes",
-                "fs_bsattn",
+                "fs_bsattn", "fs_bsattn_prepare", "fs_bsattn_run",
                 "fs_last_error", "fs_abi_version", "fs_sizeof_args"]
 
 _lib = None
@@ -100,7 +100,8 @@ def load() -> ctypes.CDLL:
     lib.fs_bsattn_work_bytes.restype = c_size_t
     lib.fs_bsattn_work_bytes.argtypes = [POINTER(AttnArgs)]
     for name, st in [("fs_pool", PoolArgs), ("fs_corr", CorrArgs), ("fs_stats", StatsArgs),
-                     ("fs_select", SelectArgs), ("fs_bsattn", AttnArgs)]:
+                     ("fs_select", SelectArgs), ("fs_bsattn", AttnArgs), ("fs_bsattn_prepare", AttnArgs),
+                     ("fs_bsattn_run", AttnArgs)]:
         fn = getattr(lib, name)
         fn.restype = c_int
         fn.argtypes = [POINTER(st), c_void_p]

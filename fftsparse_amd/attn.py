@@ -189,37 +189,64 @@ def select_blocks(query_states: torch.Tensor, key_states: torch.Tensor, *, block
     return sel
 
 
+class AttentionCall:
+    """One prepared stage-2 call: argument struct, workspace and output.
+
+    ``prepare()`` stages V^T in the workspace (fs_bsattn_prepare), ``run()``
+    orders the work items and runs the attention kernel (fs_bsattn_run), and
+    ``__call__`` does both in one C call (fs_bsattn).  Every launch goes on
+    torch's current stream."""
+
+    def __init__(self, query_states, key_states, value_states, blk_cnt=None, blk_idx=None, *,
+                 block_size=128, is_causal=True, softmax_scale=None, out=None):
+        q = _check_layout(query_states)
+        k = _check_layout(key_states)
+        v = _check_layout(value_states)
+        B, Hq, Lq, D = q.shape
+        Hk, Lk = k.shape[1], k.shape[2]
+        if v.shape[1] != Hk or v.shape[2] != Lk or k.shape[0] != B or v.shape[0] != B:
+            raise ValueError("key/value shapes do not match")
+        if q.dtype not in (torch.bfloat16, torch.float16) or k.dtype != q.dtype or v.dtype != q.dtype:
+            # flash-attention kernels accept fp16/bf16 only, as does the reference's
+            # block_sparse_attn_func.
+            raise RuntimeError("FlashAttention only supports fp16 and bf16 data type")
+        if out is None:
+            out = torch.empty(B, Lq, Hq, D, dtype=q.dtype, device=q.device)
+        scale = 1.0 / math.sqrt(D) if softmax_scale is None else float(softmax_scale)
+        args = AttnArgs(
+            q=q.data_ptr(), q_sb=q.stride(0), q_sh=q.stride(1), q_sl=q.stride(2),
+            k=k.data_ptr(), k_sb=k.stride(0), k_sh=k.stride(1), k_sl=k.stride(2),
+            v=v.data_ptr(), v_sb=v.stride(0), v_sh=v.stride(1), v_sl=v.stride(2),
+            out=out.data_ptr(), o_sb=out.stride(0), o_sh=out.stride(2), o_sl=out.stride(1),
+            dtype=_lib.FS_DTYPE[q.dtype], B=B, Hq=Hq, Hk=Hk, Lq=Lq, Lk=Lk, D=D, bs=block_size,
+            is_causal=int(bool(is_causal)), softmax_scale=scale,
+            blk_cnt=ptr(blk_cnt), blk_idx=ptr(blk_idx))
+        self.work = torch.empty(_lib.load().fs_bsattn_work_bytes(ctypes.byref(args)), dtype=torch.uint8,
+                                device=q.device)
+        args.work = self.work.data_ptr()
+        self.args = args
+        self.out = out
+        self._keep = (q, k, v, blk_cnt, blk_idx)      # the pointers in args stay valid
+
+    def prepare(self) -> None:
+        _lib.call("fs_bsattn_prepare", self.args)
+
+    def run(self) -> torch.Tensor:
+        _lib.call("fs_bsattn_run", self.args)
+        return self.out
+
+    def __call__(self) -> torch.Tensor:
+        _lib.call("fs_bsattn", self.args)
+        return self.out
+
+
 def block_sparse_attention(query_states, key_states, value_states, blk_cnt=None, blk_idx=None, *,
                            block_size=128, is_causal=True, softmax_scale=None, out=None) -> torch.Tensor:
     """Block-sparse (or, with no block lists, dense causal) attention.
 
     q [B,Hq,Lq,D], k/v [B,Hk,Lk,D] -> out [B, Lq, Hq, D] in the input dtype."""
-    q = _check_layout(query_states)
-    k = _check_layout(key_states)
-    v = _check_layout(value_states)
-    B, Hq, Lq, D = q.shape
-    Hk, Lk = k.shape[1], k.shape[2]
-    if v.shape[1] != Hk or v.shape[2] != Lk or k.shape[0] != B or v.shape[0] != B:
-        raise ValueError("key/value shapes do not match")
-    if q.dtype not in (torch.bfloat16, torch.float16) or k.dtype != q.dtype or v.dtype != q.dtype:
-        # flash-attention kernels accept fp16/bf16 only, as does the reference's
-        # block_sparse_attn_func.
-        raise RuntimeError("FlashAttention only supports fp16 and bf16 data type")
-    if out is None:
-        out = torch.empty(B, Lq, Hq, D, dtype=q.dtype, device=q.device)
-    scale = 1.0 / math.sqrt(D) if softmax_scale is None else float(softmax_scale)
-    args = AttnArgs(
-        q=q.data_ptr(), q_sb=q.stride(0), q_sh=q.stride(1), q_sl=q.stride(2),
-        k=k.data_ptr(), k_sb=k.stride(0), k_sh=k.stride(1), k_sl=k.stride(2),
-        v=v.data_ptr(), v_sb=v.stride(0), v_sh=v.stride(1), v_sl=v.stride(2),
-        out=out.data_ptr(), o_sb=out.stride(0), o_sh=out.stride(2), o_sl=out.stride(1),
-        dtype=_lib.FS_DTYPE[q.dtype], B=B, Hq=Hq, Hk=Hk, Lq=Lq, Lk=Lk, D=D, bs=block_size,
-        is_causal=int(bool(is_causal)), softmax_scale=scale,
-        blk_cnt=ptr(blk_cnt), blk_idx=ptr(blk_idx))
-    work = torch.empty(_lib.load().fs_bsattn_work_bytes(ctypes.byref(args)), dtype=torch.uint8, device=q.device)
-    args.work = work.data_ptr()
-    _lib.call("fs_bsattn", args)
-    return out
+    return AttentionCall(query_states, key_states, value_states, blk_cnt, blk_idx, block_size=block_size,
+                         is_causal=is_causal, softmax_scale=softmax_scale, out=out)()
 
 
 def myattn_prefill(

@@ -542,14 +542,11 @@ static size_t vt_bytes(const fs_attn_args& a) {
   return ((size_t)a.B * a.Hk * a.D * Nk * a.bs * 2 + 255) & ~(size_t)255;
 }
 
+// order pass (block lists only) and the main kernel, reading V^T from the workspace
 template <int BS, typename T>
-static int launch_attn(const fs_attn_args& a, int Nq, int Nk, hipStream_t s) {
+static int launch_run(const fs_attn_args& a, int Nq, int Nk, hipStream_t s) {
   const int Lp = Nk * BS;
-  uint16_t* vt = static_cast<uint16_t*>(a.work);
-  const int slabs = Lp / 64;
-  vt_kernel<<<a.B * a.Hk * slabs, 256, 0, s>>>(static_cast<const uint16_t*>(a.v), a.v_sb, a.v_sh, a.v_sl, vt,
-                                               a.Hk, a.Lk, Lp);
-  if (int rc = fs_host::launch_status("fs_bsattn (V^T)")) return rc;
+  const uint16_t* vt = static_cast<const uint16_t*>(a.work);
   int32_t* order = nullptr;
   int total;
   unsigned grid;
@@ -590,35 +587,58 @@ extern "C" size_t fs_bsattn_work_bytes(const fs_attn_args* a) {
   return vt_bytes(*a) + (size_t)a->Hq * Nq * sizeof(int32_t);
 }
 
-extern "C" int fs_bsattn(const fs_attn_args* a, void* stream) {
-  FS_CHECK_ARG(a != nullptr, "fs_bsattn: null args");
-  FS_CHECK_ARG(a->q && a->k && a->v && a->out && a->work, "fs_bsattn: null tensor pointer");
+// Argument checks shared by the three attention entry points.
+static int check_attn(const fs_attn_args* a, const char* fn) {
+  FS_CHECK_ARG(a != nullptr, "%s: null args", fn);
+  FS_CHECK_ARG(a->q && a->k && a->v && a->out && a->work, "%s: null tensor pointer", fn);
   FS_CHECK_ARG(a->B >= 1 && a->Hq >= 1 && a->Hk >= 1 && a->Hq % a->Hk == 0,
-               "fs_bsattn: Hq=%d must be a multiple of Hk=%d", a->Hq, a->Hk);
-  FS_CHECK_ARG(a->Lq >= 1 && a->Lk >= 1, "fs_bsattn: empty sequence");
-  FS_CHECK_SUPPORTED(a->D == kD, "fs_bsattn: head_dim %d unsupported (128 only)", a->D);
-  FS_CHECK_SUPPORTED(a->bs == 64 || a->bs == 128, "fs_bsattn: block size %d unsupported", a->bs);
+               "%s: Hq=%d must be a multiple of Hk=%d", fn, a->Hq, a->Hk);
+  FS_CHECK_ARG(a->Lq >= 1 && a->Lk >= 1, "%s: empty sequence", fn);
+  FS_CHECK_SUPPORTED(a->D == kD, "%s: head_dim %d unsupported (128 only)", fn, a->D);
+  FS_CHECK_SUPPORTED(a->bs == 64 || a->bs == 128, "%s: block size %d unsupported", fn, a->bs);
   FS_CHECK_SUPPORTED(a->dtype == FS_DTYPE_BF16 || a->dtype == FS_DTYPE_F16,
-                     "fs_bsattn: dtype %d unsupported (bf16/f16)", a->dtype);
+                     "%s: dtype %d unsupported (bf16/f16)", fn, a->dtype);
   FS_CHECK_ARG(a->blk_cnt == nullptr || (a->blk_idx != nullptr && a->B == 1),
-               "fs_bsattn: block lists need blk_idx and B == 1");
+               "%s: block lists need blk_idx and B == 1", fn);
   const int64_t strides[] = {a->q_sb, a->q_sh, a->q_sl, a->k_sb, a->k_sh, a->k_sl,
                              a->v_sb, a->v_sh, a->v_sl, a->o_sb, a->o_sh, a->o_sl};
-  for (int64_t st : strides) FS_CHECK_ARG(st % 8 == 0, "fs_bsattn: strides must be multiples of 8 elements");
+  for (int64_t st : strides) FS_CHECK_ARG(st % 8 == 0, "%s: strides must be multiples of 8 elements", fn);
   const uintptr_t ptrs[] = {(uintptr_t)a->q, (uintptr_t)a->k, (uintptr_t)a->v, (uintptr_t)a->out,
                             (uintptr_t)a->work};
-  for (uintptr_t p : ptrs) FS_CHECK_ARG(p % 16 == 0, "fs_bsattn: tensors must be 16-byte aligned");
+  for (uintptr_t p : ptrs) FS_CHECK_ARG(p % 16 == 0, "%s: tensors must be 16-byte aligned", fn);
+  const int64_t Nq = (a->Lq + a->bs - 1) / a->bs;
+  const int64_t Nk = (a->Lk + a->bs - 1) / a->bs;
+  FS_CHECK_SUPPORTED((int64_t)a->B * a->Hq * Nq < (1ll << 30) && (int64_t)a->B * a->Hk * Nk * a->bs / 64 < (1ll << 31),
+                     "%s: grid too large", fn);
+  // per-lane tile-copy offsets are 32-bit byte offsets: 128 rows of a row stride, 128 d rows of V^T
+  FS_CHECK_SUPPORTED(a->q_sl < (1 << 23) && a->k_sl < (1 << 23) && a->o_sl < (1 << 23) && Nk * a->bs < (1 << 23),
+                     "%s: row stride or sequence too large", fn);
+  return FS_OK;
+}
+
+extern "C" int fs_bsattn_prepare(const fs_attn_args* a, void* stream) {
+  if (int rc = check_attn(a, "fs_bsattn_prepare")) return rc;
+  const int Nk = (a->Lk + a->bs - 1) / a->bs;
+  const int Lp = Nk * a->bs;
+  vt_kernel<<<a->B * a->Hk * (Lp / 64), 256, 0, (hipStream_t)stream>>>(
+      static_cast<const uint16_t*>(a->v), a->v_sb, a->v_sh, a->v_sl, static_cast<uint16_t*>(a->work), a->Hk, a->Lk,
+      Lp);
+  return fs_host::launch_status("fs_bsattn_prepare");
+}
+
+extern "C" int fs_bsattn_run(const fs_attn_args* a, void* stream) {
+  if (int rc = check_attn(a, "fs_bsattn_run")) return rc;
   const int Nq = (a->Lq + a->bs - 1) / a->bs;
   const int Nk = (a->Lk + a->bs - 1) / a->bs;
-  FS_CHECK_SUPPORTED((int64_t)a->B * a->Hq * Nq < (1ll << 30) && (int64_t)a->B * a->Hk * Nk * a->bs / 64 < (1ll << 31),
-                     "fs_bsattn: grid too large");
-  // per-lane tile-copy offsets are 32-bit byte offsets: 128 rows of a row stride, 128 d rows of V^T
-  FS_CHECK_SUPPORTED(a->q_sl < (1 << 23) && a->k_sl < (1 << 23) && a->o_sl < (1 << 23) &&
-                         (int64_t)Nk * a->bs < (1 << 23),
-                     "fs_bsattn: row stride or sequence too large");
   hipStream_t s = (hipStream_t)stream;
   if (a->bs == 128) {
-    return a->dtype == FS_DTYPE_BF16 ? launch_attn<128, bf16_t>(*a, Nq, Nk, s) : launch_attn<128, f16_t>(*a, Nq, Nk, s);
+    return a->dtype == FS_DTYPE_BF16 ? launch_run<128, bf16_t>(*a, Nq, Nk, s) : launch_run<128, f16_t>(*a, Nq, Nk, s);
   }
-  return a->dtype == FS_DTYPE_BF16 ? launch_attn<64, bf16_t>(*a, Nq, Nk, s) : launch_attn<64, f16_t>(*a, Nq, Nk, s);
+  return a->dtype == FS_DTYPE_BF16 ? launch_run<64, bf16_t>(*a, Nq, Nk, s) : launch_run<64, f16_t>(*a, Nq, Nk, s);
+}
+
+extern "C" int fs_bsattn(const fs_attn_args* a, void* stream) {
+  if (int rc = check_attn(a, "fs_bsattn")) return rc;
+  if (int rc = fs_bsattn_prepare(a, stream)) return rc;
+  return fs_bsattn_run(a, stream);
 }

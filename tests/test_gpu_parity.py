@@ -226,6 +226,25 @@ def test_attention_noncausal_and_dense():
     _attn_check(out[0], ref)
 
 
+def test_attention_prepare_run_equals_single_call():
+    """fs_bsattn_prepare + fs_bsattn_run give fs_bsattn's output bit for bit,
+    and run() may be repeated on one prepared workspace."""
+    from fftsparse_amd import AttentionCall
+    q, k, v = make_qkv(3000, 4, 2, dtype=torch.bfloat16, seed=8)
+    N = (3000 + 127) // 128
+    mask = torch.rand(4, N, N, generator=torch.Generator().manual_seed(1)) < 0.4
+    mask = (mask | torch.eye(N, dtype=torch.bool)) & torch.ones(N, N, dtype=torch.bool).tril()
+    cnt, idx = lists_from_mask(mask, DEV)
+    qg, kg, vg = _gpu(q, k, v)
+    whole = block_sparse_attention(qg, kg, vg, cnt, idx).clone()
+    call = AttentionCall(qg, kg, vg, cnt, idx)
+    call.prepare()
+    first = call.run().clone()
+    second = call.run()
+    torch.cuda.synchronize()
+    assert torch.equal(first, whole) and torch.equal(second, whole)
+
+
 def test_myattn_prefill_end_to_end_c1_shape():
     """myattn_prefill on config 1's shape: output vs fp32 attention under the
     oracle mask on a sample of query blocks of every head."""
