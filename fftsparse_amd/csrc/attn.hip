@@ -23,10 +23,14 @@
 // LDS rows are 256 B with the 16-byte chunk c of row r stored at c ^ (r & 15)
 // so the 8 lanes of a ds_read_b128 phase hit distinct banks.
 //
-// Scheduling: workgroup w runs on XCD w % 8.  With block lists, a counting
-// sort (order_kernel) ranks the (head, query block) items by tile count and
-// the items are dealt round-robin to the XCDs, longest first; the dense path
-// gives XCD x every 8th query-block row (last rows first) of every head.
+// Scheduling: workgroup w runs on XCD w % 8.  With block lists, the query
+// blocks of a head are grouped in runs of consecutive blocks; a counting sort
+// (order_kernel) ranks the runs by tile count, and the runs are dealt
+// round-robin to the XCDs, longest first, the blocks of a run in consecutive
+// slots of one XCD (neighbouring query blocks select shifted copies of the
+// same lag diagonals and the same columns, which then hit that XCD's L2).
+// The dense path gives XCD x every 8th query-block row (last rows first) of
+// every head.
 #include "common.h"
 
 namespace fs {
@@ -169,6 +173,7 @@ struct AttnKArgs {
   int64_t q_sb, q_sh, k_sb, k_sh, o_sb, o_sh;
   int q_sl, k_sl, o_sl;
   int Hq, Hk, Lq, Lk, Nq, Nk, Lp, total, is_causal;
+  int run;                      // query blocks per scheduling unit (block lists)
   float scale;
 };
 
@@ -192,13 +197,19 @@ __global__ __launch_bounds__(AttnCfg<BS>::NT) void bsattn_kernel(AttnKArgs a) {
   const int g = a.Hq / a.Hk;
   int b, h, qb;
   if (a.order != nullptr) {
-    // block lists: items in decreasing tile count, dealt round-robin to the XCDs
-    const int p = slot * 8 + x;
-    if (p >= a.total) return;                     // total = Hq * Nq items
-    const int item = (int)((cptr32)(uintptr_t)a.order)[p];
+    // block lists: units of `run` consecutive query blocks of one head, in
+    // decreasing tile count, dealt round-robin to the XCDs; a unit's query
+    // blocks take consecutive slots of one XCD, so they run side by side and
+    // share the K/V tiles of their (shifted) lag diagonals and columns in its L2
+    const int unit_slot = slot / a.run, j = slot - unit_slot * a.run;
+    const int p = unit_slot * 8 + x;
+    if (p >= a.total) return;                     // total = Hq * ceil(Nq / run) units
+    const int unit = (int)((cptr32)(uintptr_t)a.order)[p];
+    const int nc = (a.Nq + a.run - 1) / a.run;
     b = 0;
-    h = item / a.Nq;
-    qb = item - h * a.Nq;
+    h = unit / nc;
+    qb = (unit - h * nc) * a.run + j;
+    if (qb >= a.Nq) return;
   } else {
     // dense: XCD x takes the query-block rows r = x, x + 8, ... (counted from
     // the last query block, so long rows start first) of every head; the heads
@@ -492,20 +503,29 @@ __global__ __launch_bounds__(AttnCfg<BS>::NT) void bsattn_kernel(AttnKArgs a) {
     }
 }
 
-// ---- longest-first order of (head, query block) items: counting sort by tile count
+// ---- longest-first order of the scheduling units (run consecutive query
+// blocks of one head): counting sort of their total tile count, in bins of 2^shift
 constexpr int kOrderThreads = 1024;
 constexpr int kOrderMaxBins = 8192;
-__global__ __launch_bounds__(kOrderThreads) void order_kernel(const int32_t* __restrict__ cnt, int items, int maxc,
-                                                              int32_t* __restrict__ order) {
+__global__ __launch_bounds__(kOrderThreads) void order_kernel(const int32_t* __restrict__ cnt, int Hq, int Nq, int run,
+                                                              int Nk, int shift, int32_t* __restrict__ order) {
   __shared__ int hist[kOrderMaxBins];
   __shared__ int part[kOrderThreads];
   const int tid = threadIdx.x;
-  const int nb = maxc + 1;                         // bins 0 .. maxc
+  const int nc = (Nq + run - 1) / run;
+  const int units = Hq * nc;
+  const int nb = ((run * Nk) >> shift) + 1;        // bins 0 .. (run Nk) >> shift
+  auto bin_of = [&](int u) {
+    const int h = u / nc, q0 = (u - h * nc) * run;
+    int c = 0;
+    for (int j = 0; j < run && q0 + j < Nq; ++j) c += min(max(cnt[(int64_t)h * Nq + q0 + j], 0), Nk);
+    return c >> shift;
+  };
   for (int i = tid; i < nb; i += kOrderThreads) hist[i] = 0;
   __syncthreads();
-  for (int r = tid; r < items; r += kOrderThreads) atomicAdd(&hist[min(max(cnt[r], 0), maxc)], 1);
+  for (int u = tid; u < units; u += kOrderThreads) atomicAdd(&hist[bin_of(u)], 1);
   __syncthreads();
-  // start[c] = number of items with a larger count: scan bins from maxc down
+  // start[c] = number of units in higher bins: scan bins from the top down
   const int per = (nb + kOrderThreads - 1) / kOrderThreads;
   const int c_hi = nb - 1 - tid * per;             // this thread scans bins c_hi, c_hi-1, ...
   int local = 0;
@@ -521,19 +541,19 @@ __global__ __launch_bounds__(kOrderThreads) void order_kernel(const int32_t* __r
     part[tid] += v;
     __syncthreads();
   }
-  int run = part[tid] - local;                     // exclusive prefix of this chunk
+  int acc = part[tid] - local;                     // exclusive prefix of this chunk
   for (int k = 0; k < per; ++k) {
     const int c = c_hi - k;
     if (c >= 0) {
       const int h = hist[c];
-      hist[c] = run;
-      run += h;
+      hist[c] = acc;
+      acc += h;
     }
   }
   __syncthreads();
-  for (int r = tid; r < items; r += kOrderThreads) {
-    const int pos = atomicAdd(&hist[min(max(cnt[r], 0), maxc)], 1);
-    order[pos] = r;
+  for (int u = tid; u < units; u += kOrderThreads) {
+    const int pos = atomicAdd(&hist[bin_of(u)], 1);
+    order[pos] = u;
   }
 }
 
@@ -550,12 +570,18 @@ static int launch_run(const fs_attn_args& a, int Nq, int Nk, hipStream_t s) {
   int32_t* order = nullptr;
   int total;
   unsigned grid;
-  if (a.blk_cnt && Nk < kOrderMaxBins) {
+  // Scheduling units of `run` consecutive query blocks: at C2 (Nq = 1024) a
+  // run of 16 halves the K/V bytes fetched beyond L2 (166 -> 83 GB) and
+  // still leaves 2048 units for longest-first balance over 256 CUs.
+  const int run = min(16, max(1, Nq / 64));
+  if (a.blk_cnt) {
+    int shift = 0;
+    while (((run * Nk) >> shift) + 1 > kOrderMaxBins) ++shift;
     order = reinterpret_cast<int32_t*>(static_cast<char*>(a.work) + vt_bytes(a));
-    total = a.Hq * Nq;
-    order_kernel<<<1, kOrderThreads, 0, s>>>(a.blk_cnt, total, Nk, order);
+    total = a.Hq * ((Nq + run - 1) / run);
+    order_kernel<<<1, kOrderThreads, 0, s>>>(a.blk_cnt, a.Hq, Nq, run, Nk, shift, order);
     if (int rc = fs_host::launch_status("fs_bsattn (order)")) return rc;
-    grid = (unsigned)((total + 7) / 8 * 8);
+    grid = (unsigned)((total + 7) / 8 * 8 * run);
   } else {
     total = a.B * Nq;
     grid = (unsigned)((total + 7) / 8 * a.Hq * 8);
@@ -572,6 +598,7 @@ static int launch_run(const fs_attn_args& a, int Nq, int Nk, hipStream_t s) {
   k.q_sl = (int)a.q_sl; k.k_sl = (int)a.k_sl; k.o_sl = (int)a.o_sl;
   k.Hq = a.Hq; k.Hk = a.Hk; k.Lq = a.Lq; k.Lk = a.Lk;
   k.Nq = Nq; k.Nk = Nk; k.Lp = Lp; k.total = total; k.is_causal = a.is_causal;
+  k.run = run;
   k.scale = a.softmax_scale;
   bsattn_kernel<BS, T><<<grid, AttnCfg<BS>::NT, 0, s>>>(k);
   return fs_host::launch_status("fs_bsattn");
