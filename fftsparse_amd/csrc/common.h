@@ -122,11 +122,14 @@ __device__ __forceinline__ float key_to_f32(uint32_t key) {
 
 // Block-wide top-k over vals[0..n): writes sel[i] = 1 for the k largest
 // values (ties to the lower index) and 0 elsewhere; returns the k-th largest
-// value.  k is clamped to [0, n].  The threshold key is found by a 32-step
-// bisection on the order-preserving uint32 key; equal keys are ranked in
-// index order by wave 0 with ballots.  All threads of the block must call.
-__device__ inline float block_topk_select(const float* vals, int n, int k, uint8_t* sel,
-                                          int* iscratch) {
+// value.  k is clamped to [0, n].  The k-th largest order-preserving key is
+// found by a radix select, 8 bits per pass from the top: each pass
+// histograms the digits of the keys that match the digits chosen so far and
+// wave 0 picks the digit that holds the (remaining) k-th key.  Equal keys are
+// then ranked in index order by wave 0 with ballots.  hist needs kTopkScratch
+// ints; all threads of the block must call.
+constexpr int kTopkScratch = 256 + 2;
+__device__ inline float block_topk_select(const float* vals, int n, int k, uint8_t* sel, int* hist) {
   const int tid = threadIdx.x, nt = blockDim.x;
   if (k > n) k = n;
   if (k <= 0) {
@@ -134,13 +137,41 @@ __device__ inline float block_topk_select(const float* vals, int n, int k, uint8
     __syncthreads();
     return NAN;
   }
-  uint32_t prefix = 0;
-  for (int b = 31; b >= 0; --b) {
-    const uint32_t cand = prefix | (1u << b);
-    int c = 0;
-    for (int i = tid; i < n; i += nt) c += order_key(vals[i]) >= cand;
-    c = block_sum_i(c, iscratch);
-    if (c >= k) prefix = cand;
+  uint32_t prefix = 0, mask = 0;
+  int kk = k;                                      // rank wanted among keys matching prefix under mask
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int i = tid; i < 256; i += nt) hist[i] = 0;
+    __syncthreads();
+    for (int i = tid; i < n; i += nt) {
+      const uint32_t key = order_key(vals[i]);
+      if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1);
+    }
+    __syncthreads();
+    if (tid < 64) {
+      // lane l owns digits 4l .. 4l+3; inc = keys with digit >= 4l
+      const int c0 = hist[4 * tid], c1 = hist[4 * tid + 1], c2 = hist[4 * tid + 2], c3 = hist[4 * tid + 3];
+      const int tot = c0 + c1 + c2 + c3;
+      int inc = tot;
+      for (int off = 1; off < 64; off <<= 1) {
+        const int v = __shfl_down(inc, off, 64);
+        if (tid + off < 64) inc += v;
+      }
+      const int above = inc - tot;                 // keys with digit >= 4l + 4
+      if (inc >= kk && above < kk) {
+        int d = 4 * tid + 3, s = above + c3;
+        int prev = above;
+        if (s < kk) { prev = s; s += c2; d = 4 * tid + 2; }
+        if (s < kk) { prev = s; s += c1; d = 4 * tid + 1; }
+        if (s < kk) { prev = s; s += c0; d = 4 * tid; }
+        hist[256] = d;
+        hist[257] = kk - prev;                     // rank within digit d
+      }
+    }
+    __syncthreads();
+    prefix |= (uint32_t)hist[256] << shift;
+    mask |= 255u << shift;
+    kk = hist[257];
+    __syncthreads();
   }
   int gt = 0;
   for (int i = tid; i < n; i += nt) {
@@ -148,7 +179,7 @@ __device__ inline float block_topk_select(const float* vals, int n, int k, uint8
     gt += g;
     sel[i] = g;
   }
-  gt = block_sum_i(gt, iscratch);
+  gt = block_sum_i(gt, hist);
   const int need = k - gt;
   if (tid < 64) {
     int base = 0;
@@ -162,6 +193,29 @@ __device__ inline float block_topk_select(const float* vals, int n, int k, uint8
   }
   __syncthreads();
   return key_to_f32(prefix);
+}
+
+// Partial dot product of two rows of D elements (D * sizeof(T) a multiple of
+// 16 bytes) held by a group of 16 lanes: lane `sub` takes the 16-byte chunks
+// sub, sub + 16, ...; group16_sum then adds the group's partials.  A wave so
+// reads four whole rows per load instruction.
+template <typename T>
+__device__ __forceinline__ float row_dot_part(const T* a, const T* b, int D, int sub) {
+  constexpr int V = 16 / sizeof(T);
+  float s = 0.f;
+  for (int c = sub; c * V < D; c += 16) {
+    const uint4 ra = *reinterpret_cast<const uint4*>(a + c * V);
+    const uint4 rb = *reinterpret_cast<const uint4*>(b + c * V);
+    const T* ea = reinterpret_cast<const T*>(&ra);
+    const T* eb = reinterpret_cast<const T*>(&rb);
+#pragma unroll
+    for (int e = 0; e < V; ++e) s += to_f32(ea[e]) * to_f32(eb[e]);
+  }
+  return s;
+}
+__device__ __forceinline__ float group16_sum(float v) {
+  for (int o = 8; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
 }
 
 }  // namespace fs

@@ -5,7 +5,9 @@
 //
 // Grid (Hq, 2 + n_samples), 1024 threads: y == 0 is the column task, y == 1
 // the last-row task and y >= 2 the diagonal sample y - 2.  Row dot products
-// use 16-byte loads; all arithmetic is fp32 with a fixed accumulation order.
+// are computed by groups of 16 lanes (16-byte loads, four whole rows per wave
+// load); all arithmetic is fp32 with a fixed accumulation order.  Top-k / top-n
+// use the block radix select of common.h.
 #include "common.h"
 
 namespace fs {
@@ -13,28 +15,11 @@ namespace fs {
 constexpr int kStatThreads = 1024;
 constexpr int kStatWaves = kStatThreads / 64;
 
-// fp32 dot product of two rows of D elements (D % 8 == 0), 16-byte loads,
-// sequential accumulation in d order.
-template <typename T>
-__device__ __forceinline__ float dot_rows(const T* a, const T* b, int D) {
-  constexpr int V = 16 / sizeof(T);
-  float s = 0.f;
-  for (int d0 = 0; d0 < D; d0 += V) {
-    const uint4 ra = *reinterpret_cast<const uint4*>(a + d0);
-    const uint4 rb = *reinterpret_cast<const uint4*>(b + d0);
-    const T* ea = reinterpret_cast<const T*>(&ra);
-    const T* eb = reinterpret_cast<const T*>(&rb);
-#pragma unroll
-    for (int e = 0; e < V; ++e) s += to_f32(ea[e]) * to_f32(eb[e]);
-  }
-  return s;
-}
-
 template <typename T>
 __global__ __launch_bounds__(kStatThreads) void stats_kernel(fs_stats_args a, float inv_sqrt_d) {
   extern __shared__ float sm[];          // [N] values, then [kStatWaves][D] run sums
   __shared__ float red[32];
-  __shared__ int ired[32];
+  __shared__ int ired[kTopkScratch];
   const int h = blockIdx.x, task = blockIdx.y, tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int N = a.N, D = a.D;
@@ -103,10 +88,17 @@ __global__ __launch_bounds__(kStatThreads) void stats_kernel(fs_stats_args a, fl
     if (a.last_k <= 0) return;
     float* lv = sm;
     const T* ql = qb + (int64_t)(N - 1) * D;
-    for (int j = tid; j < N; j += kStatThreads) {
-      const float s = Conv<T>::round(dot_rows(ql, kb + (int64_t)j * D, D));
-      lv[j] = s;
-      a.last_scores[(int64_t)h * N + j] = s;
+    const int g = lane >> 4, sub = lane & 15;
+    for (int j0 = wave * 4; j0 < N; j0 += kStatWaves * 4) {
+      const int j = j0 + g;
+      float d = 0.f;
+      if (j < N) d = row_dot_part(ql, kb + (int64_t)j * D, D, sub);
+      d = group16_sum(d);
+      if (sub == 0 && j < N) {
+        const float s = Conv<T>::round(d);
+        lv[j] = s;
+        a.last_scores[(int64_t)h * N + j] = s;
+      }
     }
     __syncthreads();
     block_topk_select(lv, N, a.last_k, a.last_sel + (int64_t)h * N, ired);
@@ -119,8 +111,16 @@ __global__ __launch_bounds__(kStatThreads) void stats_kernel(fs_stats_args a, fl
   float* dv = sm;
   // diagonal length minus the dropped last element; an out-of-range lag reads nothing
   const int nd = (tau >= 0 && tau < N) ? N - tau - 1 : 0;
-  for (int j = tid; j < nd; j += kStatThreads)
-    dv[j] = dot_rows(qb + (int64_t)(j + tau) * D, kb + (int64_t)j * D, D) * inv_sqrt_d;
+  {
+    const int g = lane >> 4, sub = lane & 15;
+    for (int j0 = wave * 4; j0 < nd; j0 += kStatWaves * 4) {
+      const int j = j0 + g;
+      float d = 0.f;
+      if (j < nd) d = row_dot_part(qb + (int64_t)(j + tau) * D, kb + (int64_t)j * D, D, sub);
+      d = group16_sum(d);
+      if (sub == 0 && j < nd) dv[j] = d * inv_sqrt_d;
+    }
+  }
   __syncthreads();
   float sabs = 0.f;
   for (int j = tid; j < nd; j += kStatThreads) sabs += fabsf(dv[j]);
