@@ -10,18 +10,21 @@
 // LDS.  X = (Z[f] + conj Z[M-f]) / 2 and Y = (Z[f] - conj Z[M-f]) / 2i give
 // the cross spectrum X conj(Y), summed over d in registers.
 //
-// Kernel 1 (grid Hq x ceil(D/dpg)): each workgroup stages dpg dims of one
-// head (8, 4 or 2 by N) from the pooled rows into LDS, transforms them one by
-// one and writes its partial cross spectrum (M/2+1 bins) to the work buffer.
+// Kernel 1 (grid Hq x ceil(D/dpg)): each workgroup loads dpg dims of one head
+// (dpg M <= 16384 complex values: 8 dims up to N = 1024) from the pooled rows
+// (16-byte loads) straight into the bit-reversed order of dpg transforms in
+// LDS, runs their radix-2 stages together (one barrier per stage) and writes
+// its partial cross spectrum (M/2+1 bins) to the work buffer.
 // Kernel 2 (grid Hq): sums the partials, inverts with one FFT per head, and
 // applies the reference's post-processing and threshold in the same kernel.
+#include <algorithm>
+
 #include "common.h"
 
 namespace fs {
 
-constexpr int kFftThreads = 256;
+constexpr int kFftThreads = 1024;              // 4 waves per SIMD hide the LDS latency of the butterflies
 constexpr int kMaxLogM = 13;                              // M <= 8192, N <= 4096
-constexpr int kMaxBins = ((1 << kMaxLogM) / 2 + 1 + kFftThreads - 1) / kFftThreads;
 
 __device__ __forceinline__ int bitrev(int x, int logM) { return (int)(__brev((uint32_t)x) >> (32 - logM)); }
 
@@ -56,57 +59,82 @@ __device__ void fft_dit(float2* buf, const float2* tw, int M, int logM) {
   }
 }
 
+// Radix-2 DIT stages over nf transforms of length M stored back to back in
+// buf (each in bit-reversed order); one barrier per stage for all of them.
+__device__ void fft_dit_batch(float2* buf, const float2* tw, int M, int logM, int nf) {
+  const int hm = M / 2;
+  for (int s = 1; s <= logM; ++s) {
+    const int half = 1 << (s - 1);
+    const int tws = M >> s;
+    for (int b = threadIdx.x; b < nf * hm; b += blockDim.x) {
+      const int f = b / hm, bb = b - f * hm;
+      const int grp = bb >> (s - 1);
+      const int pos = bb & (half - 1);
+      float2* x = buf + f * M;
+      const int i0 = (grp << s) + pos, i1 = i0 + half;
+      const float2 t = cmul(x[i1], tw[pos * tws]);
+      const float2 u = x[i0];
+      x[i0] = make_float2(u.x + t.x, u.y + t.y);
+      x[i1] = make_float2(u.x - t.x, u.y - t.y);
+    }
+    __syncthreads();
+  }
+}
+
 template <typename T>
 __global__ __launch_bounds__(kFftThreads) void corr_partial_kernel(fs_corr_args a, int M, int logM, int dpg,
                                                                    float2* part) {
   extern __shared__ float2 smem[];
-  float2* buf = smem;
-  float2* tw = smem + M;
-  float2* stage = smem + M + M / 2;                 // [dpg][N] (q, k) pairs of this group's dims
+  float2* tw = smem;                                // [M/2] twiddles
+  float2* buf = smem + M / 2;                       // [dpg][M] transforms of z = q + i k
   const int h = blockIdx.x, g = blockIdx.y, G = gridDim.y;
   const int hk = h / (a.Hq / a.Hk);
   const int N = a.N, D = a.D, tid = threadIdx.x;
   const T* qb = static_cast<const T*>(a.q_b) + (int64_t)h * N * D;
   const T* kb = static_cast<const T*>(a.k_b) + (int64_t)hk * N * D;
   fill_twiddles(tw, M);
-  // stage the group's dims of every row once (independent loads, row-contiguous)
+  // load the group's dims of every row (contiguous in the row) into the
+  // bit-reversed positions of the dpg transforms; rows past N are zero
   const int d0 = g * dpg;
   const int nd = min(dpg, D - d0);
-  for (int n = tid; n < N; n += kFftThreads) {
-    for (int e = 0; e < nd; ++e)
-      stage[e * N + n] = make_float2(to_f32(qb[(int64_t)n * D + d0 + e]), to_f32(kb[(int64_t)n * D + d0 + e]));
-  }
-  const int nb = M / 2 + 1;
-  float2 acc[kMaxBins];
+  constexpr int V = 16 / sizeof(T);
+  const bool vec = (nd % V) == 0 && (d0 % V) == 0 && (D % V) == 0;
+  for (int n = tid; n < M; n += kFftThreads) {
+    const int p = bitrev(n, logM);
+    if (n >= N) {
+      for (int e = 0; e < nd; ++e) buf[e * M + p] = make_float2(0.f, 0.f);
+    } else if (vec) {
+      for (int c = 0; c < nd; c += V) {
+        const uint4 rq = *reinterpret_cast<const uint4*>(qb + (int64_t)n * D + d0 + c);
+        const uint4 rk = *reinterpret_cast<const uint4*>(kb + (int64_t)n * D + d0 + c);
+        const T* eq = reinterpret_cast<const T*>(&rq);
+        const T* ek = reinterpret_cast<const T*>(&rk);
 #pragma unroll
-  for (int r = 0; r < kMaxBins; ++r) acc[r] = make_float2(0.f, 0.f);
-  __syncthreads();
-  for (int dd = 0; dd < nd; ++dd) {
-    for (int n = tid; n < M; n += kFftThreads)
-      buf[bitrev(n, logM)] = n < N ? stage[dd * N + n] : make_float2(0.f, 0.f);
-    __syncthreads();
-    fft_dit(buf, tw, M, logM);
-#pragma unroll
-    for (int r = 0; r < kMaxBins; ++r) {
-      const int f = tid + r * kFftThreads;
-      if (f < nb) {
-        const float2 A = buf[f];
-        const float2 Bc = buf[(M - f) & (M - 1)];       // B = conj(Bc)
-        // X conj(Y) = (A + B) conj(A - B) * i / 4
-        const float2 P = make_float2(A.x + Bc.x, A.y - Bc.y);
-        const float2 Qc = make_float2(A.x - Bc.x, -(A.y + Bc.y));
-        const float2 pr = cmul(P, Qc);
-        acc[r].x += -0.25f * pr.y;
-        acc[r].y += 0.25f * pr.x;
+        for (int e = 0; e < V; ++e) buf[(c + e) * M + p] = make_float2(to_f32(eq[e]), to_f32(ek[e]));
       }
+    } else {
+      for (int e = 0; e < nd; ++e)
+        buf[e * M + p] = make_float2(to_f32(qb[(int64_t)n * D + d0 + e]), to_f32(kb[(int64_t)n * D + d0 + e]));
     }
-    __syncthreads();
   }
+  __syncthreads();
+  fft_dit_batch(buf, tw, M, logM, nd);
+  // X conj(Y) summed over the group's dims, in dim order
+  const int nb = M / 2 + 1;
   float2* out = part + ((int64_t)h * G + g) * nb;
-#pragma unroll
-  for (int r = 0; r < kMaxBins; ++r) {
-    const int f = tid + r * kFftThreads;
-    if (f < nb) out[f] = acc[r];
+  for (int f = tid; f < nb; f += kFftThreads) {
+    float2 acc = make_float2(0.f, 0.f);
+    for (int e = 0; e < nd; ++e) {
+      const float2 A = buf[e * M + f];
+      const float2 Bc = buf[e * M + ((M - f) & (M - 1))];   // B = conj(Bc)
+      // X conj(Y) = (A + B) conj(A - B) * i / 4
+      const float2 P = make_float2(A.x + Bc.x, A.y - Bc.y);
+      const float2 Qc = make_float2(A.x - Bc.x, -(A.y + Bc.y));
+      const float2 pr = cmul(P, Qc);
+      acc.x += -0.25f * pr.y;
+      acc.y += 0.25f * pr.x;
+    }
+    out[f] = acc;
   }
 }
 
@@ -179,8 +207,12 @@ static int launch_partial(const fs_corr_args& a, dim3 grid, size_t smem, int M, 
   return 0;
 }
 
-// dims per workgroup: keeps the staged rows at 2 * dpg * N * 8 bytes <= 64 KiB
-static int dims_per_group(int N) { return N <= 1024 ? 8 : (N <= 2048 ? 4 : 2); }
+// dims per workgroup: dpg transforms of M complex values fill at most 128 KiB of LDS
+static int dims_per_group(int N) {
+  int logM = 1;
+  while ((1 << logM) < 2 * N) ++logM;
+  return std::min(8, 16384 >> logM);
+}
 
 static int corr_logM(int N) {
   int logM = 1;
@@ -216,7 +248,7 @@ extern "C" int fs_corr(const fs_corr_args* a, void* stream) {
   hipStream_t s = (hipStream_t)stream;
   float2* part = static_cast<float2*>(a->work);
   const size_t sm_fft = (size_t)(M + M / 2) * sizeof(float2);
-  const size_t sm1 = sm_fft + (size_t)dpg * a->N * sizeof(float2);
+  const size_t sm1 = (size_t)(M / 2 + (size_t)dpg * M) * sizeof(float2);
   dim3 g1(a->Hq, G);
   int rc = 0;
   switch (a->dtype) {

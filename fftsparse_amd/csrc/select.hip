@@ -4,7 +4,9 @@
 // columns; attn_src/fix_mask_attn/my_attn.py:39-79 for the fixed mask).
 //
 // One workgroup (4 waves) owns RPW consecutive query-block rows of one head.
-// A diffuse head first computes its score panel S[rows][0..last row] into LDS
+// Stripe heads (and the fixed mask) and diffuse heads are served by two
+// launches of the kernel, so only the diffuse launch reserves LDS for the
+// score panel.  A diffuse head first computes its score panel S[rows][0..last row] into LDS
 // (fp32 dot products, fixed order).  Each wave then walks one row at a time:
 // for a diffuse row it finds the k_i-th largest score by a 32-step bisection
 // on the ordered float key with wave-wide counts, and in a single ascending
@@ -17,7 +19,10 @@ namespace fs {
 constexpr int kSelThreads = 256;
 constexpr int kSelWaves = kSelThreads / 64;
 
-template <typename T>
+// DIFF selects the head kind a launch serves: false = stripe heads and the
+// fixed (dyn_mode 0) mask, no score panel and no dynamic LDS; true = diffuse
+// heads, with the panel.  Each launch returns at once for heads of the other kind.
+template <typename T, bool DIFF>
 __global__ __launch_bounds__(kSelThreads) void select_kernel(fs_select_args a, int rows_per_wave,
                                                              float inv_sqrt_d) {
   extern __shared__ float panel[];       // [RPW][N] scores (diffuse heads) then [RPW][D] q rows
@@ -41,17 +46,18 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(fs_select_args a, i
       mv = s / (float)a.n_samples;
       stripe = mv <= a.stripe_threshold;        // false for nan
     }
-    if (r0 == 0 && tid == 0) {
+    if (!DIFF && r0 == 0 && tid == 0) {
       if (a.mean_var) a.mean_var[h] = mv;
       if (a.is_stripe) a.is_stripe[h] = stripe ? 1 : 0;
     }
   }
   const bool diffuse = a.dyn_mode == 1 && !stripe;
+  if (diffuse != DIFF) return;                     // the other launch serves this head
   const bool use_lags = a.dyn_mode == 1 && stripe;
   const bool use_cols = a.col_mode == 2 || (a.col_mode == 1 && stripe);
   const int rend = min(N, r0 + RPW);
 
-  if (diffuse) {
+  if (DIFF) {
     // ---- score panel S[i][j] = (q_b[i] . k_b[j]) * (1/sqrt(D)), j <= i (:234-249)
     const T* qb = static_cast<const T*>(a.q_b) + (int64_t)h * N * D;
     const T* kb = static_cast<const T*>(a.k_b) + (int64_t)hk * N * D;
@@ -101,7 +107,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(fs_select_args a, i
     // ---- diffuse row: k_i-th largest of S[i][0..i] (:271-276)
     uint32_t thr = 0;
     int need = 0;
-    if (diffuse) {
+    if (DIFF) {
       int k = (int)((float)(i + 1) * a.qk_topk_ratio);
       if (k < 1) k = 1;
       const int n = i + 1;
@@ -137,14 +143,14 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(fs_select_args a, i
           const int t = i - j;
           if (t >= a.remote_start && j >= a.keep_sink && (flags[t] & 1)) in = true;
         }
-        if (diffuse && j <= i) {
+        if (DIFF && j <= i) {
           const uint32_t key = order_key(srow[j]);
           if (key > thr) in = true;
           eq = key == thr;
         }
         if (use_cols && j <= i && (fj & 2)) in = true;
       }
-      if (diffuse) {
+      if (DIFF) {
         const uint64_t me = __ballot(eq);
         if (eq && eq_seen + rank_below(me) < need) in = true;
         eq_seen += __popcll(me);
@@ -160,8 +166,13 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(fs_select_args a, i
 template <typename T>
 static int launch_select(const fs_select_args& a, unsigned grid, size_t smem, int rows_per_wave,
                          float inv_sqrt_d, hipStream_t s) {
-  if (int rc = fs_host::allow_dynamic_lds(select_kernel<T>, smem, "fs_select")) return rc;
-  select_kernel<T><<<grid, kSelThreads, smem, s>>>(a, rows_per_wave, inv_sqrt_d);
+  // stripe heads and the fixed mask: no panel
+  select_kernel<T, false><<<grid, kSelThreads, 0, s>>>(a, rows_per_wave, inv_sqrt_d);
+  if (a.dyn_mode == 1) {
+    // diffuse heads (possible only with the dynamic mask)
+    if (int rc = fs_host::allow_dynamic_lds(select_kernel<T, true>, smem, "fs_select")) return rc;
+    select_kernel<T, true><<<grid, kSelThreads, smem, s>>>(a, rows_per_wave, inv_sqrt_d);
+  }
   return 0;
 }
 
