@@ -19,7 +19,7 @@ import torch  # noqa: F401  (must precede the library load, see module docstring
 LIB_PATH = Path(os.environ.get("FFTSPARSE_AMD_LIB") or Path(__file__).resolve().with_name("libfftsparse_amd.so"))
 
 FS_DTYPE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 
 class PoolArgs(ctypes.Structure):
@@ -47,6 +47,20 @@ class StatsArgs(ctypes.Structure):
                 ("last_scores", c_void_p), ("last_sel", c_void_p)]
 
 
+class ScoresArgs(ctypes.Structure):
+    _fields_ = [("q_b", c_void_p), ("k_b", c_void_p),
+                ("dtype", c_int), ("Hq", c_int), ("Hk", c_int), ("N", c_int), ("D", c_int),
+                ("local_window", c_int), ("keep_sink", c_int), ("remote_start", c_int),
+                ("corr_threshold", c_float),
+                ("corr", c_void_p), ("corr_sum", c_void_p), ("keep_tau", c_void_p),
+                ("sample_taus", c_void_p), ("n_samples", c_int),
+                ("col_start", c_int), ("col_end", c_int), ("n_cols", c_int),
+                ("last_k", c_int),
+                ("diag_var", c_void_p), ("col_mean", c_void_p), ("col_sel", c_void_p),
+                ("last_scores", c_void_p), ("last_sel", c_void_p),
+                ("work", c_void_p)]
+
+
 class SelectArgs(ctypes.Structure):
     _fields_ = [("q_b", c_void_p), ("k_b", c_void_p),
                 ("dtype", c_int), ("Hq", c_int), ("Hk", c_int), ("N", c_int), ("Nk", c_int), ("D", c_int),
@@ -72,9 +86,10 @@ class AttnArgs(ctypes.Structure):
                 ("blk_cnt", c_void_p), ("blk_idx", c_void_p), ("work", c_void_p)]
 
 
-STRUCTS = [PoolArgs, CorrArgs, StatsArgs, SelectArgs, AttnArgs]
+STRUCTS = [PoolArgs, CorrArgs, StatsArgs, SelectArgs, AttnArgs, ScoresArgs]
 
-ENTRY_POINTS = ["fs_pool", "fs_corr_work_bytes", "fs_corr", "fs_stats", "fs_select", "fs_bsattn_work_bytes",
+ENTRY_POINTS = ["fs_pool", "fs_corr_work_bytes", "fs_corr", "fs_stats", "fs_scores_work_bytes", "fs_scores",
+                "fs_select", "fs_bsattn_work_bytes",
                 "fs_bsattn", "fs_bsattn_prepare", "fs_bsattn_run",
                 "fs_last_error", "fs_abi_version", "fs_sizeof_args"]
 
@@ -97,9 +112,11 @@ def load() -> ctypes.CDLL:
     lib.fs_sizeof_args.argtypes = [c_int]
     lib.fs_corr_work_bytes.restype = c_size_t
     lib.fs_corr_work_bytes.argtypes = [c_int, c_int, c_int]
+    lib.fs_scores_work_bytes.restype = c_size_t
+    lib.fs_scores_work_bytes.argtypes = [c_int, c_int, c_int]
     lib.fs_bsattn_work_bytes.restype = c_size_t
     lib.fs_bsattn_work_bytes.argtypes = [POINTER(AttnArgs)]
-    for name, st in [("fs_pool", PoolArgs), ("fs_corr", CorrArgs), ("fs_stats", StatsArgs),
+    for name, st in [("fs_pool", PoolArgs), ("fs_corr", CorrArgs), ("fs_stats", StatsArgs), ("fs_scores", ScoresArgs),
                      ("fs_select", SelectArgs), ("fs_bsattn", AttnArgs), ("fs_bsattn_prepare", AttnArgs),
                      ("fs_bsattn_run", AttnArgs)]:
         fn = getattr(lib, name)

@@ -25,7 +25,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from ._lib import AttnArgs, CorrArgs, PoolArgs, SelectArgs, StatsArgs, ptr
+from ._lib import AttnArgs, CorrArgs, PoolArgs, ScoresArgs, SelectArgs, StatsArgs, ptr
 from .params import PrefillParams, derive, f32
 
 _MIN_BLOCKS = 10          # my_attn_v7.py:509
@@ -135,39 +135,17 @@ def select_blocks(query_states: torch.Tensor, key_states: torch.Tensor, *, block
                                       dtype=dt, Hq=Hq, Hk=Hk, L=L_q, D=D, bs=block_size,
                                       q_b=q_b.data_ptr(), k_b=k_b.data_ptr()))
         sel.q_b, sel.k_b = q_b, k_b
-    col_sel = last_sel = None
-    keep = diag_var = None
-    n_samples = 0
-    if p.corr_enabled:
-        lib = _lib.load()
-        work = torch.empty(lib.fs_corr_work_bytes(Hq, N, D), dtype=u8, device=dev)
-        corr = torch.empty(Hq, N, dtype=torch.float32, device=dev)
-        corr_sum = torch.empty(Hq, N, dtype=torch.float32, device=dev)
-        keep = torch.empty(Hq, N, dtype=u8, device=dev)
-        _lib.call("fs_corr", CorrArgs(q_b=ptr(sel.q_b), k_b=ptr(sel.k_b), dtype=dt, Hq=Hq, Hk=Hk, N=N, D=D,
-                                      local_window=p.local_window, keep_sink=p.keep_sink,
-                                      remote_start=p.remote_start, corr_threshold=f32(corr_threshold),
-                                      work=work.data_ptr(), corr=corr.data_ptr(),
-                                      corr_sum=corr_sum.data_ptr(), keep_tau=keep.data_ptr()))
-        sel.corr, sel.corr_sum, sel.keep_tau = corr, corr_sum, keep
-        n_samples = 0 if p.stripe_all_diffuse else len(p.sample_taus)
     n_cols = p.n_cols if p.col_enabled else 0
     last_k = p.last_k if enable_last_block_mask else 0
-    if n_samples or n_cols or last_k:
-        diag_var = torch.empty(Hq, max(1, n_samples), dtype=torch.float32, device=dev)
-        col_mean = torch.empty(Hq, N, dtype=torch.float32, device=dev) if n_cols else None
-        col_sel = torch.empty(Hq, N, dtype=u8, device=dev) if n_cols else None
-        last_scores = torch.empty(Hq, N, dtype=torch.float32, device=dev) if last_k else None
-        last_sel = torch.empty(Hq, N, dtype=u8, device=dev) if last_k else None
-        taus = _sample_taus_device(p.sample_taus, dev)
-        _lib.call("fs_stats", StatsArgs(q_b=ptr(sel.q_b), k_b=ptr(sel.k_b), dtype=dt, Hq=Hq, Hk=Hk, N=N, D=D,
-                                        sample_taus=taus.data_ptr(), n_samples=n_samples,
-                                        col_start=p.col_start, col_end=p.col_end, n_cols=n_cols,
-                                        last_k=last_k, diag_var=diag_var.data_ptr(),
-                                        col_mean=ptr(col_mean), col_sel=ptr(col_sel),
-                                        last_scores=ptr(last_scores), last_sel=ptr(last_sel)))
-        sel.diag_var, sel.col_mean, sel.col_sel = diag_var, col_mean, col_sel
-        sel.last_scores, sel.last_sel = last_scores, last_sel
+    n_samples = 0 if (not p.corr_enabled or p.stripe_all_diffuse) else len(p.sample_taus)
+    if q.dtype in (torch.bfloat16, torch.float16) and D % 16 == 0 and D <= 128 and N <= 4096 and \
+            (p.corr_enabled or n_cols or last_k):
+        # 16-bit inputs: correlation and statistics in one call from MFMA block-score tiles
+        _scores(sel, p, dt, Hq, Hk, N, D, n_samples, n_cols, last_k, f32(corr_threshold))
+    else:
+        _corr_and_stats(sel, p, dt, Hq, Hk, N, D, n_samples, n_cols, last_k, f32(corr_threshold))
+    keep, diag_var = sel.keep_tau, sel.diag_var
+    col_sel, last_sel = sel.col_sel, sel.last_sel
     if p.corr_enabled:
         dyn_mode, col_mode = 1, (1 if n_cols else 0)
         sel.mean_var = torch.empty(Hq, dtype=torch.float32, device=dev)
@@ -187,6 +165,62 @@ def select_blocks(query_states: torch.Tensor, key_states: torch.Tensor, *, block
     if not keep_intermediates:
         sel.q_b = sel.k_b = None
     return sel
+
+
+def _stat_buffers(sel, Hq, N, n_samples, n_cols, last_k, dev):
+    u8 = torch.uint8
+    sel.diag_var = torch.empty(Hq, max(1, n_samples), dtype=torch.float32, device=dev)
+    sel.col_mean = torch.empty(Hq, N, dtype=torch.float32, device=dev) if n_cols else None
+    sel.col_sel = torch.empty(Hq, N, dtype=u8, device=dev) if n_cols else None
+    sel.last_scores = torch.empty(Hq, N, dtype=torch.float32, device=dev) if last_k else None
+    sel.last_sel = torch.empty(Hq, N, dtype=u8, device=dev) if last_k else None
+
+
+def _scores(sel, p, dt, Hq, Hk, N, D, n_samples, n_cols, last_k, thr):
+    """fs_scores: lag correlation and statistics from MFMA block-score tiles."""
+    dev = sel.q_b.device
+    lib = _lib.load()
+    if p.corr_enabled:
+        sel.corr = torch.empty(Hq, N, dtype=torch.float32, device=dev)
+        sel.corr_sum = torch.empty(Hq, N, dtype=torch.float32, device=dev)
+        sel.keep_tau = torch.empty(Hq, N, dtype=torch.uint8, device=dev)
+    _stat_buffers(sel, Hq, N, n_samples, n_cols, last_k, dev)
+    taus = _sample_taus_device(p.sample_taus, dev)
+    work = torch.empty(lib.fs_scores_work_bytes(Hq, N, n_samples), dtype=torch.uint8, device=dev)
+    _lib.call("fs_scores", ScoresArgs(q_b=ptr(sel.q_b), k_b=ptr(sel.k_b), dtype=dt, Hq=Hq, Hk=Hk, N=N, D=D,
+                                      local_window=p.local_window, keep_sink=p.keep_sink,
+                                      remote_start=p.remote_start, corr_threshold=thr,
+                                      corr=ptr(sel.corr), corr_sum=ptr(sel.corr_sum), keep_tau=ptr(sel.keep_tau),
+                                      sample_taus=taus.data_ptr(), n_samples=n_samples,
+                                      col_start=p.col_start, col_end=p.col_end, n_cols=n_cols, last_k=last_k,
+                                      diag_var=ptr(sel.diag_var), col_mean=ptr(sel.col_mean),
+                                      col_sel=ptr(sel.col_sel), last_scores=ptr(sel.last_scores),
+                                      last_sel=ptr(sel.last_sel), work=work.data_ptr()))
+
+
+def _corr_and_stats(sel, p, dt, Hq, Hk, N, D, n_samples, n_cols, last_k, thr):
+    """fs_corr then fs_stats (any input dtype)."""
+    dev = sel.q_b.device if sel.q_b is not None else None
+    if p.corr_enabled:
+        lib = _lib.load()
+        work = torch.empty(lib.fs_corr_work_bytes(Hq, N, D), dtype=torch.uint8, device=dev)
+        sel.corr = torch.empty(Hq, N, dtype=torch.float32, device=dev)
+        sel.corr_sum = torch.empty(Hq, N, dtype=torch.float32, device=dev)
+        sel.keep_tau = torch.empty(Hq, N, dtype=torch.uint8, device=dev)
+        _lib.call("fs_corr", CorrArgs(q_b=ptr(sel.q_b), k_b=ptr(sel.k_b), dtype=dt, Hq=Hq, Hk=Hk, N=N, D=D,
+                                      local_window=p.local_window, keep_sink=p.keep_sink,
+                                      remote_start=p.remote_start, corr_threshold=thr,
+                                      work=work.data_ptr(), corr=sel.corr.data_ptr(),
+                                      corr_sum=sel.corr_sum.data_ptr(), keep_tau=sel.keep_tau.data_ptr()))
+    if n_samples or n_cols or last_k:
+        _stat_buffers(sel, Hq, N, n_samples, n_cols, last_k, dev)
+        taus = _sample_taus_device(p.sample_taus, dev)
+        _lib.call("fs_stats", StatsArgs(q_b=ptr(sel.q_b), k_b=ptr(sel.k_b), dtype=dt, Hq=Hq, Hk=Hk, N=N, D=D,
+                                        sample_taus=taus.data_ptr(), n_samples=n_samples,
+                                        col_start=p.col_start, col_end=p.col_end, n_cols=n_cols,
+                                        last_k=last_k, diag_var=ptr(sel.diag_var),
+                                        col_mean=ptr(sel.col_mean), col_sel=ptr(sel.col_sel),
+                                        last_scores=ptr(sel.last_scores), last_sel=ptr(sel.last_sel)))
 
 
 class AttentionCall:

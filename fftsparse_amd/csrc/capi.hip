@@ -27,7 +27,7 @@ int launch_status(const char* what) {
 }  // namespace fs_host
 
 extern "C" const char* fs_last_error(void) { return fs_host::g_err; }
-extern "C" int fs_abi_version(void) { return 3; }
+extern "C" int fs_abi_version(void) { return 4; }
 
 extern "C" size_t fs_sizeof_args(int which) {
   switch (which) {
@@ -36,6 +36,7 @@ extern "C" size_t fs_sizeof_args(int which) {
     case 2: return sizeof(fs_stats_args);
     case 3: return sizeof(fs_select_args);
     case 4: return sizeof(fs_attn_args);
+    case 5: return sizeof(fs_scores_args);
     default: return 0;
   }
 }

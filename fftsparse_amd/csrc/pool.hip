@@ -49,14 +49,17 @@ __global__ __launch_bounds__(kPoolThreads) void pool_kernel(fs_pool_args a, int 
   for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
 
   if (row_in_pass < rpp) {
-    constexpr int U = 4;
+    // non-temporal loads: the streamed rows are not re-read from the caches
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    constexpr int U = 8;
     for (int r0 = row_in_pass; r0 < rows; r0 += U * rpp) {
       Vec16<T> v[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int r = r0 + u * rpp;
         if (r < rows)
-          v[u] = *reinterpret_cast<const Vec16<T>*>(src + (int64_t)(t0 + r) * sl + col);
+          v[u] = __builtin_bit_cast(
+              Vec16<T>, __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + (int64_t)(t0 + r) * sl + col)));
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {

@@ -1,0 +1,321 @@
+// Block-score statistics of the selection stage from tiles of
+// S = q_b k_b^T on bf16/f16 MFMA, in place of the FFT correlation and the
+// per-head statistics kernels for 16-bit inputs:
+//   lag sums        corr_sum[t] = sum_i S[i][i-t]          (my_attn_v7.py:117-157; the
+//                   reference takes them from zero-padded FFTs, these are the same
+//                   sums added directly in fp32)
+//   lag selection   post-processing + threshold             (:134-155, :190-208)
+//   diagonal stats  var(diff(S[j+t][j] / sqrt(D))) / mean|.| (:301-363)
+//   column scores   sum_{i=j}^{N-2} S[i][j] / sqrt(D) / max(1, N-j-1) (:390-447; the
+//                   reference forms the suffix sums of q_b first, which is the same sum)
+//   last row        S[N-1][j] rounded to the input dtype    (:54-72)
+//
+// scores_kernel: one workgroup (4 waves) per (head, 128 x 128 tile I >= J of
+// the lower triangle).  Wave w computes rows 32w .. 32w+31 of the tile with
+// v_mfma_f32_32x32x16 (operands loaded straight from the pooled rows, which
+// sit in L2), the tile is written to LDS, and fixed-order per-tile partials
+// are written to the work buffer: the 255 diagonal sums, the 128 column sums
+// over rows i >= j, i <= N-2, the elements of every sampled diagonal that
+// crosses the tile, and the last row.
+// scores_final_kernel: grid (head, job): job 0 adds the lag partials and
+// selects the lags, 1 the diagonal statistics, 2 the column scores and their
+// top-n, 3 the last-row top-k; every sum is in a fixed order (deterministic).
+#include "common.h"
+
+namespace fs {
+
+constexpr int kScoreTile = 128;
+constexpr int kScoreThreads = 256;
+constexpr int kFinalThreads = 1024;
+constexpr int kDiagSlots = 256;                 // 255 local diagonals per tile (+1 pad)
+constexpr int kMaxSamples = 1024;               // sampled diagonals per head
+
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+
+template <typename T> struct ScoreMma;
+template <> struct ScoreMma<bf16_t> {
+  static __device__ __forceinline__ f32x16_t mma(uint4 a, uint4 b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                   c, 0, 0, 0);
+  }
+};
+template <> struct ScoreMma<f16_t> {
+  static __device__ __forceinline__ f32x16_t mma(uint4 a, uint4 b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b),
+                                                  c, 0, 0, 0);
+  }
+};
+
+// tile index t of the lower triangle -> (I, J), t = I (I + 1) / 2 + J
+__device__ __forceinline__ void tile_ij(int t, int& I, int& J) {
+  int i = (int)((sqrtf(8.0f * (float)t + 1.0f) - 1.0f) * 0.5f);
+  while ((i + 1) * (i + 2) / 2 <= t) ++i;
+  while (i * (i + 1) / 2 > t) --i;
+  I = i;
+  J = t - i * (i + 1) / 2;
+}
+__device__ __forceinline__ int tile_id(int I, int J) { return I * (I + 1) / 2 + J; }
+
+template <typename T>
+__global__ __launch_bounds__(kScoreThreads) void scores_kernel(fs_scores_args a, int ntiles, float inv_sqrt_d,
+                                                               float* __restrict__ pdiag, float* __restrict__ pcol,
+                                                               float* __restrict__ dvs) {
+  // the K tile (bf16/f16 [128][D]) is staged in the same LDS as the S tile
+  // written after the MFMAs
+  __shared__ __attribute__((aligned(16))) float sl[kScoreTile][kScoreTile + 1];
+  __shared__ int taus[kMaxSamples];
+  uint16_t* kt = reinterpret_cast<uint16_t*>(&sl[0][0]);
+  const int h = blockIdx.x / ntiles, t = blockIdx.x - h * ntiles;
+  int I, J;
+  tile_ij(t, I, J);
+  const int N = a.N, D = a.D;
+  const int hk = h / (a.Hq / a.Hk);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hi = lane >> 5;
+  const uint16_t* qb = static_cast<const uint16_t*>(a.q_b) + (int64_t)h * N * D;
+  const uint16_t* kb = static_cast<const uint16_t*>(a.k_b) + (int64_t)hk * N * D;
+  const int i0 = I * kScoreTile, j0 = J * kScoreTile;
+  for (int e = tid; e < a.n_samples; e += kScoreThreads) taus[e] = a.sample_taus[e];
+
+  // ---- S tile: A = q rows (row i), B = k rows as columns (col j), K = d
+  f32x16_t acc[4];
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[jt][r] = 0.f;
+  // K tile -> LDS, rows past N zero (all loads in flight together)
+  const int cpr = D / 8;                           // 16-byte chunks per row
+  for (int c = tid; c < kScoreTile * cpr; c += kScoreThreads) {
+    const int r = c / cpr, cc = c - r * cpr;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (j0 + r < N) v = *reinterpret_cast<const uint4*>(kb + (int64_t)(j0 + r) * D + cc * 8);
+    *reinterpret_cast<uint4*>(kt + r * D + cc * 8) = v;
+  }
+  const int qi = i0 + wave * 32 + l32;
+  const uint16_t* qrow = qb + (int64_t)min(qi, N - 1) * D + hi * 8;
+  const bool qok = qi < N;
+  __syncthreads();
+  for (int st = 0; st < D / 16; ++st) {
+    uint4 av = make_uint4(0, 0, 0, 0);
+    if (qok) av = *reinterpret_cast<const uint4*>(qrow + st * 16);
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) {
+      const uint4 bv = *reinterpret_cast<const uint4*>(kt + (jt * 32 + l32) * D + st * 16 + hi * 8);
+      acc[jt] = ScoreMma<T>::mma(av, bv, acc[jt]);
+    }
+  }
+  __syncthreads();                                 // K tile consumed: the LDS becomes the S tile
+  // C layout: lane holds row (r/4)*8 + hi*4 + r%4, column l32 of each 32x32 block
+#pragma unroll
+  for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sl[wave * 32 + (r >> 2) * 8 + hi * 4 + (r & 3)][jt * 32 + l32] = acc[jt][r];
+  __syncthreads();
+
+  const int64_t tb = (int64_t)h * ntiles + t;
+  const bool diag_tile = I == J;
+  // ---- lag sums: local diagonal dl = iloc - jloc in [-127, 127], rows in ascending order
+  if (a.keep_tau != nullptr && tid < 2 * kScoreTile - 1) {
+    const int dl = tid - (kScoreTile - 1);
+    float s = 0.f;
+    if (!(diag_tile && dl < 0)) {
+      const int ib = max(0, dl), ie = min(kScoreTile - 1, kScoreTile - 1 + dl);
+#pragma unroll 8
+      for (int il = ib; il <= ie; ++il) s += sl[il][il - dl];
+    }
+    pdiag[tb * kDiagSlots + tid] = s;
+  }
+  // ---- column sums over rows i >= j, i <= N-2
+  if (a.n_cols > 0 && tid < kScoreTile) {
+    const int j = j0 + tid;
+    const int ib = diag_tile ? tid : 0;
+    const int ie = min(kScoreTile - 1, N - 2 - i0);
+    float s = 0.f;
+#pragma unroll 8
+    for (int il = ib; il <= ie; ++il) s += sl[il][tid];
+    pcol[tb * kScoreTile + tid] = (j < N) ? s : 0.f;
+  }
+  // ---- sampled diagonals: S[j + tau][j] / sqrt(D) for j < N - tau - 1
+  for (int e = tid; e < a.n_samples * kScoreTile; e += kScoreThreads) {
+    const int s = e / kScoreTile, jl = e - s * kScoreTile;
+    const int tau = taus[s];
+    const int j = j0 + jl, i = j + tau;
+    if (tau < 0 || tau >= N || j >= N - tau - 1) continue;
+    const int il = i - i0;
+    if (il < 0 || il >= kScoreTile) continue;
+    dvs[((int64_t)h * a.n_samples + s) * N + j] = sl[il][jl] * inv_sqrt_d;
+  }
+  // ---- last row, rounded to the input dtype
+  if (a.last_k > 0 && i0 <= N - 1 && N - 1 < i0 + kScoreTile && tid < kScoreTile && j0 + tid < N)
+    a.last_scores[(int64_t)h * N + j0 + tid] = Conv<T>::round(sl[N - 1 - i0][tid]);
+}
+
+__global__ __launch_bounds__(kFinalThreads) void scores_final_kernel(fs_scores_args a, int ntiles, float inv_sqrt_d,
+                                                                     const float* __restrict__ pdiag,
+                                                                     const float* __restrict__ pcol,
+                                                                     const float* __restrict__ dvs) {
+  extern __shared__ float fsm[];                   // [N]: cv, colv or lastv by job
+  __shared__ float red[32];
+  __shared__ int ired[kTopkScratch];
+  // blockIdx.y: 0 lag sums + selection, 1 diagonal statistics, 2 columns, 3 last row
+  const int h = blockIdx.x, job = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int N = a.N;
+  const int NT = (N + kScoreTile - 1) / kScoreTile;
+  const int64_t hb = (int64_t)h * ntiles;
+  float* cv = fsm;
+  float* colv = fsm;
+  float* lastv = fsm;
+
+  // ---- lag sums and the v7 post-processing (my_attn_v7.py:134-155, 193-208)
+  if (job == 0 && a.keep_tau != nullptr) {
+    const int ex = a.local_window + 1;
+    const int st = N - a.keep_sink - 5;
+    const int es = min(ex, N);
+    const int ss = st >= 0 ? min(st, N) : max(0, N + st);
+    for (int t = tid; t < N; t += kFinalThreads) {
+      float cs = 0.f;
+      const int d0 = t / kScoreTile;
+      for (int dd = d0; dd <= d0 + 1 && dd < NT; ++dd) {     // tile diagonals I - J = dd
+        const int dl = t - dd * kScoreTile;                  // local diagonal
+        if (dl < -(kScoreTile - 1) || dl > kScoreTile - 1) continue;
+#pragma unroll 8
+        for (int J = 0; J + dd < NT; ++J) cs += pdiag[(hb + tile_id(J + dd, J)) * kDiagSlots + dl + kScoreTile - 1];
+      }
+      if (a.corr_sum) a.corr_sum[(int64_t)h * N + t] = cs;
+      float v = cs / (float)max(N - t, 1);
+      if (t < es || t >= ss) v = 0.f;
+      cv[t] = v;
+    }
+    __syncthreads();
+    if (ex < st) {
+      float mn = INFINITY;
+      for (int t = ex + tid; t < st; t += kFinalThreads) mn = fminf(mn, cv[t]);
+      mn = block_min(mn, red);
+      const float den = clamp_min_nan(log10f((float)(N - ex)), 1e-6f);
+      for (int t = ex + tid; t < st; t += kFinalThreads) {
+        const float pw = log10f((float)(N - t)) / den;
+        cv[t] = (cv[t] - mn) * pw;
+      }
+      __syncthreads();
+    }
+    for (int t = tid; t < N; t += kFinalThreads) a.corr[(int64_t)h * N + t] = cv[t];
+    const int rs = a.remote_start;
+    float mx = -INFINITY;
+    for (int t = rs + tid; t < N; t += kFinalThreads) mx = fmaxf(mx, cv[t]);
+    mx = clamp_min_nan(block_max(mx, red), 1e-6f);
+    for (int t = tid; t < N; t += kFinalThreads)
+      a.keep_tau[(int64_t)h * N + t] = (t >= rs && cv[t] / mx >= a.corr_threshold) ? 1 : 0;
+  }
+
+  // ---- diagonal statistics, one wave per sample (:342-349)
+  for (int s = wave; job == 1 && s < a.n_samples; s += kFinalThreads / 64) {
+    const int tau = a.sample_taus[s];
+    const int nd = (tau >= 0 && tau < N) ? N - tau - 1 : 0;
+    const float* dv = dvs + ((int64_t)h * a.n_samples + s) * N;
+    float sabs = 0.f, se = 0.f;
+    for (int j = lane; j < nd; j += 64) {
+      sabs += fabsf(dv[j]);
+      if (j + 1 < nd) se += dv[j + 1] - dv[j];
+    }
+    const float mean_abs = wave_sum(sabs) / (float)nd;
+    const int ne = nd - 1;
+    const float mean_e = wave_sum(se) / (float)ne;
+    float sq = 0.f;
+    for (int j = lane; j < ne; j += 64) {
+      const float e = (dv[j + 1] - dv[j]) - mean_e;
+      sq += e * e;
+    }
+    const float var = wave_sum(sq) / (float)(ne - 1);
+    if (lane == 0) a.diag_var[(int64_t)h * a.n_samples + s] = var / clamp_min_nan(mean_abs, 1e-6f);
+  }
+
+  // ---- column scores and their top-n (:404-438)
+  if (job == 2 && a.n_cols > 0) {
+    for (int j = tid; j < N; j += kFinalThreads) {
+      const int Jt = j / kScoreTile, jl = j - Jt * kScoreTile;
+      float s = 0.f;
+#pragma unroll 8
+      for (int It = Jt; It < NT; ++It) s += pcol[(hb + tile_id(It, Jt)) * kScoreTile + jl];
+      const float c = (s * inv_sqrt_d) / (float)max(1, N - j - 1);
+      colv[j] = c;
+      if (a.col_mean) a.col_mean[(int64_t)h * N + j] = c;
+      if (j < a.col_start || j >= a.col_end) a.col_sel[(int64_t)h * N + j] = 0;
+    }
+    __syncthreads();
+    block_topk_select(colv + a.col_start, a.col_end - a.col_start, a.n_cols,
+                      a.col_sel + (int64_t)h * N + a.col_start, ired);
+  }
+  // ---- last-row top-k (:61-70)
+  if (job == 3 && a.last_k > 0) {
+    for (int j = tid; j < N; j += kFinalThreads) lastv[j] = a.last_scores[(int64_t)h * N + j];
+    __syncthreads();
+    block_topk_select(lastv, N, a.last_k, a.last_sel + (int64_t)h * N, ired);
+  }
+}
+
+static size_t part_offsets(int Hq, int N, int n_samples, size_t* o_col, size_t* o_dv) {
+  const int NT = (N + kScoreTile - 1) / kScoreTile;
+  const size_t ntiles = (size_t)NT * (NT + 1) / 2;
+  const size_t diag = (size_t)Hq * ntiles * kDiagSlots * sizeof(float);
+  const size_t col = (size_t)Hq * ntiles * kScoreTile * sizeof(float);
+  const size_t dv = (size_t)Hq * n_samples * N * sizeof(float);
+  if (o_col) *o_col = diag;
+  if (o_dv) *o_dv = diag + col;
+  return diag + col + dv;
+}
+
+template <typename T>
+static int launch_scores(const fs_scores_args& a, hipStream_t s) {
+  const int NT = (a.N + kScoreTile - 1) / kScoreTile;
+  const int ntiles = NT * (NT + 1) / 2;
+  size_t o_col, o_dv;
+  part_offsets(a.Hq, a.N, a.n_samples, &o_col, &o_dv);
+  char* w = static_cast<char*>(a.work);
+  float* pdiag = reinterpret_cast<float*>(w);
+  float* pcol = reinterpret_cast<float*>(w + o_col);
+  float* dvs = reinterpret_cast<float*>(w + o_dv);
+  const float inv_sqrt_d = 1.0f / (float)sqrt((double)a.D);
+  scores_kernel<T><<<a.Hq * ntiles, kScoreThreads, 0, s>>>(a, ntiles, inv_sqrt_d, pdiag, pcol, dvs);
+  if (int rc = fs_host::launch_status("fs_scores (tiles)")) return rc;
+  const size_t smem = (size_t)a.N * sizeof(float);
+  if (int rc = fs_host::allow_dynamic_lds(scores_final_kernel, smem, "fs_scores")) return rc;
+  scores_final_kernel<<<dim3(a.Hq, 4), kFinalThreads, smem, s>>>(a, ntiles, inv_sqrt_d, pdiag, pcol, dvs);
+  return fs_host::launch_status("fs_scores (final)");
+}
+
+}  // namespace fs
+
+using namespace fs;
+
+extern "C" size_t fs_scores_work_bytes(int Hq, int N, int n_samples) {
+  if (Hq <= 0 || N <= 0 || n_samples < 0) return 0;
+  return part_offsets(Hq, N, n_samples, nullptr, nullptr);
+}
+
+extern "C" int fs_scores(const fs_scores_args* a, void* stream) {
+  FS_CHECK_ARG(a != nullptr, "fs_scores: null args");
+  FS_CHECK_ARG(a->q_b && a->k_b && a->work, "fs_scores: null pointer");
+  FS_CHECK_ARG(a->Hq > 0 && a->Hk > 0 && a->Hq % a->Hk == 0, "fs_scores: Hq=%d must be a multiple of Hk=%d",
+               a->Hq, a->Hk);
+  FS_CHECK_ARG(a->N >= 1 && a->D >= 16, "fs_scores: bad sizes");
+  FS_CHECK_ARG(((uintptr_t)a->q_b % 16) == 0 && ((uintptr_t)a->k_b % 16) == 0, "fs_scores: unaligned pooled tensors");
+  FS_CHECK_ARG(a->keep_tau == nullptr || (a->corr && a->remote_start >= 0 && a->local_window >= 0),
+               "fs_scores: bad correlation arguments");
+  FS_CHECK_ARG(a->n_samples >= 0 && (a->n_samples == 0 || (a->sample_taus && a->diag_var)),
+               "fs_scores: sample arrays missing");
+  FS_CHECK_ARG(a->n_cols <= 0 || (a->col_sel && a->col_start >= 0 && a->col_end <= a->N &&
+                                  a->col_end > a->col_start && a->n_cols <= a->col_end - a->col_start),
+               "fs_scores: bad column range");
+  FS_CHECK_ARG(a->last_k <= 0 || (a->last_sel && a->last_scores && a->last_k <= a->N),
+               "fs_scores: bad last-row arguments");
+  FS_CHECK_SUPPORTED(a->dtype == FS_DTYPE_BF16 || a->dtype == FS_DTYPE_F16,
+                     "fs_scores: dtype %d unsupported (bf16/f16; fp32 uses fs_corr and fs_stats)", a->dtype);
+  // the staged K tile (128 * D 16-bit values) shares the S tile's LDS; D <= 128
+  FS_CHECK_SUPPORTED(a->D % 16 == 0 && a->D <= 128, "fs_scores: head_dim %d unsupported", a->D);
+  FS_CHECK_SUPPORTED(a->N <= 4096, "fs_scores: N=%d > 4096", a->N);
+  FS_CHECK_SUPPORTED(a->n_samples <= kMaxSamples, "fs_scores: %d diagonal samples > %d", a->n_samples, kMaxSamples);
+  hipStream_t s = (hipStream_t)stream;
+  return a->dtype == FS_DTYPE_BF16 ? launch_scores<bf16_t>(*a, s) : launch_scores<f16_t>(*a, s);
+}

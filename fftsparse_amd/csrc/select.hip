@@ -41,8 +41,10 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(fs_select_args a, i
     if (a.stripe_all_diffuse) {
       mv = INFINITY;
     } else {
+      // every wave forms the same sum (butterfly order is lane-independent)
       float s = 0.f;
-      for (int i = 0; i < a.n_samples; ++i) s += a.diag_var[(int64_t)h * a.n_samples + i];
+      for (int i = lane; i < a.n_samples; i += 64) s += a.diag_var[(int64_t)h * a.n_samples + i];
+      s = wave_sum(s);
       mv = s / (float)a.n_samples;
       stripe = mv <= a.stripe_threshold;        // false for nan
     }

@@ -14,6 +14,8 @@
  *   fs_stats     compute_stripe_variance      my_attn_v7.py:301-363 (diagonal statistics)
  *                create_column_block_mask     my_attn_v7.py:390-447 (column scores + top-n)
  *                create_last_block_query_mask my_attn_v7.py:54-72
+ *   fs_scores    fs_corr + fs_stats for bf16/f16 inputs, from MFMA tiles of
+ *                the block scores (the same reference lines)
  *   fs_select    mask composition             my_attn_v7.py:542-550, 588-641 (prior | dynamic | column)
  *                create_qk_topk_block_mask    my_attn_v7.py:256-294 (diffuse heads)
  *                create_deterministic_block_mask attn_src/fix_mask_attn/my_attn.py:39-79 (fixed role)
@@ -105,6 +107,38 @@ typedef struct {
 } fs_stats_args;
 FS_API int fs_stats(const fs_stats_args* a, void* stream);
 
+/* ---- correlation + statistics from MFMA block-score tiles (16-bit inputs)
+ * One call producing what fs_corr and fs_stats produce, for dtype bf16/f16,
+ * D % 16 == 0, D <= 128, N <= 4096 (my_attn_v7.py:117-157, 190-208,
+ * 301-363, 390-447, 54-72).  The tiles of S = q_b k_b^T (i >= j) are formed
+ * on MFMA and every statistic is a fixed-order sum over them: the lag sums
+ * corr_sum[h][t] = sum_i S[i][i-t] (the reference's FFT computes the same
+ * sums), the column scores from sum_{i=j}^{N-2} S[i][j] (the reference's
+ * suffix sums of q_b give the same sums), the sampled diagonals and the last
+ * row.  Fields and outputs mean what they mean in fs_corr_args and
+ * fs_stats_args; keep_tau == NULL skips the correlation outputs.
+ * work: fs_scores_work_bytes(Hq, N, n_samples) bytes of device scratch. */
+typedef struct {
+  const void* q_b; const void* k_b;
+  int dtype, Hq, Hk, N, D;
+  int local_window, keep_sink, remote_start;
+  float corr_threshold;
+  float* corr;           /* [Hq][N] */
+  float* corr_sum;       /* [Hq][N] or NULL */
+  uint8_t* keep_tau;     /* [Hq][N] or NULL */
+  const int32_t* sample_taus; int n_samples;
+  int col_start, col_end, n_cols;
+  int last_k;
+  float* diag_var;       /* [Hq][n_samples] */
+  float* col_mean;       /* [Hq][N] or NULL */
+  uint8_t* col_sel;      /* [Hq][N] */
+  float* last_scores;    /* [Hq][N] */
+  uint8_t* last_sel;     /* [Hq][N] */
+  void* work;
+} fs_scores_args;
+FS_API size_t fs_scores_work_bytes(int Hq, int N, int n_samples);
+FS_API int fs_scores(const fs_scores_args* a, void* stream);
+
 /* ---- mask composition -> per-row block lists ----------------------------
  * Row i of head h selects key block j (0 <= j < Nk, and j <= i if mask_causal) iff
  *   prior:  j < keep_sink || j >= Nk - keep_recent || (local_window > 0 && |i-j| <= local_window)
@@ -171,7 +205,7 @@ FS_API int fs_bsattn_run(const fs_attn_args* a, void* stream);
 
 /* Description of the last failure on this thread ("" if none). */
 FS_API const char* fs_last_error(void);
-/* sizeof the argument struct: 0 pool, 1 corr, 2 stats, 3 select, 4 attn
+/* sizeof the argument struct: 0 pool, 1 corr, 2 stats, 3 select, 4 attn, 5 scores
  * (lets a foreign-function binding check its struct layout). */
 FS_API size_t fs_sizeof_args(int which);
 /* ABI version of this library (increments on any struct change). */

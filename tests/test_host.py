@@ -35,7 +35,8 @@ def test_struct_layouts_match_library():
 
 def test_null_args_rejected_without_gpu():
     lib = _lib.load()
-    for name in ("fs_pool", "fs_corr", "fs_stats", "fs_select", "fs_bsattn", "fs_bsattn_prepare", "fs_bsattn_run"):
+    for name in ("fs_pool", "fs_corr", "fs_stats", "fs_scores", "fs_select", "fs_bsattn", "fs_bsattn_prepare",
+                 "fs_bsattn_run"):
         rc = getattr(lib, name)(None, None)
         assert rc == -1
         assert b"null args" in lib.fs_last_error()
