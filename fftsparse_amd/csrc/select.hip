@@ -6,7 +6,11 @@
 // One workgroup (4 waves) owns RPW consecutive query-block rows of one head.
 // Stripe heads (and the fixed mask) and diffuse heads are served by two
 // launches of the kernel, so only the diffuse launch reserves LDS for the
-// score panel.  A diffuse head first computes its score panel S[rows][0..last row] into LDS
+// score panel.  Stripe / fixed rows (Nk <= 4096) are built word-parallel: a
+// lane forms the 64-bit membership mask of 64 key blocks (range masks for
+// the prior, columns and causal limit; a funnel-shifted window of the
+// bit-reversed lag mask for the lag diagonals), and writes its set bits at
+// the prefix sum of the lower words' popcounts.  A diffuse head first computes its score panel S[rows][0..last row] into LDS
 // (fp32 dot products, fixed order).  Each wave then walks one row at a time:
 // for a diffuse row it finds the k_i-th largest score by a 32-step bisection
 // on the ordered float key with wave-wide counts, and in a single ascending
@@ -18,6 +22,15 @@ namespace fs {
 
 constexpr int kSelThreads = 256;
 constexpr int kSelWaves = kSelThreads / 64;
+constexpr int kMaxWords = 64;                       // word-parallel path: Nk <= 4096
+
+// bits of word w (blocks 64w .. 64w+63) that lie in [lo, hi)
+__device__ __forceinline__ uint64_t range_bits(int w, int lo, int hi) {
+  const int b0 = max(lo - 64 * w, 0), b1 = min(hi - 64 * w, 64);
+  if (b1 <= b0) return 0;
+  const uint64_t upto = b1 == 64 ? ~0ull : ((1ull << b1) - 1);
+  return upto & ~((1ull << b0) - 1);
+}
 
 // DIFF selects the head kind a launch serves: false = stripe heads and the
 // fixed (dyn_mode 0) mask, no score panel and no dynamic LDS; true = diffuse
@@ -89,7 +102,78 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(fs_select_args a, i
   }
 
   const int lw = a.local_window;
-  // per-head lag / column / last-row flags, staged in LDS (bit 0 lag, 1 column, 2 last row)
+  const bool has_last = a.last_sel != nullptr;
+  const int NW = (Nk + 63) >> 6;                   // 64-block words per row
+  if (!DIFF && NW <= kMaxWords) {
+    // ---- word-parallel rows: lane (row g, word w) builds the membership of
+    // blocks 64w .. 64w+63 of its row as a 64-bit mask from per-head masks
+    // staged in LDS, then writes its set bits at the offset given by the
+    // popcounts of the lower words.
+    __shared__ uint64_t rkw[2 * kMaxWords + 2];  // bit x: keep_tau[N-1-x] (x < N), 0 beyond
+    __shared__ uint64_t colw[kMaxWords], lastw[kMaxWords];
+    for (int q = wave; q < 2 * NW + 2; q += kSelWaves) {
+      const int x = 64 * q + lane;
+      const bool kb = use_lags && x < N && a.keep_tau[(int64_t)h * N + (N - 1 - x)];
+      const uint64_t m = __ballot(kb);
+      if (lane == 0) rkw[q] = m;
+      if (q < NW) {
+        const bool cb = use_cols && x < N && a.col_sel[(int64_t)h * N + x];
+        const bool lb = has_last && x < N && a.last_sel[(int64_t)h * N + x];
+        const uint64_t mc = __ballot(cb), ml = __ballot(lb);
+        if (lane == 0) {
+          colw[q] = mc;
+          lastw[q] = ml;
+        }
+      }
+    }
+    __syncthreads();
+    int lpr = 1;                                   // lanes per row (power of two >= NW)
+    while (lpr < NW) lpr <<= 1;
+    const int rpi = 64 / lpr;                      // rows per wave pass
+    const int w = lane & (lpr - 1), g = lane / lpr;
+    for (int rr0 = wave * rpi; rr0 < RPW; rr0 += kSelWaves * rpi) {
+      const int rr = rr0 + g;
+      const int i = r0 + rr;
+      const bool row_ok = rr < RPW && i < N;
+      uint64_t m = 0;
+      if (row_ok && w < NW) {
+        const int jlim = a.mask_causal ? min(i + 1, Nk) : Nk;
+        // prior (:83-95): sink | recent | local window
+        m = range_bits(w, 0, a.keep_sink) | range_bits(w, Nk - a.keep_recent, Nk);
+        if (lw > 0) m |= range_bits(w, i - lw, i + lw + 1);
+        if (has_last && i == N - 1) m |= lastw[w];
+        if (use_lags) {
+          // bit b <-> lag t = i - 64w - b <-> rkw bit p0 + b, p0 = N-1-i+64w >= 0
+          const int p0 = N - 1 - i + 64 * w;
+          const int qw = p0 >> 6, sh = p0 & 63;
+          uint64_t win = rkw[qw] >> sh;
+          if (sh) win |= rkw[qw + 1] << (64 - sh);
+          m |= win & range_bits(w, a.keep_sink, i - a.remote_start + 1);   // t >= rs, j >= keep_sink
+        }
+        if (use_cols) m |= colw[w] & range_bits(w, 0, i + 1);
+        m &= range_bits(w, 0, jlim);
+      }
+      const int c = __popcll(m);
+      int incl = c;
+      for (int o = 1; o < lpr; o <<= 1) {
+        const int v = __shfl_up(incl, o, lpr);
+        if (w >= o) incl += v;
+      }
+      const int total = __shfl(incl, lpr - 1, lpr);
+      if (row_ok) {
+        uint16_t* out = a.blk_idx + ((int64_t)h * N + i) * Nk;
+        int pos = incl - c;
+        while (m) {
+          const int b = __builtin_ctzll(m);
+          out[pos++] = (uint16_t)(64 * w + b);
+          m &= m - 1;
+        }
+        if (w == 0) a.blk_cnt[(int64_t)h * N + i] = total;
+      }
+    }
+    return;
+  }
+  // ---- per-head lag / column / last-row flags, staged in LDS (bit 0 lag, 1 column, 2 last row)
   __shared__ uint8_t flags[4096];
   for (int j = tid; j < N; j += kSelThreads) {
     uint8_t f = 0;
@@ -99,7 +183,6 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(fs_select_args a, i
     flags[j] = f;
   }
   __syncthreads();
-  const bool has_last = a.last_sel != nullptr;
 
   for (int rr = wave; rr < RPW; rr += kSelWaves) {
     const int i = r0 + rr;
