@@ -18,8 +18,9 @@
 // over rows i >= j, i <= N-2, the elements of every sampled diagonal that
 // crosses the tile, and the last row.
 // scores_final_kernel: grid (head, job): job 0 adds the lag partials and
-// selects the lags, 1 the diagonal statistics, 2 the column scores and their
-// top-n, 3 the last-row top-k; every sum is in a fixed order (deterministic).
+// selects the lags, 2 the column scores and their top-n, 3 the last-row
+// top-k, 4 .. 7 the diagonal statistics (one wave per sample; job 1 is
+// idle); every sum is in a fixed order (deterministic).
 #include "common.h"
 
 namespace fs {
@@ -29,6 +30,7 @@ constexpr int kScoreThreads = 256;
 constexpr int kFinalThreads = 1024;
 constexpr int kDiagSlots = 256;                 // 255 local diagonals per tile (+1 pad)
 constexpr int kMaxSamples = 1024;               // sampled diagonals per head
+constexpr int kDiagJobs = 4;                    // final-kernel workgroups per head for the diagonal statistics
 
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -77,7 +79,6 @@ __global__ __launch_bounds__(kScoreThreads) void scores_kernel(fs_scores_args a,
   const uint16_t* qb = static_cast<const uint16_t*>(a.q_b) + (int64_t)h * N * D;
   const uint16_t* kb = static_cast<const uint16_t*>(a.k_b) + (int64_t)hk * N * D;
   const int i0 = I * kScoreTile, j0 = J * kScoreTile;
-  for (int e = tid; e < a.n_samples; e += kScoreThreads) taus[e] = a.sample_taus[e];
 
   // ---- S tile: A = q rows (row i), B = k rows as columns (col j), K = d
   f32x16_t acc[4];
@@ -85,21 +86,40 @@ __global__ __launch_bounds__(kScoreThreads) void scores_kernel(fs_scores_args a,
   for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[jt][r] = 0.f;
-  // K tile -> LDS, rows past N zero (all loads in flight together)
-  const int cpr = D / 8;                           // 16-byte chunks per row
-  for (int c = tid; c < kScoreTile * cpr; c += kScoreThreads) {
-    const int r = c / cpr, cc = c - r * cpr;
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if (j0 + r < N) v = *reinterpret_cast<const uint4*>(kb + (int64_t)(j0 + r) * D + cc * 8);
-    *reinterpret_cast<uint4*>(kt + r * D + cc * 8) = v;
-  }
+  // Every global load of the tile is issued before the first wait: this
+  // wave's Q operands (all D/16 steps, in registers), the K tile (to LDS,
+  // rows past N zero) and the sampled lags.
+  constexpr int kMaxSteps = 128 / 16;              // D <= 128
   const int qi = i0 + wave * 32 + l32;
   const uint16_t* qrow = qb + (int64_t)min(qi, N - 1) * D + hi * 8;
   const bool qok = qi < N;
+  uint4 qv[kMaxSteps];
+#pragma unroll
+  for (int st = 0; st < kMaxSteps; ++st)
+    qv[st] = (qok && st < D / 16) ? *reinterpret_cast<const uint4*>(qrow + st * 16) : make_uint4(0, 0, 0, 0);
+  const int cpr = D / 8;                           // 16-byte chunks per row
+  constexpr int kMaxChunks = kScoreTile * (128 / 8) / kScoreThreads;   // per thread, D <= 128
+  uint4 kv[kMaxChunks];
+#pragma unroll
+  for (int u = 0; u < kMaxChunks; ++u) {
+    const int c = tid + u * kScoreThreads, r = c / cpr, cc = c - r * cpr;
+    kv[u] = (c < kScoreTile * cpr && j0 + r < N) ? *reinterpret_cast<const uint4*>(kb + (int64_t)(j0 + r) * D + cc * 8)
+                                                : make_uint4(0, 0, 0, 0);
+  }
+  int tv = 0;
+  if (tid < a.n_samples) tv = a.sample_taus[tid];
+  for (int e = tid + kScoreThreads; e < a.n_samples; e += kScoreThreads) taus[e] = a.sample_taus[e];
+  if (tid < a.n_samples) taus[tid] = tv;
+#pragma unroll
+  for (int u = 0; u < kMaxChunks; ++u) {
+    const int c = tid + u * kScoreThreads, r = c / cpr, cc = c - r * cpr;
+    if (c < kScoreTile * cpr) *reinterpret_cast<uint4*>(kt + r * D + cc * 8) = kv[u];
+  }
   __syncthreads();
-  for (int st = 0; st < D / 16; ++st) {
-    uint4 av = make_uint4(0, 0, 0, 0);
-    if (qok) av = *reinterpret_cast<const uint4*>(qrow + st * 16);
+#pragma unroll
+  for (int st = 0; st < kMaxSteps; ++st) {
+    if (st >= D / 16) break;
+    const uint4 av = qv[st];
 #pragma unroll
     for (int jt = 0; jt < 4; ++jt) {
       const uint4 bv = *reinterpret_cast<const uint4*>(kt + (jt * 32 + l32) * D + st * 16 + hi * 8);
@@ -159,7 +179,7 @@ __global__ __launch_bounds__(kFinalThreads) void scores_final_kernel(fs_scores_a
   extern __shared__ float fsm[];                   // [N]: cv, colv or lastv by job
   __shared__ float red[32];
   __shared__ int ired[kTopkScratch];
-  // blockIdx.y: 0 lag sums + selection, 1 diagonal statistics, 2 columns, 3 last row
+  // blockIdx.y: 0 lag sums + selection, 2 columns, 3 last row, 4.. diagonal statistics
   const int h = blockIdx.x, job = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int N = a.N;
   const int NT = (N + kScoreTile - 1) / kScoreTile;
@@ -209,12 +229,14 @@ __global__ __launch_bounds__(kFinalThreads) void scores_final_kernel(fs_scores_a
       a.keep_tau[(int64_t)h * N + t] = (t >= rs && cv[t] / mx >= a.corr_threshold) ? 1 : 0;
   }
 
-  // ---- diagonal statistics, one wave per sample (:342-349)
-  for (int s = wave; job == 1 && s < a.n_samples; s += kFinalThreads / 64) {
+  // ---- diagonal statistics, one wave per sample, jobs 4 .. 4+kDiagJobs-1 (:342-349)
+  for (int s = (job - 4) * (kFinalThreads / 64) + wave; job >= 4 && s < a.n_samples;
+       s += kDiagJobs * (kFinalThreads / 64)) {
     const int tau = a.sample_taus[s];
     const int nd = (tau >= 0 && tau < N) ? N - tau - 1 : 0;
     const float* dv = dvs + ((int64_t)h * a.n_samples + s) * N;
     float sabs = 0.f, se = 0.f;
+#pragma unroll 4
     for (int j = lane; j < nd; j += 64) {
       sabs += fabsf(dv[j]);
       if (j + 1 < nd) se += dv[j + 1] - dv[j];
@@ -223,6 +245,7 @@ __global__ __launch_bounds__(kFinalThreads) void scores_final_kernel(fs_scores_a
     const int ne = nd - 1;
     const float mean_e = wave_sum(se) / (float)ne;
     float sq = 0.f;
+#pragma unroll 4
     for (int j = lane; j < ne; j += 64) {
       const float e = (dv[j + 1] - dv[j]) - mean_e;
       sq += e * e;
@@ -281,7 +304,7 @@ static int launch_scores(const fs_scores_args& a, hipStream_t s) {
   if (int rc = fs_host::launch_status("fs_scores (tiles)")) return rc;
   const size_t smem = (size_t)a.N * sizeof(float);
   if (int rc = fs_host::allow_dynamic_lds(scores_final_kernel, smem, "fs_scores")) return rc;
-  scores_final_kernel<<<dim3(a.Hq, 4), kFinalThreads, smem, s>>>(a, ntiles, inv_sqrt_d, pdiag, pcol, dvs);
+  scores_final_kernel<<<dim3(a.Hq, 4 + kDiagJobs), kFinalThreads, smem, s>>>(a, ntiles, inv_sqrt_d, pdiag, pcol, dvs);
   return fs_host::launch_status("fs_scores (final)");
 }
 
