@@ -43,6 +43,8 @@ def parse():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-dense", action="store_true", help="skip the dense comparators")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--select-groups", type=int, default=None,
+                    help="KV-head groups of the selection pipeline (default: the library's choice)")
     ap.add_argument("--cpu-heads", type=int, default=2,
                     help="query heads (all their query blocks) timed for the CPU attention sample")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
@@ -153,7 +155,7 @@ def main():
     def step(ev=None):
         if ev:
             ev[0].record()
-        sel = select_blocks(q, k, **kw)
+        sel = select_blocks(q, k, pipeline_groups=args.select_groups, **kw)
         if ev:
             ev[1].record()
         call = AttentionCall(q, k, v, sel.blk_cnt, sel.blk_idx, block_size=bs)
@@ -267,7 +269,7 @@ def main():
                             "frac": round(sel_bytes / (t_sel * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
                             "traffic": pmc_traffic("select", cfg.name),
                             "work": "Q and K read once (L*(Hq+Hkv)*D*2 bytes)",
-                            "timed": "the four selection launches (pool, corr x2, stats, select)"},
+                            "timed": "select_blocks: pool, block-score tiles + statistics (2 launches), block lists (2 launches)"},
         "cpu_baseline": cpu,
         "input_gen_s": round(t_gen, 1),
     }

@@ -92,7 +92,7 @@ def select_blocks(query_states: torch.Tensor, key_states: torch.Tensor, *, block
                   column_start_exclude_ratio=0.1, column_end_exclude_ratio=0.2,
                   enable_last_block_mask=True, diag_sample_ratio=0.15, min_diag_samples=5,
                   max_diag_samples=64, stripe_threshold=0.3, qk_topk_ratio=0.2,
-                  keep_intermediates=False) -> BlockSelection:
+                  keep_intermediates=False, pipeline_groups=None) -> BlockSelection:
     """Stage 1 of my_attn_v7.myattn_prefill (:533-641): block lists for every
     (query head, query block).  q [1,Hq,L,D], k [1,Hk,L,D]."""
     q = _check_layout(query_states)
@@ -122,49 +122,126 @@ def select_blocks(query_states: torch.Tensor, key_states: torch.Tensor, *, block
     dev = q.device
     dt = _lib.FS_DTYPE[q.dtype]
     N, Nk = p.N, p.Nk
+    G = Hq // Hk
     need_pool = enable_last_block_mask or p.corr_enabled or p.col_enabled   # :553
-    sel = BlockSelection(params=p,
-                         blk_cnt=torch.empty(Hq, N, dtype=torch.int32, device=dev),
-                         blk_idx=torch.empty(Hq, N, Nk, dtype=torch.uint16, device=dev))
-    u8 = torch.uint8
-    if need_pool:
-        q_b = torch.empty(Hq, N, D, dtype=q.dtype, device=dev)
-        k_b = torch.empty(Hk, N, D, dtype=q.dtype, device=dev)
-        _lib.call("fs_pool", PoolArgs(q=q.data_ptr(), q_sh=q.stride(1), q_sl=q.stride(2),
-                                      k=k.data_ptr(), k_sh=k.stride(1), k_sl=k.stride(2),
-                                      dtype=dt, Hq=Hq, Hk=Hk, L=L_q, D=D, bs=block_size,
-                                      q_b=q_b.data_ptr(), k_b=k_b.data_ptr()))
-        sel.q_b, sel.k_b = q_b, k_b
     n_cols = p.n_cols if p.col_enabled else 0
     last_k = p.last_k if enable_last_block_mask else 0
     n_samples = 0 if (not p.corr_enabled or p.stripe_all_diffuse) else len(p.sample_taus)
-    if q.dtype in (torch.bfloat16, torch.float16) and D % 16 == 0 and D <= 128 and N <= 4096 and \
-            (p.corr_enabled or n_cols or last_k):
-        # 16-bit inputs: correlation and statistics in one call from MFMA block-score tiles
-        _scores(sel, p, dt, Hq, Hk, N, D, n_samples, n_cols, last_k, f32(corr_threshold))
-    else:
-        _corr_and_stats(sel, p, dt, Hq, Hk, N, D, n_samples, n_cols, last_k, f32(corr_threshold))
-    keep, diag_var = sel.keep_tau, sel.diag_var
-    col_sel, last_sel = sel.col_sel, sel.last_sel
+    # 16-bit inputs: correlation and statistics in one call from MFMA block-score tiles
+    use_scores = (q.dtype in (torch.bfloat16, torch.float16) and D % 16 == 0 and D <= 128 and N <= 4096
+                  and (p.corr_enabled or n_cols or last_k))
+    thr = f32(corr_threshold)
+    sel = BlockSelection(params=p,
+                         blk_cnt=torch.empty(Hq, N, dtype=torch.int32, device=dev),
+                         blk_idx=torch.empty(Hq, N, Nk, dtype=torch.uint16, device=dev))
+    if need_pool:
+        sel.q_b = torch.empty(Hq, N, D, dtype=q.dtype, device=dev)
+        sel.k_b = torch.empty(Hk, N, D, dtype=q.dtype, device=dev)
     if p.corr_enabled:
-        dyn_mode, col_mode = 1, (1 if n_cols else 0)
+        sel.corr = torch.empty(Hq, N, dtype=torch.float32, device=dev)
+        sel.corr_sum = torch.empty(Hq, N, dtype=torch.float32, device=dev)
+        sel.keep_tau = torch.empty(Hq, N, dtype=torch.uint8, device=dev)
         sel.mean_var = torch.empty(Hq, dtype=torch.float32, device=dev)
-        sel.is_stripe = torch.empty(Hq, dtype=u8, device=dev)
-    else:
-        dyn_mode, col_mode = 0, (2 if n_cols else 0)
-    _lib.call("fs_select", SelectArgs(q_b=ptr(sel.q_b), k_b=ptr(sel.k_b), dtype=dt, Hq=Hq, Hk=Hk, N=N, Nk=Nk,
-                                      D=D, mask_causal=1, keep_sink=p.keep_sink, keep_recent=p.keep_recent,
-                                      local_window=p.local_window, remote_start=p.remote_start,
-                                      dyn_mode=dyn_mode, stripe_all_diffuse=int(p.stripe_all_diffuse),
-                                      diag_var=ptr(diag_var), n_samples=n_samples,
-                                      stripe_threshold=f32(stripe_threshold), keep_tau=ptr(keep),
-                                      qk_topk_ratio=f32(qk_topk_ratio), col_mode=col_mode,
-                                      col_sel=ptr(col_sel), last_sel=ptr(last_sel),
-                                      mean_var=ptr(sel.mean_var), is_stripe=ptr(sel.is_stripe),
-                                      blk_cnt=sel.blk_cnt.data_ptr(), blk_idx=sel.blk_idx.data_ptr()))
+        sel.is_stripe = torch.empty(Hq, dtype=torch.uint8, device=dev)
+    if n_samples or n_cols or last_k:
+        _stat_buffers(sel, Hq, N, n_samples, n_cols, last_k, dev)
+    taus = _sample_taus_device(p.sample_taus, dev)
+    dyn_mode = 1 if p.corr_enabled else 0
+    col_mode = (1 if n_cols else 0) if p.corr_enabled else (2 if n_cols else 0)
+
+    # Optional pipeline over groups of KV heads (each with its query heads):
+    # pooling of group g+1 (HBM bound) runs on the caller's stream while the
+    # latency-bound statistics and block-list kernels of group g run on a side
+    # stream.  Heads are independent, so the result does not depend on the
+    # grouping.  One group is the default: at config 2 the cross-stream waits
+    # cost more than the overlap saves (0.30 ms with 1 group, 0.41 ms with 4).
+    ngroups = max(1, min(pipeline_groups or 1, Hk)) if need_pool else 1
+    bounds = [Hk * g // ngroups for g in range(ngroups + 1)]
+    lib = _lib.load()
+    works = []
+    for g in range(ngroups):
+        hq = (bounds[g + 1] - bounds[g]) * G
+        if use_scores:
+            nbytes = lib.fs_scores_work_bytes(hq, N, n_samples)
+        elif p.corr_enabled:
+            nbytes = lib.fs_corr_work_bytes(hq, N, D)
+        else:
+            nbytes = 0
+        works.append(torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev))
+    main = torch.cuda.current_stream(dev)
+    side = _side_stream(dev) if ngroups > 1 else main
+    if side is not main:
+        side.wait_stream(main)                    # buffers above are allocated before the side work
+    sl = lambda t, a0, a1: None if t is None else t[a0:a1]   # noqa: E731
+    for g in range(ngroups):
+        k0, k1 = bounds[g], bounds[g + 1]
+        h0, h1 = k0 * G, k1 * G
+        hq, hk = h1 - h0, k1 - k0
+        if need_pool:
+            qg, kg = q[:, h0:h1], k[:, k0:k1]
+            _lib.call("fs_pool", PoolArgs(q=qg.data_ptr(), q_sh=q.stride(1), q_sl=q.stride(2),
+                                          k=kg.data_ptr(), k_sh=k.stride(1), k_sl=k.stride(2),
+                                          dtype=dt, Hq=hq, Hk=hk, L=L_q, D=D, bs=block_size,
+                                          q_b=sel.q_b[h0:h1].data_ptr(), k_b=sel.k_b[k0:k1].data_ptr()))
+        if side is not main:
+            ev = torch.cuda.Event()
+            ev.record(main)
+            side.wait_event(ev)
+        with torch.cuda.stream(side):
+            q_b, k_b = sl(sel.q_b, h0, h1), sl(sel.k_b, k0, k1)
+            if use_scores:
+                _lib.call("fs_scores", ScoresArgs(
+                    q_b=ptr(q_b), k_b=ptr(k_b), dtype=dt, Hq=hq, Hk=hk, N=N, D=D,
+                    local_window=p.local_window, keep_sink=p.keep_sink, remote_start=p.remote_start,
+                    corr_threshold=thr, corr=ptr(sl(sel.corr, h0, h1)), corr_sum=ptr(sl(sel.corr_sum, h0, h1)),
+                    keep_tau=ptr(sl(sel.keep_tau, h0, h1)), sample_taus=taus.data_ptr(), n_samples=n_samples,
+                    col_start=p.col_start, col_end=p.col_end, n_cols=n_cols, last_k=last_k,
+                    diag_var=ptr(sl(sel.diag_var, h0, h1)), col_mean=ptr(sl(sel.col_mean, h0, h1)),
+                    col_sel=ptr(sl(sel.col_sel, h0, h1)), last_scores=ptr(sl(sel.last_scores, h0, h1)),
+                    last_sel=ptr(sl(sel.last_sel, h0, h1)), work=works[g].data_ptr()))
+            else:
+                if p.corr_enabled:
+                    _lib.call("fs_corr", CorrArgs(
+                        q_b=ptr(q_b), k_b=ptr(k_b), dtype=dt, Hq=hq, Hk=hk, N=N, D=D,
+                        local_window=p.local_window, keep_sink=p.keep_sink, remote_start=p.remote_start,
+                        corr_threshold=thr, work=works[g].data_ptr(), corr=ptr(sl(sel.corr, h0, h1)),
+                        corr_sum=ptr(sl(sel.corr_sum, h0, h1)), keep_tau=ptr(sl(sel.keep_tau, h0, h1))))
+                if n_samples or n_cols or last_k:
+                    _lib.call("fs_stats", StatsArgs(
+                        q_b=ptr(q_b), k_b=ptr(k_b), dtype=dt, Hq=hq, Hk=hk, N=N, D=D,
+                        sample_taus=taus.data_ptr(), n_samples=n_samples,
+                        col_start=p.col_start, col_end=p.col_end, n_cols=n_cols, last_k=last_k,
+                        diag_var=ptr(sl(sel.diag_var, h0, h1)), col_mean=ptr(sl(sel.col_mean, h0, h1)),
+                        col_sel=ptr(sl(sel.col_sel, h0, h1)), last_scores=ptr(sl(sel.last_scores, h0, h1)),
+                        last_sel=ptr(sl(sel.last_sel, h0, h1))))
+            _lib.call("fs_select", SelectArgs(
+                q_b=ptr(q_b), k_b=ptr(k_b), dtype=dt, Hq=hq, Hk=hk, N=N, Nk=Nk, D=D, mask_causal=1,
+                keep_sink=p.keep_sink, keep_recent=p.keep_recent, local_window=p.local_window,
+                remote_start=p.remote_start, dyn_mode=dyn_mode, stripe_all_diffuse=int(p.stripe_all_diffuse),
+                diag_var=ptr(sl(sel.diag_var, h0, h1)), n_samples=n_samples,
+                stripe_threshold=f32(stripe_threshold), keep_tau=ptr(sl(sel.keep_tau, h0, h1)),
+                qk_topk_ratio=f32(qk_topk_ratio), col_mode=col_mode, col_sel=ptr(sl(sel.col_sel, h0, h1)),
+                last_sel=ptr(sl(sel.last_sel, h0, h1)), mean_var=ptr(sl(sel.mean_var, h0, h1)),
+                is_stripe=ptr(sl(sel.is_stripe, h0, h1)), blk_cnt=sel.blk_cnt[h0:h1].data_ptr(),
+                blk_idx=sel.blk_idx[h0:h1].data_ptr()))
+    if side is not main:
+        main.wait_stream(side)                    # every output is ready on the caller's stream
     if not keep_intermediates:
         sel.q_b = sel.k_b = None
     return sel
+
+
+_side = {}
+
+
+def _side_stream(dev):
+    """One default-priority side stream per device for the selection pipeline."""
+    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    st = _side.get(key)
+    if st is None:
+        st = torch.cuda.Stream(device=dev)
+        _side[key] = st
+    return st
 
 
 def _stat_buffers(sel, Hq, N, n_samples, n_cols, last_k, dev):
@@ -174,53 +251,6 @@ def _stat_buffers(sel, Hq, N, n_samples, n_cols, last_k, dev):
     sel.col_sel = torch.empty(Hq, N, dtype=u8, device=dev) if n_cols else None
     sel.last_scores = torch.empty(Hq, N, dtype=torch.float32, device=dev) if last_k else None
     sel.last_sel = torch.empty(Hq, N, dtype=u8, device=dev) if last_k else None
-
-
-def _scores(sel, p, dt, Hq, Hk, N, D, n_samples, n_cols, last_k, thr):
-    """fs_scores: lag correlation and statistics from MFMA block-score tiles."""
-    dev = sel.q_b.device
-    lib = _lib.load()
-    if p.corr_enabled:
-        sel.corr = torch.empty(Hq, N, dtype=torch.float32, device=dev)
-        sel.corr_sum = torch.empty(Hq, N, dtype=torch.float32, device=dev)
-        sel.keep_tau = torch.empty(Hq, N, dtype=torch.uint8, device=dev)
-    _stat_buffers(sel, Hq, N, n_samples, n_cols, last_k, dev)
-    taus = _sample_taus_device(p.sample_taus, dev)
-    work = torch.empty(lib.fs_scores_work_bytes(Hq, N, n_samples), dtype=torch.uint8, device=dev)
-    _lib.call("fs_scores", ScoresArgs(q_b=ptr(sel.q_b), k_b=ptr(sel.k_b), dtype=dt, Hq=Hq, Hk=Hk, N=N, D=D,
-                                      local_window=p.local_window, keep_sink=p.keep_sink,
-                                      remote_start=p.remote_start, corr_threshold=thr,
-                                      corr=ptr(sel.corr), corr_sum=ptr(sel.corr_sum), keep_tau=ptr(sel.keep_tau),
-                                      sample_taus=taus.data_ptr(), n_samples=n_samples,
-                                      col_start=p.col_start, col_end=p.col_end, n_cols=n_cols, last_k=last_k,
-                                      diag_var=ptr(sel.diag_var), col_mean=ptr(sel.col_mean),
-                                      col_sel=ptr(sel.col_sel), last_scores=ptr(sel.last_scores),
-                                      last_sel=ptr(sel.last_sel), work=work.data_ptr()))
-
-
-def _corr_and_stats(sel, p, dt, Hq, Hk, N, D, n_samples, n_cols, last_k, thr):
-    """fs_corr then fs_stats (any input dtype)."""
-    dev = sel.q_b.device if sel.q_b is not None else None
-    if p.corr_enabled:
-        lib = _lib.load()
-        work = torch.empty(lib.fs_corr_work_bytes(Hq, N, D), dtype=torch.uint8, device=dev)
-        sel.corr = torch.empty(Hq, N, dtype=torch.float32, device=dev)
-        sel.corr_sum = torch.empty(Hq, N, dtype=torch.float32, device=dev)
-        sel.keep_tau = torch.empty(Hq, N, dtype=torch.uint8, device=dev)
-        _lib.call("fs_corr", CorrArgs(q_b=ptr(sel.q_b), k_b=ptr(sel.k_b), dtype=dt, Hq=Hq, Hk=Hk, N=N, D=D,
-                                      local_window=p.local_window, keep_sink=p.keep_sink,
-                                      remote_start=p.remote_start, corr_threshold=thr,
-                                      work=work.data_ptr(), corr=sel.corr.data_ptr(),
-                                      corr_sum=sel.corr_sum.data_ptr(), keep_tau=sel.keep_tau.data_ptr()))
-    if n_samples or n_cols or last_k:
-        _stat_buffers(sel, Hq, N, n_samples, n_cols, last_k, dev)
-        taus = _sample_taus_device(p.sample_taus, dev)
-        _lib.call("fs_stats", StatsArgs(q_b=ptr(sel.q_b), k_b=ptr(sel.k_b), dtype=dt, Hq=Hq, Hk=Hk, N=N, D=D,
-                                        sample_taus=taus.data_ptr(), n_samples=n_samples,
-                                        col_start=p.col_start, col_end=p.col_end, n_cols=n_cols,
-                                        last_k=last_k, diag_var=ptr(sel.diag_var),
-                                        col_mean=ptr(sel.col_mean), col_sel=ptr(sel.col_sel),
-                                        last_scores=ptr(sel.last_scores), last_sel=ptr(sel.last_sel)))
 
 
 class AttentionCall:

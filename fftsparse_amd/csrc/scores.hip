@@ -12,8 +12,8 @@
 //
 // scores_kernel: one workgroup (4 waves) per (head, 128 x 128 tile I >= J of
 // the lower triangle).  Wave w computes rows 32w .. 32w+31 of the tile with
-// v_mfma_f32_32x32x16 (operands loaded straight from the pooled rows, which
-// sit in L2), the tile is written to LDS, and fixed-order per-tile partials
+// v_mfma_f32_32x32x16 (K tile staged in LDS), the tile is written to LDS in
+// two halves of 64 columns, and fixed-order per-tile partials
 // are written to the work buffer: the 255 diagonal sums, the 128 column sums
 // over rows i >= j, i <= N-2, the elements of every sampled diagonal that
 // crosses the tile, and the last row.
@@ -64,9 +64,9 @@ template <typename T>
 __global__ __launch_bounds__(kScoreThreads) void scores_kernel(fs_scores_args a, int ntiles, float inv_sqrt_d,
                                                                float* __restrict__ pdiag, float* __restrict__ pcol,
                                                                float* __restrict__ dvs) {
-  // the K tile (bf16/f16 [128][D]) is staged in the same LDS as the S tile
-  // written after the MFMAs
-  __shared__ __attribute__((aligned(16))) float sl[kScoreTile][kScoreTile + 1];
+  // the K tile (bf16/f16 [128][D], D <= 128: 32 KiB) is staged in the same
+  // LDS as the S half-tiles written after the MFMAs
+  __shared__ __attribute__((aligned(16))) float sl[kScoreTile][kScoreTile / 2 + 1];
   __shared__ int taus[kMaxSamples];
   uint16_t* kt = reinterpret_cast<uint16_t*>(&sl[0][0]);
   const int h = blockIdx.x / ntiles, t = blockIdx.x - h * ntiles;
@@ -126,50 +126,54 @@ __global__ __launch_bounds__(kScoreThreads) void scores_kernel(fs_scores_args a,
       acc[jt] = ScoreMma<T>::mma(av, bv, acc[jt]);
     }
   }
-  __syncthreads();                                 // K tile consumed: the LDS becomes the S tile
-  // C layout: lane holds row (r/4)*8 + hi*4 + r%4, column l32 of each 32x32 block
-#pragma unroll
-  for (int jt = 0; jt < 4; ++jt)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) sl[wave * 32 + (r >> 2) * 8 + hi * 4 + (r & 3)][jt * 32 + l32] = acc[jt][r];
-  __syncthreads();
 
+  // The S tile goes through LDS in two halves of 64 columns (a smaller LDS
+  // footprint, so more workgroups per CU).  C layout: lane holds row
+  // (r/4)*8 + hi*4 + r%4, column l32 of each 32x32 block.
   const int64_t tb = (int64_t)h * ntiles + t;
   const bool diag_tile = I == J;
-  // ---- lag sums: local diagonal dl = iloc - jloc in [-127, 127], rows in ascending order
-  if (a.keep_tau != nullptr && tid < 2 * kScoreTile - 1) {
-    const int dl = tid - (kScoreTile - 1);
-    float s = 0.f;
-    if (!(diag_tile && dl < 0)) {
-      const int ib = max(0, dl), ie = min(kScoreTile - 1, kScoreTile - 1 + dl);
+  const int dl = tid - (kScoreTile - 1);           // this thread's local diagonal iloc - jloc
+  const bool lag_on = a.keep_tau != nullptr && tid < 2 * kScoreTile - 1 && !(diag_tile && dl < 0);
+  float lag = 0.f;
+  for (int hf = 0; hf < 2; ++hf) {
+    const int c0 = hf * (kScoreTile / 2);          // first tile column of this half
+    __syncthreads();                               // K tile / previous half consumed
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sl[wave * 32 + (r >> 2) * 8 + hi * 4 + (r & 3)][jj * 32 + l32] = acc[2 * hf + jj][r];
+    __syncthreads();
+    // ---- lag sums along the local diagonal, rows ascending (this half's columns)
+    if (lag_on) {
+      const int ib = max(0, dl + c0), ie = min(kScoreTile - 1, dl + c0 + kScoreTile / 2 - 1);
 #pragma unroll 8
-      for (int il = ib; il <= ie; ++il) s += sl[il][il - dl];
+      for (int il = ib; il <= ie; ++il) lag += sl[il][il - dl - c0];
     }
-    pdiag[tb * kDiagSlots + tid] = s;
-  }
-  // ---- column sums over rows i >= j, i <= N-2
-  if (a.n_cols > 0 && tid < kScoreTile) {
-    const int j = j0 + tid;
-    const int ib = diag_tile ? tid : 0;
-    const int ie = min(kScoreTile - 1, N - 2 - i0);
-    float s = 0.f;
+    // ---- column sums over rows i >= j, i <= N-2
+    if (a.n_cols > 0 && tid < kScoreTile / 2) {
+      const int jl = c0 + tid, j = j0 + jl;
+      const int ib = diag_tile ? jl : 0;
+      const int ie = min(kScoreTile - 1, N - 2 - i0);
+      float s = 0.f;
 #pragma unroll 8
-    for (int il = ib; il <= ie; ++il) s += sl[il][tid];
-    pcol[tb * kScoreTile + tid] = (j < N) ? s : 0.f;
+      for (int il = ib; il <= ie; ++il) s += sl[il][tid];
+      pcol[tb * kScoreTile + jl] = (j < N) ? s : 0.f;
+    }
+    // ---- sampled diagonals: S[j + tau][j] / sqrt(D) for j < N - tau - 1
+    for (int e = tid; e < a.n_samples * (kScoreTile / 2); e += kScoreThreads) {
+      const int s = e / (kScoreTile / 2), jh = e - s * (kScoreTile / 2);
+      const int tau = taus[s];
+      const int j = j0 + c0 + jh, i = j + tau;
+      if (tau < 0 || tau >= N || j >= N - tau - 1) continue;
+      const int il = i - i0;
+      if (il < 0 || il >= kScoreTile) continue;
+      dvs[((int64_t)h * a.n_samples + s) * N + j] = sl[il][jh] * inv_sqrt_d;
+    }
+    // ---- last row, rounded to the input dtype
+    if (a.last_k > 0 && i0 <= N - 1 && N - 1 < i0 + kScoreTile && tid < kScoreTile / 2 && j0 + c0 + tid < N)
+      a.last_scores[(int64_t)h * N + j0 + c0 + tid] = Conv<T>::round(sl[N - 1 - i0][tid]);
   }
-  // ---- sampled diagonals: S[j + tau][j] / sqrt(D) for j < N - tau - 1
-  for (int e = tid; e < a.n_samples * kScoreTile; e += kScoreThreads) {
-    const int s = e / kScoreTile, jl = e - s * kScoreTile;
-    const int tau = taus[s];
-    const int j = j0 + jl, i = j + tau;
-    if (tau < 0 || tau >= N || j >= N - tau - 1) continue;
-    const int il = i - i0;
-    if (il < 0 || il >= kScoreTile) continue;
-    dvs[((int64_t)h * a.n_samples + s) * N + j] = sl[il][jl] * inv_sqrt_d;
-  }
-  // ---- last row, rounded to the input dtype
-  if (a.last_k > 0 && i0 <= N - 1 && N - 1 < i0 + kScoreTile && tid < kScoreTile && j0 + tid < N)
-    a.last_scores[(int64_t)h * N + j0 + tid] = Conv<T>::round(sl[N - 1 - i0][tid]);
+  if (a.keep_tau != nullptr && tid < 2 * kScoreTile - 1) pdiag[tb * kDiagSlots + tid] = lag;
 }
 
 __global__ __launch_bounds__(kFinalThreads) void scores_final_kernel(fs_scores_args a, int ntiles, float inv_sqrt_d,

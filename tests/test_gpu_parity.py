@@ -183,6 +183,22 @@ def test_block_lists_are_ascending_and_deterministic():
             assert bool((row[1:] > row[:-1]).all()) and int(row[-1]) == i and int(row[0]) == 0
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_pipeline_grouping_does_not_change_lists(dtype):
+    """The head-group pipeline (pooling of one group overlapping the statistics
+    of the previous one on a side stream) gives bit-identical block lists and
+    statistics for every grouping."""
+    q, k, _ = make_qkv(32768, 8, 4, dtype=dtype, seed=9)
+    qg, kg = _gpu(q, k)
+    ref = select_blocks(qg, kg, **PROD, keep_intermediates=True, pipeline_groups=1)
+    for groups in (2, 4):
+        got = select_blocks(qg, kg, **PROD, keep_intermediates=True, pipeline_groups=groups)
+        torch.cuda.synchronize()
+        assert torch.equal(got.dense_mask(), ref.dense_mask()), groups
+        for f in ("corr", "keep_tau", "diag_var", "col_mean", "last_scores", "mean_var"):
+            assert torch.equal(getattr(got, f), getattr(ref, f)), (groups, f)
+
+
 # --------------------------------------------------------------------------- attention
 def _attn_check(out, ref, rows=None):
     o = out.float().cpu()
