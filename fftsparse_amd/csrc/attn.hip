@@ -31,6 +31,9 @@
 // same lag diagonals and the same columns, which then hit that XCD's L2).
 // The dense path gives XCD x every 8th query-block row (last rows first) of
 // every head.
+#include <climits>
+#include <type_traits>
+
 #include "common.h"
 
 namespace fs {
@@ -358,18 +361,31 @@ __global__ __launch_bounds__(AttnCfg<BS>::NT) void bsattn_kernel(AttnKArgs a) {
       }
     }
   };
-  // Masking (diagonal / partial tiles only), online softmax and
-  // O^T += V^T P^T for the tile kb whose scores are in s (V^T in buffer vbuf).
-  // The O rescale is rare (see kSlack).
-  auto softmax_pv = [&](int kb, int vbuf, f32x16_t* s) {
+  // whether any key of this wave's half of tile kb is visible to its queries
+  auto active_for = [&](int kb) {
+    const int kw0 = kb * BS + kbase;
+    return kb < Nk && kw0 < a.Lk && !(a.is_causal && kw0 > qw0 + 31 + off);
+  };
+
+  // Masking (diagonal / partial / invisible half tiles only) and the running
+  // max of the tile kb whose scores are in s.  A raise of the running max is
+  // not applied to O here: it is returned as alpha (1 when none) and applied
+  // right after the P V of the previous tile has been added to O.
+  auto mask_max = [&](int kb, f32x16_t* s) -> float {
     const int kw0 = kb * BS + kbase;                // first key of this wave
-    if ((kw0 + C::KH > a.Lk) || (a.is_causal && kw0 + C::KH - 1 > qw0 + off)) {
+    const bool act = active_for(kb);
+    if (!act || (kw0 + C::KH > a.Lk) || (a.is_causal && kw0 + C::KH - 1 > qw0 + off)) {
+      // element (kt, r) holds key kw0 + hi*4 + c with the constant c below; it
+      // is visible iff c < lim (key < Lk, and key <= qrow + off when causal)
+      int lim = a.Lk - kw0 - hi * 4;
+      if (a.is_causal) lim = min(lim, qrow + off - kw0 - hi * 4 + 1);
+      if (!act) lim = INT_MIN;
 #pragma unroll
       for (int kt = 0; kt < C::KT; ++kt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int key = kw0 + kt * 32 + (r >> 2) * 8 + hi * 4 + (r & 3);
-          if (key >= a.Lk || (a.is_causal && key > qrow + off)) s[kt][r] = -INFINITY;
+          const int c = kt * 32 + (r >> 2) * 8 + (r & 3);
+          if (c >= lim) s[kt][r] = -INFINITY;
         }
     }
     float mx = -INFINITY;
@@ -378,18 +394,18 @@ __global__ __launch_bounds__(AttnCfg<BS>::NT) void bsattn_kernel(AttnKArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kt][r]);
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * sc;
+    float alpha = 1.0f;
     if (__builtin_amdgcn_ballot_w64(mx > m_run + kSlack) != 0) {
       const float m_new = fmaxf(m_run, mx);
-      const float alpha = __builtin_amdgcn_exp2f(m_run - (m_new == -INFINITY ? 0.f : m_new));
+      alpha = __builtin_amdgcn_exp2f(m_run - (m_new == -INFINITY ? 0.f : m_new));
       l_run *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < kD / 32; ++dt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
       m_run = m_new;
     }
+    return alpha;
+  };
+  // P = 2^(s sc - m) packed to the MFMA input type; its row sum goes to l
+  auto exp_p = [&](f32x16_t* s, V8* pb) {
     const float m_use = m_run == -INFINITY ? 0.f : m_run;
-    const char* vt_base = reinterpret_cast<const char*>(lds[1][vbuf]);
     float rs = 0.f;
 #pragma unroll
     for (int kk = 0; kk < C::KH / 16; ++kk) {
@@ -397,68 +413,111 @@ __global__ __launch_bounds__(AttnCfg<BS>::NT) void bsattn_kernel(AttnKArgs a) {
       float pv[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) pv[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][8 * half + j], sc, -m_use));
-      const V8 pb = Ops::pack(pv);
-      rs = Ops::sum8(pb, rs);                       // row sum of the rounded P actually multiplied
+      pb[kk] = Ops::pack(pv);
+      rs = Ops::sum8(pb[kk], rs);                   // row sum of the rounded P actually multiplied
+    }
+    l_run += rs + __shfl_xor(rs, 32, 64);
+  };
+  // O^T += V^T P^T for the V^T tile in buffer vbuf
+  auto pv_mma = [&](int vbuf, const V8* pb) {
+    const char* vt_base = reinterpret_cast<const char*>(lds[1][vbuf]);
+#pragma unroll
+    for (int kk = 0; kk < C::KH / 16; ++kk) {
       const uint32_t lo = lane_off_v ^ (uint32_t)(((kbase >> 3) + 2 * kk) << 4);
 #pragma unroll
       for (int dt = 0; dt < kD / 32; ++dt) {
         const V8 va = __builtin_bit_cast(V8, lds16(vt_base + dt * VROW, lo));
-        o[dt] = Ops::mma(va, pb, o[dt]);
+        o[dt] = Ops::mma(va, pb[kk], o[dt]);
       }
     }
-    l_run += rs + __shfl_xor(rs, 32, 64);
   };
-  // whether any key of this wave's half of tile kb is visible to its queries
-  auto active_for = [&](int kb) {
-    const int kw0 = kb * BS + kbase;
-    return kb < Nk && kw0 < a.Lk && !(a.is_causal && kw0 > qw0 + 31 + off);
-  };
-
-  // Retire the Q loads here, through a wait the compiler sees: otherwise it
-  // guards their first use inside the loop with a vmcnt(0) on every iteration,
-  // which would also wait for the tile copies in flight.
-  __builtin_amdgcn_s_waitcnt(0);
-  // Pipeline: K runs one tile ahead of V.  At the top of iteration t the
-  // copies of K(t+1) and V(t) have landed; after one barrier the copies of
-  // K(t+2) (into the buffer of K(t)) and V(t+1) (into the buffer of V(t-1))
-  // start, the MFMAs of S(t+1) are issued, and the softmax of tile t runs on
-  // the VALU while they execute, followed by the P V MFMAs of tile t.
-  f32x16_t sa[C::KT], sb[C::KT];
-  int kb0 = 0, kb1 = 0, kb2 = 0;
-  if (cnt > 0) {
-    kb0 = block_at(0);
-    issue_k(kb0, 0);
-    issue_v(kb0, 0);
-    if (cnt > 1) {
-      kb1 = block_at(1);
-      issue_k(kb1, 1);
+  auto scale_o = [&](float alpha) {
+    if (alpha != 1.0f) {                             // per query row (lane); rare
+#pragma unroll
+      for (int dt = 0; dt < kD / 32; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    if (active_for(kb0)) compute_s(0, sa);
-  }
-  auto step = [&](int t, f32x16_t* s_cur, f32x16_t* s_next) {
-    // K(t+1), V(t) landed; every wave is past iteration t-1 and its LDS reads
+  };
+  __builtin_amdgcn_s_waitcnt(0);                   // retire the Q loads (see below)
+  // Pipeline with P V deferred by one tile.  Iteration t: wait for K(t+1)
+  // and V(t-1), one barrier, copy K(t+2) (into the buffer of K(t)) and V(t)
+  // (into that of V(t-2)); then one straight-line block with S(t+1) and
+  // P V(t-1) on the MFMA pipe interleaved with the exponentials of tile t on
+  // the VALU (independent work); then the pending O rescale and the mask /
+  // running max of tile t+1.
+  f32x16_t sa[C::KT], sb[C::KT];
+  V8 pa[C::KH / 16], pb[C::KH / 16];
+  float alpha = 1.0f;
+  int kb0 = 0, kb1 = 0, kb2 = 0;                   // blocks of tiles t, t+1, t+2
+  typedef std::integral_constant<bool, true> yes;
+  typedef std::integral_constant<bool, false> no;
+  auto iter = [&](int t, f32x16_t* s_next, f32x16_t* s_cur, V8* p_prev, V8* p_cur, auto hasS, auto hasPV,
+                  auto hasE) {
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     if (t + 2 < cnt) {
       kb2 = block_at(t + 2);
       issue_k(kb2, t & 1);
     }
-    if (t + 1 < cnt) {
-      issue_v(kb1, (t + 1) & 1);
-      if (active_for(kb1)) compute_s((t + 1) & 1, s_next);
+    if (t < cnt) issue_v(kb0, t & 1);
+    if constexpr (decltype(hasS)::value) compute_s((t + 1) & 1, s_next);
+    if constexpr (decltype(hasPV)::value) pv_mma((t - 1) & 1, p_prev);
+    if constexpr (decltype(hasE)::value) exp_p(s_cur, p_cur);
+    if constexpr (decltype(hasS)::value && decltype(hasPV)::value && decltype(hasE)::value) {
+      // Steady state: the scheduler interleaves one MFMA with two VALU
+      // instructions (a wave issues in order, so MFMAs issued back to back
+      // would hold its exponentials until the last one), the LDS operand
+      // reads running six MFMAs ahead.
+      constexpr int NM = C::KT * (kD / 16) + (C::KH / 16) * (kD / 32);
+      constexpr int LA = 6;
+      __builtin_amdgcn_sched_group_barrier(0x100, LA, 0);        // DS reads
+#pragma unroll
+      for (int i = 0; i < NM; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // MFMA
+        if (i + LA < NM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);       // VALU
+      }
     }
-    if (active_for(kb0)) softmax_pv(kb0, t & 1, s_cur);
+    scale_o(alpha);                                  // O holds P V up to t-1 now
+    alpha = 1.0f;
+    if constexpr (decltype(hasS)::value) alpha = mask_max(kb1, s_next);
     kb0 = kb1;
     kb1 = kb2;
   };
-  int t = 0;
-  for (; t + 1 < cnt; t += 2) {
-    step(t, sa, sb);
-    step(t + 1, sb, sa);
+  if (cnt > 0) {
+    kb0 = block_at(0);
+    issue_k(kb0, 0);
+    if (cnt > 1) {
+      kb1 = block_at(1);
+      issue_k(kb1, 1);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    compute_s(0, sa);
+    alpha = mask_max(kb0, sa);                       // O is zero: nothing to rescale
+    alpha = 1.0f;
+    // t = 0: S(1) if it exists, exponentials of tile 0, no P V yet
+    if (cnt > 1) iter(0, sb, sa, pb, pa, yes(), no(), yes());
+    else iter(0, sb, sa, pb, pa, no(), no(), yes());
+    int t = 1;
+    for (; t + 2 < cnt; t += 2) {                    // steady state: t and t+1 both have S(t+1)
+      iter(t, sa, sb, pa, pb, yes(), yes(), yes());
+      iter(t + 1, sb, sa, pb, pa, yes(), yes(), yes());
+    }
+    // remaining iterations t .. cnt: at most one more steady step, the last
+    // tile (no S(t+1)) and the final P V
+    if (t + 1 < cnt) {                               // t odd, t+1 = cnt-1 even
+      iter(t, sa, sb, pa, pb, yes(), yes(), yes());
+      iter(t + 1, sb, sa, pb, pa, no(), yes(), yes());
+      iter(t + 2, sa, sb, pa, pb, no(), yes(), no());
+    } else if (t < cnt) {                            // t = cnt-1, odd
+      iter(t, sa, sb, pa, pb, no(), yes(), yes());
+      iter(t + 1, sb, sa, pb, pa, no(), yes(), no());
+    } else {                                         // t = cnt (cnt == 1): the final P V
+      iter(t, sa, sb, pa, pb, no(), yes(), no());
+    }
   }
-  if (t < cnt) step(t, sa, sb);
   __syncthreads();
 
   // ---- merge the two key halves through LDS, normalise, store
