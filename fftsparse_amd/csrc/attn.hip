@@ -332,9 +332,9 @@ __global__ __launch_bounds__(AttnCfg<BS>::NT) void bsattn_kernel(AttnKArgs a) {
                 : (uint32_t)((l32 >> 1) * 256 + (((((l32 & 1) << 3) | hi) ^ (l32 >> 1)) << 4));
   constexpr int VROW = BS == 128 ? 32 * 256 : 16 * 256;   // bytes per 32 d rows of V^T
 
-  // Running max is kept in the exp2 domain of raw scores times sc; it is only
-  // raised (and O rescaled) when a new score exceeds it by more than 2^8, so
-  // p = 2^(s*sc - m) <= 256 and most tiles skip the rescale.
+  // Running max (per query row) is kept in the exp2 domain of raw scores
+  // times sc; it is only raised (and O rescaled) when a new score exceeds it
+  // by more than 2^8, so p = 2^(s*sc - m) <= 256 and most tiles skip the rescale.
   const float sc = a.scale * 1.44269504088896340736f;
   constexpr float kSlack = 8.0f;
   float m_run = -INFINITY, l_run = 0.f;
@@ -367,16 +367,13 @@ __global__ __launch_bounds__(AttnCfg<BS>::NT) void bsattn_kernel(AttnKArgs a) {
     return kb < Nk && kw0 < a.Lk && !(a.is_causal && kw0 > qw0 + 31 + off);
   };
 
-  // Masking (diagonal / partial / invisible half tiles only) and the running
-  // max of the tile kb whose scores are in s.  A raise of the running max is
-  // not applied to O here: it is returned as alpha (1 when none) and applied
-  // right after the P V of the previous tile has been added to O.
-  auto mask_max = [&](int kb, f32x16_t* s) -> float {
-    const int kw0 = kb * BS + kbase;                // first key of this wave
+  // Masking (diagonal / partial / invisible half tiles only) of the tile kb
+  // whose scores are in s; the running max is taken later, beside the
+  // exponentials of that tile.
+  auto mask_only = [&](int kb, f32x16_t* s) {
+    const int kw0 = kb * BS + kbase;
     const bool act = active_for(kb);
     if (!act || (kw0 + C::KH > a.Lk) || (a.is_causal && kw0 + C::KH - 1 > qw0 + off)) {
-      // element (kt, r) holds key kw0 + hi*4 + c with the constant c below; it
-      // is visible iff c < lim (key < Lk, and key <= qrow + off when causal)
       int lim = a.Lk - kw0 - hi * 4;
       if (a.is_causal) lim = min(lim, qrow + off - kw0 - hi * 4 + 1);
       if (!act) lim = INT_MIN;
@@ -388,24 +385,10 @@ __global__ __launch_bounds__(AttnCfg<BS>::NT) void bsattn_kernel(AttnKArgs a) {
           if (c >= lim) s[kt][r] = -INFINITY;
         }
     }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int kt = 0; kt < C::KT; ++kt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kt][r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * sc;
-    float alpha = 1.0f;
-    if (__builtin_amdgcn_ballot_w64(mx > m_run + kSlack) != 0) {
-      const float m_new = fmaxf(m_run, mx);
-      alpha = __builtin_amdgcn_exp2f(m_run - (m_new == -INFINITY ? 0.f : m_new));
-      l_run *= alpha;
-      m_run = m_new;
-    }
-    return alpha;
   };
-  // P = 2^(s sc - m) packed to the MFMA input type; its row sum goes to l
-  auto exp_p = [&](f32x16_t* s, V8* pb) {
-    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+  // P = 2^(s sc - m) with m = m_use, packed to the MFMA input type; returns
+  // the row sum of the rounded P over this lane's keys
+  auto exp_part = [&](const f32x16_t* s, V8* pb, float m_use) -> float {
     float rs = 0.f;
 #pragma unroll
     for (int kk = 0; kk < C::KH / 16; ++kk) {
@@ -414,9 +397,24 @@ __global__ __launch_bounds__(AttnCfg<BS>::NT) void bsattn_kernel(AttnKArgs a) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) pv[j] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][8 * half + j], sc, -m_use));
       pb[kk] = Ops::pack(pv);
-      rs = Ops::sum8(pb[kk], rs);                   // row sum of the rounded P actually multiplied
+      rs = Ops::sum8(pb[kk], rs);
     }
-    l_run += rs + __shfl_xor(rs, 32, 64);
+    return rs;
+  };
+  // v and the value of the lane 32 apart (the same query's other keys): one
+  // v_permlane32_swap, both operand orders identical in the two halves
+  auto halves = [](float v, float& lo, float& hi_) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    lo = __uint_as_float(r[0]);
+    hi_ = __uint_as_float(r[1]);
+  };
+  auto row_max = [&](const f32x16_t* s) -> float {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < C::KT; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kt][r]);
+    return mx;
   };
   // O^T += V^T P^T for the V^T tile in buffer vbuf
   auto pv_mma = [&](int vbuf, const V8* pb) {
@@ -443,12 +441,12 @@ __global__ __launch_bounds__(AttnCfg<BS>::NT) void bsattn_kernel(AttnKArgs a) {
   // Pipeline with P V deferred by one tile.  Iteration t: wait for K(t+1)
   // and V(t-1), one barrier, copy K(t+2) (into the buffer of K(t)) and V(t)
   // (into that of V(t-2)); then one straight-line block with S(t+1) and
-  // P V(t-1) on the MFMA pipe interleaved with the exponentials of tile t on
-  // the VALU (independent work); then the pending O rescale and the mask /
-  // running max of tile t+1.
+  // P V(t-1) on the MFMA pipe interleaved with the row max, running-max raise
+  // and exponentials of tile t on the VALU (independent work); then the O
+  // rescale of a raise (rare) and the masking of tile t+1 (diagonal and
+  // partial tiles only).
   f32x16_t sa[C::KT], sb[C::KT];
   V8 pa[C::KH / 16], pb[C::KH / 16];
-  float alpha = 1.0f;
   int kb0 = 0, kb1 = 0, kb2 = 0;                   // blocks of tiles t, t+1, t+2
   typedef std::integral_constant<bool, true> yes;
   typedef std::integral_constant<bool, false> no;
@@ -461,16 +459,30 @@ __global__ __launch_bounds__(AttnCfg<BS>::NT) void bsattn_kernel(AttnKArgs a) {
       issue_k(kb2, t & 1);
     }
     if (t < cnt) issue_v(kb0, t & 1);
+    // The row max of tile t, the raise of the running max and the
+    // exponentials of tile t are VALU work independent of the MFMAs of S(t+1)
+    // and P V(t-1), so all of it goes into the interleaved block; only the
+    // rescale of O, which must follow P V(t-1), is left after it (rare).
+    float rs = 0.f, al = 1.0f;
     if constexpr (decltype(hasS)::value) compute_s((t + 1) & 1, s_next);
     if constexpr (decltype(hasPV)::value) pv_mma((t - 1) & 1, p_prev);
-    if constexpr (decltype(hasE)::value) exp_p(s_cur, p_cur);
+    if constexpr (decltype(hasE)::value) {
+      float mx = row_max(s_cur), m0, m1;
+      halves(mx, m0, m1);
+      mx = fmaxf(m0, m1) * sc;
+      // a row raises its running max only when a score exceeds it by more than the slack
+      const bool up = mx > m_run + kSlack;
+      al = up ? __builtin_amdgcn_exp2f(m_run - mx) : 1.0f;
+      m_run = up ? mx : m_run;
+      rs = exp_part(s_cur, p_cur, m_run == -INFINITY ? 0.f : m_run);
+    }
     if constexpr (decltype(hasS)::value && decltype(hasPV)::value && decltype(hasE)::value) {
       // Steady state: the scheduler interleaves one MFMA with two VALU
       // instructions (a wave issues in order, so MFMAs issued back to back
       // would hold its exponentials until the last one), the LDS operand
-      // reads running six MFMAs ahead.
+      // reads running four MFMAs ahead (measured best of 2, 3, 4, 6, 8).
       constexpr int NM = C::KT * (kD / 16) + (C::KH / 16) * (kD / 32);
-      constexpr int LA = 6;
+      constexpr int LA = 4;
       __builtin_amdgcn_sched_group_barrier(0x100, LA, 0);        // DS reads
 #pragma unroll
       for (int i = 0; i < NM; ++i) {
@@ -479,9 +491,13 @@ __global__ __launch_bounds__(AttnCfg<BS>::NT) void bsattn_kernel(AttnKArgs a) {
         __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);       // VALU
       }
     }
-    scale_o(alpha);                                  // O holds P V up to t-1 now
-    alpha = 1.0f;
-    if constexpr (decltype(hasS)::value) alpha = mask_max(kb1, s_next);
+    if constexpr (decltype(hasE)::value) {
+      float r0, r1;
+      halves(rs, r0, r1);
+      l_run = l_run * al + (r0 + r1);
+      if (__builtin_amdgcn_ballot_w64(al != 1.0f) != 0) scale_o(al);   // O holds P V up to t-1 now
+    }
+    if constexpr (decltype(hasS)::value) mask_only(kb1, s_next);
     kb0 = kb1;
     kb1 = kb2;
   };
@@ -495,8 +511,7 @@ __global__ __launch_bounds__(AttnCfg<BS>::NT) void bsattn_kernel(AttnKArgs a) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     compute_s(0, sa);
-    alpha = mask_max(kb0, sa);                       // O is zero: nothing to rescale
-    alpha = 1.0f;
+    mask_only(kb0, sa);
     // t = 0: S(1) if it exists, exponentials of tile 0, no P V yet
     if (cnt > 1) iter(0, sb, sa, pb, pa, yes(), no(), yes());
     else iter(0, sb, sa, pb, pa, no(), no(), yes());
