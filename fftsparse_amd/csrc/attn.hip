@@ -92,6 +92,18 @@ template <> struct MfmaOps<f16_t> {
 };
 
 constexpr int kD = 128;
+#ifndef FS_TK
+#define FS_TK 64
+#endif
+#ifndef FS_RUN
+#define FS_RUN 16
+#endif
+#ifndef FS_LA
+#define FS_LA 4
+#endif
+#ifndef FS_VPM
+#define FS_VPM 2
+#endif
 
 // position of key k inside its 16-key group in the V^T layout (an involution)
 __device__ __forceinline__ int vt_pos(int k) {
@@ -137,16 +149,21 @@ __global__ __launch_bounds__(256) void vt_kernel(const uint16_t* __restrict__ v,
 }
 
 // ---- main kernel -------------------------------------------------------------
-template <int BS>
+// BS: query / key block size of the block lists; TK: keys per LDS tile
+// (BS, or BS / 2 for two tiles per key block).
+template <int BS, int TK>
 struct AttnCfg {
   static constexpr int QW = BS / 32;          // query waves (32 queries each)
-  static constexpr int NW = QW * 2;           // waves (x2 key halves)
+  static constexpr int KG = 2 * TK / BS;      // key groups: waves sharing the keys of a tile (2 or 1)
+  static constexpr int NW = QW * KG;          // waves
   static constexpr int NT = NW * 64;          // threads
-  static constexpr int KH = BS / 2;           // keys per wave per tile
+  static constexpr int KH = TK / KG;          // keys per wave per tile
   static constexpr int KT = KH / 32;          // 32-key sub-tiles per wave
-  static constexpr int TILE = BS * kD;        // elements of one K (or V^T) tile
+  static constexpr int TPB = BS / TK;         // tiles per key block
+  static constexpr int TILE = TK * kD;        // elements of one K (or V^T) tile
   static constexpr int REGIONS = TILE * 2 / 1024;   // 1 KiB DMA regions per tile
   static constexpr int DMA_PER_WAVE = 2 * REGIONS / NW;
+  static_assert(KG == 1 || KG == 2, "tile is a block or half a block");
 };
 
 // element offset of 16-byte chunk c of 256-byte row r, swizzled
@@ -185,9 +202,10 @@ __device__ __forceinline__ uint4 lds16(const char* base, uint32_t off) {
   return *reinterpret_cast<const uint4*>(base + off);
 }
 
-template <int BS, typename T>
-__global__ __launch_bounds__(AttnCfg<BS>::NT) void bsattn_kernel(AttnKArgs a) {
-  using C = AttnCfg<BS>;
+template <int BS, int TK, typename T>
+__global__ __launch_bounds__((AttnCfg<BS, TK>::NT)) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void bsattn_kernel(AttnKArgs a) {
+  using C = AttnCfg<BS, TK>;
   using Ops = MfmaOps<T>;
   using V8 = typename Ops::V8;
   // [K | V^T][buffer] tiles; 256-byte rows with swizzled 16-byte chunks
@@ -251,26 +269,32 @@ __global__ __launch_bounds__(AttnCfg<BS>::NT) void bsattn_kernel(AttnKArgs a) {
   // Block lists are read through the scalar unit (constant address space):
   // their completion is tracked by lgkmcnt, so reading the next index never
   // waits on the tile copies in flight (vmcnt).
-  int cnt;
   const bool listed = a.blk_cnt != nullptr;
   int64_t lbase = 0;
-  if (listed) {
-    cnt = (int)((cptr32)(uintptr_t)a.blk_cnt)[(int64_t)h * a.Nq + qb];
-    lbase = ((int64_t)h * a.Nq + qb) * a.Nk;
-  } else {
-    const int last_key = a.is_causal ? min(a.Lk - 1, q0 + BS - 1 + off) : a.Lk - 1;
-    cnt = last_key < 0 ? 0 : last_key / BS + 1;
-  }
-  auto block_at = [&](int t) -> int {
-    if (!listed) return t;
-    const int64_t gi = lbase + t;
+  auto block_at = [&](int i) -> int {              // i-th listed key block
+    const int64_t gi = lbase + i;
     const uint32_t w = ((cptr32)(uintptr_t)a.blk_idx)[gi >> 1];
     return (int)((gi & 1) ? (w >> 16) : (w & 0xffffu));
   };
-  // drop trailing blocks entirely above the diagonal (lists are ascending)
-  if (a.is_causal) {
-    while (cnt > 0 && block_at(cnt - 1) * BS > q0 + BS - 1 + off) --cnt;
+  int cnt;                                         // key tiles of this query block
+  if (listed) {
+    int nb = (int)((cptr32)(uintptr_t)a.blk_cnt)[(int64_t)h * a.Nq + qb];
+    lbase = ((int64_t)h * a.Nq + qb) * a.Nk;
+    // drop trailing blocks entirely above the diagonal (lists are ascending)
+    if (a.is_causal) {
+      while (nb > 0 && block_at(nb - 1) * BS > q0 + BS - 1 + off) --nb;
+    }
+    cnt = nb * C::TPB;
+  } else {
+    const int last_key = a.is_causal ? min(a.Lk - 1, q0 + BS - 1 + off) : a.Lk - 1;
+    cnt = last_key < 0 ? 0 : last_key / TK + 1;
   }
+  // first key of tile t (-1: an out-of-range list entry, skipped)
+  auto key_of = [&](int t) -> int {
+    if (!listed) return t * TK;
+    const int kb = block_at(t / C::TPB);
+    return kb < a.Nk ? kb * BS + (t % C::TPB) * TK : -1;
+  };
 
   // ---- tile DMA: wave w copies 1 KiB regions w*NR .. w*NR+NR-1 of the K tile
   // and of the V^T tile.  koff / voff are this lane's byte offsets inside a
@@ -284,35 +308,34 @@ __global__ __launch_bounds__(AttnCfg<BS>::NT) void bsattn_kernel(AttnKArgs a) {
     const int r = 4 * R + (lane >> 4);
     const int c = (lane & 15) ^ (r & 15);
     koff[i] = (uint32_t)(r * a.k_sl + c * 8) * 2u;
-    voff[i] = (BS == 128 ? (uint32_t)(r * a.Lp + c * 8)                          // d = r
+    voff[i] = (TK == 128 ? (uint32_t)(r * a.Lp + c * 8)                          // d = r
                          : (uint32_t)((2 * r + (c >> 3)) * a.Lp + (c & 7) * 8))  // two d rows per LDS row
               * 2u;
   }
-  const int Nk = a.Nk;
-  const int k0_last = (Nk - 1) * BS;
-  const bool last_partial = k0_last + BS > a.Lk;
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&lds[0][0][0]);
-  auto issue_k = [&](int kb, int buf) {
-    kb = min(kb, Nk - 1);                          // out-of-range entries are skipped at compute
-    const uint16_t* base = kp + (int64_t)(kb * BS) * a.k_sl;
+  auto issue_k = [&](int key0, int buf) {
     const uint32_t lk = lds0 + (uint32_t)(buf * C::TILE * 2 + wave * NR * 1024);
-    if (last_partial && kb == Nk - 1) {
-      // the last, partial block: K rows past Lk read the last row instead (their scores are masked)
+    if (key0 >= 0 && key0 + TK <= a.Lk) {
+      const uint16_t* base = kp + (int64_t)key0 * a.k_sl;
+#pragma unroll
+      for (int i = 0; i < NR; ++i) dma16s(lk + i * 1024, base, koff[i]);
+    } else {
+      // a tile reaching past Lk, or an out-of-range entry: rows past Lk read
+      // row Lk-1 instead (their scores are masked)
+      const int kc = min(max(key0, 0), a.Lk - 1);
+      const uint16_t* base = kp + (int64_t)kc * a.k_sl;
       int ln = lane;
       asm volatile("" : "+v"(ln));                 // keep this rare path's offsets out of the loop preheader
 #pragma unroll
       for (int i = 0; i < NR; ++i) {
         const int r = 4 * (wave * NR + i) + (ln >> 4);
         const int c = (ln & 15) ^ (r & 15);
-        dma16s(lk + i * 1024, base, (uint32_t)(min(r, a.Lk - 1 - k0_last) * a.k_sl + c * 8) * 2u);
+        dma16s(lk + i * 1024, base, (uint32_t)(min(r, a.Lk - 1 - kc) * a.k_sl + c * 8) * 2u);
       }
-    } else {
-#pragma unroll
-      for (int i = 0; i < NR; ++i) dma16s(lk + i * 1024, base, koff[i]);
     }
   };
-  auto issue_v = [&](int kb, int buf) {
-    const uint16_t* base = vtp + min(kb, Nk - 1) * BS;
+  auto issue_v = [&](int key0, int buf) {
+    const uint16_t* base = vtp + max(key0, 0);     // V^T is zero padded to Lp = Nk * BS
     const uint32_t lv = lds0 + (uint32_t)((2 + buf) * C::TILE * 2 + wave * NR * 1024);
 #pragma unroll
     for (int i = 0; i < NR; ++i) dma16s(lv + i * 1024, base, voff[i]);
@@ -323,14 +346,14 @@ __global__ __launch_bounds__(AttnCfg<BS>::NT) void bsattn_kernel(AttnKArgs a) {
   // (row & 15); the group origin R0 is a multiple of 16 and the pair origin C0
   // is even, so the operand at (R0, C0) of a tile is at byte
   //   tile + R0 * 256 + (lane_off ^ (C0 << 4)),   lane_off = l32 * 256 + ((hi ^ (l32 & 15)) << 4).
-  // For V^T at BS = 64 an LDS row holds two d rows (d = 2 r + (chunk >> 3)):
+  // For V^T tiles of 64 keys an LDS row holds two d rows (d = 2 r + (chunk >> 3)):
   // the lane's d row dt * 32 + l32 sits in LDS row dt * 16 + (l32 >> 1), chunk
   // (l32 & 1) * 8 + C0 + hi.
   const uint32_t lane_off = (uint32_t)(l32 * 256 + ((hi ^ (l32 & 15)) << 4));
   const uint32_t lane_off_v =
-      BS == 128 ? lane_off
+      TK == 128 ? lane_off
                 : (uint32_t)((l32 >> 1) * 256 + (((((l32 & 1) << 3) | hi) ^ (l32 >> 1)) << 4));
-  constexpr int VROW = BS == 128 ? 32 * 256 : 16 * 256;   // bytes per 32 d rows of V^T
+  constexpr int VROW = TK == 128 ? 32 * 256 : 16 * 256;   // bytes per 32 d rows of V^T
 
   // Running max (per query row) is kept in the exp2 domain of raw scores
   // times sc; it is only raised (and O rescaled) when a new score exceeds it
@@ -362,17 +385,17 @@ __global__ __launch_bounds__(AttnCfg<BS>::NT) void bsattn_kernel(AttnKArgs a) {
     }
   };
   // whether any key of this wave's half of tile kb is visible to its queries
-  auto active_for = [&](int kb) {
-    const int kw0 = kb * BS + kbase;
-    return kb < Nk && kw0 < a.Lk && !(a.is_causal && kw0 > qw0 + 31 + off);
+  auto active_for = [&](int key0) {
+    const int kw0 = key0 + kbase;
+    return key0 >= 0 && kw0 < a.Lk && !(a.is_causal && kw0 > qw0 + 31 + off);
   };
 
   // Masking (diagonal / partial / invisible half tiles only) of the tile kb
   // whose scores are in s; the running max is taken later, beside the
   // exponentials of that tile.
-  auto mask_only = [&](int kb, f32x16_t* s) {
-    const int kw0 = kb * BS + kbase;
-    const bool act = active_for(kb);
+  auto mask_only = [&](int key0, f32x16_t* s) {
+    const int kw0 = key0 + kbase;
+    const bool act = active_for(key0);
     if (!act || (kw0 + C::KH > a.Lk) || (a.is_causal && kw0 + C::KH - 1 > qw0 + off)) {
       int lim = a.Lk - kw0 - hi * 4;
       if (a.is_causal) lim = min(lim, qrow + off - kw0 - hi * 4 + 1);
@@ -447,7 +470,7 @@ __global__ __launch_bounds__(AttnCfg<BS>::NT) void bsattn_kernel(AttnKArgs a) {
   // partial tiles only).
   f32x16_t sa[C::KT], sb[C::KT];
   V8 pa[C::KH / 16], pb[C::KH / 16];
-  int kb0 = 0, kb1 = 0, kb2 = 0;                   // blocks of tiles t, t+1, t+2
+  int kb0 = 0, kb1 = 0, kb2 = 0;                   // first keys of tiles t, t+1, t+2
   typedef std::integral_constant<bool, true> yes;
   typedef std::integral_constant<bool, false> no;
   auto iter = [&](int t, f32x16_t* s_next, f32x16_t* s_cur, V8* p_prev, V8* p_cur, auto hasS, auto hasPV,
@@ -455,7 +478,7 @@ __global__ __launch_bounds__(AttnCfg<BS>::NT) void bsattn_kernel(AttnKArgs a) {
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     if (t + 2 < cnt) {
-      kb2 = block_at(t + 2);
+      kb2 = key_of(t + 2);
       issue_k(kb2, t & 1);
     }
     if (t < cnt) issue_v(kb0, t & 1);
@@ -482,13 +505,13 @@ __global__ __launch_bounds__(AttnCfg<BS>::NT) void bsattn_kernel(AttnKArgs a) {
       // would hold its exponentials until the last one), the LDS operand
       // reads running four MFMAs ahead (measured best of 2, 3, 4, 6, 8).
       constexpr int NM = C::KT * (kD / 16) + (C::KH / 16) * (kD / 32);
-      constexpr int LA = 4;
+      constexpr int LA = FS_LA;
       __builtin_amdgcn_sched_group_barrier(0x100, LA, 0);        // DS reads
 #pragma unroll
       for (int i = 0; i < NM; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // MFMA
         if (i + LA < NM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);       // VALU
+        __builtin_amdgcn_sched_group_barrier(0x002, FS_VPM, 0);       // VALU
       }
     }
     if constexpr (decltype(hasE)::value) {
@@ -502,10 +525,10 @@ __global__ __launch_bounds__(AttnCfg<BS>::NT) void bsattn_kernel(AttnKArgs a) {
     kb1 = kb2;
   };
   if (cnt > 0) {
-    kb0 = block_at(0);
+    kb0 = key_of(0);
     issue_k(kb0, 0);
     if (cnt > 1) {
-      kb1 = block_at(1);
+      kb1 = key_of(1);
       issue_k(kb1, 1);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -533,30 +556,32 @@ __global__ __launch_bounds__(AttnCfg<BS>::NT) void bsattn_kernel(AttnKArgs a) {
       iter(t, sa, sb, pa, pb, no(), yes(), no());
     }
   }
-  __syncthreads();
-
-  // ---- merge the two key halves through LDS, normalise, store
-  float* red = reinterpret_cast<float*>(&lds[0][0][0]);   // [QW][PER][64]
+  // ---- merge the two key halves through LDS (split tiles), normalise, store
+  float f0 = 1.0f, f1 = 0.0f, l = l_run;
   constexpr int PER = (kD / 32) * 16 + 2;
-  if (kh == 1) {
-    float* dst = red + (size_t)qq * PER * 64;
+  const float* src = reinterpret_cast<const float*>(&lds[0][0][0]) + (size_t)qq * PER * 64;   // [QW][PER][64]
+  if constexpr (C::KG == 2) {
+    __syncthreads();
+    if (kh == 1) {
+      float* dst = reinterpret_cast<float*>(&lds[0][0][0]) + (size_t)qq * PER * 64;
 #pragma unroll
-    for (int dt = 0; dt < kD / 32; ++dt)
+      for (int dt = 0; dt < kD / 32; ++dt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) dst[(dt * 16 + r) * 64 + lane] = o[dt][r];
-    dst[(PER - 2) * 64 + lane] = m_run;
-    dst[(PER - 1) * 64 + lane] = l_run;
+        for (int r = 0; r < 16; ++r) dst[(dt * 16 + r) * 64 + lane] = o[dt][r];
+      dst[(PER - 2) * 64 + lane] = m_run;
+      dst[(PER - 1) * 64 + lane] = l_run;
+    }
+    __syncthreads();
+    if (kh == 1 || qrow >= a.Lq) return;
+    const float m1 = src[(PER - 2) * 64 + lane];
+    const float l1 = src[(PER - 1) * 64 + lane];
+    const float m = fmaxf(m_run, m1);
+    const float mu = m == -INFINITY ? 0.f : m;
+    f0 = __builtin_amdgcn_exp2f(m_run - mu);
+    f1 = __builtin_amdgcn_exp2f(m1 - mu);
+    l = l_run * f0 + l1 * f1;
   }
-  __syncthreads();
-  if (kh == 1 || qrow >= a.Lq) return;
-  const float* src = red + (size_t)qq * PER * 64;
-  const float m1 = src[(PER - 2) * 64 + lane];
-  const float l1 = src[(PER - 1) * 64 + lane];
-  const float m = fmaxf(m_run, m1);
-  const float mu = m == -INFINITY ? 0.f : m;
-  const float f0 = __builtin_amdgcn_exp2f(m_run - mu);
-  const float f1 = __builtin_amdgcn_exp2f(m1 - mu);
-  const float l = l_run * f0 + l1 * f1;
+  if (qrow >= a.Lq) return;
   const float inv = l > 0.f ? 1.0f / l : 0.f;
   uint16_t* op = a.out + b * a.o_sb + h * a.o_sh + (int64_t)qrow * a.o_sl;
 #pragma unroll
@@ -567,7 +592,9 @@ __global__ __launch_bounds__(AttnCfg<BS>::NT) void bsattn_kernel(AttnKArgs a) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int r = g4 * 4 + e;
-        v4[e] = (o[dt][r] * f0 + src[(dt * 16 + r) * 64 + lane] * f1) * inv;
+        float acc = o[dt][r] * f0;
+        if constexpr (C::KG == 2) acc += src[(dt * 16 + r) * 64 + lane] * f1;
+        v4[e] = acc * inv;
       }
       const int d0 = dt * 32 + g4 * 8 + hi * 4;
       uint2 w;
@@ -637,7 +664,7 @@ static size_t vt_bytes(const fs_attn_args& a) {
 }
 
 // order pass (block lists only) and the main kernel, reading V^T from the workspace
-template <int BS, typename T>
+template <int BS, int TK, typename T>
 static int launch_run(const fs_attn_args& a, int Nq, int Nk, hipStream_t s) {
   const int Lp = Nk * BS;
   const uint16_t* vt = static_cast<const uint16_t*>(a.work);
@@ -647,7 +674,7 @@ static int launch_run(const fs_attn_args& a, int Nq, int Nk, hipStream_t s) {
   // Scheduling units of `run` consecutive query blocks: at C2 (Nq = 1024) a
   // run of 16 halves the K/V bytes fetched beyond L2 (166 -> 83 GB) and
   // still leaves 2048 units for longest-first balance over 256 CUs.
-  const int run = min(16, max(1, Nq / 64));
+  const int run = min(FS_RUN, max(1, Nq / 64));
   if (a.blk_cnt) {
     int shift = 0;
     while (((run * Nk) >> shift) + 1 > kOrderMaxBins) ++shift;
@@ -674,7 +701,7 @@ static int launch_run(const fs_attn_args& a, int Nq, int Nk, hipStream_t s) {
   k.Nq = Nq; k.Nk = Nk; k.Lp = Lp; k.total = total; k.is_causal = a.is_causal;
   k.run = run;
   k.scale = a.softmax_scale;
-  bsattn_kernel<BS, T><<<grid, AttnCfg<BS>::NT, 0, s>>>(k);
+  bsattn_kernel<BS, TK, T><<<grid, AttnCfg<BS, TK>::NT, 0, s>>>(k);
   return fs_host::launch_status("fs_bsattn");
 }
 
@@ -733,9 +760,10 @@ extern "C" int fs_bsattn_run(const fs_attn_args* a, void* stream) {
   const int Nk = (a->Lk + a->bs - 1) / a->bs;
   hipStream_t s = (hipStream_t)stream;
   if (a->bs == 128) {
-    return a->dtype == FS_DTYPE_BF16 ? launch_run<128, bf16_t>(*a, Nq, Nk, s) : launch_run<128, f16_t>(*a, Nq, Nk, s);
+    return a->dtype == FS_DTYPE_BF16 ? launch_run<128, FS_TK, bf16_t>(*a, Nq, Nk, s)
+                                     : launch_run<128, FS_TK, f16_t>(*a, Nq, Nk, s);
   }
-  return a->dtype == FS_DTYPE_BF16 ? launch_run<64, bf16_t>(*a, Nq, Nk, s) : launch_run<64, f16_t>(*a, Nq, Nk, s);
+  return a->dtype == FS_DTYPE_BF16 ? launch_run<64, 64, bf16_t>(*a, Nq, Nk, s) : launch_run<64, 64, f16_t>(*a, Nq, Nk, s);
 }
 
 extern "C" int fs_bsattn(const fs_attn_args* a, void* stream) {
