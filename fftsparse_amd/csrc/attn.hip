@@ -11,15 +11,18 @@
 // ds_read_b128 from a row-major LDS tile.
 //
 // Main kernel: one workgroup per (batch, query head, query block of BS
-// tokens); BS/32 x 2 waves, two waves per SIMD so one wave's softmax runs
-// while the other's MFMAs issue.  Wave (qq, kh) owns query rows
-// qq*32 .. qq*32+31 of the block (Q held in registers as the B operand of
-// S^T = K Q^T) and key columns kh*BS/2 .. of every key tile (split-K inside
-// the workgroup: each wave keeps its own running max / sum / O^T, merged
-// through LDS at the end).  Per selected key block the workgroup copies
-// K [BS][D] and V^T [D][BS] into LDS with global_load_lds_dwordx4 (no
-// register staging); tiles are double-buffered, the copy of tile t+1 is in
-// flight while tile t is consumed.
+// tokens).  Keys are consumed in LDS tiles of TK keys: K [TK][D] and
+// V^T [D][TK] copied with global_load_lds_dwordx4 (no register staging),
+// double-buffered so the copies of the next tiles are in flight while one is
+// consumed.  Wave (qq, kh) owns query rows qq*32 .. qq*32+31 of the block (Q
+// held in registers as the B operand of S^T = K Q^T) and keys kh*TK/KG .. of
+// every tile, with its own running max / sum / O^T.
+//  - BS = 128 uses TK = 64: 4 waves, each over all 64 keys of a tile (no
+//    split), 64 KiB of LDS, so two workgroups share a CU and the two waves
+//    on a SIMD belong to independent workgroups (one's softmax or barrier
+//    wait overlaps the other's MFMAs).
+//  - BS = 64 uses TK = 64 split between two key groups (4 waves), merged
+//    through LDS at the end.
 // LDS rows are 256 B with the 16-byte chunk c of row r stored at c ^ (r & 15)
 // so the 8 lanes of a ds_read_b128 phase hit distinct banks.
 //
@@ -92,18 +95,6 @@ template <> struct MfmaOps<f16_t> {
 };
 
 constexpr int kD = 128;
-#ifndef FS_TK
-#define FS_TK 64
-#endif
-#ifndef FS_RUN
-#define FS_RUN 16
-#endif
-#ifndef FS_LA
-#define FS_LA 4
-#endif
-#ifndef FS_VPM
-#define FS_VPM 2
-#endif
 
 // position of key k inside its 16-key group in the V^T layout (an involution)
 __device__ __forceinline__ int vt_pos(int k) {
@@ -503,15 +494,15 @@ void bsattn_kernel(AttnKArgs a) {
       // Steady state: the scheduler interleaves one MFMA with two VALU
       // instructions (a wave issues in order, so MFMAs issued back to back
       // would hold its exponentials until the last one), the LDS operand
-      // reads running four MFMAs ahead (measured best of 2, 3, 4, 6, 8).
+      // reads running six MFMAs ahead (measured best of 2 .. 8).
       constexpr int NM = C::KT * (kD / 16) + (C::KH / 16) * (kD / 32);
-      constexpr int LA = FS_LA;
+      constexpr int LA = 6;
       __builtin_amdgcn_sched_group_barrier(0x100, LA, 0);        // DS reads
 #pragma unroll
       for (int i = 0; i < NM; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // MFMA
         if (i + LA < NM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, FS_VPM, 0);       // VALU
+        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);       // VALU
       }
     }
     if constexpr (decltype(hasE)::value) {
@@ -674,7 +665,7 @@ static int launch_run(const fs_attn_args& a, int Nq, int Nk, hipStream_t s) {
   // Scheduling units of `run` consecutive query blocks: at C2 (Nq = 1024) a
   // run of 16 halves the K/V bytes fetched beyond L2 (166 -> 83 GB) and
   // still leaves 2048 units for longest-first balance over 256 CUs.
-  const int run = min(FS_RUN, max(1, Nq / 64));
+  const int run = min(16, max(1, Nq / 64));
   if (a.blk_cnt) {
     int shift = 0;
     while (((run * Nk) >> shift) + 1 > kOrderMaxBins) ++shift;
@@ -760,8 +751,8 @@ extern "C" int fs_bsattn_run(const fs_attn_args* a, void* stream) {
   const int Nk = (a->Lk + a->bs - 1) / a->bs;
   hipStream_t s = (hipStream_t)stream;
   if (a->bs == 128) {
-    return a->dtype == FS_DTYPE_BF16 ? launch_run<128, FS_TK, bf16_t>(*a, Nq, Nk, s)
-                                     : launch_run<128, FS_TK, f16_t>(*a, Nq, Nk, s);
+    return a->dtype == FS_DTYPE_BF16 ? launch_run<128, 64, bf16_t>(*a, Nq, Nk, s)
+                                     : launch_run<128, 64, f16_t>(*a, Nq, Nk, s);
   }
   return a->dtype == FS_DTYPE_BF16 ? launch_run<64, 64, bf16_t>(*a, Nq, Nk, s) : launch_run<64, 64, f16_t>(*a, Nq, Nk, s);
 }
