@@ -245,7 +245,8 @@ def main():
         "data": f"synthetic (fftsparse_amd.synth recipe, seed {args.seed})",
         "config": {"workload": f"{cfg.name}: one layer, L={L}, Hq={Hq}, Hkv={Hk}, D={D}, block {bs}, "
                                f"corr_threshold {args.threshold}, production kwargs",
-                   "seq_len": L, "global_batch": 1, "parallelism": "none (1 GPU)"},
+                   "seq_len": L, "global_batch": 1, "block_size": bs, "corr_threshold": args.threshold,
+                   "parallelism": "none (1 GPU)"},
         "speedup_vs_dense": round(dense_ms / ms, 3) if dense_ms == dense_ms else None,
         "dense_ms": round(dense_ms, 3) if dense_ms == dense_ms else None,
         "dense": {k2: (round(v2, 3) if isinstance(v2, float) else v2) for k2, v2 in dense.items()},
