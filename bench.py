@@ -47,6 +47,8 @@ def parse():
                     help="KV-head groups of the selection pipeline (default: the library's choice)")
     ap.add_argument("--cpu-heads", type=int, default=2,
                     help="query heads (all their query blocks) timed for the CPU attention sample")
+    ap.add_argument("--c4-len", type=int, default=131072, help="config c4: prefill length")
+    ap.add_argument("--dense-steps", type=int, default=1, help="config c4: timed SDPA forwards")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (5 times) to calibrate "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE, then exit")
@@ -133,6 +135,8 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"copy_calib_bytes": n, "launches": 5}))
         return
+    if args.config == "c4":
+        return run_c4(args)
     import fftsparse_amd  # noqa: F401
     from fftsparse_amd import AttentionCall, block_sparse_attention, select_blocks
     from fftsparse_amd.synth import CONFIGS, make_config
@@ -275,6 +279,103 @@ def main():
         "input_gen_s": round(t_gen, 1),
     }
     print(json.dumps(line), flush=True)
+
+
+C4_METRIC = "end-to-end prefill ms, 32-layer random-init Llama-3.1-8B at 128K, attention share, 1 GPU"
+
+
+def run_c4(args):
+    """Config 4: a full 32-layer Llama-3.1-8B-shaped model (random init, bf16,
+    built on the GPU) prefilling 131072 random token ids, with the FFTSparse
+    prefill registered as the model's attention (fftsparse_amd.hf) in every
+    layer, then the same model on torch SDPA (flash) for the dense
+    comparison.  A step is one forward pass without KV cache that keeps the
+    last position's logits only.  The attention share is the sum of the
+    per-layer prefill call times (HIP events around each registered call)
+    over the forward time."""
+    import torch
+    from transformers import LlamaConfig, LlamaForCausalLM
+    import fftsparse_amd.hf as fh
+
+    L = args.c4_len
+    cfg = LlamaConfig(hidden_size=4096, intermediate_size=14336, num_hidden_layers=32, num_attention_heads=32,
+                      num_key_value_heads=8, head_dim=128, vocab_size=128256, max_position_embeddings=131072,
+                      rms_norm_eps=1e-5, tie_word_embeddings=False,
+                      rope_parameters={"rope_type": "llama3", "rope_theta": 500000.0, "factor": 8.0,
+                                       "low_freq_factor": 1.0, "high_freq_factor": 4.0,
+                                       "original_max_position_embeddings": 8192})
+    dev = torch.device("cuda:0")
+    t0 = time.perf_counter()
+    torch.manual_seed(args.seed)
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    with dev:
+        model = LlamaForCausalLM(cfg)
+    torch.set_default_dtype(prev)
+    model.eval()
+    n_params = sum(p.numel() for p in model.parameters())
+    g = torch.Generator().manual_seed(args.seed)
+    ids = torch.randint(0, cfg.vocab_size, (1, L), generator=g).to(dev)
+    torch.cuda.synchronize()
+    t_build = time.perf_counter() - t0
+    print(f"[c4] model built: {n_params / 1e9:.2f} B parameters, {t_build:.1f} s", file=sys.stderr, flush=True)
+
+    def forward():
+        with torch.no_grad():
+            return model(input_ids=ids, use_cache=False, logits_to_keep=1).logits
+
+    def timed(n):
+        out = []
+        for _ in range(n):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record()
+            logits = forward()
+            e1.record()
+            torch.cuda.synchronize()
+            out.append(e0.elapsed_time(e1))
+            print(f"[c4] forward ({model.config._attn_implementation}): {out[-1]:.1f} ms", file=sys.stderr, flush=True)
+        return out, logits
+
+    fh.patch_model(model, corr_threshold=args.threshold)
+    fh.record_prefill_events(False)
+    timed(args.warmup)
+    fh.record_prefill_events(True)
+    sparse_ms, logits = timed(args.steps)
+    ev = fh.prefill_events()
+    fh.record_prefill_events(False)
+    attn_total = sum(e.ms() for e in ev) / args.steps
+    per_layer = [0.0] * cfg.num_hidden_layers
+    density = [0.0] * cfg.num_hidden_layers
+    for e in ev:
+        per_layer[e.layer_idx] += e.ms() / args.steps
+        density[e.layer_idx] = e.density()
+    finite = bool(torch.isfinite(logits.float()).all())
+    ms = sum(sparse_ms) / len(sparse_ms)
+
+    dense_ms = float("nan")
+    if not args.no_dense:
+        model.set_attn_implementation("sdpa")
+        d, _ = timed(1 + args.dense_steps)
+        dense_ms = sum(d[1:]) / max(1, len(d) - 1) if len(d) > 1 else d[0]
+    line = {
+        "metric": C4_METRIC, "value": round(ms, 2), "unit": "ms", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 2), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": f"random-init weights (seed {args.seed}), random token ids",
+        "config": {"workload": f"c4: 32-layer Llama-3.1-8B shape ({n_params / 1e9:.2f} B parameters), "
+                               f"prefill of {L} tokens, FFTSparse prefill in every layer, "
+                               f"corr_threshold {args.threshold}, production kwargs",
+                   "seq_len": L, "global_batch": 1, "parallelism": "none (1 GPU)"},
+        "attention_ms": round(attn_total, 2), "attention_share": round(attn_total / ms, 4),
+        "non_attention_ms": round(ms - attn_total, 2),
+        "attention_ms_per_layer": [round(x, 3) for x in per_layer],
+        "density_per_layer": [round(x, 4) for x in density],
+        "dense_sdpa_ms": round(dense_ms, 2) if dense_ms == dense_ms else None,
+        "speedup_vs_dense_model": round(dense_ms / ms, 3) if dense_ms == dense_ms else None,
+        "logits_finite": finite, "build_s": round(t_build, 1),
+    }
+    print(json.dumps(line))
 
 
 if __name__ == "__main__":

@@ -352,27 +352,39 @@ def myattn_prefill(
     assert query_states.is_cuda, "input tensors must be on the GPU"   # :502
     bsz = query_states.shape[0]
     L_q = query_states.shape[2]
-    L_k = key_states.shape[2]
     H = query_states.shape[1]
+    o = v7_prefill(query_states, key_states, value_states, block_size=block_size, is_causal=is_causal,
+                   sink_ratio=sink_ratio, recent_ratio=recent_ratio, local_span_ratio=local_span_ratio,
+                   enable_correlation_mask=enable_correlation_mask,
+                   correlation_selection_mode=correlation_selection_mode,
+                   correlation_topk_ratio=correlation_topk_ratio, corr_threshold=corr_threshold,
+                   enable_column_mask=enable_column_mask, column_topk_ratio=column_topk_ratio,
+                   column_start_exclude_ratio=column_start_exclude_ratio,
+                   column_end_exclude_ratio=column_end_exclude_ratio,
+                   enable_last_block_mask=enable_last_block_mask,
+                   diag_sample_ratio=diag_sample_ratio, min_diag_samples=min_diag_samples,
+                   max_diag_samples=max_diag_samples, stripe_threshold=stripe_threshold,
+                   qk_topk_ratio=qk_topk_ratio)
+    return o.reshape(bsz, L_q, H * query_states.shape[3])
+
+
+def v7_prefill(query_states, key_states, value_states, *, block_size=128, is_causal=True, softmax_scale=None,
+               return_selection=False, **select_kw):
+    """The body of myattn_prefill (my_attn_v7.py:502-786) with the result left as [bsz, L_q, H, D]
+    and an optional softmax scale (default 1/sqrt(D), the reference's): dense causal attention
+    below 10 key blocks (:509-519), else v7 selection and block-sparse attention.  ``select_kw``
+    are select_blocks' keyword arguments.  With ``return_selection`` the result is (output,
+    BlockSelection or None for the dense path)."""
+    assert query_states.is_cuda, "input tensors must be on the GPU"   # :502
+    L_k = key_states.shape[2]
     if L_k < block_size * _MIN_BLOCKS:                                 # :509-519
-        o = block_sparse_attention(query_states, key_states, value_states,
-                                   block_size=block_size if block_size in (64, 128) else 128,
-                                   is_causal=True)
-        return o.reshape(bsz, L_q, -1)
+        out = block_sparse_attention(query_states, key_states, value_states,
+                                     block_size=block_size if block_size in (64, 128) else 128,
+                                     is_causal=True, softmax_scale=softmax_scale)
+        return (out, None) if return_selection else out
     if query_states.dtype not in (torch.bfloat16, torch.float16):
         raise RuntimeError("FlashAttention only supports fp16 and bf16 data type")
-    sel = select_blocks(query_states, key_states, block_size=block_size, sink_ratio=sink_ratio,
-                        recent_ratio=recent_ratio, local_span_ratio=local_span_ratio,
-                        enable_correlation_mask=enable_correlation_mask,
-                        correlation_selection_mode=correlation_selection_mode,
-                        correlation_topk_ratio=correlation_topk_ratio, corr_threshold=corr_threshold,
-                        enable_column_mask=enable_column_mask, column_topk_ratio=column_topk_ratio,
-                        column_start_exclude_ratio=column_start_exclude_ratio,
-                        column_end_exclude_ratio=column_end_exclude_ratio,
-                        enable_last_block_mask=enable_last_block_mask,
-                        diag_sample_ratio=diag_sample_ratio, min_diag_samples=min_diag_samples,
-                        max_diag_samples=max_diag_samples, stripe_threshold=stripe_threshold,
-                        qk_topk_ratio=qk_topk_ratio)
-    o = block_sparse_attention(query_states, key_states, value_states, sel.blk_cnt, sel.blk_idx,
-                               block_size=block_size, is_causal=is_causal)
-    return o.reshape(bsz, L_q, H * query_states.shape[3])
+    sel = select_blocks(query_states, key_states, block_size=block_size, **select_kw)
+    out = block_sparse_attention(query_states, key_states, value_states, sel.blk_cnt, sel.blk_idx,
+                                 block_size=block_size, is_causal=is_causal, softmax_scale=softmax_scale)
+    return (out, sel) if return_selection else out
