@@ -19,7 +19,7 @@ import torch  # noqa: F401  (must precede the library load, see module docstring
 LIB_PATH = Path(os.environ.get("FFTSPARSE_AMD_LIB") or Path(__file__).resolve().with_name("libfftsparse_amd.so"))
 
 FS_DTYPE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 
 class PoolArgs(ctypes.Structure):
@@ -33,7 +33,7 @@ class CorrArgs(ctypes.Structure):
     _fields_ = [("q_b", c_void_p), ("k_b", c_void_p),
                 ("dtype", c_int), ("Hq", c_int), ("Hk", c_int), ("N", c_int), ("D", c_int),
                 ("local_window", c_int), ("keep_sink", c_int), ("remote_start", c_int),
-                ("corr_threshold", c_float),
+                ("corr_threshold", c_float), ("corr_mode", c_int), ("corr_quantile", c_float),
                 ("work", c_void_p), ("corr", c_void_p), ("corr_sum", c_void_p), ("keep_tau", c_void_p)]
 
 
@@ -51,7 +51,7 @@ class ScoresArgs(ctypes.Structure):
     _fields_ = [("q_b", c_void_p), ("k_b", c_void_p),
                 ("dtype", c_int), ("Hq", c_int), ("Hk", c_int), ("N", c_int), ("D", c_int),
                 ("local_window", c_int), ("keep_sink", c_int), ("remote_start", c_int),
-                ("corr_threshold", c_float),
+                ("corr_threshold", c_float), ("corr_mode", c_int), ("corr_quantile", c_float),
                 ("corr", c_void_p), ("corr_sum", c_void_p), ("keep_tau", c_void_p),
                 ("sample_taus", c_void_p), ("n_samples", c_int),
                 ("col_start", c_int), ("col_end", c_int), ("n_cols", c_int),

@@ -117,8 +117,6 @@ def select_blocks(query_states: torch.Tensor, key_states: torch.Tensor, *, block
         # my_attn_v7.py:190-191 returns a single tensor there and the six-way
         # unpacking at :568 raises.
         raise ValueError("not enough values to unpack (expected 6, got 1)")
-    if p.corr_enabled and correlation_selection_mode == "topk":
-        raise NotImplementedError("correlation_selection_mode='topk' is not implemented on the GPU path yet")
     dev = q.device
     dt = _lib.FS_DTYPE[q.dtype]
     N, Nk = p.N, p.Nk
@@ -131,6 +129,8 @@ def select_blocks(query_states: torch.Tensor, key_states: torch.Tensor, *, block
     use_scores = (q.dtype in (torch.bfloat16, torch.float16) and D % 16 == 0 and D <= 128 and N <= 4096
                   and (p.corr_enabled or n_cols or last_k))
     thr = f32(corr_threshold)
+    corr_mode = 1 if correlation_selection_mode == "topk" else 0
+    corr_q = f32(1.0 - correlation_topk_ratio)                  # torch.quantile's q in fp32 (:200-201)
     sel = BlockSelection(params=p,
                          blk_cnt=torch.empty(Hq, N, dtype=torch.int32, device=dev),
                          blk_idx=torch.empty(Hq, N, Nk, dtype=torch.uint16, device=dev))
@@ -193,7 +193,8 @@ def select_blocks(query_states: torch.Tensor, key_states: torch.Tensor, *, block
                 _lib.call("fs_scores", ScoresArgs(
                     q_b=ptr(q_b), k_b=ptr(k_b), dtype=dt, Hq=hq, Hk=hk, N=N, D=D,
                     local_window=p.local_window, keep_sink=p.keep_sink, remote_start=p.remote_start,
-                    corr_threshold=thr, corr=ptr(sl(sel.corr, h0, h1)), corr_sum=ptr(sl(sel.corr_sum, h0, h1)),
+                    corr_threshold=thr, corr_mode=corr_mode, corr_quantile=corr_q,
+                    corr=ptr(sl(sel.corr, h0, h1)), corr_sum=ptr(sl(sel.corr_sum, h0, h1)),
                     keep_tau=ptr(sl(sel.keep_tau, h0, h1)), sample_taus=taus.data_ptr(), n_samples=n_samples,
                     col_start=p.col_start, col_end=p.col_end, n_cols=n_cols, last_k=last_k,
                     diag_var=ptr(sl(sel.diag_var, h0, h1)), col_mean=ptr(sl(sel.col_mean, h0, h1)),
@@ -204,7 +205,8 @@ def select_blocks(query_states: torch.Tensor, key_states: torch.Tensor, *, block
                     _lib.call("fs_corr", CorrArgs(
                         q_b=ptr(q_b), k_b=ptr(k_b), dtype=dt, Hq=hq, Hk=hk, N=N, D=D,
                         local_window=p.local_window, keep_sink=p.keep_sink, remote_start=p.remote_start,
-                        corr_threshold=thr, work=works[g].data_ptr(), corr=ptr(sl(sel.corr, h0, h1)),
+                        corr_threshold=thr, corr_mode=corr_mode, corr_quantile=corr_q,
+                        work=works[g].data_ptr(), corr=ptr(sl(sel.corr, h0, h1)),
                         corr_sum=ptr(sl(sel.corr_sum, h0, h1)), keep_tau=ptr(sl(sel.keep_tau, h0, h1))))
                 if n_samples or n_cols or last_k:
                     _lib.call("fs_stats", StatsArgs(

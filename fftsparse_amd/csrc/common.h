@@ -129,14 +129,10 @@ __device__ __forceinline__ float key_to_f32(uint32_t key) {
 // then ranked in index order by wave 0 with ballots.  hist needs kTopkScratch
 // ints; all threads of the block must call.
 constexpr int kTopkScratch = 256 + 2;
-__device__ inline float block_topk_select(const float* vals, int n, int k, uint8_t* sel, int* hist) {
+// Order-preserving key of the k-th largest of vals[0..n), 1 <= k <= n (radix
+// select, 8 bits per pass from the top).  All threads of the block must call.
+__device__ inline uint32_t block_kth_key(const float* vals, int n, int k, int* hist) {
   const int tid = threadIdx.x, nt = blockDim.x;
-  if (k > n) k = n;
-  if (k <= 0) {
-    for (int i = tid; i < n; i += nt) sel[i] = 0;
-    __syncthreads();
-    return NAN;
-  }
   uint32_t prefix = 0, mask = 0;
   int kk = k;                                      // rank wanted among keys matching prefix under mask
   for (int shift = 24; shift >= 0; shift -= 8) {
@@ -173,6 +169,18 @@ __device__ inline float block_topk_select(const float* vals, int n, int k, uint8
     kk = hist[257];
     __syncthreads();
   }
+  return prefix;
+}
+
+__device__ inline float block_topk_select(const float* vals, int n, int k, uint8_t* sel, int* hist) {
+  const int tid = threadIdx.x, nt = blockDim.x;
+  if (k > n) k = n;
+  if (k <= 0) {
+    for (int i = tid; i < n; i += nt) sel[i] = 0;
+    __syncthreads();
+    return NAN;
+  }
+  const uint32_t prefix = block_kth_key(vals, n, k, hist);
   int gt = 0;
   for (int i = tid; i < n; i += nt) {
     const bool g = order_key(vals[i]) > prefix;
@@ -193,6 +201,19 @@ __device__ inline float block_topk_select(const float* vals, int n, int k, uint8
   }
   __syncthreads();
   return key_to_f32(prefix);
+}
+
+// torch.quantile(vals[0..n), q) with linear interpolation (n >= 1): the fp32
+// rank q (n - 1), the order statistics at its floor and ceiling, and torch's
+// two-sided lerp between them.  All threads of the block must call.
+__device__ inline float block_quantile(const float* vals, int n, float q, int* hist) {
+  const float rank = q * (float)(n - 1);
+  const int lo = (int)rank, hi = (int)ceilf(rank);
+  const float w = rank - (float)lo;
+  const float below = key_to_f32(block_kth_key(vals, n, n - lo, hist));     // ascending index lo
+  const float above = hi == lo ? below : key_to_f32(block_kth_key(vals, n, n - hi, hist));
+  const float d = above - below;
+  return fabsf(w) < 0.5f ? below + w * d : above - d * (1.0f - w);
 }
 
 // Partial dot product of two rows of D elements (D * sizeof(T) a multiple of

@@ -145,6 +145,7 @@ __global__ __launch_bounds__(kFftThreads) void corr_final_kernel(fs_corr_args a,
   float2* tw = smem + M;
   float* cv = reinterpret_cast<float*>(smem + M + M / 2);
   __shared__ float red[32];
+  __shared__ int ired[kTopkScratch];
   const int h = blockIdx.x, tid = threadIdx.x, N = a.N;
   const int nb = M / 2 + 1;
   fill_twiddles(tw, M);
@@ -190,13 +191,19 @@ __global__ __launch_bounds__(kFftThreads) void corr_final_kernel(fs_corr_args a,
     __syncthreads();
   }
   for (int t = tid; t < N; t += kFftThreads) a.corr[(int64_t)h * N + t] = cv[t];
-  // :193-208: threshold on the max-normalised remote lags
   const int rs = a.remote_start;
-  float mx = -INFINITY;
-  for (int t = rs + tid; t < N; t += kFftThreads) mx = fmaxf(mx, cv[t]);
-  mx = clamp_min_nan(block_max(mx, red), 1e-6f);
-  for (int t = tid; t < N; t += kFftThreads)
-    a.keep_tau[(int64_t)h * N + t] = (t >= rs && cv[t] / mx >= a.corr_threshold) ? 1 : 0;
+  if (a.corr_mode == 1) {
+    // :196-203 ("topk"): the quantile of the remote lags
+    const float qv = block_quantile(cv + rs, N - rs, a.corr_quantile, ired);
+    for (int t = tid; t < N; t += kFftThreads) a.keep_tau[(int64_t)h * N + t] = (t >= rs && cv[t] >= qv) ? 1 : 0;
+  } else {
+    // :205-208 ("threshold"): threshold on the max-normalised remote lags
+    float mx = -INFINITY;
+    for (int t = rs + tid; t < N; t += kFftThreads) mx = fmaxf(mx, cv[t]);
+    mx = clamp_min_nan(block_max(mx, red), 1e-6f);
+    for (int t = tid; t < N; t += kFftThreads)
+      a.keep_tau[(int64_t)h * N + t] = (t >= rs && cv[t] / mx >= a.corr_threshold) ? 1 : 0;
+  }
 }
 
 template <typename T>
@@ -239,6 +246,9 @@ extern "C" int fs_corr(const fs_corr_args* a, void* stream) {
                a->Hq, a->Hk);
   FS_CHECK_ARG(a->N >= 1 && a->D >= 1, "fs_corr: bad sizes");
   FS_CHECK_ARG(a->remote_start >= 0 && a->local_window >= 0, "fs_corr: bad lag parameters");
+  FS_CHECK_ARG(a->corr_mode == 0 || (a->corr_mode == 1 && a->remote_start < a->N && a->corr_quantile >= 0.f &&
+                                     a->corr_quantile <= 1.f),
+               "fs_corr: corr_mode must be 0 or 1; topk mode needs remote_start < N and a quantile in [0, 1]");
   const int logM = corr_logM(a->N);
   FS_CHECK_SUPPORTED(logM <= kMaxLogM, "fs_corr: N=%d exceeds the LDS FFT limit (N <= %d)", a->N,
                      1 << (kMaxLogM - 1));

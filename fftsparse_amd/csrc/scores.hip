@@ -226,11 +226,16 @@ __global__ __launch_bounds__(kFinalThreads) void scores_final_kernel(fs_scores_a
     }
     for (int t = tid; t < N; t += kFinalThreads) a.corr[(int64_t)h * N + t] = cv[t];
     const int rs = a.remote_start;
-    float mx = -INFINITY;
-    for (int t = rs + tid; t < N; t += kFinalThreads) mx = fmaxf(mx, cv[t]);
-    mx = clamp_min_nan(block_max(mx, red), 1e-6f);
-    for (int t = tid; t < N; t += kFinalThreads)
-      a.keep_tau[(int64_t)h * N + t] = (t >= rs && cv[t] / mx >= a.corr_threshold) ? 1 : 0;
+    if (a.corr_mode == 1) {                       // "topk": quantile of the remote lags (:196-203)
+      const float qv = block_quantile(cv + rs, N - rs, a.corr_quantile, ired);
+      for (int t = tid; t < N; t += kFinalThreads) a.keep_tau[(int64_t)h * N + t] = (t >= rs && cv[t] >= qv) ? 1 : 0;
+    } else {                                      // "threshold" (:205-208)
+      float mx = -INFINITY;
+      for (int t = rs + tid; t < N; t += kFinalThreads) mx = fmaxf(mx, cv[t]);
+      mx = clamp_min_nan(block_max(mx, red), 1e-6f);
+      for (int t = tid; t < N; t += kFinalThreads)
+        a.keep_tau[(int64_t)h * N + t] = (t >= rs && cv[t] / mx >= a.corr_threshold) ? 1 : 0;
+    }
   }
 
   // ---- diagonal statistics, one wave per sample, jobs 4 .. 4+kDiagJobs-1 (:342-349)
@@ -330,6 +335,9 @@ extern "C" int fs_scores(const fs_scores_args* a, void* stream) {
   FS_CHECK_ARG(((uintptr_t)a->q_b % 16) == 0 && ((uintptr_t)a->k_b % 16) == 0, "fs_scores: unaligned pooled tensors");
   FS_CHECK_ARG(a->keep_tau == nullptr || (a->corr && a->remote_start >= 0 && a->local_window >= 0),
                "fs_scores: bad correlation arguments");
+  FS_CHECK_ARG(a->keep_tau == nullptr || a->corr_mode == 0 ||
+                   (a->corr_mode == 1 && a->remote_start < a->N && a->corr_quantile >= 0.f && a->corr_quantile <= 1.f),
+               "fs_scores: corr_mode must be 0 or 1; topk mode needs remote_start < N and a quantile in [0, 1]");
   FS_CHECK_ARG(a->n_samples >= 0 && (a->n_samples == 0 || (a->sample_taus && a->diag_var)),
                "fs_scores: sample arrays missing");
   FS_CHECK_ARG(a->n_cols <= 0 || (a->col_sel && a->col_start >= 0 && a->col_end <= a->N &&

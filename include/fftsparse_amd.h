@@ -67,14 +67,18 @@ FS_API int fs_pool(const fs_pool_args* a, void* stream);
  * For query head h (key head h / (Hq/Hk)):
  *   corr_sum[h][t] = sum_i <q_b[h][i], k_b[hk][i-t]>  via zero-padded FFTs,
  *   corr[h][t]     = post-processed value (my_attn_v7.py:134-155),
- *   keep_tau[h][t] = 1 iff t >= remote_start and
- *                    corr[h][t] / max(max_{t'>=rs} corr[h][t'], 1e-6) >= corr_threshold.
+ *   keep_tau[h][t] = 1 iff t >= remote_start and, by corr_mode,
+ *     0 "threshold" (:205-208): corr[h][t] / max(max_{t'>=rs} corr[h][t'], 1e-6) >= corr_threshold;
+ *     1 "topk" (:196-203): corr[h][t] >= the corr_quantile quantile of corr[h][rs..N-1]
+ *       (torch.quantile, linear interpolation; corr_quantile = 1 - correlation_topk_ratio in fp32).
  * work: fs_corr_work_bytes(Hq, N, D) bytes of device scratch. */
 typedef struct {
   const void* q_b; const void* k_b;
   int dtype, Hq, Hk, N, D;
   int local_window, keep_sink, remote_start;
   float corr_threshold;
+  int corr_mode;        /* 0 threshold, 1 topk */
+  float corr_quantile;  /* topk mode */
   void* work;
   float* corr;          /* [Hq][N] */
   float* corr_sum;      /* [Hq][N] */
@@ -123,6 +127,8 @@ typedef struct {
   int dtype, Hq, Hk, N, D;
   int local_window, keep_sink, remote_start;
   float corr_threshold;
+  int corr_mode;         /* 0 threshold, 1 topk (as in fs_corr_args) */
+  float corr_quantile;
   float* corr;           /* [Hq][N] */
   float* corr_sum;       /* [Hq][N] or NULL */
   uint8_t* keep_tau;     /* [Hq][N] or NULL */

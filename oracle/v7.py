@@ -20,6 +20,8 @@ Parity pins (what checks each function against something other than itself):
   fft_lag_correlation      -- brute-force diagonal sums of Q_b K_b^T (O(N^2 D));
                               post-processing checked on hand-built inputs
   correlation_keep         -- closed form (threshold of max-normalised values)
+  correlation_keep_topk    -- hand-computed linear-interpolation quantiles and
+                              numpy.quantile (the "topk" selection mode)
   block_scores             -- numpy float64 GEMM
   stripe_variance          -- numpy unbiased variance on torch.diagonal slices;
                               constant / linear diagonals (closed forms)

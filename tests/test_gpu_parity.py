@@ -128,6 +128,8 @@ SEL_CASES = [
     ("c0-nocol-nolast", dict(enable_column_mask=False, enable_last_block_mask=False)),
     ("c0-defaults", "defaults"),
     ("c0-T0.95", dict(corr_threshold=0.95)),
+    ("c0-topk", dict(correlation_selection_mode="topk")),
+    ("c0-topk-0.05", dict(correlation_selection_mode="topk", correlation_topk_ratio=0.05)),
 ]
 
 
@@ -152,6 +154,8 @@ def test_selection_parity_c0(name, over):
     (32768, 8, 2, 128, torch.bfloat16, dict(stripe_threshold=0.0)),
     (24000, 7, 1, 64, torch.bfloat16, {}),                       # ragged L, bs 64, GQA 7
     (16384, 4, 4, 128, torch.float16, dict(corr_threshold=0.5)),
+    (32768, 8, 2, 128, torch.bfloat16, dict(correlation_selection_mode="topk")),
+    (24000, 7, 1, 64, torch.bfloat16, dict(correlation_selection_mode="topk", correlation_topk_ratio=0.3)),
 ])
 def test_selection_parity_bf16(L, Hq, Hk, bs, dtype, over):
     _print_case("selection", L=L, Hq=Hq, Hk=Hk, bs=bs, dtype=dtype, over=over)
@@ -162,6 +166,26 @@ def test_selection_parity_bf16(L, Hq, Hk, bs, dtype, over):
     frac, exact, unexc = block_match(sel.dense_mask(), ref.mask, ref.excusable)
     print(f"  match={frac:.6f} exact={exact:.6f} unexcused={unexc}")
     assert frac >= MATCH_MIN
+
+
+@pytest.mark.parametrize("dtype,ratio", [(torch.float32, 0.2), (torch.bfloat16, 0.2), (torch.bfloat16, 0.01),
+                                         (torch.bfloat16, 0.999)])
+def test_topk_lag_keep_matches_quantile_of_own_corr(dtype, ratio):
+    """The "topk" lag selection (my_attn_v7.py:196-203) applied by the kernel
+    to its own corr values equals torch.quantile's selection on the same
+    values, up to values within 1e-6 of the quantile (the lerp's rounding)."""
+    _print_case("topk keep", dtype=dtype, ratio=ratio)
+    q, k, _ = make_qkv(16384, 8, 2, dtype=dtype, seed=6)
+    kw = {**PROD, "correlation_selection_mode": "topk", "correlation_topk_ratio": ratio}
+    sel = select_blocks(*_gpu(q, k), keep_intermediates=True, **kw)
+    corr = sel.corr.cpu()
+    rs = sel.params.remote_start
+    keep_ref, qv = v7.correlation_keep_topk(corr, rs, ratio)
+    keep = sel.keep_tau.cpu().bool()
+    near = (corr - qv[:, None]).abs() <= 1e-6 * qv.abs()[:, None]
+    assert not ((keep != keep_ref) & ~near).any()
+    assert not keep[:, :rs].any()
+    assert (keep.sum(-1) >= 1).all()
 
 
 def test_block_lists_are_ascending_and_deterministic():

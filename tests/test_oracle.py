@@ -160,6 +160,29 @@ def test_stripe_variance_matches_numpy_on_random_scores():
 
 
 # --------------------------------------------------------------------------- top-k selections
+def test_correlation_keep_topk_closed_forms():
+    """my_attn_v7.py:196-203: keep lags >= torch.quantile(corr[rs:], 1 - ratio),
+    linear interpolation.  Pinned by hand-computed quantiles and by numpy."""
+    corr = torch.tensor([[9.0, 9.0, 0.0, 1.0, 2.0, 3.0, 4.0]])      # remote lags 0..4 (rs = 2)
+    keep, q = v7.correlation_keep_topk(corr, 2, 0.2)                   # rank 0.8 * 4 = 3.2 -> 3.2
+    assert abs(float(q) - 3.2) < 1e-6
+    assert keep.tolist() == [[False, False, False, False, False, False, True]]
+    keep, q = v7.correlation_keep_topk(corr, 2, 0.5)                   # rank 2 -> the median, 2
+    assert float(q) == 2.0 and keep.tolist() == [[False, False, False, False, True, True, True]]
+    keep, q = v7.correlation_keep_topk(corr, 2, 1.0)                   # q = 0: the minimum, all kept
+    assert float(q) == 0.0 and keep[0, 2:].all() and not keep[0, :2].any()
+    keep, q = v7.correlation_keep_topk(torch.full((1, 6), 5.0), 1, 0.3)  # all equal: all kept
+    assert float(q) == 5.0 and keep[0, 1:].all()
+    g = torch.Generator().manual_seed(0)
+    c = torch.randn(4, 300, generator=g)
+    for ratio in (0.2, 0.05, 0.37):
+        keep, q = v7.correlation_keep_topk(c, 11, ratio)
+        ref = np.quantile(c[:, 11:].double().numpy(), 1 - ratio, axis=-1)
+        assert np.allclose(q.double().numpy(), ref, rtol=1e-6, atol=1e-6)
+        for h in range(4):
+            assert keep[h].sum() == int((c[h, 11:] >= q[h]).sum())
+
+
 def test_qk_topk_rows_brute_force():
     S = _rand(2, 40, 40)
     mask, kth = v7.qk_topk_rows(S, 0.3)
