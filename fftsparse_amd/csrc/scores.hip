@@ -98,6 +98,10 @@ __global__ __launch_bounds__(kScoreThreads) void scores_kernel(fs_scores_args a,
   for (int st = 0; st < kMaxSteps; ++st)
     qv[st] = (qok && st < D / 16) ? *reinterpret_cast<const uint4*>(qrow + st * 16) : make_uint4(0, 0, 0, 0);
   const int cpr = D / 8;                           // 16-byte chunks per row
+  // K rows are stored with 16-byte chunk c of row r at c ^ (r & sw): the 32
+  // lanes of an MFMA operand read take one row each, and without the swizzle
+  // every row's chunk would sit in the same banks
+  const int sw = (cpr & (cpr - 1)) == 0 ? cpr - 1 : 0;
   constexpr int kMaxChunks = kScoreTile * (128 / 8) / kScoreThreads;   // per thread, D <= 128
   uint4 kv[kMaxChunks];
 #pragma unroll
@@ -113,7 +117,7 @@ __global__ __launch_bounds__(kScoreThreads) void scores_kernel(fs_scores_args a,
 #pragma unroll
   for (int u = 0; u < kMaxChunks; ++u) {
     const int c = tid + u * kScoreThreads, r = c / cpr, cc = c - r * cpr;
-    if (c < kScoreTile * cpr) *reinterpret_cast<uint4*>(kt + r * D + cc * 8) = kv[u];
+    if (c < kScoreTile * cpr) *reinterpret_cast<uint4*>(kt + r * D + ((cc ^ (r & sw)) * 8)) = kv[u];
   }
   __syncthreads();
 #pragma unroll
@@ -122,7 +126,8 @@ __global__ __launch_bounds__(kScoreThreads) void scores_kernel(fs_scores_args a,
     const uint4 av = qv[st];
 #pragma unroll
     for (int jt = 0; jt < 4; ++jt) {
-      const uint4 bv = *reinterpret_cast<const uint4*>(kt + (jt * 32 + l32) * D + st * 16 + hi * 8);
+      const int kr = jt * 32 + l32;
+      const uint4 bv = *reinterpret_cast<const uint4*>(kt + kr * D + (((2 * st + hi) ^ (kr & sw)) * 8));
       acc[jt] = ScoreMma<T>::mma(av, bv, acc[jt]);
     }
   }
