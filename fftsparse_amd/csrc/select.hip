@@ -46,6 +46,37 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(fs_select_args a, i
   const int r0 = (blockIdx.x - h * chunks) * RPW;
   const int hk = h / (a.Hq / a.Hk);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int NW = (Nk + 63) >> 6;                   // 64-block words per row
+  const bool words = !DIFF && NW <= kMaxWords;     // word-parallel rows (below)
+
+  // The word-parallel path stages the head's lag / column / last-row flags.
+  // Their loads are issued here, before the decision's, so that one wait
+  // covers both: flag bytes j = 4 w .. 4 w + 3 of word w = tid + 256 u.
+  constexpr int kFlagWords = 4096 / 4 / kSelThreads;
+  uint32_t fkr[kFlagWords], fcr[kFlagWords], flr[kFlagWords];
+  const int nw4 = (N + 3) >> 2;
+  if (words) {
+    const int64_t hb = (int64_t)h * N;
+    const bool v4 = (N & 3) == 0;                  // row starts 4-byte aligned (buffers are)
+#pragma unroll
+    for (int u = 0; u < kFlagWords; ++u) {
+      const int w4 = tid + u * kSelThreads;
+      fkr[u] = fcr[u] = flr[u] = 0;
+      if (w4 >= nw4) continue;
+      if (v4) {
+        if (a.keep_tau) fkr[u] = reinterpret_cast<const uint32_t*>(a.keep_tau + hb)[w4];
+        if (a.col_sel) fcr[u] = reinterpret_cast<const uint32_t*>(a.col_sel + hb)[w4];
+        if (a.last_sel) flr[u] = reinterpret_cast<const uint32_t*>(a.last_sel + hb)[w4];
+      } else {
+        for (int b = 0; b < 4 && 4 * w4 + b < N; ++b) {
+          const int64_t j = hb + 4 * w4 + b;
+          if (a.keep_tau) fkr[u] |= (uint32_t)a.keep_tau[j] << (8 * b);
+          if (a.col_sel) fcr[u] |= (uint32_t)a.col_sel[j] << (8 * b);
+          if (a.last_sel) flr[u] |= (uint32_t)a.last_sel[j] << (8 * b);
+        }
+      }
+    }
+  }
 
   // ---- stripe / diffuse decision (:359-363); identical in every workgroup of the head
   bool stripe = false;
@@ -103,22 +134,33 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(fs_select_args a, i
 
   const int lw = a.local_window;
   const bool has_last = a.last_sel != nullptr;
-  const int NW = (Nk + 63) >> 6;                   // 64-block words per row
-  if (!DIFF && NW <= kMaxWords) {
+  if (words) {
     // ---- word-parallel rows: lane (row g, word w) builds the membership of
     // blocks 64w .. 64w+63 of its row as a 64-bit mask from per-head masks
     // staged in LDS, then writes its set bits at the offset given by the
     // popcounts of the lower words.
     __shared__ uint64_t rkw[2 * kMaxWords + 2];  // bit x: keep_tau[N-1-x] (x < N), 0 beyond
     __shared__ uint64_t colw[kMaxWords], lastw[kMaxWords];
+    __shared__ uint32_t fk[4096 / 4], fc[4096 / 4], fl[4096 / 4];   // the staged flag bytes
+#pragma unroll
+    for (int u = 0; u < kFlagWords; ++u) {
+      const int w4 = tid + u * kSelThreads;
+      if (w4 < nw4) {
+        fk[w4] = fkr[u];
+        fc[w4] = fcr[u];
+        fl[w4] = flr[u];
+      }
+    }
+    __syncthreads();
+    auto flag = [](const uint32_t* f, int j) { return ((f[j >> 2] >> (8 * (j & 3))) & 255u) != 0; };
     for (int q = wave; q < 2 * NW + 2; q += kSelWaves) {
       const int x = 64 * q + lane;
-      const bool kb = use_lags && x < N && a.keep_tau[(int64_t)h * N + (N - 1 - x)];
+      const bool kb = use_lags && x < N && flag(fk, N - 1 - x);
       const uint64_t m = __ballot(kb);
       if (lane == 0) rkw[q] = m;
       if (q < NW) {
-        const bool cb = use_cols && x < N && a.col_sel[(int64_t)h * N + x];
-        const bool lb = has_last && x < N && a.last_sel[(int64_t)h * N + x];
+        const bool cb = use_cols && x < N && flag(fc, x);
+        const bool lb = has_last && x < N && flag(fl, x);
         const uint64_t mc = __ballot(cb), ml = __ballot(lb);
         if (lane == 0) {
           colw[q] = mc;
