@@ -466,6 +466,9 @@ void bsattn_kernel(AttnKArgs a) {
   typedef std::integral_constant<bool, false> no;
   auto iter = [&](int t, f32x16_t* s_next, f32x16_t* s_cur, V8* p_prev, V8* p_cur, auto hasS, auto hasPV,
                   auto hasE) {
+    // a wave waiting here yields issue priority to the other workgroup's
+    // wave on its SIMD, which is in its MFMA block (priority raised below)
+    __builtin_amdgcn_s_setprio(0);
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     if (t + 2 < cnt) {
@@ -473,6 +476,7 @@ void bsattn_kernel(AttnKArgs a) {
       issue_k(kb2, t & 1);
     }
     if (t < cnt) issue_v(kb0, t & 1);
+    __builtin_amdgcn_s_setprio(2);
     // The row max of tile t, the raise of the running max and the
     // exponentials of tile t are VALU work independent of the MFMAs of S(t+1)
     // and P V(t-1), so all of it goes into the interleaved block; only the
