@@ -64,6 +64,9 @@ class BlockSelection:
         return int(self.blk_cnt.sum().item())
 
 
+# largest block count of the selection kernels (LDS FFT length 8192, 64 membership words per row)
+MAX_SELECT_BLOCKS = 4096
+
 _tau_cache: dict = {}
 
 
@@ -113,6 +116,9 @@ def select_blocks(query_states: torch.Tensor, key_states: torch.Tensor, *, block
                enable_correlation_mask, correlation_topk_ratio, enable_column_mask,
                column_topk_ratio, column_start_exclude_ratio, column_end_exclude_ratio,
                enable_last_block_mask, diag_sample_ratio, min_diag_samples, max_diag_samples)
+    if p.N > MAX_SELECT_BLOCKS:
+        raise RuntimeError(f"{p.N} query blocks (L={L_q}, block_size={block_size}) exceed the selection "
+                           f"kernels' maximum of {MAX_SELECT_BLOCKS}")
     if p.corr_enabled and p.remote_start >= p.N:
         # my_attn_v7.py:190-191 returns a single tensor there and the six-way
         # unpacking at :568 raises.

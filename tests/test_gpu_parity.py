@@ -355,3 +355,43 @@ def test_full_length_c2_properties():
         for i in (0, 511, 1023):
             row = idx[h, i, : cnt[h, i]]
             assert int(row[0]) == 0 and int(row[-1]) == i and bool((row[1:] > row[:-1]).all())
+
+
+def test_maximum_block_count_properties():
+    """The largest supported selection, N = 4096 blocks (L = 524288 at block
+    128): every row's list ascending, causal, with the sink block and the
+    diagonal; selection deterministic; attention output finite."""
+    _print_case("max-blocks", L=4096 * 128, Hq=2, Hk=1)
+    g = torch.Generator(device=DEV).manual_seed(12)
+    L, Hq, Hk = 4096 * 128, 2, 1
+    q = torch.randn(1, Hq, L, 128, device=DEV, generator=g, dtype=torch.bfloat16)
+    k = torch.randn(1, Hk, L, 128, device=DEV, generator=g, dtype=torch.bfloat16)
+    v = torch.randn(1, Hk, L, 128, device=DEV, generator=g, dtype=torch.bfloat16)
+    k[:, :, :4] *= 6
+    sel = select_blocks(q, k, **PROD)
+    sel2 = select_blocks(q, k, **PROD)
+    torch.cuda.synchronize()
+    assert sel.params.N == 4096
+    assert torch.equal(sel.blk_cnt, sel2.blk_cnt)
+    cnt = sel.blk_cnt.cpu()
+    assert bool((cnt >= 1).all()) and bool((cnt <= torch.arange(1, 4097)[None, :]).all())
+    idx = sel.blk_idx.view(torch.int16).cpu().to(torch.int64) & 0xFFFF
+    for h in range(Hq):
+        for i in (0, 1, 2047, 4094, 4095):
+            row = idx[h, i, : cnt[h, i]]
+            assert int(row[0]) == 0 and int(row[-1]) == i and bool((row[1:] > row[:-1]).all())
+    assert torch.equal(sel.dense_mask(), sel2.dense_mask())
+    out = block_sparse_attention(q, k, v, sel.blk_cnt, sel.blk_idx)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out.float()).all())
+
+
+def test_block_count_above_the_limit_is_rejected():
+    """N = 4097 blocks is past the selection kernels' limit: a clear error, no launch."""
+    _print_case("over-limit", L=4097 * 128)
+    L = 4097 * 128
+    q = torch.zeros(1, 1, L, 128, device=DEV, dtype=torch.bfloat16)
+    k = torch.zeros(1, 1, L, 128, device=DEV, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="exceed the selection kernels' maximum of 4096"):
+        select_blocks(q, k, **PROD)
+        torch.cuda.synchronize()
