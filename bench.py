@@ -49,6 +49,11 @@ def parse():
                     help="query heads (all their query blocks) timed for the CPU attention sample")
     ap.add_argument("--c4-len", type=int, default=131072, help="config c4: prefill length")
     ap.add_argument("--dense-steps", type=int, default=1, help="config c4: timed SDPA forwards")
+    ap.add_argument("--c4-rope", choices=("fused", "model"), default="fused",
+                    help="config c4: rotary embedding fused with the block pooling (fs_rope_pool, default) "
+                         "or the model's own RoPE before the registered attention")
+    ap.add_argument("--c4-compare-rope", action="store_true",
+                    help="config c4: also time the other --c4-rope variant (same steps)")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (5 times) to calibrate "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE, then exit")
@@ -291,8 +296,9 @@ def run_c4(args):
     layer, then the same model on torch SDPA (flash) for the dense
     comparison.  A step is one forward pass without KV cache that keeps the
     last position's logits only.  The attention share is the sum of the
-    per-layer prefill call times (HIP events around each registered call)
-    over the forward time."""
+    per-layer prefill call times (HIP events around each registered call;
+    with the fused RoPE, around the rotary embedding + pooling pass and the
+    attention) over the forward time."""
     import torch
     from transformers import LlamaConfig, LlamaForCausalLM
     import fftsparse_amd.hf as fh
@@ -337,13 +343,21 @@ def run_c4(args):
             print(f"[c4] forward ({model.config._attn_implementation}): {out[-1]:.1f} ms", file=sys.stderr, flush=True)
         return out, logits
 
-    fh.patch_model(model, corr_threshold=args.threshold)
+    fused = args.c4_rope == "fused"
+    fh.patch_model(model, fused_rope=fused, corr_threshold=args.threshold)
     fh.record_prefill_events(False)
     timed(args.warmup)
     fh.record_prefill_events(True)
     sparse_ms, logits = timed(args.steps)
     ev = fh.prefill_events()
     fh.record_prefill_events(False)
+    other_ms = None
+    if args.c4_compare_rope:
+        fh.patch_model(model, fused_rope=not fused, corr_threshold=args.threshold)
+        timed(1)
+        o, _ = timed(args.steps)
+        other_ms = sum(o) / len(o)
+        fh.patch_model(model, fused_rope=fused, corr_threshold=args.threshold)
     attn_total = sum(e.ms() for e in ev) / args.steps
     per_layer = [0.0] * cfg.num_hidden_layers
     density = [0.0] * cfg.num_hidden_layers
@@ -355,6 +369,7 @@ def run_c4(args):
 
     dense_ms = float("nan")
     if not args.no_dense:
+        fh.patch_model(model, fused_rope=False)        # class forwards back
         model.set_attn_implementation("sdpa")
         d, _ = timed(1 + args.dense_steps)
         dense_ms = sum(d[1:]) / max(1, len(d) - 1) if len(d) > 1 else d[0]
@@ -365,8 +380,10 @@ def run_c4(args):
         "data": f"random-init weights (seed {args.seed}), random token ids",
         "config": {"workload": f"c4: 32-layer Llama-3.1-8B shape ({n_params / 1e9:.2f} B parameters), "
                                f"prefill of {L} tokens, FFTSparse prefill in every layer, "
-                               f"corr_threshold {args.threshold}, production kwargs",
+                               f"corr_threshold {args.threshold}, production kwargs, "
+                               f"RoPE {'fused with the block pooling' if fused else 'of the model'}",
                    "seq_len": L, "global_batch": 1, "parallelism": "none (1 GPU)"},
+        "rope": args.c4_rope,
         "attention_ms": round(attn_total, 2), "attention_share": round(attn_total / ms, 4),
         "non_attention_ms": round(ms - attn_total, 2),
         "attention_ms_per_layer": [round(x, 3) for x in per_layer],
@@ -374,6 +391,7 @@ def run_c4(args):
         "dense_sdpa_ms": round(dense_ms, 2) if dense_ms == dense_ms else None,
         "speedup_vs_dense_model": round(dense_ms / ms, 3) if dense_ms == dense_ms else None,
         "logits_finite": finite, "build_s": round(t_build, 1),
+        "other_rope_ms": round(other_ms, 2) if other_ms is not None else None,
     }
     print(json.dumps(line))
 

@@ -8,9 +8,12 @@ attn_src/fix_mask_attn/my_attn.py):
     fix_mask.myattn_prefill(q, k, v, layer_idx, ...) fixed sink/recent/local mask
     select_blocks(q, k, ...)                        stage 1 only (block lists)
     block_sparse_attention(q, k, v, cnt, idx, ...)  stage 2 only
+    rope_pool(q, k, cos, sin, ...)                  the rotary embedding before the call, fused
+                                                    with the block pooling (select_blocks(pooled=...))
 """
-from .attn import AttentionCall, BlockSelection, block_sparse_attention, myattn_prefill, select_blocks  # noqa: F401
+from .attn import (AttentionCall, BlockSelection, block_sparse_attention, myattn_prefill, rope_pool,  # noqa: F401
+                   select_blocks)
 from . import fix_mask  # noqa: F401
 
-__all__ = ["myattn_prefill", "select_blocks", "block_sparse_attention", "AttentionCall", "BlockSelection",
-           "fix_mask"]
+__all__ = ["myattn_prefill", "select_blocks", "block_sparse_attention", "rope_pool", "AttentionCall",
+           "BlockSelection", "fix_mask"]

@@ -19,12 +19,22 @@ import torch  # noqa: F401  (must precede the library load, see module docstring
 LIB_PATH = Path(os.environ.get("FFTSPARSE_AMD_LIB") or Path(__file__).resolve().with_name("libfftsparse_amd.so"))
 
 FS_DTYPE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 
 class PoolArgs(ctypes.Structure):
     _fields_ = [("q", c_void_p), ("q_sh", c_int64), ("q_sl", c_int64),
                 ("k", c_void_p), ("k_sh", c_int64), ("k_sl", c_int64),
+                ("dtype", c_int), ("Hq", c_int), ("Hk", c_int), ("L", c_int), ("D", c_int), ("bs", c_int),
+                ("q_b", c_void_p), ("k_b", c_void_p)]
+
+
+class RopePoolArgs(ctypes.Structure):
+    _fields_ = [("q", c_void_p), ("q_sh", c_int64), ("q_sl", c_int64),
+                ("k", c_void_p), ("k_sh", c_int64), ("k_sl", c_int64),
+                ("cos", c_void_p), ("sin", c_void_p), ("cs_sl", c_int64),
+                ("q_out", c_void_p), ("qo_sh", c_int64), ("qo_sl", c_int64),
+                ("k_out", c_void_p), ("ko_sh", c_int64), ("ko_sl", c_int64),
                 ("dtype", c_int), ("Hq", c_int), ("Hk", c_int), ("L", c_int), ("D", c_int), ("bs", c_int),
                 ("q_b", c_void_p), ("k_b", c_void_p)]
 
@@ -86,10 +96,10 @@ class AttnArgs(ctypes.Structure):
                 ("blk_cnt", c_void_p), ("blk_idx", c_void_p), ("work", c_void_p)]
 
 
-STRUCTS = [PoolArgs, CorrArgs, StatsArgs, SelectArgs, AttnArgs, ScoresArgs]
+STRUCTS = [PoolArgs, CorrArgs, StatsArgs, SelectArgs, AttnArgs, ScoresArgs, RopePoolArgs]
 
-ENTRY_POINTS = ["fs_pool", "fs_corr_work_bytes", "fs_corr", "fs_stats", "fs_scores_work_bytes", "fs_scores",
-                "fs_select", "fs_bsattn_work_bytes",
+ENTRY_POINTS = ["fs_pool", "fs_rope_pool", "fs_corr_work_bytes", "fs_corr", "fs_stats", "fs_scores_work_bytes",
+                "fs_scores", "fs_select", "fs_bsattn_work_bytes",
                 "fs_bsattn", "fs_bsattn_prepare", "fs_bsattn_run",
                 "fs_last_error", "fs_abi_version", "fs_sizeof_args"]
 
@@ -116,8 +126,8 @@ def load() -> ctypes.CDLL:
     lib.fs_scores_work_bytes.argtypes = [c_int, c_int, c_int]
     lib.fs_bsattn_work_bytes.restype = c_size_t
     lib.fs_bsattn_work_bytes.argtypes = [POINTER(AttnArgs)]
-    for name, st in [("fs_pool", PoolArgs), ("fs_corr", CorrArgs), ("fs_stats", StatsArgs), ("fs_scores", ScoresArgs),
-                     ("fs_select", SelectArgs), ("fs_bsattn", AttnArgs), ("fs_bsattn_prepare", AttnArgs),
+    for name, st in [("fs_pool", PoolArgs), ("fs_rope_pool", RopePoolArgs), ("fs_corr", CorrArgs),
+                     ("fs_stats", StatsArgs), ("fs_scores", ScoresArgs), ("fs_select", SelectArgs), ("fs_bsattn", AttnArgs), ("fs_bsattn_prepare", AttnArgs),
                      ("fs_bsattn_run", AttnArgs)]:
         fn = getattr(lib, name)
         fn.restype = c_int

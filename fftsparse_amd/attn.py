@@ -25,7 +25,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from ._lib import AttnArgs, CorrArgs, PoolArgs, ScoresArgs, SelectArgs, StatsArgs, ptr
+from ._lib import AttnArgs, CorrArgs, PoolArgs, RopePoolArgs, ScoresArgs, SelectArgs, StatsArgs, ptr
 from .params import PrefillParams, derive, f32
 
 _MIN_BLOCKS = 10          # my_attn_v7.py:509
@@ -95,9 +95,11 @@ def select_blocks(query_states: torch.Tensor, key_states: torch.Tensor, *, block
                   column_start_exclude_ratio=0.1, column_end_exclude_ratio=0.2,
                   enable_last_block_mask=True, diag_sample_ratio=0.15, min_diag_samples=5,
                   max_diag_samples=64, stripe_threshold=0.3, qk_topk_ratio=0.2,
-                  keep_intermediates=False, pipeline_groups=None) -> BlockSelection:
+                  keep_intermediates=False, pipeline_groups=None, pooled=None) -> BlockSelection:
     """Stage 1 of my_attn_v7.myattn_prefill (:533-641): block lists for every
-    (query head, query block).  q [1,Hq,L,D], k [1,Hk,L,D]."""
+    (query head, query block).  q [1,Hq,L,D], k [1,Hk,L,D].  ``pooled``: the
+    block means (q_b [Hq,N,D], k_b [Hk,N,D]) already formed by ``rope_pool``,
+    which then replace the pooling pass."""
     q = _check_layout(query_states)
     k = _check_layout(key_states)
     if q.shape[0] != 1 or k.shape[0] != 1:
@@ -140,7 +142,13 @@ def select_blocks(query_states: torch.Tensor, key_states: torch.Tensor, *, block
     sel = BlockSelection(params=p,
                          blk_cnt=torch.empty(Hq, N, dtype=torch.int32, device=dev),
                          blk_idx=torch.empty(Hq, N, Nk, dtype=torch.uint16, device=dev))
-    if need_pool:
+    if pooled is not None:
+        q_b, k_b = pooled
+        if (tuple(q_b.shape) != (Hq, N, D) or tuple(k_b.shape) != (Hk, N, D) or q_b.dtype != q.dtype
+                or k_b.dtype != q.dtype or not q_b.is_contiguous() or not k_b.is_contiguous()):
+            raise ValueError(f"pooled block means must be contiguous [{Hq},{N},{D}] and [{Hk},{N},{D}] in {q.dtype}")
+        sel.q_b, sel.k_b = q_b, k_b
+    elif need_pool:
         sel.q_b = torch.empty(Hq, N, D, dtype=q.dtype, device=dev)
         sel.k_b = torch.empty(Hk, N, D, dtype=q.dtype, device=dev)
     if p.corr_enabled:
@@ -183,7 +191,7 @@ def select_blocks(query_states: torch.Tensor, key_states: torch.Tensor, *, block
         k0, k1 = bounds[g], bounds[g + 1]
         h0, h1 = k0 * G, k1 * G
         hq, hk = h1 - h0, k1 - k0
-        if need_pool:
+        if need_pool and pooled is None:
             qg, kg = q[:, h0:h1], k[:, k0:k1]
             _lib.call("fs_pool", PoolArgs(q=qg.data_ptr(), q_sh=q.stride(1), q_sl=q.stride(2),
                                           k=kg.data_ptr(), k_sh=k.stride(1), k_sl=k.stride(2),
@@ -237,6 +245,53 @@ def select_blocks(query_states: torch.Tensor, key_states: torch.Tensor, *, block
     if not keep_intermediates:
         sel.q_b = sel.k_b = None
     return sel
+
+
+def rope_pool(query_states: torch.Tensor, key_states: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, *,
+              block_size=128):
+    """The attention forward's rotary embedding (eval/LongBench/pred.py:195:
+    transformers' apply_rotary_pos_emb) fused with the block pooling of the
+    rotated states (my_attn_v7.py:105-114) in one pass over Q and K.
+
+    q [1,Hq,L,D], k [1,Hk,L,D] before RoPE (strided views, e.g. the
+    projections' ``view().transpose(1, 2)``); cos / sin [L,D] or [1,L,D], the
+    model's position embeddings.  Returns (q_rot, k_rot, q_b, k_b): the rotated
+    states as [1,H,L,D] views of [1,L,H,D] storage, bit-identical to
+    apply_rotary_pos_emb, and their block means [H,N,D], bit-identical to the
+    pooling pass of ``select_blocks`` on q_rot / k_rot."""
+    q = _check_layout(query_states)
+    k = _check_layout(key_states)
+    if q.shape[0] != 1 or k.shape[0] != 1:
+        raise ValueError("rope_pool takes batch size 1 (my_attn_v7.py:521)")
+    Hq, L, D = q.shape[1], q.shape[2], q.shape[3]
+    Hk = k.shape[1]
+    if k.shape[2] != L or k.shape[3] != D or Hq % Hk:
+        raise ValueError(f"query {tuple(q.shape)} and key {tuple(k.shape)} shapes do not match")
+    if q.dtype != k.dtype or q.dtype not in _lib.FS_DTYPE:
+        raise TypeError(f"unsupported dtypes {q.dtype}, {k.dtype}")
+    cs = []
+    for t in (cos, sin):
+        t = t[0] if t.dim() == 3 else t
+        if t.shape != (L, D) or t.dtype != q.dtype:
+            raise ValueError(f"cos/sin must be [{L},{D}] (or [1,{L},{D}]) in {q.dtype}, got {tuple(t.shape)} {t.dtype}")
+        if t.stride(1) != 1 or t.stride(0) % 8 or t.data_ptr() % 16:
+            t = t.contiguous()
+        cs.append(t)
+    if cs[0].stride(0) != cs[1].stride(0):
+        cs = [t.contiguous() for t in cs]
+    N = (L + block_size - 1) // block_size
+    dev = q.device
+    q_rot = torch.empty(1, L, Hq, D, dtype=q.dtype, device=dev).transpose(1, 2)
+    k_rot = torch.empty(1, L, Hk, D, dtype=q.dtype, device=dev).transpose(1, 2)
+    q_b = torch.empty(Hq, N, D, dtype=q.dtype, device=dev)
+    k_b = torch.empty(Hk, N, D, dtype=q.dtype, device=dev)
+    _lib.call("fs_rope_pool", RopePoolArgs(
+        q=q.data_ptr(), q_sh=q.stride(1), q_sl=q.stride(2), k=k.data_ptr(), k_sh=k.stride(1), k_sl=k.stride(2),
+        cos=cs[0].data_ptr(), sin=cs[1].data_ptr(), cs_sl=cs[0].stride(0),
+        q_out=q_rot.data_ptr(), qo_sh=q_rot.stride(1), qo_sl=q_rot.stride(2),
+        k_out=k_rot.data_ptr(), ko_sh=k_rot.stride(1), ko_sl=k_rot.stride(2),
+        dtype=_lib.FS_DTYPE[q.dtype], Hq=Hq, Hk=Hk, L=L, D=D, bs=block_size, q_b=q_b.data_ptr(), k_b=k_b.data_ptr()))
+    return q_rot, k_rot, q_b, k_b
 
 
 _side = {}

@@ -27,7 +27,7 @@ int launch_status(const char* what) {
 }  // namespace fs_host
 
 extern "C" const char* fs_last_error(void) { return fs_host::g_err; }
-extern "C" int fs_abi_version(void) { return 5; }
+extern "C" int fs_abi_version(void) { return 6; }
 
 extern "C" size_t fs_sizeof_args(int which) {
   switch (which) {
@@ -37,6 +37,7 @@ extern "C" size_t fs_sizeof_args(int which) {
     case 3: return sizeof(fs_select_args);
     case 4: return sizeof(fs_attn_args);
     case 5: return sizeof(fs_scores_args);
+    case 6: return sizeof(fs_rope_pool_args);
     default: return 0;
   }
 }

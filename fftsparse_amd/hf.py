@@ -19,14 +19,22 @@ one registered function::
 
 K/V arrive with their native KV-head count; the kernels read them as they
 are, so the reference's ``repeat_kv`` copies are not made.
+
+``patch_model(model, fused_rope=True)`` also replaces the forward of each
+Llama-family attention module, as the reference does (pred.py:160-250): a
+fresh batch-1 prefill applies the rotary embedding and forms the block means
+of the rotated Q/K in one pass (``rope_pool``), so the selection does not
+re-read Q and K; every other call runs the model's own RoPE and the
+registered attention.
 """
 from __future__ import annotations
 
+import types
 from typing import NamedTuple
 
 import torch
 
-from .attn import v7_prefill
+from .attn import _MIN_BLOCKS, rope_pool, v7_prefill
 
 NAME = "fftsparse"
 
@@ -36,7 +44,7 @@ PRODUCTION_KWARGS = dict(block_size=128, sink_ratio=0.01, recent_ratio=0.0, loca
                          corr_threshold=0.9, column_topk_ratio=0.2, qk_topk_ratio=0.3, stripe_threshold=0.3,
                          diag_sample_ratio=0.15, min_diag_samples=5, max_diag_samples=64)
 
-_state = {"kwargs": dict(PRODUCTION_KWARGS), "events": None}
+_state = {"kwargs": dict(PRODUCTION_KWARGS), "events": None, "name": NAME}
 
 
 def fftsparse_attention(module, query, key, value, attention_mask, dropout=0.0, scaling=None, **kwargs):
@@ -58,18 +66,78 @@ def fftsparse_attention(module, query, key, value, attention_mask, dropout=0.0, 
     if dropout:
         raise ValueError("the FFTSparse prefill has no dropout")
     kw = _state["kwargs"]
-    ev = _state["events"]
-    if ev is None:
+    if _state["events"] is None:
         return v7_prefill(query, key, value, softmax_scale=scaling, **kw), None   # [1, L, Hq, D]
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
+    e0 = _event()
     out, sel = v7_prefill(query, key, value, softmax_scale=scaling, return_selection=True, **kw)
-    e1.record()
-    # selected tiles (a device scalar, read after the run) over the causal tiles
-    nnz = sel.blk_cnt.sum() if sel is not None else None
-    nq = -(-query.shape[2] // kw.get("block_size", 128))
-    ev.append(PrefillEvent(getattr(module, "layer_idx", None), e0, e1, nnz, query.shape[1] * nq * (nq + 1) // 2))
+    _record(module, e0, sel, query.shape[1], query.shape[2])
     return out, None
+
+
+def _event():
+    e = torch.cuda.Event(enable_timing=True)
+    e.record()
+    return e
+
+
+def _record(module, e0, sel, Hq, L):
+    """Closes a prefill event: its time, and the selected tiles (a device
+    scalar, read after the run) over the causal tiles."""
+    e1 = _event()
+    nnz = sel.blk_cnt.sum() if sel is not None else None
+    nq = -(-L // _state["kwargs"].get("block_size", 128))
+    _state["events"].append(PrefillEvent(getattr(module, "layer_idx", None), e0, e1, nnz, Hq * nq * (nq + 1) // 2))
+
+
+# attention classes whose forward is q/k/v projections, RoPE, cache update,
+# attention, o_proj (models/llama/modeling_llama.py LlamaAttention.forward)
+_FUSABLE = ("LlamaAttention", "MistralAttention", "Qwen2Attention")
+
+
+def fused_attention_forward(self, hidden_states, position_embeddings=None, attention_mask=None,
+                            past_key_values=None, **kwargs):
+    """LlamaAttention.forward with the FFTSparse prefill (the reference's
+    patched forward, eval/LongBench/pred.py:160-250).  A fresh batch-1 causal
+    prefill of at least 10 blocks runs ``rope_pool`` (the rotary embedding of
+    pred.py:195 and the selection's block pooling in one pass), stores the
+    rotated K and V in the cache, and runs the v7 selection on those block
+    means and the block-sparse attention.  Any other call (decode, a chunk
+    after cached tokens, masks, training) applies the model's RoPE and the
+    registered attention, exactly as the unpatched forward does."""
+    from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
+    bsz, q_len = hidden_states.shape[:2]
+    shape = (bsz, q_len, -1, self.head_dim)
+    q = self.q_proj(hidden_states).view(shape).transpose(1, 2)
+    k = self.k_proj(hidden_states).view(shape).transpose(1, 2)
+    v = self.v_proj(hidden_states).view(shape).transpose(1, 2)
+    cos, sin = position_embeddings
+    kw = _state["kwargs"]
+    bs = kw.get("block_size", 128)
+    fresh = past_key_values is None or past_key_values.get_seq_length(self.layer_idx) == 0
+    ours = self.config._attn_implementation == _state["name"]
+    if (ours and q.is_cuda and bsz == 1 and attention_mask is None and fresh and not self.training
+            and q_len >= bs * _MIN_BLOCKS and q.dtype in (torch.bfloat16, torch.float16)):
+        e0 = _event() if _state["events"] is not None else None
+        q, k, q_b, k_b = rope_pool(q, k, cos, sin, block_size=bs)
+        if past_key_values is not None:
+            k, v = past_key_values.update(k, v, self.layer_idx)
+        out, sel = v7_prefill(q, k, v, softmax_scale=self.scaling, return_selection=True, pooled=(q_b, k_b), **kw)
+        if e0 is not None:
+            _record(self, e0, sel, q.shape[1], q_len)
+    else:
+        q, k = apply_rotary_pos_emb(q, k, cos, sin)
+        if past_key_values is not None:
+            k, v = past_key_values.update(k, v, self.layer_idx)
+        if ours:
+            out, _ = fftsparse_attention(self, q, k, v, attention_mask, dropout=0.0, scaling=self.scaling, **kwargs)
+        else:
+            from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
+            from transformers.models.llama.modeling_llama import eager_attention_forward
+            fn = ALL_ATTENTION_FUNCTIONS.get_interface(self.config._attn_implementation, eager_attention_forward)
+            out, _ = fn(self, q, k, v, attention_mask, dropout=0.0 if not self.training else self.attention_dropout,
+                        scaling=self.scaling, **kwargs)
+    out = out.reshape(bsz, q_len, -1).contiguous()
+    return self.o_proj(out), None
 
 
 def register(name: str = NAME, **overrides) -> str:
@@ -81,16 +149,26 @@ def register(name: str = NAME, **overrides) -> str:
     from transformers.masking_utils import ALL_MASK_ATTENTION_FUNCTIONS, AttentionMaskInterface
 
     _state["kwargs"] = {**PRODUCTION_KWARGS, **overrides}
+    _state["name"] = name
     AttentionInterface.register(name, fftsparse_attention)
     AttentionMaskInterface.register(name, ALL_MASK_ATTENTION_FUNCTIONS["sdpa"])
     return name
 
 
-def patch_model(model, name: str = NAME, **overrides):
+def patch_model(model, name: str = NAME, fused_rope: bool = False, **overrides):
     """Switches a loaded model to the FFTSparse prefill (the counterpart of the
-    reference's forward replacement, pred.py:655-661) and returns it."""
+    reference's forward replacement, pred.py:655-661) and returns it.  With
+    ``fused_rope`` the Llama-family attention modules also take
+    ``fused_attention_forward``; without it any such replacement is undone."""
     register(name, **overrides)
     model.set_attn_implementation(name)
+    for m in model.modules():
+        if type(m).__name__ not in _FUSABLE:
+            continue
+        if fused_rope:
+            m.forward = types.MethodType(fused_attention_forward, m)
+        elif "forward" in vars(m):
+            del m.forward                           # back to the class's forward
     return model
 
 

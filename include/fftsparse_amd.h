@@ -9,6 +9,8 @@
  *
  * Reference interfaces replaced (paths relative to the FFTSparse repository):
  *   fs_pool      block_mean_pool              attn_src/fft_attn/my_attn_v7.py:105-114 (call :553-555)
+ *   fs_rope_pool the rotary embedding before the call (eval/LongBench/pred.py:195, transformers
+ *                apply_rotary_pos_emb) fused with block_mean_pool (my_attn_v7.py:105-114)
  *   fs_corr      batch_fft_cross_correlation  my_attn_v7.py:117-157
  *                + threshold lag selection     my_attn_v7.py:190-208 (create_correlation_block_mask)
  *   fs_stats     compute_stripe_variance      my_attn_v7.py:301-363 (diagonal statistics)
@@ -62,6 +64,30 @@ typedef struct {
   void* k_b;
 } fs_pool_args;
 FS_API int fs_pool(const fs_pool_args* a, void* stream);
+
+/* ---- rotary embedding + block pooling in one pass -----------------------
+ * Replaces the attention forward's RoPE step (eval/LongBench/pred.py:195,
+ * transformers models/llama/modeling_llama.py apply_rotary_pos_emb) followed by
+ * block_mean_pool of the rotated states (my_attn_v7.py:105-114, call :553-555).
+ * q: pre-RoPE [Hq, L, D] view (element strides q_sh, q_sl; d contiguous), k
+ * likewise [Hk, L, D]; cos / sin: [L, D] rows (row stride cs_sl) in dtype, the
+ * caller's position embeddings of these L positions.  Writes the rotated
+ *   out[d] = rnd(rnd(x[d] * cos[d]) + rnd(r[d] * sin[d])),  r = (-x[D/2:], x[:D/2]),
+ * (each step in fp32, rounded to dtype, as the reference's elementwise ops)
+ * to q_out / k_out (own strides), and to q_b [Hq][N][D] / k_b [Hk][N][D] the
+ * block means fs_pool would compute from q_out / k_out (bit-identical).
+ * D / (16 / sizeof(dtype)) must be a power of two <= 64 (D = 128 for every dtype). */
+typedef struct {
+  const void* q; int64_t q_sh, q_sl;
+  const void* k; int64_t k_sh, k_sl;
+  const void* cos; const void* sin; int64_t cs_sl;
+  void* q_out; int64_t qo_sh, qo_sl;
+  void* k_out; int64_t ko_sh, ko_sl;
+  int dtype, Hq, Hk, L, D, bs;
+  void* q_b;
+  void* k_b;
+} fs_rope_pool_args;
+FS_API int fs_rope_pool(const fs_rope_pool_args* a, void* stream);
 
 /* ---- FFT lag correlation + lag selection (my_attn_v7.py:117-208) --------
  * For query head h (key head h / (Hq/Hk)):
@@ -211,7 +237,7 @@ FS_API int fs_bsattn_run(const fs_attn_args* a, void* stream);
 
 /* Description of the last failure on this thread ("" if none). */
 FS_API const char* fs_last_error(void);
-/* sizeof the argument struct: 0 pool, 1 corr, 2 stats, 3 select, 4 attn, 5 scores
+/* sizeof the argument struct: 0 pool, 1 corr, 2 stats, 3 select, 4 attn, 5 scores, 6 rope_pool
  * (lets a foreign-function binding check its struct layout). */
 FS_API size_t fs_sizeof_args(int which);
 /* ABI version of this library (increments on any struct change). */

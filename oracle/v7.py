@@ -16,6 +16,10 @@ this module accumulates in float64 and rounds once, so it sits within one
 rounding of any order.
 
 Parity pins (what checks each function against something other than itself):
+  rotary_embedding         -- transformers' apply_rotary_pos_emb (the function the
+                              reference's patched forward calls) on CPU tensors,
+                              bit for bit; cos = 1 / sin = 0 and cos = 0 / sin = 1
+                              closed forms
   block_mean_pool          -- brute force over tokens; closed form on constant blocks
   fft_lag_correlation      -- brute-force diagonal sums of Q_b K_b^T (O(N^2 D));
                               post-processing checked on hand-built inputs
@@ -138,6 +142,22 @@ def derive_params(L_q, L_k, block_size=128, sink_ratio=0.1, recent_ratio=0.1,
 def to_lhd(x: torch.Tensor) -> torch.Tensor:
     """[1,H,L,D] -> [L,H,D] (my_attn_v7.py:528-530)."""
     return x.squeeze(0).transpose(0, 1)
+
+
+def rotary_embedding(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """The RoPE step before the path: eval/LongBench/pred.py:195 applies
+    transformers' apply_rotary_pos_emb (models/llama/modeling_llama.py
+    rotate_half / apply_rotary_pos_emb) to q and k:
+        out = x * cos + rotate_half(x) * sin,  rotate_half(x) = cat(-x[..., D/2:], x[..., :D/2]).
+    Each elementwise op runs in x's dtype, i.e. is formed in fp32 and rounded
+    once to the dtype (fp32 inputs: plain fp32 ops, no fused multiply-add).
+    x [..., L, D]; cos / sin [L, D] in x's dtype -> x's shape and dtype."""
+    D = x.shape[-1]
+    xf, c, s = x.float(), cos.float(), sin.float()
+    rot = torch.cat([-xf[..., D // 2:], xf[..., :D // 2]], dim=-1)
+    a = (xf * c).to(x.dtype).float()
+    b = (rot * s).to(x.dtype).float()
+    return (a + b).to(x.dtype)
 
 
 def block_mean_pool(x: torch.Tensor, bs: int) -> torch.Tensor:

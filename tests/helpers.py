@@ -37,3 +37,15 @@ def lists_from_mask(mask: torch.Tensor, device):
     order = torch.argsort((~mask).to(torch.int8), dim=-1, stable=True)
     idx = order.to(torch.int16).view(torch.uint16).contiguous()
     return cnt.to(device), idx.to(device)
+
+
+def rope_tables(L, D, theta, dtype):
+    """cos / sin [L, D] of the model's rotary embedding (transformers'
+    LlamaRotaryEmbedding at positions 0 .. L-1), on the CPU."""
+    from transformers import LlamaConfig
+    from transformers.models.llama.modeling_llama import LlamaRotaryEmbedding
+    cfg = LlamaConfig(hidden_size=4 * D, num_attention_heads=4, num_key_value_heads=2, head_dim=D,
+                      rope_theta=theta, max_position_embeddings=max(L, 2048))
+    x = torch.zeros(1, dtype=dtype)
+    cos, sin = LlamaRotaryEmbedding(cfg)(x, torch.arange(L)[None])
+    return cos[0], sin[0]

@@ -12,10 +12,10 @@ import math
 import pytest
 import torch
 
-from fftsparse_amd import block_sparse_attention, fix_mask, myattn_prefill, select_blocks
+from fftsparse_amd import _lib, block_sparse_attention, fix_mask, myattn_prefill, rope_pool, select_blocks
 from fftsparse_amd.synth import make_qkv, make_config
 from oracle import v7
-from tests.helpers import BAND, MATCH_MIN, PROD, block_match, lists_from_mask
+from tests.helpers import BAND, MATCH_MIN, PROD, block_match, lists_from_mask, rope_tables
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -56,6 +56,60 @@ def test_pool_parity(dtype, L, bs):
             ri = ref.view(torch.int16).to(torch.int32)
             assert (gi - ri).abs().max().item() <= 1
             assert (gi == ri).float().mean().item() >= 0.999
+
+
+# --------------------------------------------------------------------------- RoPE + pooling
+def _fs_pool(q, k, bs):
+    """fs_pool alone on [1,H,L,D] views -> (q_b [Hq,N,D], k_b [Hk,N,D])."""
+    Hq, L, D = q.shape[1:]
+    N = (L + bs - 1) // bs
+    q_b = torch.empty(Hq, N, D, dtype=q.dtype, device=DEV)
+    k_b = torch.empty(k.shape[1], N, D, dtype=q.dtype, device=DEV)
+    _lib.call("fs_pool", _lib.PoolArgs(q=q.data_ptr(), q_sh=q.stride(1), q_sl=q.stride(2), k=k.data_ptr(),
+                                       k_sh=k.stride(1), k_sl=k.stride(2), dtype=_lib.FS_DTYPE[q.dtype], Hq=Hq,
+                                       Hk=k.shape[1], L=L, D=D, bs=bs, q_b=q_b.data_ptr(), k_b=k_b.data_ptr()))
+    return q_b, k_b
+
+
+def _proj_layout(L, H, dtype, g, scale=3.0):
+    """A projection's output as the attention forward sees it: [1,H,L,D] view of [1,L,H,D] storage."""
+    return (torch.randn(1, L, H, 128, generator=g) * scale).to(dtype).to(DEV).transpose(1, 2)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("L,bs,Hq,Hk", [(8192, 128, 4, 1), (5000, 128, 4, 2), (4100, 64, 8, 8)])
+def test_rope_pool_parity(dtype, L, bs, Hq, Hk):
+    """fs_rope_pool: rotated Q/K bit-identical to transformers' apply_rotary_pos_emb
+    on the GPU (the reference's RoPE step) and to the oracle; block means
+    bit-identical to fs_pool on the rotated tensors."""
+    from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
+    _print_case("rope_pool", dtype=dtype, L=L, bs=bs, Hq=Hq, Hk=Hk)
+    g = torch.Generator().manual_seed(21)
+    q, k = _proj_layout(L, Hq, dtype, g), _proj_layout(L, Hk, dtype, g)
+    cos, sin = rope_tables(L, 128, 500000.0, dtype)
+    cg, sg = cos.to(DEV), sin.to(DEV)
+    q_rot, k_rot, q_b, k_b = rope_pool(q, k, cg, sg, block_size=bs)
+    ref_q, ref_k = apply_rotary_pos_emb(q, k, cg[None], sg[None])
+    assert torch.equal(q_rot, ref_q) and torch.equal(k_rot, ref_k)
+    assert torch.equal(q_rot.cpu(), v7.rotary_embedding(q.cpu(), cos, sin))
+    assert q_rot.stride() == ref_q.stride()
+    p_q, p_k = _fs_pool(q_rot, k_rot, bs)
+    assert torch.equal(q_b, p_q) and torch.equal(k_b, p_k)
+
+
+def test_select_blocks_on_fused_means_equals_unfused():
+    """select_blocks(pooled=rope_pool's means) gives the block lists of
+    select_blocks on the rotated tensors (bf16, config-0 shape)."""
+    g = torch.Generator().manual_seed(22)
+    q, k = _proj_layout(8192, 4, torch.bfloat16, g, 1.0), _proj_layout(8192, 1, torch.bfloat16, g, 1.0)
+    cos, sin = rope_tables(8192, 128, 500000.0, torch.bfloat16)
+    q_rot, k_rot, q_b, k_b = rope_pool(q, k, cos.to(DEV), sin.to(DEV))
+    a = select_blocks(q_rot, k_rot, **PROD)
+    b = select_blocks(q_rot, k_rot, pooled=(q_b, k_b), **PROD)
+    assert torch.equal(a.blk_cnt, b.blk_cnt)
+    assert torch.equal(a.dense_mask(), b.dense_mask())
+    with pytest.raises(ValueError):
+        select_blocks(q_rot, k_rot, pooled=(q_b[:, :-1], k_b), **PROD)
 
 
 # --------------------------------------------------------------------------- FFT correlation
@@ -264,6 +318,34 @@ def test_attention_noncausal_and_dense():
     out = block_sparse_attention(*_gpu(q, k, v), block_size=128, is_causal=True)
     ref = v7.dense_causal_attention(q, k, v)[0]
     _attn_check(out[0], ref)
+
+
+@pytest.mark.parametrize("growth", [300.0, 3000.0])
+def test_attention_running_max_raises(growth):
+    """Scores that grow along the keys (k_t carries t/L * growth along q's
+    shared direction): the running max is raised on nearly every tile, and at
+    growth 3000 the exponentials taken against the stale max overflow to inf
+    before the check replaces them.  Dense causal and listed (every causal
+    block, ascending) paths, both block sizes."""
+    _print_case("attention-raise", growth=growth)
+    L, D = 2048, 128
+    g = torch.Generator().manual_seed(11)
+    u = torch.randn(D, generator=g)
+    u /= u.norm()
+    q = torch.randn(1, 2, L, D, generator=g) + 10.0 * u
+    ramp = (torch.arange(L, dtype=torch.float32) / L * growth)[:, None]
+    k = torch.randn(1, 1, L, D, generator=g) + ramp * u
+    v = torch.randn(1, 1, L, D, generator=g)
+    q, k, v = (x.to(torch.bfloat16) for x in (q, k, v))
+    ref = v7.dense_causal_attention(q, k, v)[0]
+    out = block_sparse_attention(*_gpu(q, k, v), block_size=128, is_causal=True)
+    _attn_check(out[0], ref)
+    for bs in (128, 64):
+        N = L // bs
+        mask = torch.tril(torch.ones(2, N, N, dtype=torch.bool))
+        cnt, idx = lists_from_mask(mask, DEV)
+        out = block_sparse_attention(*_gpu(q, k, v), cnt, idx, block_size=bs)
+        _attn_check(out[0], ref)
 
 
 def test_attention_prepare_run_equals_single_call():

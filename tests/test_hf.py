@@ -54,6 +54,35 @@ def test_prefill_on_cpu_raises_like_the_reference():
         m(torch.randint(0, 1000, (1, 64)))
 
 
+def test_fused_forward_on_cpu_keeps_reference_errors():
+    """The fused forward falls back to the model's RoPE and the registered
+    attention off the GPU, which raises like the reference (my_attn_v7.py:502);
+    patch_model without fused_rope restores the class forward."""
+    m = _tiny()
+    fh.patch_model(m, fused_rope=True)
+    assert "forward" in vars(m.model.layers[0].self_attn)
+    with pytest.raises(AssertionError):
+        m(torch.randint(0, 1000, (1, 64)))
+    fh.patch_model(m)
+    assert "forward" not in vars(m.model.layers[0].self_attn)
+
+
+def test_fused_forward_follows_another_implementation():
+    """With the model switched to another attention implementation, the
+    patched forward is the model's own: identical logits on the CPU."""
+    m = _tiny().eval()
+    ids = torch.randint(0, 1000, (1, 64), generator=torch.Generator().manual_seed(5))
+    m.set_attn_implementation("sdpa")
+    with torch.no_grad():
+        ref = m(input_ids=ids).logits
+    fh.patch_model(m, fused_rope=True)
+    m.set_attn_implementation("sdpa")
+    with torch.no_grad():
+        out = m(input_ids=ids).logits
+    fh.patch_model(m)
+    assert torch.equal(out, ref)
+
+
 @pytest.mark.gpu
 def test_prefill_rejects_batches_and_masks():
     dev = torch.device("cuda:0")
@@ -107,3 +136,31 @@ def test_small_llama_prefill_runs():
     assert all(0.0 < e.density() <= 1.0 and e.ms() > 0.0 for e in ev)
     assert torch.isfinite(out.logits.float()).all()
     assert torch.isfinite(nxt.logits.float()).all()
+
+
+@pytest.mark.gpu
+def test_fused_rope_forward_equals_unfused():
+    """patch_model(fused_rope=True): the prefill (RoPE and block pooling in one
+    pass) gives the logits of the registered attention on the model's own RoPE
+    bit for bit, fills the cache with the same rotated keys, and a decoding
+    step after it matches too; patching back restores the class forward."""
+    dev = torch.device("cuda:0")
+    m = _tiny(heads=8, kv=2, hidden=1024).to(dev, torch.bfloat16).eval()
+    ids = torch.randint(0, 1000, (1, 4096), generator=torch.Generator().manual_seed(4)).to(dev)
+    print("[case] hf fused rope prefill 4096", flush=True)
+    outs = []
+    for fused in (False, True):
+        fh.patch_model(m, fused_rope=fused)
+        assert ("forward" in vars(m.model.layers[0].self_attn)) == fused
+        with torch.no_grad():
+            out = m(input_ids=ids, use_cache=True)
+            nxt = m(input_ids=ids[:, -1:], past_key_values=out.past_key_values, use_cache=True)
+        outs.append((out, nxt))
+    torch.cuda.synchronize()
+    (a, an), (b, bn) = outs
+    assert torch.equal(a.logits, b.logits)
+    assert torch.equal(an.logits, bn.logits)
+    for la, lb in zip(a.past_key_values.layers, b.past_key_values.layers):
+        assert torch.equal(la.keys, lb.keys) and torch.equal(la.values, lb.values)
+    fh.patch_model(m)
+    assert "forward" not in vars(m.model.layers[0].self_attn)

@@ -35,7 +35,7 @@ def test_struct_layouts_match_library():
 
 def test_null_args_rejected_without_gpu():
     lib = _lib.load()
-    for name in ("fs_pool", "fs_corr", "fs_stats", "fs_scores", "fs_select", "fs_bsattn", "fs_bsattn_prepare",
+    for name in ("fs_pool", "fs_rope_pool", "fs_corr", "fs_stats", "fs_scores", "fs_select", "fs_bsattn", "fs_bsattn_prepare",
                  "fs_bsattn_run"):
         rc = getattr(lib, name)(None, None)
         assert rc == -1
@@ -44,6 +44,12 @@ def test_null_args_rejected_without_gpu():
 
 def test_bad_shapes_rejected_without_gpu():
     lib = _lib.load()
+    r = _lib.RopePoolArgs(q=16, k=16, cos=16, sin=16, q_out=16, k_out=16, q_b=16, k_b=16, dtype=1, Hq=4, Hk=1,
+                          L=10, D=96, bs=128)
+    assert lib.fs_rope_pool(ctypes.byref(r), None) == -2          # 12 chunks per row: not a power of two
+    assert b"D=96" in lib.fs_last_error()
+    r.D, r.q_sl = 128, 100                                       # 200-byte row stride
+    assert lib.fs_rope_pool(ctypes.byref(r), None) == -1
     a = _lib.AttnArgs(q=16, k=16, v=16, out=16, dtype=1, B=1, Hq=3, Hk=2, Lq=10, Lk=10, D=128, bs=128)
     assert lib.fs_bsattn(ctypes.byref(a), None) == -1
     a = _lib.AttnArgs(q=16, k=16, v=16, out=16, work=16, dtype=1, B=1, Hq=4, Hk=2, Lq=10, Lk=10, D=96, bs=128)

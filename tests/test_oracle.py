@@ -10,7 +10,7 @@ import torch
 
 from fftsparse_amd.synth import make_qkv
 from oracle import v7
-from tests.helpers import PROD
+from tests.helpers import PROD, rope_tables
 
 G = torch.Generator().manual_seed(1234)
 
@@ -54,6 +54,33 @@ def test_k_per_row_is_fp32_product_truncated():
 
 
 # --------------------------------------------------------------------------- pooling
+# --------------------------------------------------------------------------- rotary embedding
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_rotary_embedding_matches_transformers(dtype):
+    """The restatement equals the library function the reference's forward
+    calls (transformers apply_rotary_pos_emb), bit for bit, on the projections'
+    strided [1, H, L, D] views."""
+    pytest.importorskip("transformers")
+    from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
+    L, D = 1500, 128
+    cos, sin = rope_tables(L, D, 500000.0, dtype)
+    q = (_rand(1, L, 4, D) * 3).to(dtype).transpose(1, 2)
+    k = (_rand(1, L, 2, D) * 3).to(dtype).transpose(1, 2)
+    qr, kr = apply_rotary_pos_emb(q, k, cos[None], sin[None])
+    assert torch.equal(v7.rotary_embedding(q, cos, sin), qr)
+    assert torch.equal(v7.rotary_embedding(k, cos, sin), kr)
+
+
+def test_rotary_embedding_closed_forms():
+    """cos = 1, sin = 0 is the identity; cos = 0, sin = 1 is rotate_half exactly;
+    a half-turn (cos = -1) negates."""
+    x = _rand(2, 10, 16).to(torch.bfloat16)
+    one, zero = torch.ones(10, 16, dtype=torch.bfloat16), torch.zeros(10, 16, dtype=torch.bfloat16)
+    assert torch.equal(v7.rotary_embedding(x, one, zero), x)
+    assert torch.equal(v7.rotary_embedding(x, zero, one), torch.cat([-x[..., 8:], x[..., :8]], -1))
+    assert torch.equal(v7.rotary_embedding(x, -one, zero), -x)
+
+
 @pytest.mark.parametrize("L,bs", [(1000, 128), (1024, 128), (700, 64)])
 def test_block_mean_pool_brute_force(L, bs):
     x = _rand(L, 3, 16)
