@@ -39,7 +39,7 @@ int cu_count() {
 }  // namespace fs_host
 
 extern "C" const char* fs_last_error(void) { return fs_host::g_err; }
-extern "C" int fs_abi_version(void) { return 6; }
+extern "C" int fs_abi_version(void) { return 7; }
 
 extern "C" size_t fs_sizeof_args(int which) {
   switch (which) {
@@ -50,6 +50,7 @@ extern "C" size_t fs_sizeof_args(int which) {
     case 4: return sizeof(fs_attn_args);
     case 5: return sizeof(fs_scores_args);
     case 6: return sizeof(fs_rope_pool_args);
+    case 7: return sizeof(fs_xattn_args);
     default: return 0;
   }
 }

@@ -1,0 +1,399 @@
+// XAttention block selection on gfx950 -- the reference's other selector
+// (attn_src/xattn/src/Xattention.py:14-303 xattn_estimate + :306-406
+// Xattention_prefill; its Triton kernels attn_src/xattn/src/kernels.py:5-97 and
+// :195-234; attn_src/xattn/src/utils.py:44-200 find_blocks_chunked), feeding
+// the same block-sparse attention kernel as the FFT selector.
+//
+// Reshaped scores (stride S, "inverse" mode): for reshaped query row r and key
+// n,  A[r][n] = sum_{j<S} q[rS + S-1-j] . k[nS + j]  -- a GEMM with an S*D
+// reduction whose operands are S token rows each; the fp32 result is rounded
+// to the input dtype, as the reference's kernel stores it.  Then, in the exp2
+// domain, x = A * log2(e) / sqrt(D) / S / norm, each real row is normalised
+// over its causal keys n <= r, and the probabilities are summed over
+// (bs/S) x (bs/S) squares: the block sums, rounded to the input dtype.
+//
+// xattn_scores_kernel<T, PASS>: one workgroup (4 waves, 32 reshaped rows
+// each) per (head, 128 reshaped rows), longest rows first; key tiles of 64
+// reshaped keys up to the diagonal.  For each tile and each j < S the
+// workgroup stages the 128 query token rows rS + S-1-j and the 64 key token
+// rows nS + j in LDS (zero past L; 256-byte rows, 16-byte chunk c of row r at
+// c ^ (r & 15)) and accumulates S^T = K' Q'^T with v_mfma_f32_32x32x16.  Pass 1
+// keeps each row's running max and exp2 sum (the reference's first loop);
+// pass 2 recomputes the tile, forms p = exp2(x - max) / sum and reduces the
+// lanes of each block with xor shuffles (the second loop).
+//
+// xattn_select_kernel: one workgroup per (head, block row I): the causal
+// block sums of the row, the forced first and diagonal blocks, the others in
+// decreasing order (ties: lower index first) by a bitonic sort in LDS, their
+// exclusive prefix masses in fp64, and each other block kept iff
+// forced mass + prefix < row total * threshold.  Output: ascending per-row
+// block lists (the causal tril; keep_sink fills row 0, keep_recent the
+// diagonal).
+#include "common.h"
+
+namespace fs {
+
+constexpr int kXD = 128;          // head dim
+constexpr int kXRows = 128;       // reshaped rows per workgroup: 4 waves x 32
+constexpr int kXKeys = 64;        // reshaped keys per tile
+constexpr int kXThreads = 256;
+constexpr int kXSelThreads = 256;
+constexpr int kXMaxBlocks = 4096;
+
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+
+template <typename T> struct XMma;
+template <> struct XMma<bf16_t> {
+  static __device__ __forceinline__ f32x16_t mma(uint4 a, uint4 b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                   c, 0, 0, 0);
+  }
+};
+template <> struct XMma<f16_t> {
+  static __device__ __forceinline__ f32x16_t mma(uint4 a, uint4 b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b),
+                                                  c, 0, 0, 0);
+  }
+};
+
+struct XScoreK {
+  const uint16_t* q;
+  const uint16_t* k;
+  int64_t q_sh, q_sl, k_sh, k_sl;
+  int Hq, Hk, L, S, Lr, real, rbs, Nb;
+  float scale;                  // log2(e) / sqrt(D) / S / norm
+  float* m;                     // [Hq][Lr] row max (exp2 domain)
+  float* l;                     // [Hq][Lr] row sum
+  float* sums;                  // [Hq][Nb][Nb] block sums (values of T), causal part
+};
+
+template <typename T, int PASS>
+__global__ __launch_bounds__(kXThreads) void xattn_scores_kernel(XScoreK a) {
+  __shared__ __attribute__((aligned(16))) uint16_t lq[kXRows * kXD];   // Q'_j rows, 32 KiB
+  __shared__ __attribute__((aligned(16))) uint16_t lk[kXKeys * kXD];   // K'_j rows, 16 KiB
+  const int nrt = (a.Lr + kXRows - 1) / kXRows;
+  const int rt = nrt - 1 - (int)(blockIdx.x / a.Hq);                 // longest rows first
+  const int h = (int)(blockIdx.x % a.Hq);
+  const int hk = h / (a.Hq / a.Hk);
+  const int r0 = rt * kXRows;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, hi = lane >> 5;
+  const int row = r0 + wave * 32 + l32;            // this lane's reshaped row (column of S^T)
+  const uint16_t* qh = a.q + (int64_t)h * a.q_sh;
+  const uint16_t* kh = a.k + (int64_t)hk * a.k_sh;
+  const int S = a.S;
+  const int last_row = min(a.Lr, r0 + kXRows) - 1;
+  const int nct = last_row / kXKeys + 1;           // key tiles up to the diagonal
+  const bool row_ok = row < a.Lr;
+
+  float m_run = -INFINITY, l_run = 0.f, inv_l = 0.f;
+  if (PASS == 2 && row_ok) {
+    m_run = a.m[(int64_t)h * a.Lr + row];
+    inv_l = 1.0f / a.l[(int64_t)h * a.Lr + row];
+  }
+  const int rbs = a.rbs;                           // reshaped rows / keys per block: 8, 16 or 32
+  const int cbh = 32 / rbs;                        // blocks per 32-key half
+
+  for (int ct = 0; ct < nct; ++ct) {
+    const int n0 = ct * kXKeys;
+    f32x16_t acc[2];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[kk][r] = 0.f;
+    for (int j = 0; j < S; ++j) {
+      __syncthreads();                             // previous stage consumed
+      uint4 kv[kXKeys * 16 / kXThreads], qv[kXRows * 16 / kXThreads];
+#pragma unroll
+      for (int u = 0; u < kXKeys * 16 / kXThreads; ++u) {
+        const int e = tid + u * kXThreads, c = e >> 4, ch = e & 15;
+        const int t = (n0 + c) * S + j;
+        kv[u] = t < a.L ? *reinterpret_cast<const uint4*>(kh + (int64_t)t * a.k_sl + ch * 8) : make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < kXRows * 16 / kXThreads; ++u) {
+        const int e = tid + u * kXThreads, rr = e >> 4, ch = e & 15;
+        const int t = (r0 + rr) * S + S - 1 - j;
+        qv[u] = t < a.L ? *reinterpret_cast<const uint4*>(qh + (int64_t)t * a.q_sl + ch * 8) : make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < kXKeys * 16 / kXThreads; ++u) {
+        const int e = tid + u * kXThreads, c = e >> 4, ch = e & 15;
+        *reinterpret_cast<uint4*>(lk + c * kXD + ((ch ^ (c & 15)) << 3)) = kv[u];
+      }
+#pragma unroll
+      for (int u = 0; u < kXRows * 16 / kXThreads; ++u) {
+        const int e = tid + u * kXThreads, rr = e >> 4, ch = e & 15;
+        *reinterpret_cast<uint4*>(lq + rr * kXD + ((ch ^ (rr & 15)) << 3)) = qv[u];
+      }
+      __syncthreads();
+      const int qr = wave * 32 + l32;
+#pragma unroll
+      for (int st = 0; st < kXD / 16; ++st) {
+        const uint4 bq = *reinterpret_cast<const uint4*>(lq + qr * kXD + (((2 * st + hi) ^ (qr & 15)) << 3));
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          const int kr = kk * 32 + l32;
+          const uint4 ak = *reinterpret_cast<const uint4*>(lk + kr * kXD + (((2 * st + hi) ^ (kr & 15)) << 3));
+          acc[kk] = XMma<T>::mma(ak, bq, acc[kk]);
+        }
+      }
+    }
+
+    // ---- epilogue: lane holds keys n0 + 32 kk + (r/4) 8 + hi 4 + r%4 of its row
+    float x[2][16];
+    bool valid[2][16];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int n = n0 + kk * 32 + (r >> 2) * 8 + hi * 4 + (r & 3);
+        valid[kk][r] = row_ok && n <= row;
+        x[kk][r] = Conv<T>::round(acc[kk][r]) * a.scale;
+      }
+    if (PASS == 1) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (valid[kk][r]) mx = fmaxf(mx, x[kk][r]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));      // the row's other keys sit in lane ^ 32
+      const float m_new = fmaxf(m_run, mx);
+      if (m_new > -INFINITY) {
+        float s = 0.f;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if (valid[kk][r]) s += __builtin_amdgcn_exp2f(x[kk][r] - m_new);
+        l_run = l_run * __builtin_amdgcn_exp2f(m_run - m_new) + s;
+        m_run = m_new;
+      }
+    } else {
+      // block partials of this lane: block cb of half kk holds r with (r/4) / (rbs/8) == cb
+      const bool real_row = row_ok && row < a.real;
+      float part[2][4];
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) part[kk][cb] = 0.f;
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float p = (real_row && valid[kk][r]) ? __builtin_amdgcn_exp2f(x[kk][r] - m_run) * inv_l : 0.f;
+          const int cb = (r >> 2) / (rbs >> 3);
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            if (c == cb) part[kk][c] += p;
+        }
+      // sum over the rbs rows of the lane's block row and the two lane halves
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) {
+          if (cb >= cbh) continue;
+          float v = part[kk][cb];
+          for (int o = 1; o < rbs; o <<= 1) v += __shfl_xor(v, o, 64);
+          v += __shfl_xor(v, 32, 64);
+          part[kk][cb] = v;
+        }
+      if (hi == 0 && (l32 % rbs) == 0) {
+        const int I = (r0 + wave * 32 + l32) / rbs;
+        if (I < a.Nb) {
+#pragma unroll
+          for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb) {
+              if (cb >= cbh) continue;
+              const int J = (n0 + kk * 32) / rbs + cb;
+              if (J <= I) a.sums[((int64_t)h * a.Nb + I) * a.Nb + J] = Conv<T>::round(part[kk][cb]);
+            }
+        }
+      }
+    }
+  }
+  if (PASS == 1) {
+    const float lt = l_run + __shfl_xor(l_run, 32, 64);
+    if (row_ok && hi == 0) {
+      a.m[(int64_t)h * a.Lr + row] = m_run;
+      a.l[(int64_t)h * a.Lr + row] = lt;
+    }
+  }
+}
+
+struct XSelK {
+  const float* sums;            // [Hq][Nb][Nb]
+  const double* thr;            // [Hq]
+  int32_t* blk_cnt;             // [Hq][N]
+  uint16_t* blk_idx;            // [Hq][N][Nk]
+  int Hq, Nb, N, Nk, keep_sink;
+};
+
+__global__ __launch_bounds__(kXSelThreads) void xattn_select_kernel(XSelK a) {
+  __shared__ uint64_t key[kXMaxBlocks];             // (~value bits) << 32 | index: ascending = value desc, index asc
+  __shared__ double part[kXSelThreads];
+  __shared__ uint8_t sel[kXMaxBlocks];
+  const int h = (int)(blockIdx.x / a.N), I = (int)(blockIdx.x % a.N);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const float* row = a.sums + ((int64_t)h * a.Nb + I) * a.Nb;
+  const int n = I + 1;                              // causal blocks of the row
+  int P = 1;
+  while (P < n) P <<= 1;
+
+  // keys (the forced blocks enter the sorted list as zeros, as the
+  // reference's masked_fill does) and the row total in a fixed order
+  double tot = 0.0;
+  for (int J = tid; J < P; J += kXSelThreads) {
+    uint64_t kk = ~0ull;
+    if (J < n) {
+      const float v = row[J];
+      tot += (double)v;
+      const float vo = (J == 0 || J == I) ? 0.f : v;
+      kk = ((uint64_t)(~__float_as_uint(vo)) << 32) | (uint32_t)J;
+    }
+    key[J] = kk;
+    sel[J] = 0;
+  }
+  part[tid] = tot;
+  __syncthreads();
+  for (int s = kXSelThreads / 2; s > 0; s >>= 1) {
+    if (tid < s) part[tid] += part[tid + s];
+    __syncthreads();
+  }
+  const double total = part[0];
+  const double forced = (double)row[0] + (I > 0 ? (double)row[I] : 0.0);
+  const double required = total * a.thr[h];
+  __syncthreads();
+
+  // bitonic sort of key[0 .. P) ascending
+  for (int k2 = 2; k2 <= P; k2 <<= 1) {
+    for (int j2 = k2 >> 1; j2 > 0; j2 >>= 1) {
+      for (int i = tid; i < P; i += kXSelThreads) {
+        const int ixj = i ^ j2;
+        if (ixj > i) {
+          const uint64_t x = key[i], y = key[ixj];
+          const bool up = (i & k2) == 0;
+          if ((x > y) == up) {
+            key[i] = y;
+            key[ixj] = x;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+
+  // exclusive prefix masses of the sorted values: thread t owns positions
+  // [t * per, (t + 1) * per), its run summed in order, then a fixed-order scan
+  const int per = (P + kXSelThreads - 1) / kXSelThreads;
+  const int p0 = tid * per;
+  auto value_at = [&](int p) -> double {
+    const uint64_t kk = key[p];
+    if ((uint32_t)kk >= (uint32_t)n) return 0.0;   // padding
+    return (double)__uint_as_float(~(uint32_t)(kk >> 32));
+  };
+  double run = 0.0;
+  for (int p = p0; p < min(P, p0 + per); ++p) run += value_at(p);
+  part[tid] = run;
+  __syncthreads();
+  for (int off = 1; off < kXSelThreads; off <<= 1) {  // inclusive scan (Hillis-Steele, fixed order)
+    const double v = tid >= off ? part[tid - off] : 0.0;
+    __syncthreads();
+    part[tid] += v;
+    __syncthreads();
+  }
+  double before = forced + (part[tid] - run);
+  for (int p = p0; p < min(P, p0 + per); ++p) {
+    const uint32_t J = (uint32_t)key[p];
+    if (J < (uint32_t)n && before < required) sel[J] = 1;
+    before += value_at(p);
+  }
+  __syncthreads();
+
+  // ascending list: forced blocks, chosen blocks, the causal tril; keep_sink fills row 0
+  if (wave == 0) {
+    const int limit = (I == 0 && a.keep_sink) ? a.Nk : n;
+    uint16_t* out = a.blk_idx + ((int64_t)h * a.N + I) * a.Nk;
+    int cnt = 0;
+    for (int J0 = 0; J0 < limit; J0 += 64) {
+      const int J = J0 + lane;
+      bool in = false;
+      if (J < limit) in = J >= n || J == 0 || J == I || sel[J];
+      const uint64_t m = __ballot(in);
+      if (in) out[cnt + rank_below(m)] = (uint16_t)J;
+      cnt += __popcll(m);
+    }
+    if (lane == 0) a.blk_cnt[(int64_t)h * a.N + I] = cnt;
+  }
+}
+
+static size_t xattn_work(int Hq, int L, int stride, int bs) {
+  const int64_t Lp = ((int64_t)L + bs - 1) / bs * bs;
+  const int64_t Lr = Lp / stride;
+  return ((size_t)Hq * Lr * 2 * sizeof(float) + 255) & ~(size_t)255;
+}
+
+}  // namespace fs
+
+using namespace fs;
+
+extern "C" size_t fs_xattn_work_bytes(int Hq, int L, int stride, int bs) {
+  if (Hq <= 0 || L <= 0 || stride <= 0 || bs <= 0) return 0;
+  return xattn_work(Hq, L, stride, bs);
+}
+
+extern "C" int fs_xattn(const fs_xattn_args* a, void* stream) {
+  FS_CHECK_ARG(a != nullptr, "fs_xattn: null args");
+  FS_CHECK_ARG(a->q && a->k && a->threshold && a->sums && a->blk_cnt && a->blk_idx && a->work,
+               "fs_xattn: null pointer");
+  FS_CHECK_ARG(a->Hq > 0 && a->Hk > 0 && a->Hq % a->Hk == 0, "fs_xattn: Hq=%d must be a multiple of Hk=%d", a->Hq,
+               a->Hk);
+  FS_CHECK_ARG(a->L > 0, "fs_xattn: empty sequence");
+  FS_CHECK_SUPPORTED(a->dtype == FS_DTYPE_BF16 || a->dtype == FS_DTYPE_F16, "fs_xattn: dtype %d unsupported (bf16/f16)",
+                     a->dtype);
+  FS_CHECK_SUPPORTED(a->D == kXD, "fs_xattn: head_dim %d unsupported (128 only)", a->D);
+  // the reference asserts block_size == 128 (Xattention.py:360)
+  FS_CHECK_SUPPORTED(a->bs == 128, "fs_xattn: block size %d unsupported (128 only)", a->bs);
+  FS_CHECK_SUPPORTED(a->stride == 4 || a->stride == 8 || a->stride == 16, "fs_xattn: stride %d unsupported (4, 8, 16)",
+                     a->stride);
+  FS_CHECK_ARG(a->norm > 0.f, "fs_xattn: norm must be positive");
+  FS_CHECK_ARG(((uintptr_t)a->q % 16) == 0 && ((uintptr_t)a->k % 16) == 0 && a->q_sl % 8 == 0 && a->k_sl % 8 == 0 &&
+                   a->q_sh % 8 == 0 && a->k_sh % 8 == 0,
+               "fs_xattn: q/k must be 16-byte aligned with strides of whole 16-byte chunks");
+  const int N = (a->L + a->bs - 1) / a->bs;
+  FS_CHECK_SUPPORTED(N <= kXMaxBlocks, "fs_xattn: %d blocks > %d", N, kXMaxBlocks);
+  XScoreK k{};
+  k.q = static_cast<const uint16_t*>(a->q);
+  k.k = static_cast<const uint16_t*>(a->k);
+  k.q_sh = a->q_sh; k.q_sl = a->q_sl; k.k_sh = a->k_sh; k.k_sl = a->k_sl;
+  k.Hq = a->Hq; k.Hk = a->Hk; k.L = a->L; k.S = a->stride;
+  k.Lr = N * a->bs / a->stride;
+  k.real = (a->L + a->stride - 1) / a->stride;
+  k.rbs = a->bs / a->stride;
+  k.Nb = N;
+  k.scale = (float)(1.4426950408889634 / sqrt((double)a->D) / a->stride / a->norm);
+  k.m = static_cast<float*>(a->work);
+  k.l = k.m + (size_t)a->Hq * k.Lr;
+  k.sums = a->sums;
+  const unsigned grid = (unsigned)(a->Hq * ((k.Lr + kXRows - 1) / kXRows));
+  hipStream_t s = (hipStream_t)stream;
+  if (a->dtype == FS_DTYPE_BF16) {
+    xattn_scores_kernel<bf16_t, 1><<<grid, kXThreads, 0, s>>>(k);
+    xattn_scores_kernel<bf16_t, 2><<<grid, kXThreads, 0, s>>>(k);
+  } else {
+    xattn_scores_kernel<f16_t, 1><<<grid, kXThreads, 0, s>>>(k);
+    xattn_scores_kernel<f16_t, 2><<<grid, kXThreads, 0, s>>>(k);
+  }
+  if (int rc = fs_host::launch_status("fs_xattn (scores)")) return rc;
+  XSelK sk{};
+  sk.sums = a->sums;
+  sk.thr = a->threshold;
+  sk.blk_cnt = a->blk_cnt;
+  sk.blk_idx = a->blk_idx;
+  sk.Hq = a->Hq; sk.Nb = N; sk.N = N; sk.Nk = N; sk.keep_sink = a->keep_sink;
+  xattn_select_kernel<<<(unsigned)(a->Hq * N), kXSelThreads, 0, s>>>(sk);
+  return fs_host::launch_status("fs_xattn (select)");
+}

@@ -1,0 +1,157 @@
+"""XAttention's block selection on the gfx950 kernels, attending through the
+same block-sparse kernel as the FFT selector.
+
+Mirrors attn_src/xattn/src/Xattention.py: ``xattn_estimate`` (:14-303) and
+``Xattention_prefill`` (:306-406), whose callers use the Triton path
+(use_triton=True, "inverse" reshaping, kdb 1): reshaped antidiagonal scores,
+an exp2-domain causal softmax per reshaped row, block sums, and
+find_blocks_chunked's cumulative-mass choice per block row
+(attn_src/xattn/src/utils.py:44-200).  One C call (fs_xattn) runs all of it and
+emits the per-row block lists fs_bsattn reads.
+
+K/V may carry Hq heads (the reference asserts that: its callers pass
+repeat_kv'd K/V) or Hkv heads with Hq % Hkv == 0 (native GQA, read as they are).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from ._lib import XattnArgs
+from .attn import _check_layout, block_sparse_attention
+
+
+@dataclass
+class XSelection:
+    """Device-resident result of the XAttention selection."""
+    blk_cnt: torch.Tensor       # int32 [Hq, N]
+    blk_idx: torch.Tensor       # uint16 [Hq, N, N] (first blk_cnt entries of each row valid, ascending)
+    sums: torch.Tensor          # float32 [Hq, N, N]: block sums (values of the input dtype), causal part
+    stride: int
+    block_size: int
+
+    def dense_mask(self) -> torch.Tensor:
+        """[Hq, N, N] bool mask rebuilt from the block lists."""
+        H, N = self.blk_cnt.shape
+        idx = self.blk_idx.view(torch.int16).to(torch.int64) & 0xFFFF
+        valid = torch.arange(N, device=idx.device)[None, None, :] < self.blk_cnt[:, :, None].to(torch.int64)
+        m = torch.zeros(H, N, N + 1, dtype=torch.bool, device=idx.device)
+        m.scatter_(2, torch.where(valid, idx, torch.full_like(idx, N)), True)
+        return m[:, :, :N]
+
+    def nnz(self) -> int:
+        return int(self.blk_cnt.sum().item())
+
+
+_thr_cache: dict = {}
+
+
+def _thresholds(threshold, H: int, device) -> torch.Tensor:
+    """Per-head float64 thresholds as find_blocks_chunked forms them
+    (utils.py:90-105): a tensor (or sequence) is cast to float64 (a sequence
+    becomes a float32 tensor first, as torch.tensor makes it) and truncated or
+    padded with its last value to H heads; a number applies to every head."""
+    if isinstance(threshold, (int, float)):
+        t = torch.full((H,), float(threshold), dtype=torch.float64)
+    else:
+        t = torch.as_tensor(threshold)
+        if not t.is_floating_point():
+            t = t.float()
+        t = t.detach().to("cpu", torch.float64).flatten()
+        if t.numel() == 0:
+            raise ValueError("empty threshold")
+        t = t[:H] if t.numel() >= H else torch.cat([t, t[-1:].expand(H - t.numel())])
+    # device copies are cached: a fresh host-to-device copy would wait for the stream
+    key = (tuple(t.tolist()), str(device))
+    d = _thr_cache.get(key)
+    if d is None:
+        d = t.to(device)
+        _thr_cache[key] = d
+    return d
+
+
+def xattn_select(query_states: torch.Tensor, key_states: torch.Tensor, *, stride: int = 8, threshold=0.9,
+                 norm: float = 1.0, block_size: int = 128, keep_sink: bool = False,
+                 keep_recent: bool = False) -> XSelection:
+    """The causal block selection of xattn_estimate (Xattention.py:14-303) as
+    block lists.  q [1,Hq,L,D], k [1,Hq or Hkv,L,D] on the GPU (bf16/f16,
+    D = 128).  ``keep_recent`` adds the diagonal, which the selection always
+    keeps, so it changes nothing."""
+    q = _check_layout(query_states)
+    k = _check_layout(key_states)
+    assert q.shape[0] == 1 and k.shape[0] == 1, "batch size 1 only"          # Xattention.py:361
+    assert block_size == 128, "block_size must be 128"                          # Xattention.py:360
+    Hq, L, D = q.shape[1], q.shape[2], q.shape[3]
+    Hk = k.shape[1]
+    if k.shape[2] != L or k.shape[3] != D or Hq % Hk:
+        raise ValueError(f"query {tuple(q.shape)} and key {tuple(k.shape)} shapes do not match")
+    if q.dtype != k.dtype or q.dtype not in (torch.bfloat16, torch.float16):
+        raise TypeError(f"unsupported dtypes {q.dtype}, {k.dtype} (bf16/f16)")
+    N = -(-L // block_size)
+    dev = q.device
+    thr = _thresholds(threshold, Hq, dev)
+    sel = XSelection(blk_cnt=torch.empty(Hq, N, dtype=torch.int32, device=dev),
+                     blk_idx=torch.empty(Hq, N, N, dtype=torch.uint16, device=dev),
+                     sums=torch.zeros(Hq, N, N, dtype=torch.float32, device=dev),
+                     stride=stride, block_size=block_size)
+    lib = _lib.load()
+    work = torch.empty(max(1, lib.fs_xattn_work_bytes(Hq, L, stride, block_size)), dtype=torch.uint8, device=dev)
+    _lib.call("fs_xattn", XattnArgs(
+        q=q.data_ptr(), q_sh=q.stride(1), q_sl=q.stride(2), k=k.data_ptr(), k_sh=k.stride(1), k_sl=k.stride(2),
+        dtype=_lib.FS_DTYPE[q.dtype], Hq=Hq, Hk=Hk, L=L, D=D, stride=stride, bs=block_size, norm=float(norm),
+        threshold=thr.data_ptr(), keep_sink=int(bool(keep_sink)), sums=sel.sums.data_ptr(),
+        blk_cnt=sel.blk_cnt.data_ptr(), blk_idx=sel.blk_idx.data_ptr(), work=work.data_ptr()))
+    sel._keep = (thr, work)                          # alive until the stream has used them
+    return sel
+
+
+def xattn_estimate(query_states, key_states, block_size, stride, norm=1, softmax=True, threshold=0.9,
+                   chunk_size=16384, select_mode="inverse", use_triton=True, causal=True, kdb: int = 1,
+                   keep_sink=False, keep_recent=False):
+    """Xattention.py:14-303 on the GPU kernels: returns (attn_sums, simple_masks),
+    [1, H, N, N] in the input dtype and bool, N = ceil(L / block_size) (the
+    reference pads both to whole chunks; its Xattention_prefill keeps this
+    N x N corner).  The Triton path is the one computed, whatever
+    ``use_triton`` says; ``chunk_size`` only sizes the reference's working
+    buffers and does not change the result."""
+    if kdb != 1:
+        raise ValueError("use_triton and kdb cannot be used together")           # Xattention.py:144
+    if not causal:
+        raise NotImplementedError("the non-causal XAttention selection is not built")
+    if not softmax:
+        raise NotImplementedError("softmax=False is not built")
+    if select_mode not in ("inverse", ""):
+        raise NotImplementedError(f"select_mode {select_mode!r} is not built (the Triton path is 'inverse')")
+    sel = xattn_select(query_states, key_states, stride=stride, threshold=threshold, norm=norm,
+                       block_size=block_size, keep_sink=keep_sink, keep_recent=keep_recent)
+    return sel.sums.to(query_states.dtype)[None], sel.dense_mask()[None]
+
+
+def Xattention_prefill(query_states: torch.Tensor, key_states: torch.Tensor, value_states: torch.Tensor, stride,
+                       norm=1, threshold=0.8, block_size=128, use_triton=True, causal=True, kdb=1,
+                       chunk_size=None, keep_sink=False, keep_recent=False):
+    """Xattention.py:306-406: the XAttention selection, then block-sparse
+    causal attention over the chosen blocks.  q [1,H,L,D], k/v [1,H or Hkv,L,D]
+    -> [1, H, L, D] (a view of [1, L, H, D] storage, as the reference returns)."""
+    assert query_states.is_cuda, "input tensors must be on the GPU"
+    if kdb != 1:
+        raise ValueError("use_triton and kdb cannot be used together")
+    if not causal:
+        raise NotImplementedError("the non-causal XAttention selection is not built")
+    sel = xattn_select(query_states, key_states, stride=stride, threshold=threshold, norm=norm,
+                       block_size=block_size, keep_sink=keep_sink, keep_recent=keep_recent)
+    out = block_sparse_attention(query_states, key_states, value_states, sel.blk_cnt, sel.blk_idx,
+                                 block_size=block_size, is_causal=True)
+    return out.transpose(1, 2)
+
+
+def density(sel: XSelection) -> float:
+    """Selected tiles over the causal tiles (row 0's keep_sink blocks above the
+    diagonal are not computed and not counted)."""
+    H, N = sel.blk_cnt.shape
+    return min(1.0, sel.nnz() / (H * N * (N + 1) / 2))
+
+
+__all__ = ["XSelection", "xattn_select", "xattn_estimate", "Xattention_prefill", "density"]

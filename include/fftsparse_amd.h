@@ -24,6 +24,9 @@
  *                The dense [1,H,N,N] bool mask the reference hands to the
  *                kernel (my_attn_v7.py:710,780) is replaced by per-row lists
  *                of selected key blocks.
+ *   fs_xattn     XAttention's selector        attn_src/xattn/src/Xattention.py:14-303 (xattn_estimate),
+ *                                            utils.py:44-200 (find_blocks_chunked); the mask its
+ *                                            Xattention_prefill (:306-406) hands to block_sparse_attn_func
  *   fs_bsattn    block_sparse_attn_func call  my_attn_v7.py:775-786, fix_mask_attn/my_attn.py:196-207
  *                flash_attn_func(causal=True) my_attn_v7.py:509-519 (blk_cnt == NULL: dense causal)
  */
@@ -202,6 +205,38 @@ typedef struct {
 } fs_select_args;
 FS_API int fs_select(const fs_select_args* a, void* stream);
 
+/* ---- XAttention block selection ------------------------------------------
+ * The reference's other selector (attn_src/xattn/src/Xattention.py:14-303,
+ * Triton path: kernels.py:5-97, 195-234; find_blocks_chunked utils.py:44-200),
+ * causal, "inverse" reshaping, kdb 1, block size 128.  For query head h (key
+ * head h / (Hq/Hk)), stride S, reshaped row r and key n (tokens zero past L):
+ *   A[r][n]  = sum_{j<S} q[rS+S-1-j] . k[nS+j]  rounded to dtype,
+ *   p[r][n]  = exp2(x - max_r) / sum_r,  x = A log2(e) / sqrt(D) / S / norm, n <= r,
+ *              rows r >= ceil(L/S) zero,
+ *   sums[h][I][J] = sum of p over reshaped rows / keys of blocks I, J, rounded to dtype;
+ * then per block row I the blocks 0 and I, and the other blocks in decreasing
+ * order of sums while  sums(0) + sums(I) + (mass of the larger others) <
+ * row total * threshold[h]  (float64; ties: lower index first).  Outputs the
+ * ascending block lists blk_cnt [Hq][N], blk_idx [Hq][N][N] (N = ceil(L/bs),
+ * causal; keep_sink: row 0 lists every block) and the causal part of sums
+ * [Hq][N][N].  threshold: device array of Hq float64 values.  work:
+ * fs_xattn_work_bytes(Hq, L, stride, bs) bytes of device scratch.
+ * bf16/f16, D = 128, bs = 128, stride 4, 8 or 16, N <= 4096. */
+typedef struct {
+  const void* q; int64_t q_sh, q_sl;
+  const void* k; int64_t k_sh, k_sl;
+  int dtype, Hq, Hk, L, D, stride, bs;
+  float norm;
+  const double* threshold;
+  int keep_sink;
+  float* sums;
+  int32_t* blk_cnt;
+  uint16_t* blk_idx;
+  void* work;
+} fs_xattn_args;
+FS_API size_t fs_xattn_work_bytes(int Hq, int L, int stride, int bs);
+FS_API int fs_xattn(const fs_xattn_args* a, void* stream);
+
 /* ---- block-sparse attention prefill --------------------------------------
  * out[b][t][h] = softmax(q[b][h][t] . k[b][hk][s] * scale) v[b][hk][s] over the
  * key tokens s of the selected key blocks of query block t / bs (and s <= t +
@@ -237,7 +272,7 @@ FS_API int fs_bsattn_run(const fs_attn_args* a, void* stream);
 
 /* Description of the last failure on this thread ("" if none). */
 FS_API const char* fs_last_error(void);
-/* sizeof the argument struct: 0 pool, 1 corr, 2 stats, 3 select, 4 attn, 5 scores, 6 rope_pool
+/* sizeof the argument struct: 0 pool, 1 corr, 2 stats, 3 select, 4 attn, 5 scores, 6 rope_pool, 7 xattn
  * (lets a foreign-function binding check its struct layout). */
 FS_API size_t fs_sizeof_args(int which);
 /* ABI version of this library (increments on any struct change). */

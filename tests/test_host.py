@@ -35,7 +35,7 @@ def test_struct_layouts_match_library():
 
 def test_null_args_rejected_without_gpu():
     lib = _lib.load()
-    for name in ("fs_pool", "fs_rope_pool", "fs_corr", "fs_stats", "fs_scores", "fs_select", "fs_bsattn", "fs_bsattn_prepare",
+    for name in ("fs_pool", "fs_rope_pool", "fs_xattn", "fs_corr", "fs_stats", "fs_scores", "fs_select", "fs_bsattn", "fs_bsattn_prepare",
                  "fs_bsattn_run"):
         rc = getattr(lib, name)(None, None)
         assert rc == -1
@@ -50,6 +50,14 @@ def test_bad_shapes_rejected_without_gpu():
     assert b"D=96" in lib.fs_last_error()
     r.D, r.q_sl = 128, 100                                       # 200-byte row stride
     assert lib.fs_rope_pool(ctypes.byref(r), None) == -1
+    x = _lib.XattnArgs(q=16, k=16, threshold=16, sums=16, blk_cnt=16, blk_idx=16, work=16, dtype=1, Hq=4, Hk=1,
+                       L=4096, D=128, stride=8, bs=64, norm=1.0)
+    assert lib.fs_xattn(ctypes.byref(x), None) == -2              # the reference asserts block_size == 128
+    assert b"block size" in lib.fs_last_error()
+    x.bs, x.stride = 128, 32
+    assert lib.fs_xattn(ctypes.byref(x), None) == -2
+    x.stride, x.Hk = 8, 3
+    assert lib.fs_xattn(ctypes.byref(x), None) == -1
     a = _lib.AttnArgs(q=16, k=16, v=16, out=16, dtype=1, B=1, Hq=3, Hk=2, Lq=10, Lk=10, D=128, bs=128)
     assert lib.fs_bsattn(ctypes.byref(a), None) == -1
     a = _lib.AttnArgs(q=16, k=16, v=16, out=16, work=16, dtype=1, B=1, Hq=4, Hk=2, Lq=10, Lk=10, D=96, bs=128)
