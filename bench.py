@@ -41,6 +41,10 @@ def parse():
     ap.add_argument("--config", default="c2")
     ap.add_argument("--threshold", type=float, default=0.9)
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--selector", choices=("fftsparse", "xattn"), default="fftsparse",
+                    help="block selection: FFTSparse v7 (default) or XAttention (the reference's comparison "
+                         "selector, attn_src/xattn), both attending with the same block-sparse kernel")
+    ap.add_argument("--xattn-stride", type=int, default=8, help="XAttention's antidiagonal stride")
     ap.add_argument("--no-dense", action="store_true", help="skip the dense comparators")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--select-groups", type=int, default=None,
@@ -96,6 +100,41 @@ def cpu_baseline(q, k, v, kw, bs, nnz_total, sample_heads):
         "attn_ms_scaled": round(t_att * 1e3, 1),
         "cpu_model": _cpu_model(),
         "os_cpu_count": os.cpu_count(),
+    }
+
+
+def cpu_baseline_xattn(q, k, v, args, bs, nnz_total, sel):
+    """The XAttention oracle (oracle/xattn.py) on this host's cores, on a
+    bounded sample: the selection of one head over the first 16384 tokens,
+    scaled by the reshaped-score count to all heads and the full length (the
+    estimate is quadratic in L), and fp32 block-sparse attention over the first
+    query head's selected tiles, scaled by the tile count."""
+    import torch
+    from oracle import v7, xattn as xo
+    threads = torch.get_num_threads()
+    Ls = min(16384, q.shape[2])
+    qs, ks = q[:, :1, :Ls].cpu(), k[:, :1, :Ls].cpu()
+    t0 = time.perf_counter()
+    xo.xattn_mask(qs, ks, stride=args.xattn_stride, threshold=args.threshold, block_size=bs)
+    t_s = time.perf_counter() - t0
+    L, Hq = q.shape[2], q.shape[1]
+    t_sel = t_s * (L / Ls) ** 2 * Hq
+    mask = sel.dense_mask().cpu()
+    heads = [0]
+    tiles = int(mask[heads].sum())
+    qc, kc, vc = q.cpu(), k.cpu(), v.cpu()
+    t0 = time.perf_counter()
+    v7.block_sparse_attention(qc, kc, vc, mask, bs, heads=heads)
+    t_a = time.perf_counter() - t0
+    t_att = t_a * nnz_total / max(1, tiles)
+    return {
+        "value": round((t_sel + t_att) * 1e3, 1), "unit": "ms", "cores": threads, "kind": "port",
+        "sample": (f"oracle/xattn.py on this host ({threads} torch threads): selection of head 0 over the first "
+                   f"{Ls} tokens ({t_s:.1f} s) scaled x{(L / Ls) ** 2 * Hq:.0f} (quadratic in L, all heads); fp32 "
+                   f"block-sparse attention over head 0 ({tiles} tiles, {t_a:.1f} s) scaled x"
+                   f"{nnz_total / max(1, tiles):.1f} to {nnz_total} tiles"),
+        "select_ms": round(t_sel * 1e3, 1), "attn_ms_scaled": round(t_att * 1e3, 1),
+        "cpu_model": _cpu_model(), "os_cpu_count": os.cpu_count(),
     }
 
 
@@ -161,10 +200,17 @@ def main():
     # One step = selection (pool, corr, stats, select) + attention (V^T
     # pre-pass, then order + attention kernel), all on torch's current stream,
     # which is the stream the events below are recorded on.
+    xattn = args.selector == "xattn"
+    if xattn:
+        from fftsparse_amd.xattn import xattn_select
+
     def step(ev=None):
         if ev:
             ev[0].record()
-        sel = select_blocks(q, k, pipeline_groups=args.select_groups, **kw)
+        if xattn:
+            sel = xattn_select(q, k, stride=args.xattn_stride, threshold=args.threshold, block_size=bs)
+        else:
+            sel = select_blocks(q, k, pipeline_groups=args.select_groups, **kw)
         if ev:
             ev[1].record()
         call = AttentionCall(q, k, v, sel.blk_cnt, sel.blk_idx, block_size=bs)
@@ -193,7 +239,7 @@ def main():
     ms = statistics.mean(tot_ms)
 
     nnz = sel.nnz()
-    N = sel.params.N
+    N = -(-L // bs)
     density = nnz / (Hq * N * (N + 1) / 2)
     attn_flops = 4.0 * D * bs * bs * nnz
     t_att = statistics.mean(att_ms)
@@ -202,7 +248,7 @@ def main():
     esz = q.element_size()
     sel_bytes = L * Hq * D * esz + L * Hk * D * esz
     t_sel = statistics.mean(sel_ms)
-    stripe = int(sel.is_stripe.sum().item()) if sel.is_stripe is not None else None
+    stripe = int(sel.is_stripe.sum().item()) if not xattn and sel.is_stripe is not None else None
 
     dense = {}
     if not args.no_dense:
@@ -237,8 +283,31 @@ def main():
     cpu = None
     if not args.no_cpu:
         torch.cuda.synchronize()
-        cpu = cpu_baseline(q, k, v, kw, bs, nnz, args.cpu_heads)
+        if xattn:
+            cpu = cpu_baseline_xattn(q, k, v, args, bs, nnz, sel)
+        else:
+            cpu = cpu_baseline(q, k, v, kw, bs, nnz, args.cpu_heads)
 
+    if xattn:
+        # the two MFMA passes over the causal reshaped scores: 2 * S*D MACs per entry per pass
+        S = args.xattn_stride
+        Lr = N * bs // S
+        est_flops = 2 * Hq * (Lr * (Lr + 1) / 2) * 2.0 * S * D
+        roofline_select = {"bound": "mfma", "achieved": round(est_flops / (t_sel * 1e-3) / 1e12, 1),
+                           "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                           "frac": round(est_flops / (t_sel * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                           "work": f"2 passes x 2*S*D flop per causal reshaped score (S={S}, {Lr} reshaped rows per head)",
+                           "timed": "xattn_select: scores pass 1 (row stats), pass 2 (block sums), selection"}
+    else:
+        roofline_select = {"bound": "hbm", "achieved": round(sel_bytes / (t_sel * 1e-3) / 1e9, 1),
+                           "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                           "frac": round(sel_bytes / (t_sel * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                           "traffic": pmc_traffic("select", cfg.name),
+                           "work": "Q and K read once (L*(Hq+Hkv)*D*2 bytes)",
+                           "timed": "select_blocks: pool, block-score tiles + statistics (2 launches), block lists "
+                                    "(2 launches)"}
+    sel_desc = (f"XAttention selection (stride {args.xattn_stride}, threshold {args.threshold})" if xattn
+                else f"corr_threshold {args.threshold}, production kwargs")
     line = {
         "metric": METRIC,
         "value": round(ms, 4),
@@ -252,9 +321,10 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16" if q.dtype == torch.bfloat16 else str(q.dtype).replace("torch.", ""),
         "data": f"synthetic (fftsparse_amd.synth recipe, seed {args.seed})",
-        "config": {"workload": f"{cfg.name}: one layer, L={L}, Hq={Hq}, Hkv={Hk}, D={D}, block {bs}, "
-                               f"corr_threshold {args.threshold}, production kwargs",
-                   "seq_len": L, "global_batch": 1, "block_size": bs, "corr_threshold": args.threshold,
+        "config": {"workload": f"{cfg.name}: one layer, L={L}, Hq={Hq}, Hkv={Hk}, D={D}, block {bs}, {sel_desc}",
+                   "selector": args.selector,
+                   "seq_len": L, "global_batch": 1, "block_size": bs,
+                   ("xattn_threshold" if xattn else "corr_threshold"): args.threshold,
                    "parallelism": "none (1 GPU)"},
         "speedup_vs_dense": round(dense_ms / ms, 3) if dense_ms == dense_ms else None,
         "dense_ms": round(dense_ms, 3) if dense_ms == dense_ms else None,
@@ -270,16 +340,11 @@ def main():
         "stripe_heads": stripe,
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": pmc_traffic("bsattn", cfg.name),
+                     "traffic": None if xattn else pmc_traffic("bsattn", cfg.name),
                      "kernel": f"fs::bsattn_kernel<{bs},{'bf16' if q.dtype == torch.bfloat16 else 'f16'}>",
                      "work": f"4*D*bs^2 flop per selected (query block, key block) tile x {nnz} tiles",
                      "timed": "fs_bsattn_run (order pass + attention kernel), HIP events on the launch stream"},
-        "roofline_select": {"bound": "hbm", "achieved": round(sel_bytes / (t_sel * 1e-3) / 1e9, 1),
-                            "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                            "frac": round(sel_bytes / (t_sel * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-                            "traffic": pmc_traffic("select", cfg.name),
-                            "work": "Q and K read once (L*(Hq+Hkv)*D*2 bytes)",
-                            "timed": "select_blocks: pool, block-score tiles + statistics (2 launches), block lists (2 launches)"},
+        "roofline_select": roofline_select,
         "cpu_baseline": cpu,
         "input_gen_s": round(t_gen, 1),
     }
