@@ -24,18 +24,6 @@ int launch_status(const char* what) {
   return FS_OK;
 }
 
-int cu_count() {
-  static int cached[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] <= 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cached[dev] = n;
-  }
-  return cached[dev];
-}
-
 }  // namespace fs_host
 
 extern "C" const char* fs_last_error(void) { return fs_host::g_err; }

@@ -245,8 +245,6 @@ __device__ __forceinline__ float group16_sum(float v) {
 namespace fs_host {
 void set_error(const char* fmt, ...);
 int launch_status(const char* what);
-// compute units of the current device (cached per device)
-int cu_count();
 
 // Allow a kernel more than the default 64 KiB of dynamic LDS (gfx950: 160 KiB).
 template <typename K>

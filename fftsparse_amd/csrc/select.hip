@@ -32,19 +32,18 @@ __device__ __forceinline__ uint64_t range_bits(int w, int lo, int hi) {
   return upto & ~((1ull << b0) - 1);
 }
 
-// One work item: RPW consecutive query-block rows (r0 = (item % chunks) * RPW)
-// of head item / chunks.  DIFF selects the head kind served: false = stripe
-// heads and the fixed (dyn_mode 0) mask, no score panel and no dynamic LDS
-// (returns at once for a diffuse head); true = a diffuse head (the caller
-// has decided that), with the panel.
+// DIFF selects the head kind a launch serves: false = stripe heads and the
+// fixed (dyn_mode 0) mask, no score panel and no dynamic LDS; true = diffuse
+// heads, with the panel.  Each launch returns at once for heads of the other kind.
 template <typename T, bool DIFF>
-__device__ __forceinline__ void select_item(const fs_select_args& a, int item, int rows_per_wave, float inv_sqrt_d,
-                                            float* panel) {
+__global__ __launch_bounds__(kSelThreads) void select_kernel(fs_select_args a, int rows_per_wave,
+                                                             float inv_sqrt_d) {
+  extern __shared__ float panel[];       // [RPW][N] scores (diffuse heads) then [RPW][D] q rows
   const int RPW = rows_per_wave * kSelWaves;
   const int N = a.N, Nk = a.Nk, D = a.D;
   const int chunks = (N + RPW - 1) / RPW;
-  const int h = item / chunks;
-  const int r0 = (item - h * chunks) * RPW;
+  const int h = blockIdx.x / chunks;
+  const int r0 = (blockIdx.x - h * chunks) * RPW;
   const int hk = h / (a.Hq / a.Hk);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int NW = (Nk + 63) >> 6;                   // 64-block words per row
@@ -81,7 +80,7 @@ __device__ __forceinline__ void select_item(const fs_select_args& a, int item, i
 
   // ---- stripe / diffuse decision (:359-363); identical in every workgroup of the head
   bool stripe = false;
-  if (!DIFF && a.dyn_mode == 1) {
+  if (a.dyn_mode == 1) {
     float mv;
     if (a.stripe_all_diffuse) {
       mv = INFINITY;
@@ -93,13 +92,13 @@ __device__ __forceinline__ void select_item(const fs_select_args& a, int item, i
       mv = s / (float)a.n_samples;
       stripe = mv <= a.stripe_threshold;        // false for nan
     }
-    if (r0 == 0 && tid == 0) {
+    if (!DIFF && r0 == 0 && tid == 0) {
       if (a.mean_var) a.mean_var[h] = mv;
       if (a.is_stripe) a.is_stripe[h] = stripe ? 1 : 0;
     }
   }
-  const bool diffuse = DIFF || (a.dyn_mode == 1 && !stripe);
-  if (diffuse != DIFF) return;                     // the diffuse launch serves this head
+  const bool diffuse = a.dyn_mode == 1 && !stripe;
+  if (diffuse != DIFF) return;                     // the other launch serves this head
   const bool use_lags = a.dyn_mode == 1 && stripe;
   const bool use_cols = a.col_mode == 2 || (a.col_mode == 1 && stripe);
   const int rend = min(N, r0 + RPW);
@@ -291,64 +290,15 @@ __device__ __forceinline__ void select_item(const fs_select_args& a, int item, i
   }
 }
 
-constexpr int kMaxSelHeads = 1024;
-
-// DIFF = false: one workgroup per item.  DIFF = true: a persistent grid; each
-// workgroup takes the stripe / diffuse decision of every head once (the same
-// sums, in the same order, as the stripe launch), then serves the items of
-// the diffuse heads round-robin, so a launch with no diffuse head costs one
-// load round instead of one per item.
-template <typename T, bool DIFF>
-__global__ __launch_bounds__(kSelThreads) void select_kernel(fs_select_args a, int rows_per_wave, float inv_sqrt_d) {
-  extern __shared__ float panel[];       // [RPW][N] scores (diffuse heads) then [RPW][D] q rows
-  if constexpr (!DIFF) {
-    select_item<T, false>(a, blockIdx.x, rows_per_wave, inv_sqrt_d, panel);
-  } else {
-    __shared__ uint8_t diff_head[kMaxSelHeads];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int RPW = rows_per_wave * kSelWaves;
-    const int ns = a.n_samples;
-    if (a.stripe_all_diffuse) {
-      for (int hh = tid; hh < a.Hq; hh += kSelThreads) diff_head[hh] = 1;
-    } else {
-      // diag_var rows of as many heads as the panel holds, staged per round
-      const int cap = RPW * (a.N + a.D);
-      const int hpr = max(1, cap / ns);
-      for (int h0 = 0; h0 < a.Hq; h0 += hpr) {
-        const int nh = min(hpr, a.Hq - h0);
-        for (int e = tid; e < nh * ns; e += kSelThreads) panel[e] = a.diag_var[(int64_t)h0 * ns + e];
-        __syncthreads();
-        for (int hh = wave; hh < nh; hh += kSelWaves) {
-          float s = 0.f;
-          for (int i = lane; i < ns; i += 64) s += panel[hh * ns + i];
-          s = wave_sum(s);
-          if (lane == 0) diff_head[h0 + hh] = !(s / (float)ns <= a.stripe_threshold);   // nan: diffuse
-        }
-        __syncthreads();
-      }
-    }
-    __syncthreads();
-    const int chunks = (a.N + RPW - 1) / RPW;
-    for (int item = blockIdx.x; item < a.Hq * chunks; item += gridDim.x) {
-      if (!diff_head[item / chunks]) continue;
-      select_item<T, true>(a, item, rows_per_wave, inv_sqrt_d, panel);
-      __syncthreads();                             // the panel is reused by the next item
-    }
-  }
-}
-
 template <typename T>
 static int launch_select(const fs_select_args& a, unsigned grid, size_t smem, int rows_per_wave,
                          float inv_sqrt_d, hipStream_t s) {
   // stripe heads and the fixed mask: no panel
   select_kernel<T, false><<<grid, kSelThreads, 0, s>>>(a, rows_per_wave, inv_sqrt_d);
   if (a.dyn_mode == 1) {
-    // diffuse heads (possible only with the dynamic mask): a persistent grid
-    // of as many workgroups as the CUs hold at once with this LDS footprint
+    // diffuse heads (possible only with the dynamic mask)
     if (int rc = fs_host::allow_dynamic_lds(select_kernel<T, true>, smem, "fs_select")) return rc;
-    const int per_cu = max(1, (int)((160u * 1024u) / (smem + kMaxSelHeads + 4096u)));   // + static LDS
-    const unsigned pgrid = min(grid, (unsigned)(fs_host::cu_count() * per_cu));
-    select_kernel<T, true><<<pgrid, kSelThreads, smem, s>>>(a, rows_per_wave, inv_sqrt_d);
+    select_kernel<T, true><<<grid, kSelThreads, smem, s>>>(a, rows_per_wave, inv_sqrt_d);
   }
   return 0;
 }
@@ -372,7 +322,6 @@ extern "C" int fs_select(const fs_select_args* a, void* stream) {
   FS_CHECK_ARG((a->dyn_mode == 0 && a->col_mode == 0 && a->last_sel == nullptr) || a->N == a->Nk,
                "fs_select: dynamic, column and last-row masks need N == Nk");
   FS_CHECK_SUPPORTED(a->N <= 4096 && (a->dyn_mode == 0 || a->D <= 256), "fs_select: N=%d too large", a->N);
-  FS_CHECK_SUPPORTED(a->Hq <= kMaxSelHeads, "fs_select: %d query heads > %d", a->Hq, kMaxSelHeads);
   const int rows_per_wave = a->N <= 1024 ? 4 : (a->N <= 2048 ? 2 : 1);
   const int RPW = rows_per_wave * kSelWaves;
   const int chunks = (a->N + RPW - 1) / RPW;
