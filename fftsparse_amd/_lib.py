@@ -19,7 +19,7 @@ import torch  # noqa: F401  (must precede the library load, see module docstring
 LIB_PATH = Path(os.environ.get("FFTSPARSE_AMD_LIB") or Path(__file__).resolve().with_name("libfftsparse_amd.so"))
 
 FS_DTYPE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 
 class PoolArgs(ctypes.Structure):
@@ -45,6 +45,16 @@ class XattnArgs(ctypes.Structure):
                 ("dtype", c_int), ("Hq", c_int), ("Hk", c_int), ("L", c_int), ("D", c_int), ("stride", c_int),
                 ("bs", c_int), ("norm", c_float), ("threshold", c_void_p), ("keep_sink", c_int),
                 ("sums", c_void_p), ("blk_cnt", c_void_p), ("blk_idx", c_void_p), ("work", c_void_p)]
+
+
+class FlexArgs(ctypes.Structure):
+    _fields_ = [("q", c_void_p), ("q_sh", c_int64), ("q_sl", c_int64),
+                ("k", c_void_p), ("k_sh", c_int64), ("k_sl", c_int64),
+                ("dtype", c_int), ("Hq", c_int), ("Hk", c_int), ("L", c_int), ("D", c_int), ("bs", c_int),
+                ("gamma", c_float), ("tau", c_float), ("min_blocks", c_int), ("max_blocks", c_int),
+                ("gqa_interleave", c_int), ("blk_cnt", c_void_p), ("blk_idx", c_void_p),
+                ("head_info", c_void_p), ("head_js", c_void_p), ("vertical", c_void_p), ("slash", c_void_p),
+                ("work", c_void_p)]
 
 
 class CorrArgs(ctypes.Structure):
@@ -104,11 +114,12 @@ class AttnArgs(ctypes.Structure):
                 ("blk_cnt", c_void_p), ("blk_idx", c_void_p), ("work", c_void_p)]
 
 
-STRUCTS = [PoolArgs, CorrArgs, StatsArgs, SelectArgs, AttnArgs, ScoresArgs, RopePoolArgs, XattnArgs]
+STRUCTS = [PoolArgs, CorrArgs, StatsArgs, SelectArgs, AttnArgs, ScoresArgs, RopePoolArgs, XattnArgs, FlexArgs]
 
 ENTRY_POINTS = ["fs_pool", "fs_rope_pool", "fs_corr_work_bytes", "fs_corr", "fs_stats", "fs_scores_work_bytes",
                 "fs_scores", "fs_select", "fs_bsattn_work_bytes",
                 "fs_bsattn", "fs_bsattn_prepare", "fs_bsattn_run", "fs_xattn_work_bytes", "fs_xattn",
+                "fs_flex_work_bytes", "fs_flex",
                 "fs_last_error", "fs_abi_version", "fs_sizeof_args"]
 
 _lib = None
@@ -132,13 +143,16 @@ def load() -> ctypes.CDLL:
     lib.fs_corr_work_bytes.argtypes = [c_int, c_int, c_int]
     lib.fs_scores_work_bytes.restype = c_size_t
     lib.fs_scores_work_bytes.argtypes = [c_int, c_int, c_int]
+    lib.fs_flex_work_bytes.restype = c_size_t
+    lib.fs_flex_work_bytes.argtypes = [c_int, c_int, c_int, c_int]
     lib.fs_xattn_work_bytes.restype = c_size_t
     lib.fs_xattn_work_bytes.argtypes = [c_int, c_int, c_int, c_int]
     lib.fs_bsattn_work_bytes.restype = c_size_t
     lib.fs_bsattn_work_bytes.argtypes = [POINTER(AttnArgs)]
     for name, st in [("fs_pool", PoolArgs), ("fs_rope_pool", RopePoolArgs), ("fs_corr", CorrArgs),
                      ("fs_stats", StatsArgs), ("fs_scores", ScoresArgs), ("fs_select", SelectArgs), ("fs_bsattn", AttnArgs), ("fs_bsattn_prepare", AttnArgs),
-                     ("fs_bsattn_run", AttnArgs), ("fs_xattn", XattnArgs)]:
+                     ("fs_bsattn_run", AttnArgs), ("fs_xattn", XattnArgs),
+                     ("fs_flex", FlexArgs)]:
         fn = getattr(lib, name)
         fn.restype = c_int
         fn.argtypes = [POINTER(st), c_void_p]

@@ -27,7 +27,7 @@ int launch_status(const char* what) {
 }  // namespace fs_host
 
 extern "C" const char* fs_last_error(void) { return fs_host::g_err; }
-extern "C" int fs_abi_version(void) { return 7; }
+extern "C" int fs_abi_version(void) { return 8; }
 
 extern "C" size_t fs_sizeof_args(int which) {
   switch (which) {
@@ -39,6 +39,7 @@ extern "C" size_t fs_sizeof_args(int which) {
     case 5: return sizeof(fs_scores_args);
     case 6: return sizeof(fs_rope_pool_args);
     case 7: return sizeof(fs_xattn_args);
+    case 8: return sizeof(fs_flex_args);
     default: return 0;
   }
 }

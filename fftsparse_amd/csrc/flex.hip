@@ -1,0 +1,829 @@
+// FlexPrefill block selection on gfx950 -- the reference's third selector
+// (attn_src/Flexprefill.py:946-1061 get_active_blocks, with the budget
+// arithmetic of Flexprefill_prefill :1063-1098), emitting the per-row block
+// lists of the shared block-sparse attention kernel.
+//
+// flex_lastq_kernel<T, PASS, BS>: one workgroup (4 waves) per (head, chunk of
+// kFChunk key columns).  The last bs queries, q / sqrt(D) rounded to T, are
+// the B operand of v_mfma_f32_32x32x16 (wave w: row group w % (bs/32), column
+// group w / (bs/32)); the 128-key K tiles are staged in swizzled LDS.  Scores
+// are rounded to T (the reference's bf16 einsum), the last bs columns causal.
+//  PASS 1: each row's max and sum of exp(x - max) over the chunk (partials).
+//  PASS 2: the partials combined per row in a fixed order, p = exp(x - M) / S
+//  written to an LDS tile [bs][128]; column sums (vertical) and the sums along
+//  the diagonals ending at each column of the last row (slash), carried from
+//  tile to tile (a diagonal spans bs columns), each / bs.  A chunk starts one
+//  tile early so its first diagonals get their carry.
+//  The block size is a template parameter: with a run-time sub-tile count the
+//  MFMA chain holds branches, and on the path that leaves it after the first
+//  32x32x16 the compiler's wait before reading that result's last accumulator
+//  register was found too short (the read saw the value before the last MFMA).
+// flex_kpool_kernel: block means of K over each block's real rows, in T.
+// flex_head_kernel: one workgroup (1024 threads) per head:
+//   cover counts  n = #(descending prefix sums <= gamma) + 1 of vertical and
+//                 slash (a bisection on the value, fp64 fixed-order sums),
+//                 // 128 + 1, clamped to the block budgets;
+//   pooled        block sums of vertical / slash; the bs-row mean of the
+//                 scaled last queries against the K block means (T), softmax;
+//   js            square-root Jensen-Shannon divergence to the pooled vertical
+//                 (a zero probability gives nan, as in the reference);
+//   sparse heads  js < tau: both budgets become min_budget;
+//   choice        the top budgets of pooled vertical (block 0 forced) and
+//                 pooled slash (offset 0 forced), ties by the lower index, as
+//                 bit masks.
+// flex_cover_kernel: for each sparse head, the block-level causal attention
+//   softmax(avg_q / sqrt(D) avg_k^T) (block means of q, the last one rescaled
+//   to its real rows), and the entries whose descending prefix sum is at most
+//   gamma * N, as an N x N bit mask.
+// flex_lists_kernel: per (head, block row r): the vertical columns <= r, the
+//   diagonals r - s of the chosen slash offsets, the sparse cover's row, as an
+//   ascending list (64-bit words, popcount offsets).
+#include "common.h"
+
+namespace fs {
+
+constexpr int kFD = 128;
+constexpr int kFThreads = 256;
+constexpr int kFTile = 128;                      // key columns per tile
+constexpr int kFChunk = 2048;                    // key columns per workgroup
+constexpr int kFHeadThreads = 1024;
+constexpr int kFMaxBlocks = 4096;
+constexpr int kFWords = kFMaxBlocks / 64;
+
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+
+template <typename T> struct FMma;
+template <> struct FMma<bf16_t> {
+  static __device__ __forceinline__ f32x16_t mma(uint4 a, uint4 b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                   c, 0, 0, 0);
+  }
+};
+template <> struct FMma<f16_t> {
+  static __device__ __forceinline__ f32x16_t mma(uint4 a, uint4 b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b),
+                                                  c, 0, 0, 0);
+  }
+};
+
+struct FlexK {
+  const uint16_t* q;            // [Hq][L][D] view (strides q_sh, q_sl)
+  const uint16_t* k;
+  int64_t q_sh, q_sl, k_sh, k_sl;
+  int Hq, Hk, L, bs, nb, gqa_interleave, nchunk;
+  float sqrt_d;
+  float* part;                  // [Hq][nchunk][bs][2] (max, sum) per chunk
+  float* vert;                  // [Hq][L]
+  float* slash;                 // [Hq][L]
+};
+
+__device__ __forceinline__ int kv_head(int h, int Hq, int Hk, int interleave) {
+  return interleave ? (h % Hk) : (h / (Hq / Hk));
+}
+
+template <typename T, int PASS, int BS>
+__global__ __launch_bounds__(kFThreads) void flex_lastq_kernel(FlexK a) {
+  __shared__ __attribute__((aligned(16))) uint16_t lk[kFTile * kFD];        // 32 KiB
+  extern __shared__ float ptile[];                                           // PASS 2: [bs][kFTile] + carry
+  const int h = blockIdx.x / a.nchunk, chunk = blockIdx.x % a.nchunk;
+  const int kvh = kv_head(h, a.Hq, a.Hk, a.gqa_interleave);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, hi = lane >> 5;
+  constexpr int bs = BS;
+  const int L = a.L;
+  constexpr int RG = bs / 32, CG = 4 / RG;        // row groups, column groups
+  const int rg = wave % RG, cg = wave / RG;
+  constexpr int nsub = (kFTile / CG) / 32;        // 32-column sub-tiles per wave: 4 / CG
+  const int row = rg * 32 + l32;                  // this lane's query row (0 .. bs-1)
+  const int qtok = L - bs + row;
+  const uint16_t* qh = a.q + (int64_t)h * a.q_sh;
+  const uint16_t* kh = a.k + (int64_t)kvh * a.k_sh;
+
+  // B operand: q[L-bs+row] / sqrt(D) rounded to T, dims st*16 + hi*8 .. +7
+  uint4 qf[kFD / 16];
+#pragma unroll
+  for (int st = 0; st < kFD / 16; ++st) {
+    const uint4 raw = *reinterpret_cast<const uint4*>(qh + (int64_t)qtok * a.q_sl + st * 16 + hi * 8);
+    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float lo = to_f32(T{(uint16_t)(w[e] & 0xffffu)}) / a.sqrt_d;
+      const float up = to_f32(T{(uint16_t)(w[e] >> 16)}) / a.sqrt_d;
+      o[e] = (uint32_t)__builtin_bit_cast(uint16_t, Conv<T>::store(lo)) |
+             ((uint32_t)__builtin_bit_cast(uint16_t, Conv<T>::store(up)) << 16);
+    }
+    qf[st] = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+
+  const int c_begin = chunk * kFChunk;
+  const int c_end = min(L, c_begin + kFChunk);
+  // PASS 2 starts one tile early (carry of the diagonals that cross into the chunk)
+  const int t_first = (PASS == 2 && chunk > 0) ? c_begin - kFTile : c_begin;
+  float m_run = -INFINITY, l_run = 0.f;           // PASS 1, per lane (partial over its columns)
+  float M = 0.f, inv_s = 0.f;
+  float* ptl = ptile;                              // [bs][kFTile]
+  float* carry = ptile + bs * kFTile;              // [kFTile + bs] diagonal partials in flight
+  if (PASS == 2) {
+    // combine the chunk partials of this thread's rows in a fixed order
+    // (threads tid < bs each own row tid; the tile code reads them from LDS)
+    float* rowstat = carry + kFTile + bs;          // [bs][2]
+    if (tid < bs) {
+      const float* pp = a.part + ((int64_t)h * a.nchunk) * bs * 2;
+      float mx = -INFINITY;
+      for (int c = 0; c < a.nchunk; ++c) mx = fmaxf(mx, pp[((int64_t)c * bs + tid) * 2]);
+      float s = 0.f;
+      for (int c = 0; c < a.nchunk; ++c) {
+        const float mc = pp[((int64_t)c * bs + tid) * 2], lc = pp[((int64_t)c * bs + tid) * 2 + 1];
+        if (mc > -INFINITY) s += lc * expf(mc - mx);
+      }
+      rowstat[tid * 2] = mx;
+      rowstat[tid * 2 + 1] = 1.0f / s;
+    }
+    for (int e = tid; e < kFTile + bs; e += kFThreads) carry[e] = 0.f;
+    __syncthreads();
+    M = rowstat[row * 2];
+    inv_s = rowstat[row * 2 + 1];
+  }
+
+  for (int t0 = t_first; t0 < c_end; t0 += kFTile) {
+    __syncthreads();                               // previous K tile / p tile consumed
+    {
+      uint4 kv[kFTile * 16 / kFThreads];
+#pragma unroll
+      for (int u = 0; u < kFTile * 16 / kFThreads; ++u) {
+        const int e = tid + u * kFThreads, c = e >> 4, ch = e & 15;
+        const int t = t0 + c;
+        kv[u] = t < L ? *reinterpret_cast<const uint4*>(kh + (int64_t)t * a.k_sl + ch * 8) : make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < kFTile * 16 / kFThreads; ++u) {
+        const int e = tid + u * kFThreads, c = e >> 4, ch = e & 15;
+        *reinterpret_cast<uint4*>(lk + c * kFD + ((ch ^ (c & 15)) << 3)) = kv[u];
+      }
+    }
+    __syncthreads();
+    f32x16_t acc[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[s][r] = 0.f;
+#pragma unroll
+    for (int st = 0; st < kFD / 16; ++st) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        if (s >= nsub) break;
+        const int kr = (cg * nsub + s) * 32 + l32;
+        const uint4 ak = *reinterpret_cast<const uint4*>(lk + kr * kFD + (((2 * st + hi) ^ (kr & 15)) << 3));
+        acc[s] = FMma<T>::mma(ak, qf[st], acc[s]);
+      }
+    }
+    // lane: keys t0 + (cg nsub + s) 32 + (r/4) 8 + hi 4 + r%4 of query row `row`
+    const int lim_causal = L - bs + row;           // the last block: key <= query
+    if (PASS == 1) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        if (s >= nsub) break;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int c = t0 + (cg * nsub + s) * 32 + (r >> 2) * 8 + hi * 4 + (r & 3);
+          if (c < c_end && c <= lim_causal) mx = fmaxf(mx, Conv<T>::round(acc[s][r]));
+        }
+      }
+      const float m_new = fmaxf(m_run, mx);
+      if (m_new > -INFINITY) {
+        float sum = 0.f;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          if (s >= nsub) break;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int c = t0 + (cg * nsub + s) * 32 + (r >> 2) * 8 + hi * 4 + (r & 3);
+            if (c < c_end && c <= lim_causal) sum += expf(Conv<T>::round(acc[s][r]) - m_new);
+          }
+        }
+        l_run = l_run * expf(m_run - m_new) + sum;
+        m_run = m_new;
+      }
+    } else {
+      // p tile [bs][kFTile] in LDS
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        if (s >= nsub) break;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int cl = (cg * nsub + s) * 32 + (r >> 2) * 8 + hi * 4 + (r & 3);
+          const int c = t0 + cl;
+          const float p = (c < L && c <= lim_causal) ? expf(Conv<T>::round(acc[s][r]) - M) * inv_s : 0.f;
+          ptl[row * kFTile + cl] = p;
+        }
+      }
+      __syncthreads();
+      // vertical: column sums over the bs rows, in row order
+      if (t0 >= c_begin) {
+        for (int cl = tid; cl < kFTile; cl += kFThreads) {
+          const int c = t0 + cl;
+          if (c >= c_end) continue;
+          float s = 0.f;
+          for (int i = 0; i < bs; ++i) s += ptl[i * kFTile + cl];
+          a.vert[(int64_t)h * L + c] = s / (float)bs;
+        }
+      }
+      // slash: diagonal x (ending at column x of the last row) takes p[i][x + i - (bs-1)];
+      // this tile adds to the diagonals x in [t0, t0 + kFTile + bs - 1)
+      float dpart[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int j = tid + u * kFThreads;       // x = t0 + j
+        float s = 0.f;
+        if (j < kFTile + bs - 1) {
+          for (int i = 0; i < bs; ++i) {
+            const int cl = j + i - (bs - 1);
+            if (cl >= 0 && cl < kFTile) s += ptl[i * kFTile + cl];
+          }
+        }
+        dpart[u] = s;
+      }
+      __syncthreads();                             // carry read below is rewritten after
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int j = tid + u * kFThreads;
+        if (j < kFTile) {
+          const int x = t0 + j;
+          const float v = carry[j] + dpart[u];     // complete: no later column reaches x
+          if (t0 >= c_begin && x < c_end) a.slash[(int64_t)h * L + x] = v / (float)bs;
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int j = tid + u * kFThreads;
+        if (j >= kFTile && j < kFTile + bs - 1) carry[j - kFTile] = dpart[u];
+      }
+      for (int e = bs - 1 + tid; e < kFTile + bs; e += kFThreads) carry[e] = 0.f;
+    }
+  }
+  if (PASS == 1) {
+    // combine the row's columns held by the lanes of all column groups and both halves
+    float* red = ptile;                            // [4 waves][64 lanes][2]
+    red[(wave * 64 + lane) * 2] = m_run;
+    red[(wave * 64 + lane) * 2 + 1] = l_run;
+    __syncthreads();
+    if (tid < bs) {
+      const int rgi = tid / 32, li = tid % 32;
+      float mx = -INFINITY;
+      for (int c = 0; c < CG; ++c)
+        for (int hh = 0; hh < 2; ++hh) mx = fmaxf(mx, red[(((c * RG + rgi) * 64) + hh * 32 + li) * 2]);
+      float s = 0.f;
+      for (int c = 0; c < CG; ++c)
+        for (int hh = 0; hh < 2; ++hh) {
+          const int idx = (((c * RG + rgi) * 64) + hh * 32 + li) * 2;
+          if (red[idx] > -INFINITY) s += red[idx + 1] * expf(red[idx] - mx);
+        }
+      float* pp = a.part + (((int64_t)h * a.nchunk + chunk) * bs + tid) * 2;
+      pp[0] = mx;
+      pp[1] = s;
+    }
+  }
+}
+
+// block means of K over each block's real rows (triton_bnhd_pool "avg", Flexprefill.py:656-782)
+template <typename T>
+__global__ __launch_bounds__(kFThreads) void flex_kpool_kernel(const uint16_t* __restrict__ k, int64_t k_sh,
+                                                               int64_t k_sl, int L, int bs, int nb,
+                                                               uint16_t* __restrict__ avg_k) {
+  const int hk = blockIdx.x / nb, j = blockIdx.x % nb;
+  const int t0 = j * bs, rows = min(bs, L - t0);
+  const uint16_t* src = k + (int64_t)hk * k_sh;
+  for (int d = threadIdx.x; d < kFD; d += kFThreads) {
+    float s = 0.f;
+    for (int r = 0; r < rows; ++r) s += to_f32(T{src[(int64_t)(t0 + r) * k_sl + d]});
+    avg_k[((int64_t)hk * nb + j) * kFD + d] = __builtin_bit_cast(uint16_t, Conv<T>::store(s / (float)rows));
+  }
+}
+
+// ---- block reductions over 1024 threads (fixed order) ---------------------
+__device__ __forceinline__ double block_sum_d(double v, double* red) {
+  const int tid = threadIdx.x;
+  red[tid] = v;
+  __syncthreads();
+  for (int s = kFHeadThreads / 2; s > 0; s >>= 1) {
+    if (tid < s) red[tid] += red[tid + s];
+    __syncthreads();
+  }
+  const double r = red[0];
+  __syncthreads();
+  return r;
+}
+__device__ __forceinline__ float block_sum_f(float v, double* red) {
+  return (float)block_sum_d((double)v, red);
+}
+__device__ __forceinline__ float block_max_f(float v, double* red) {
+  const int tid = threadIdx.x;
+  red[tid] = (double)v;
+  __syncthreads();
+  for (int s = kFHeadThreads / 2; s > 0; s >>= 1) {
+    if (tid < s) red[tid] = fmax(red[tid], red[tid + s]);
+    __syncthreads();
+  }
+  const float r = (float)red[0];
+  __syncthreads();
+  return r;
+}
+
+// Count of the descending prefix sums of x[0 .. n) that are <= g (score_cover_topk
+// minus its + 1): the largest key t with sum(x >= t) <= g by bisection on the
+// order-preserving key, then the equal-valued elements just below t that still fit.
+__device__ int cover_count_dev(const float* x, int n, double g, double* red) {
+  const int tid = threadIdx.x;
+  auto mass_ge = [&](uint32_t key, int* cnt) -> double {
+    double s = 0.0;
+    int c = 0;
+    for (int i = tid; i < n; i += kFHeadThreads)
+      if (order_key(x[i]) >= key) {
+        s += (double)x[i];
+        ++c;
+      }
+    if (cnt) *cnt = (int)block_sum_d((double)c, red);
+    return block_sum_d(s, red);
+  };
+  // t* = smallest key with mass(>= t) <= g  (mass is nonincreasing in t)
+  uint32_t lo = 0, hi = 0xffffffffu;               // mass(>= hi) <= g for hi = max key (only +inf/nan above)
+  if (mass_ge(hi, nullptr) > g) return 0;
+  while (lo < hi) {
+    const uint32_t mid = lo + (hi - lo) / 2;
+    if (mass_ge(mid, nullptr) <= g) hi = mid;
+    else lo = mid + 1;
+  }
+  int cnt = 0;
+  const double m = mass_ge(hi, &cnt);
+  // elements just below t: the largest value u < t and how many equal it
+  float u = -INFINITY;
+  for (int i = tid; i < n; i += kFHeadThreads)
+    if (order_key(x[i]) < hi) u = fmaxf(u, x[i]);
+  u = block_max_f(u, red);
+  if (u == -INFINITY) return cnt;                 // nothing below
+  int mu = 0;
+  for (int i = tid; i < n; i += kFHeadThreads) mu += x[i] == u;
+  mu = (int)block_sum_d((double)mu, red);
+  if (u == 0.f) return cnt + mu;                   // zeros keep every prefix sum <= g
+  int extra = 0;
+  double s = m;
+  while (extra < mu && s + (double)u <= g) {
+    s += (double)u;
+    ++extra;
+  }
+  return cnt + extra;
+}
+
+struct FlexHeadK {
+  const uint16_t* q;
+  int64_t q_sh, q_sl;
+  const uint16_t* avg_k;        // [Hk][nb][D]
+  const float* vert;            // [Hq][L]
+  const float* slash;
+  int Hq, Hk, L, bs, nb, gqa_interleave, min_b, max_b;
+  float sqrt_d, gamma, tau;
+  uint64_t* vmask;              // [Hq][kFWords] chosen vertical blocks
+  uint64_t* smask;              // [Hq][kFWords] chosen slash offsets
+  int32_t* info;                // [Hq][4]: num_vertical, num_slash, sparse, cover counts packed below
+  float* js;                    // [Hq]
+};
+
+// the upper midpoint of [lo, hi], lo < hi, in (lo, hi]: the 64-bit sum keeps
+// hi - lo + 1 from wrapping to 0 on the full key range
+__device__ __forceinline__ uint32_t upper_mid(uint32_t lo, uint32_t hi) {
+  return lo + (uint32_t)(((uint64_t)hi - lo + 1) >> 1);
+}
+
+// the K largest of v[0 .. n) (ties: lower index first) as bits of out[kFWords]
+__device__ void topk_bits(const float* v, int n, int K, uint64_t* out, double* red) {
+  const int tid = threadIdx.x;
+  for (int w = tid; w < kFWords; w += kFHeadThreads) out[w] = 0;
+  __syncthreads();
+  if (K <= 0) return;
+  // smallest key t with count(>= t) <= K ... find the K-th largest key by bisection
+  auto count_ge = [&](uint32_t key) -> int {
+    int c = 0;
+    for (int i = tid; i < n; i += kFHeadThreads) c += order_key(v[i]) >= key;
+    return (int)block_sum_d((double)c, red);
+  };
+  uint32_t lo = 0, hi = 0xffffffffu;               // largest t with count(>= t) >= K
+  while (lo < hi) {
+    const uint32_t mid = upper_mid(lo, hi);
+    if (count_ge(mid) >= K) lo = mid;
+    else hi = mid - 1;
+  }
+  const uint32_t kth = lo;
+  const int above = count_ge(kth == 0xffffffffu ? kth : kth + 1);
+  int need = K - above;                            // equal-keyed elements to take, lowest index first
+  // serial pass in index order for the ties (n <= 4096)
+  if (tid == 0) {
+    for (int i = 0; i < n; ++i) {
+      const uint32_t ki = order_key(v[i]);
+      if (ki > kth || (ki == kth && need > 0)) {
+        if (ki == kth) --need;
+        out[i >> 6] |= 1ull << (i & 63);
+      }
+    }
+  }
+  __syncthreads();
+}
+
+template <typename T>
+__global__ __launch_bounds__(kFHeadThreads) void flex_head_kernel(FlexHeadK a) {
+  __shared__ double red[kFHeadThreads];
+  __shared__ float pv[kFMaxBlocks], ps[kFMaxBlocks], pk[kFMaxBlocks];
+  __shared__ float lqm[kFD];
+  const int h = blockIdx.x, tid = threadIdx.x;
+  const int L = a.L, bs = a.bs, nb = a.nb;
+  const float* vt = a.vert + (int64_t)h * L;
+  const float* st = a.slash + (int64_t)h * L;
+  const int kvh = kv_head(h, a.Hq, a.Hk, a.gqa_interleave);
+
+  // cover counts (score_cover_topk) -> block budgets
+  int nv = cover_count_dev(vt, L, (double)a.gamma, red) + 1;
+  int ns = cover_count_dev(st, L, (double)a.gamma, red) + 1;
+  nv = nv / 128 + 1;
+  ns = ns / 128 + 1;
+  nv = min(max(nv, a.min_b), a.max_b);
+  ns = min(max(ns, a.min_b), a.max_b);
+
+  // pooled vertical / slash (block sums in order)
+  for (int j = tid; j < nb; j += kFHeadThreads) {
+    float sv = 0.f, ss = 0.f;
+    for (int c = j * bs; c < min(L, (j + 1) * bs); ++c) {
+      sv += vt[c];
+      ss += st[c];
+    }
+    pv[j] = sv;
+    ps[j] = ss;
+  }
+  // mean over the bs rows of the scaled last queries, in T
+  if (tid < kFD) {
+    const uint16_t* qh = a.q + (int64_t)h * a.q_sh;
+    float s = 0.f;
+    for (int i = 0; i < bs; ++i) {
+      const float x = to_f32(T{qh[(int64_t)(L - bs + i) * a.q_sl + tid]}) / a.sqrt_d;
+      s += Conv<T>::round(x);
+    }
+    lqm[tid] = Conv<T>::round(s / (float)bs);
+  }
+  __syncthreads();
+  // avg_qk (T) and its softmax over the blocks
+  float mx = -INFINITY;
+  for (int j = tid; j < nb; j += kFHeadThreads) {
+    const uint16_t* kr = a.avg_k + ((int64_t)kvh * nb + j) * kFD;
+    float s = 0.f;
+    for (int d = 0; d < kFD; ++d) s += lqm[d] * to_f32(T{kr[d]});
+    pk[j] = Conv<T>::round(s);
+    mx = fmaxf(mx, pk[j]);
+  }
+  mx = block_max_f(mx, red);
+  float se = 0.f;
+  for (int j = tid; j < nb; j += kFHeadThreads) {
+    pk[j] = expf(pk[j] - mx);
+    se += pk[j];
+  }
+  se = block_sum_f(se, red);
+  // square-root JS divergence (nan when a probability is 0, as the reference's p log(p/m))
+  float t1 = 0.f, t2 = 0.f;
+  for (int j = tid; j < nb; j += kFHeadThreads) {
+    const float p = pk[j] / se, qq = pv[j];
+    const float m = (p + qq) / 2.f;
+    t1 += p * logf(p / m);
+    t2 += qq * logf(qq / m);
+  }
+  t1 = block_sum_f(t1, red);
+  t2 = block_sum_f(t2, red);
+  const float js = sqrtf(0.5f * t1 + 0.5f * t2);
+  const bool sparse = js < a.tau;
+  if (sparse) nv = ns = a.min_b;
+  if (tid == 0) {
+    pv[0] = INFINITY;
+    ps[nb - 1] = INFINITY;
+  }
+  __syncthreads();
+  topk_bits(pv, nb, min(nv, nb), a.vmask + (int64_t)h * kFWords, red);
+  // slash: top ns pooled entries j -> offsets nb - 1 - j
+  __shared__ uint64_t sb[kFWords];
+  topk_bits(ps, nb, min(ns, nb), sb, red);
+  for (int w = tid; w < kFWords; w += kFHeadThreads) a.smask[(int64_t)h * kFWords + w] = 0;
+  __syncthreads();
+  if (tid == 0) {
+    uint64_t* out = a.smask + (int64_t)h * kFWords;
+    for (int j = 0; j < nb; ++j)
+      if ((sb[j >> 6] >> (j & 63)) & 1) {
+        const int off = nb - 1 - j;
+        out[off >> 6] |= 1ull << (off & 63);
+      }
+    a.info[h * 4 + 0] = nv;
+    a.info[h * 4 + 1] = ns;
+    a.info[h * 4 + 2] = sparse ? 1 : 0;
+    a.info[h * 4 + 3] = 0;
+    a.js[h] = js;
+  }
+}
+
+struct FlexCoverK {
+  const uint16_t* q;
+  int64_t q_sh, q_sl;
+  const uint16_t* avg_k;        // [Hk][nb][D]
+  const int32_t* info;          // [Hq][4]
+  float* attn;                  // [Hq][nb][nb] work (sparse heads)
+  uint64_t* cover;              // [Hq][nb][kFWords]
+  int Hq, Hk, L, bs, nb, gqa_interleave;
+  float sqrt_d, gamma;
+};
+
+// block-level causal attention rows of a sparse head: one workgroup per (head, block row)
+template <typename T>
+__global__ __launch_bounds__(kFThreads) void flex_cover_rows_kernel(FlexCoverK a) {
+  __shared__ float aq[kFD];
+  __shared__ float rowv[kFMaxBlocks];
+  __shared__ float red[kFThreads];
+  const int h = blockIdx.x / a.nb, i = blockIdx.x % a.nb;
+  if (a.info[h * 4 + 2] == 0) return;              // not a sparse head
+  const int tid = threadIdx.x, bs = a.bs, nb = a.nb, L = a.L;
+  const int kvh = kv_head(h, a.Hq, a.Hk, a.gqa_interleave);
+  const int pad = nb * bs - L;
+  if (tid < kFD) {
+    // block mean of q over bs rows (zero padded), in T; the last block rescaled
+    // as (mean * bs) / (bs - pad), each step rounded to T
+    const uint16_t* qh = a.q + (int64_t)h * a.q_sh;
+    float s = 0.f;
+    for (int r = 0; r < bs; ++r) {
+      const int t = i * bs + r;
+      if (t < L) s += to_f32(T{qh[(int64_t)t * a.q_sl + tid]});
+    }
+    float m = Conv<T>::round(s / (float)bs);
+    if (pad && i == nb - 1) m = Conv<T>::round(Conv<T>::round(m * (float)bs) / (float)(bs - pad));
+    aq[tid] = Conv<T>::round(m / a.sqrt_d);
+  }
+  __syncthreads();
+  float mx = -INFINITY;
+  for (int j = tid; j <= i; j += kFThreads) {
+    const uint16_t* kr = a.avg_k + ((int64_t)kvh * nb + j) * kFD;
+    float s = 0.f;
+    for (int d = 0; d < kFD; ++d) s += aq[d] * to_f32(T{kr[d]});
+    rowv[j] = Conv<T>::round(s);
+    mx = fmaxf(mx, rowv[j]);
+  }
+  red[tid] = mx;
+  __syncthreads();
+  for (int s = kFThreads / 2; s > 0; s >>= 1) {
+    if (tid < s) red[tid] = fmaxf(red[tid], red[tid + s]);
+    __syncthreads();
+  }
+  mx = red[0];
+  __syncthreads();
+  float se = 0.f;
+  for (int j = tid; j <= i; j += kFThreads) {
+    rowv[j] = expf(rowv[j] - mx);
+    se += rowv[j];
+  }
+  red[tid] = se;
+  __syncthreads();
+  for (int s = kFThreads / 2; s > 0; s >>= 1) {
+    if (tid < s) red[tid] += red[tid + s];
+    __syncthreads();
+  }
+  se = red[0];
+  float* out = a.attn + ((int64_t)h * nb + i) * nb;
+  for (int j = tid; j < nb; j += kFThreads) out[j] = j <= i ? rowv[j] / se : 0.f;
+}
+
+// the cover of gamma * N over a sparse head's N x N probabilities (score_cover_idx)
+__global__ __launch_bounds__(kFHeadThreads) void flex_cover_select_kernel(FlexCoverK a) {
+  __shared__ double red[kFHeadThreads];
+  const int h = blockIdx.x, tid = threadIdx.x, nb = a.nb;
+  if (a.info[h * 4 + 2] == 0) return;
+  const float* x = a.attn + (int64_t)h * nb * nb;
+  const int n = nb * nb;
+  const int cnt = cover_count_dev(x, n, (double)a.gamma * nb, red);   // entries kept (no + 1)
+  // the cnt largest, ties by the lower flat index: bisection for the cnt-th largest key
+  uint64_t* cov = a.cover + (int64_t)h * nb * kFWords;
+  for (int e = tid; e < nb * kFWords; e += kFHeadThreads) cov[e] = 0;
+  __syncthreads();
+  if (cnt > 0) {
+    auto count_ge = [&](uint32_t key) -> int {
+      int c = 0;
+      for (int i = tid; i < n; i += kFHeadThreads) c += order_key(x[i]) >= key;
+      return (int)block_sum_d((double)c, red);
+    };
+    uint32_t lo = 0, hi = 0xffffffffu;
+    while (lo < hi) {
+      const uint32_t mid = upper_mid(lo, hi);
+      if (count_ge(mid) >= cnt) lo = mid;
+      else hi = mid - 1;
+    }
+    const uint32_t kth = lo;
+    const int above = kth == 0xffffffffu ? 0 : count_ge(kth + 1);
+    int need = cnt - above;
+    // strictly larger ones in parallel; equal ones in index order by one thread
+    for (int i = tid; i < n; i += kFHeadThreads)
+      if (order_key(x[i]) > kth) atomicOr(reinterpret_cast<unsigned long long*>(&cov[(i / nb) * kFWords + ((i % nb) >> 6)]),
+                                          1ull << ((i % nb) & 63));
+    __syncthreads();
+    // equal keys in flat index order: each thread owns a contiguous range, a
+    // fixed-order scan of the per-thread counts gives each element its rank
+    const int per = (n + kFHeadThreads - 1) / kFHeadThreads;
+    const int i0 = tid * per, i1 = min(n, i0 + per);
+    int mine = 0;
+    for (int i = i0; i < i1; ++i) mine += order_key(x[i]) == kth;
+    __shared__ int scan[kFHeadThreads];
+    scan[tid] = mine;
+    __syncthreads();
+    for (int off = 1; off < kFHeadThreads; off <<= 1) {
+      const int v = tid >= off ? scan[tid - off] : 0;
+      __syncthreads();
+      scan[tid] += v;
+      __syncthreads();
+    }
+    int rank = scan[tid] - mine;
+    for (int i = i0; i < i1 && rank < need; ++i)
+      if (order_key(x[i]) == kth) {
+        atomicOr(reinterpret_cast<unsigned long long*>(&cov[(i / nb) * kFWords + ((i % nb) >> 6)]),
+                 1ull << ((i % nb) & 63));
+        ++rank;
+      }
+  }
+  __syncthreads();
+  if (tid == 0) cov[0] |= 1ull;                    // entry 0 (the padding value of score_cover_idx)
+}
+
+struct FlexListK {
+  const uint64_t* vmask;
+  const uint64_t* smask;
+  const uint64_t* cover;        // [Hq][nb][kFWords] (rows of sparse heads)
+  const int32_t* info;
+  int32_t* blk_cnt;
+  uint16_t* blk_idx;
+  int Hq, nb;
+};
+
+// one wave per (head, block row): 64-bit membership words, popcount offsets
+__global__ __launch_bounds__(64) void flex_lists_kernel(FlexListK a) {
+  const int h = blockIdx.x / a.nb, r = blockIdx.x % a.nb;
+  const int lane = threadIdx.x, nb = a.nb;
+  const int NW = (nb + 63) >> 6;
+  const uint64_t* vm = a.vmask + (int64_t)h * kFWords;
+  const uint64_t* sm = a.smask + (int64_t)h * kFWords;
+  const bool sparse = a.info[h * 4 + 2] != 0;
+  uint64_t m = 0;
+  const int w = lane;
+  if (w < NW) {
+    // vertical columns v <= r
+    m = vm[w];
+    // slash: column c = r - s for offset s; bit b of word w is c = 64 w + b, s = r - c
+    for (int b = 0; b < 64; ++b) {
+      const int c = 64 * w + b;
+      if (c > r) break;
+      const int s = r - c;
+      if ((sm[s >> 6] >> (s & 63)) & 1) m |= 1ull << b;
+    }
+    if (sparse) m |= a.cover[((int64_t)h * nb + r) * kFWords + w];
+    const int b0 = 0, b1 = min(64, r + 1 - 64 * w);   // causal: columns <= r
+    if (b1 <= b0) m = 0;
+    else if (b1 < 64) m &= (1ull << b1) - 1;
+  }
+  const int c = __popcll(m);
+  int incl = c;
+  for (int o = 1; o < 64; o <<= 1) {
+    const int v = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += v;
+  }
+  const int total = __shfl(incl, 63, 64);
+  uint16_t* out = a.blk_idx + ((int64_t)h * nb + r) * nb;
+  int pos = incl - c;
+  while (m) {
+    const int b = __builtin_ctzll(m);
+    out[pos++] = (uint16_t)(64 * w + b);
+    m &= m - 1;
+  }
+  if (lane == 0) a.blk_cnt[(int64_t)h * nb + r] = total;
+}
+
+static size_t flex_work(int Hq, int Hk, int L, int bs, size_t* o_vert, size_t* o_slash, size_t* o_avgk,
+                        size_t* o_vmask, size_t* o_smask, size_t* o_info, size_t* o_attn, size_t* o_cover) {
+  const int nb = (L + bs - 1) / bs;
+  const int nchunk = (L + kFChunk - 1) / kFChunk;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off = (off + bytes + 255) & ~(size_t)255;
+    return at;
+  };
+  take((size_t)Hq * nchunk * bs * 2 * sizeof(float));                 // part at 0
+  const size_t v = take((size_t)Hq * L * sizeof(float));
+  const size_t s = take((size_t)Hq * L * sizeof(float));
+  const size_t k = take((size_t)Hk * nb * kFD * sizeof(uint16_t));
+  const size_t vm = take((size_t)Hq * kFWords * sizeof(uint64_t));
+  const size_t sm = take((size_t)Hq * kFWords * sizeof(uint64_t));
+  const size_t in = take((size_t)Hq * 4 * sizeof(int32_t) + (size_t)Hq * sizeof(float));
+  const size_t at = take((size_t)Hq * nb * nb * sizeof(float));
+  const size_t cv = take((size_t)Hq * nb * kFWords * sizeof(uint64_t));
+  if (o_vert) *o_vert = v;
+  if (o_slash) *o_slash = s;
+  if (o_avgk) *o_avgk = k;
+  if (o_vmask) *o_vmask = vm;
+  if (o_smask) *o_smask = sm;
+  if (o_info) *o_info = in;
+  if (o_attn) *o_attn = at;
+  if (o_cover) *o_cover = cv;
+  return off;
+}
+
+template <typename T, int BS>
+static int launch_lastq(const FlexK& k, unsigned grid, size_t smem1, size_t smem2, hipStream_t s) {
+  if (int rc = fs_host::allow_dynamic_lds(flex_lastq_kernel<T, 2, BS>, smem2, "fs_flex")) return rc;
+  flex_lastq_kernel<T, 1, BS><<<grid, kFThreads, smem1, s>>>(k);
+  flex_lastq_kernel<T, 2, BS><<<grid, kFThreads, smem2, s>>>(k);
+  return 0;
+}
+
+template <typename T>
+static int launch_flex(const fs_flex_args& a, hipStream_t s) {
+  const int nb = (a.L + a.bs - 1) / a.bs;
+  const int nchunk = (a.L + kFChunk - 1) / kFChunk;
+  size_t o_v, o_s, o_k, o_vm, o_sm, o_in, o_at, o_cv;
+  flex_work(a.Hq, a.Hk, a.L, a.bs, &o_v, &o_s, &o_k, &o_vm, &o_sm, &o_in, &o_at, &o_cv);
+  char* w = static_cast<char*>(a.work);
+  FlexK k{};
+  k.q = static_cast<const uint16_t*>(a.q);
+  k.k = static_cast<const uint16_t*>(a.k);
+  k.q_sh = a.q_sh; k.q_sl = a.q_sl; k.k_sh = a.k_sh; k.k_sl = a.k_sl;
+  k.Hq = a.Hq; k.Hk = a.Hk; k.L = a.L; k.bs = a.bs; k.nb = nb; k.gqa_interleave = a.gqa_interleave;
+  k.nchunk = nchunk;
+  k.sqrt_d = (float)sqrt((double)a.D);
+  k.part = reinterpret_cast<float*>(w);
+  k.vert = a.vertical ? a.vertical : reinterpret_cast<float*>(w + o_v);
+  k.slash = a.slash ? a.slash : reinterpret_cast<float*>(w + o_s);
+  const unsigned grid = (unsigned)(a.Hq * nchunk);
+  const size_t smem1 = (size_t)4 * 64 * 2 * sizeof(float);
+  const size_t smem2 = ((size_t)a.bs * kFTile + kFTile + a.bs + (size_t)a.bs * 2) * sizeof(float);
+  if (int rc = a.bs == 32    ? launch_lastq<T, 32>(k, grid, smem1, smem2, s)
+               : a.bs == 64 ? launch_lastq<T, 64>(k, grid, smem1, smem2, s)
+                            : launch_lastq<T, 128>(k, grid, smem1, smem2, s))
+    return rc;
+  uint16_t* avg_k = reinterpret_cast<uint16_t*>(w + o_k);
+  flex_kpool_kernel<T><<<(unsigned)(a.Hk * nb), kFThreads, 0, s>>>(k.k, a.k_sh, a.k_sl, a.L, a.bs, nb, avg_k);
+  if (int rc = fs_host::launch_status("fs_flex (scores)")) return rc;
+  FlexHeadK hk{};
+  hk.q = k.q; hk.q_sh = a.q_sh; hk.q_sl = a.q_sl;
+  hk.avg_k = avg_k; hk.vert = k.vert; hk.slash = k.slash;
+  hk.Hq = a.Hq; hk.Hk = a.Hk; hk.L = a.L; hk.bs = a.bs; hk.nb = nb; hk.gqa_interleave = a.gqa_interleave;
+  hk.min_b = a.min_blocks; hk.max_b = a.max_blocks;
+  hk.sqrt_d = k.sqrt_d; hk.gamma = a.gamma; hk.tau = a.tau;
+  hk.vmask = reinterpret_cast<uint64_t*>(w + o_vm);
+  hk.smask = reinterpret_cast<uint64_t*>(w + o_sm);
+  hk.info = a.head_info ? a.head_info : reinterpret_cast<int32_t*>(w + o_in);
+  hk.js = a.head_js ? a.head_js : reinterpret_cast<float*>(w + o_in + (size_t)a.Hq * 4 * sizeof(int32_t));
+  flex_head_kernel<T><<<(unsigned)a.Hq, kFHeadThreads, 0, s>>>(hk);
+  FlexCoverK ck{};
+  ck.q = k.q; ck.q_sh = a.q_sh; ck.q_sl = a.q_sl; ck.avg_k = avg_k; ck.info = hk.info;
+  ck.attn = reinterpret_cast<float*>(w + o_at);
+  ck.cover = reinterpret_cast<uint64_t*>(w + o_cv);
+  ck.Hq = a.Hq; ck.Hk = a.Hk; ck.L = a.L; ck.bs = a.bs; ck.nb = nb; ck.gqa_interleave = a.gqa_interleave;
+  ck.sqrt_d = k.sqrt_d; ck.gamma = a.gamma;
+  flex_cover_rows_kernel<T><<<(unsigned)(a.Hq * nb), kFThreads, 0, s>>>(ck);
+  flex_cover_select_kernel<<<(unsigned)a.Hq, kFHeadThreads, 0, s>>>(ck);
+  if (int rc = fs_host::launch_status("fs_flex (heads)")) return rc;
+  FlexListK lk{};
+  lk.vmask = hk.vmask; lk.smask = hk.smask; lk.cover = ck.cover; lk.info = hk.info;
+  lk.blk_cnt = a.blk_cnt; lk.blk_idx = a.blk_idx; lk.Hq = a.Hq; lk.nb = nb;
+  flex_lists_kernel<<<(unsigned)(a.Hq * nb), 64, 0, s>>>(lk);
+  return fs_host::launch_status("fs_flex (lists)");
+}
+
+}  // namespace fs
+
+using namespace fs;
+
+extern "C" size_t fs_flex_work_bytes(int Hq, int Hk, int L, int bs) {
+  if (Hq <= 0 || Hk <= 0 || L <= 0 || bs <= 0) return 0;
+  return flex_work(Hq, Hk, L, bs, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr);
+}
+
+extern "C" int fs_flex(const fs_flex_args* a, void* stream) {
+  FS_CHECK_ARG(a != nullptr, "fs_flex: null args");
+  FS_CHECK_ARG(a->q && a->k && a->blk_cnt && a->blk_idx && a->work, "fs_flex: null pointer");
+  FS_CHECK_ARG(a->Hq > 0 && a->Hk > 0 && a->Hq % a->Hk == 0, "fs_flex: Hq=%d must be a multiple of Hk=%d", a->Hq,
+               a->Hk);
+  FS_CHECK_SUPPORTED(a->dtype == FS_DTYPE_BF16 || a->dtype == FS_DTYPE_F16, "fs_flex: dtype %d unsupported (bf16/f16)",
+                     a->dtype);
+  FS_CHECK_SUPPORTED(a->D == kFD, "fs_flex: head_dim %d unsupported (128 only)", a->D);
+  FS_CHECK_SUPPORTED(a->bs == 32 || a->bs == 64 || a->bs == 128, "fs_flex: block size %d unsupported (32, 64, 128)",
+                     a->bs);
+  FS_CHECK_ARG(a->L > a->bs, "fs_flex: the sequence must be longer than one block");
+  FS_CHECK_ARG(a->min_blocks >= 1 && a->max_blocks >= 1, "fs_flex: bad budgets");
+  FS_CHECK_ARG(((uintptr_t)a->q % 16) == 0 && ((uintptr_t)a->k % 16) == 0 && a->q_sl % 8 == 0 && a->k_sl % 8 == 0 &&
+                   a->q_sh % 8 == 0 && a->k_sh % 8 == 0,
+               "fs_flex: q/k must be 16-byte aligned with strides of whole 16-byte chunks");
+  const int nb = (a->L + a->bs - 1) / a->bs;
+  FS_CHECK_SUPPORTED(nb <= kFMaxBlocks, "fs_flex: %d blocks > %d", nb, kFMaxBlocks);
+  hipStream_t s = (hipStream_t)stream;
+  return a->dtype == FS_DTYPE_BF16 ? launch_flex<bf16_t>(*a, s) : launch_flex<f16_t>(*a, s);
+}

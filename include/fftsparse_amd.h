@@ -27,6 +27,8 @@
  *   fs_xattn     XAttention's selector        attn_src/xattn/src/Xattention.py:14-303 (xattn_estimate),
  *                                            utils.py:44-200 (find_blocks_chunked); the mask its
  *                                            Xattention_prefill (:306-406) hands to block_sparse_attn_func
+ *   fs_flex      FlexPrefill's selector       attn_src/Flexprefill.py:946-1061 (get_active_blocks), the
+ *                                            block index sets its Flexprefill_prefill (:1063-1098) attends
  *   fs_bsattn    block_sparse_attn_func call  my_attn_v7.py:775-786, fix_mask_attn/my_attn.py:196-207
  *                flash_attn_func(causal=True) my_attn_v7.py:509-519 (blk_cnt == NULL: dense causal)
  */
@@ -237,6 +239,43 @@ typedef struct {
 FS_API size_t fs_xattn_work_bytes(int Hq, int L, int stride, int bs);
 FS_API int fs_xattn(const fs_xattn_args* a, void* stream);
 
+/* ---- FlexPrefill block selection -----------------------------------------
+ * The reference's third selector (attn_src/Flexprefill.py:946-1061,
+ * get_active_blocks; budgets as Flexprefill_prefill :1080-1096 derives them).
+ * For query head h (key head h / (Hq/Hk), or h % Hk with gqa_interleave):
+ * the last bs queries / sqrt(D) against every key (scores in dtype, the last
+ * block causal, fp32 softmax); vertical = mean over those rows, slash = sums
+ * along the diagonals ending at each column of the last row / bs; budgets
+ * (#descending prefix sums <= gamma, + 1) / 128 + 1 clamped to
+ * [min_blocks, max_blocks]; heads whose square-root JS divergence between the
+ * softmax of (row-mean last query) . (K block means) and the pooled vertical
+ * is below tau take min_blocks and, in addition, the cover of gamma * N of
+ * their block-level causal attention; the top pooled vertical columns (block 0
+ * forced) in every row at or after them and the top pooled slash offsets
+ * (offset 0 forced) as block diagonals (ties: lower index).  Outputs ascending
+ * block lists blk_cnt [Hq][N], blk_idx [Hq][N][N] (N = ceil(L/bs)), optionally
+ * head_info [Hq][4] (vertical budget, slash budget, sparse, 0), head_js [Hq]
+ * and the per-token vertical / slash profiles [Hq][L] (fp32).
+ * work: fs_flex_work_bytes(Hq, Hk, L, bs) bytes.  bf16/f16, D = 128,
+ * bs 32, 64 or 128, L > bs, N <= 4096. */
+typedef struct {
+  const void* q; int64_t q_sh, q_sl;
+  const void* k; int64_t k_sh, k_sl;
+  int dtype, Hq, Hk, L, D, bs;
+  float gamma, tau;
+  int min_blocks, max_blocks;
+  int gqa_interleave;
+  int32_t* blk_cnt;
+  uint16_t* blk_idx;
+  int32_t* head_info;
+  float* head_js;
+  float* vertical;
+  float* slash;
+  void* work;
+} fs_flex_args;
+FS_API size_t fs_flex_work_bytes(int Hq, int Hk, int L, int bs);
+FS_API int fs_flex(const fs_flex_args* a, void* stream);
+
 /* ---- block-sparse attention prefill --------------------------------------
  * out[b][t][h] = softmax(q[b][h][t] . k[b][hk][s] * scale) v[b][hk][s] over the
  * key tokens s of the selected key blocks of query block t / bs (and s <= t +
@@ -272,7 +311,8 @@ FS_API int fs_bsattn_run(const fs_attn_args* a, void* stream);
 
 /* Description of the last failure on this thread ("" if none). */
 FS_API const char* fs_last_error(void);
-/* sizeof the argument struct: 0 pool, 1 corr, 2 stats, 3 select, 4 attn, 5 scores, 6 rope_pool, 7 xattn
+/* sizeof the argument struct: 0 pool, 1 corr, 2 stats, 3 select, 4 attn, 5 scores, 6 rope_pool, 7 xattn,
+ * 8 flex
  * (lets a foreign-function binding check its struct layout). */
 FS_API size_t fs_sizeof_args(int which);
 /* ABI version of this library (increments on any struct change). */

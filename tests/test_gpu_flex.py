@@ -1,0 +1,269 @@
+"""GPU parity of the FlexPrefill selector (fs_flex through the C ABI) against
+the CPU oracle (oracle/flex.py), and of attention under its block lists.
+
+Bars:
+  profiles   the per-token vertical / slash profiles within 2e-5 of the
+             oracle's in L1 per head (their total is 1; the fp32 MFMA sums put
+             about 1 score in 1e4 on the other side of a rounding step of the
+             input dtype, which moves the profiles by ~1e-7);
+  budgets    vertical / slash budgets, the sparse-head test and the JS
+             divergence (within 1e-4) as the oracle's, except where a
+             prefix sum that would change a budget lies within 1e-4 of gamma
+             or the divergence within 2e-4 of tau;
+  own rule   the oracle's rule applied to the kernel's own profiles gives the
+             kernel's block lists exactly (positions whose decision rests on a
+             pooled value within 1e-5 relative of its top-K boundary, or a
+             sparse head's block attention within 0.2% of the cover's boundary
+             value, excused);
+  blocks     exact for >= 99% of the causal blocks, and exact or excused
+             where a near-tie decides them (pooled values 1e-4 relative, cover
+             values 0.2%) for >= 99.9%;
+  attention  under the kernel's lists within max-abs 2e-2 and mean-abs 1e-3 of
+             fp32 attention under the same mask.
+"""
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from fftsparse_amd.flex import Flexprefill_prefill, density, flex_select
+from fftsparse_amd.synth import make_qkv
+from oracle import flex as fo
+from oracle import v7
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+def _case(**kw):
+    print("[case] flex " + " ".join(f"{k}={v}" for k, v in kw.items()), flush=True)
+
+
+def _blhd(q, k, v=None):
+    """make_qkv's [1, H, L, D] as the reference's [1, L, H, D]."""
+    out = [x.transpose(1, 2).contiguous() for x in ((q, k) if v is None else (q, k, v))]
+    return out
+
+
+def _near_ties(ref: fo.FlexSelection, rel: float, nb: int, cover_rel: float) -> torch.Tensor:
+    """[H, nb, nb] positions whose decision rests on a pooled vertical or slash
+    value within ``rel`` of the top-K boundary, or (sparse heads) on a
+    block-level attention value within ``cover_rel`` of the cover's boundary
+    value (the block scores are rounded to the input dtype: a score on the
+    other side of a rounding step moves its probability by ~0.4% in bf16)."""
+    H = ref.mask.shape[0]
+    ex = torch.zeros(H, nb, nb, dtype=torch.bool)
+    for h in torch.nonzero(ref.sparse).flatten().tolist():
+        b = float(ref.cover_boundary[h])
+        ex[h] |= (ref.cover_attn[h] - b).abs() <= cover_rel * b
+    rows = torch.arange(nb)
+    for h in range(H):
+        for pooled, K, is_v in ((ref.vertical[h], int(ref.num_vertical[h]), True),
+                                (ref.slash[h], int(ref.num_slash[h]), False)):
+            if K >= nb:
+                continue
+            vals = pooled.double().sort(descending=True).values
+            if not torch.isfinite(vals[K - 1]):
+                continue                              # only the forced entry is chosen: no tie to break
+            bnd = 0.5 * (vals[K - 1] + vals[K])
+            near = ((pooled.double() - bnd).abs() <= rel * bnd.abs()).nonzero().flatten().tolist()
+            for j in near:
+                if is_v:
+                    ex[h, j:, j] = True
+                else:
+                    s = nb - 1 - j
+                    r = rows[:nb - s]
+                    ex[h, r + s, r] = True
+    return ex
+
+
+def _head_excused(ref: fo.FlexSelection, tau: float, band: float) -> torch.Tensor:
+    """Heads whose budgets or sparse test rest on a near-tie: a prefix sum that
+    would change a block budget within ``band`` of gamma, or the divergence
+    within 2 band of tau."""
+    return (ref.v_budget_margin <= band) | (ref.s_budget_margin <= band) | ((ref.js - tau).abs() <= 2 * band)
+
+
+def _pick_tau(q, k, bs, gamma, **kw):
+    """A tau between the oracle's divergences, so that some heads are sparse and
+    some are not, away from every head's divergence."""
+    js = fo.active_blocks(q, k, bs, gamma, 0.0, **kw).js.double().sort().values
+    H = js.numel()
+    gaps = [(float(js[i + 1] - js[i]), i) for i in range(H - 1)]
+    gap, i = max(gaps, key=lambda g: (g[0] > 0.01, -abs(g[1] - (H - 1) / 2), g[0]))
+    return float(0.5 * (js[i] + js[i + 1]))
+
+
+def _check(q, k, *, bs, gamma, tau, min_budget=None, max_budget=None, gqa_interleave=False):
+    """q, k [1, L, H, D] on the CPU."""
+    L = q.shape[1]
+    nb = -(-L // bs)
+    kw = dict(min_budget=min_budget, max_budget=max_budget, gqa_interleave=gqa_interleave)
+    sel = flex_select(q.to(DEV), k.to(DEV), gamma=gamma, tau=tau, block_size=bs, **kw)
+    torch.cuda.synchronize()
+    ref = fo.active_blocks(q, k, bs, gamma, tau, **kw)
+    H = ref.mask.shape[0]
+    # profiles
+    gv, gs = sel.vertical.cpu(), sel.slash.cpu()
+    l1v = (gv - ref.vertical_t).abs().sum(-1).max().item()
+    l1s = (gs - ref.slash_t).abs().sum(-1).max().item()
+    print(f"  profiles: L1 vertical {l1v:.2e} slash {l1s:.2e}")
+    assert l1v <= 2e-5 and l1s <= 2e-5
+    # budgets, sparse heads, divergence
+    info = sel.head_info.cpu()
+    js = sel.js.cpu()
+    band = 1e-4
+    hx = _head_excused(ref, tau, band)
+    print(f"  heads: nv {info[:, 0].tolist()} ns {info[:, 1].tolist()} sparse {info[:, 2].tolist()} "
+          f"js {[round(x, 4) for x in js.tolist()]} tau {tau:.4f} excused {hx.tolist()}")
+    for h in range(H):
+        if hx[h]:
+            continue
+        assert int(info[h, 0]) == int(ref.num_vertical[h]) and int(info[h, 1]) == int(ref.num_slash[h]), h
+        assert bool(info[h, 2]) == bool(ref.sparse[h]), h
+        assert abs(js[h].item() - ref.js[h].item()) <= band, h
+    # the oracle's rule on the kernel's own profiles gives the kernel's lists
+    g_mask = sel.dense_mask().cpu()
+    own = fo.active_blocks(q, k, bs, gamma, tau, profiles=(gv, gs), **kw)
+    assert torch.equal(info[:, 0], own.num_vertical.to(torch.int32))
+    assert torch.equal(info[:, 1], own.num_slash.to(torch.int32))
+    own_hx = _head_excused(own, tau, 1e-5)
+    own_ex = _near_ties(own, 1e-5, nb, 2e-3) | own_hx[:, None, None]
+    d_own = (own.mask != g_mask) & ~own_ex
+    assert not d_own.any(), torch.nonzero(d_own)[:5]
+    for h in range(H):
+        if not own_hx[h]:
+            assert bool(info[h, 2]) == bool(own.sparse[h])
+    # blocks against the oracle, near ties excused
+    tril = torch.tril(torch.ones(nb, nb, dtype=torch.bool))
+    diff = (g_mask != ref.mask) & tril
+    excused = _near_ties(ref, 1e-4, nb, 2e-3) | hx[:, None, None]
+    total = int(tril.sum()) * H
+    unexc = int((diff & ~excused).sum())
+    frac = (total - unexc) / total
+    print(f"  blocks: exact {1 - int(diff.sum()) / total:.6f}, exact-or-excused {frac:.6f}, "
+          f"excusable {int((excused & tril).sum()) / total:.4f}, density {density(sel):.4f}")
+    assert frac >= 0.999
+    assert int(diff.sum()) <= 0.01 * total                 # and exact for >= 99% outright
+    # invariants: causal, column 0 and the diagonal in every row
+    assert not (g_mask & ~tril).any()
+    assert g_mask[:, :, 0].all() and g_mask[:, torch.arange(nb), torch.arange(nb)].all()
+    return sel, g_mask, info
+
+
+@pytest.mark.parametrize("L,Hq,Hk,bs,gamma,dtype,budget", [
+    (8192, 4, 2, 128, 0.9, torch.bfloat16, (None, None)),
+    (6000, 4, 1, 64, 0.95, torch.bfloat16, (256, 2048)),        # ragged: L % 64 != 0, token budgets
+    (4100, 2, 2, 32, 0.9, torch.float16, (1024, None)),         # ragged, 32-token blocks
+    (8192, 8, 8, 64, 0.99, torch.bfloat16, (None, 512)),        # MHA, max budget clamps
+])
+def test_flex_selection_parity(L, Hq, Hk, bs, gamma, dtype, budget):
+    _case(L=L, Hq=Hq, Hk=Hk, bs=bs, gamma=gamma, dtype=dtype, budget=budget)
+    q, k, _ = make_qkv(L, Hq, Hk, dtype=dtype, seed=41)
+    q, k = _blhd(q, k)
+    mn, mx = budget
+    tau = _pick_tau(q, k, bs, gamma, min_budget=mn, max_budget=mx)
+    _, _, info = _check(q, k, bs=bs, gamma=gamma, tau=tau, min_budget=mn, max_budget=mx)
+    assert 0 < int(info[:, 2].sum()) < Hq, "both sparse and non-sparse heads exercised"
+
+
+def test_flex_tau_zero_and_gqa_interleave():
+    """tau = 0 (the reference's default: no sparse heads) and interleaved GQA
+    (query head h reads key head h % Hk)."""
+    _case(L=4096, tau=0, gqa_interleave=True)
+    q, k, _ = make_qkv(4096, 4, 2, dtype=torch.bfloat16, seed=42)
+    q, k = _blhd(q, k)
+    _, _, info = _check(q, k, bs=64, gamma=0.9, tau=0.0, gqa_interleave=True)
+    assert int(info[:, 2].sum()) == 0
+    tau = _pick_tau(q, k, 64, 0.9, gqa_interleave=True)
+    _check(q, k, bs=64, gamma=0.9, tau=tau, gqa_interleave=True)
+
+
+def test_flex_strided_layout_equals_contiguous():
+    """The projections' [1, L, H, D] layout as given and made contiguous per head give the same lists."""
+    _case(L=4096, layout="strided")
+    q, k, _ = make_qkv(4096, 4, 2, dtype=torch.bfloat16, seed=43)
+    qa, ka = _blhd(q, k)
+    a = flex_select(qa.to(DEV), ka.to(DEV), gamma=0.9, tau=0.3, block_size=128)
+    qb = q.to(DEV).transpose(1, 2)                       # [1, L, H, D] view of [1, H, L, D] memory
+    kb = k.to(DEV).transpose(1, 2)
+    b = flex_select(qb, kb, gamma=0.9, tau=0.3, block_size=128)
+    assert torch.equal(a.blk_cnt, b.blk_cnt) and torch.equal(a.dense_mask(), b.dense_mask())
+    assert torch.equal(a.head_info, b.head_info) and torch.equal(a.vertical, b.vertical)
+
+
+def test_flex_prefill_attention_parity():
+    """Flexprefill_prefill: [B, L, H, D] in and out; attention under the
+    kernel's own lists against fp32 attention under the same mask."""
+    _case(L=8192, prefill=True)
+    q, k, v = make_qkv(8192, 4, 1, dtype=torch.bfloat16, seed=44)
+    ql, kl, vl = _blhd(q, k, v)
+    tau = _pick_tau(ql, kl, 128, 0.9)
+    out = Flexprefill_prefill(ql.to(DEV), kl.to(DEV), vl.to(DEV), gamma=0.9, tau=tau, block_size=128)
+    torch.cuda.synchronize()
+    assert out.shape == (1, 8192, 4, 128) and out.dtype == torch.bfloat16
+    sel = flex_select(ql.to(DEV), kl.to(DEV), gamma=0.9, tau=tau, block_size=128)
+    mask = sel.dense_mask().cpu()
+    ref = v7.block_sparse_attention(q, k, v, mask, 128)            # [L, H, D]
+    err = (out[0].float().cpu() - ref).abs()
+    print(f"  density {density(sel):.4f} max_abs={err.max().item():.3e} mean_abs={err.mean().item():.3e}")
+    assert err.max().item() <= 2e-2 and err.mean().item() <= 1e-3
+
+
+def test_flex_prefill_short_sequence_is_dense_and_small_blocks_raise():
+    """L <= max(2 bs, ceil(min_budget / bs) bs) takes dense causal attention
+    (Flexprefill.py:1084-1085); 32-token attention blocks are not built."""
+    _case(L=256, dense=True)
+    q, k, v = make_qkv(256, 2, 1, dtype=torch.bfloat16, seed=45)
+    ql, kl, vl = _blhd(q, k, v)
+    out = Flexprefill_prefill(ql.to(DEV), kl.to(DEV), vl.to(DEV), block_size=128)
+    ref = v7.block_sparse_attention(q, k, v, torch.ones(2, 2, 2, dtype=torch.bool), 128)
+    err = (out[0].float().cpu() - ref).abs()
+    assert err.max().item() <= 2e-2 and err.mean().item() <= 1e-3
+    q, k, v = make_qkv(1024, 2, 1, dtype=torch.bfloat16, seed=46)
+    ql, kl, vl = _blhd(q, k, v)
+    with pytest.raises(NotImplementedError):
+        Flexprefill_prefill(ql.to(DEV), kl.to(DEV), vl.to(DEV), block_size=32)
+    # min_budget of the whole sequence: dense as well
+    out = Flexprefill_prefill(ql.to(DEV), kl.to(DEV), vl.to(DEV), block_size=32, min_budget=1024)
+    ref = v7.block_sparse_attention(q, k, v, torch.ones(2, 8, 8, dtype=torch.bool), 128)
+    err = (out[0].float().cpu() - ref).abs()
+    assert err.max().item() <= 2e-2 and err.mean().item() <= 1e-3
+
+
+def test_flex_full_length_properties():
+    """Config-2 shape (L = 131072, 32 / 8 heads, 128-token blocks): lists
+    ascending and causal, block 0 first and the diagonal last, deterministic
+    across calls, profiles that each sum to one."""
+    _case(L=131072, full=True)
+    from fftsparse_amd.synth import make_config
+    q, k, _ = make_config("c2")
+    qg, kg = q.to(DEV).transpose(1, 2), k.to(DEV).transpose(1, 2)
+    del q, k
+    a = flex_select(qg, kg, gamma=0.95, tau=0.1, block_size=128)
+    b = flex_select(qg, kg, gamma=0.95, tau=0.1, block_size=128)
+    torch.cuda.synchronize()
+    assert torch.equal(a.blk_cnt, b.blk_cnt) and torch.equal(a.dense_mask(), b.dense_mask())
+    assert torch.equal(a.head_info, b.head_info)
+    H, N = a.blk_cnt.shape
+    cnt = a.blk_cnt.to(torch.int64)
+    idx = a.blk_idx.view(torch.int16).to(torch.int64) & 0xFFFF
+    pos = torch.arange(N, device=DEV)
+    valid = pos[None, None, :] < cnt[:, :, None]
+    rows = pos[None, :, None].expand(H, N, N)
+    assert bool(((idx <= rows) | ~valid).all())
+    assert bool(((idx[:, :, 1:] > idx[:, :, :-1]) | ~valid[:, :, 1:]).all())
+    assert bool((idx[:, :, 0] == 0).all())
+    last = idx.gather(2, (cnt - 1).clamp(min=0)[:, :, None])[:, :, 0]
+    assert bool((last == pos[None, :]).all())
+    for prof in (a.vertical, a.slash):
+        assert bool(((prof.double().sum(-1) - 1.0).abs() <= 1e-4).all())
+    # the budgets bound each row: at most nv columns + ns diagonals (non-sparse heads)
+    info = a.head_info.cpu()
+    for h in range(H):
+        if not info[h, 2]:
+            assert int(a.blk_cnt[h].max()) <= int(info[h, 0]) + int(info[h, 1])
+    print(f"  density {density(a):.4f} sparse heads {int(info[:, 2].sum())}")
+    assert not math.isnan(a.js.float().cpu().sum().item())

@@ -35,7 +35,7 @@ def test_struct_layouts_match_library():
 
 def test_null_args_rejected_without_gpu():
     lib = _lib.load()
-    for name in ("fs_pool", "fs_rope_pool", "fs_xattn", "fs_corr", "fs_stats", "fs_scores", "fs_select", "fs_bsattn", "fs_bsattn_prepare",
+    for name in ("fs_pool", "fs_rope_pool", "fs_xattn", "fs_flex", "fs_corr", "fs_stats", "fs_scores", "fs_select", "fs_bsattn", "fs_bsattn_prepare",
                  "fs_bsattn_run"):
         rc = getattr(lib, name)(None, None)
         assert rc == -1
@@ -58,6 +58,19 @@ def test_bad_shapes_rejected_without_gpu():
     assert lib.fs_xattn(ctypes.byref(x), None) == -2
     x.stride, x.Hk = 8, 3
     assert lib.fs_xattn(ctypes.byref(x), None) == -1
+    f = _lib.FlexArgs(q=16, k=16, blk_cnt=16, blk_idx=16, work=16, dtype=1, Hq=4, Hk=1, L=4096, D=128, bs=16,
+                      gamma=0.9, tau=0.1, min_blocks=1, max_blocks=64, q_sl=128, k_sl=128, q_sh=128, k_sh=128)
+    assert lib.fs_flex(ctypes.byref(f), None) == -2              # 16-token blocks: not built
+    assert b"block size" in lib.fs_last_error()
+    f.bs, f.L = 64, 64                                           # one block: the reference attends densely
+    assert lib.fs_flex(ctypes.byref(f), None) == -1
+    f.L, f.Hk = 4096, 3
+    assert lib.fs_flex(ctypes.byref(f), None) == -1
+    f.Hk, f.q_sl = 1, 100                                        # 200-byte row stride
+    assert lib.fs_flex(ctypes.byref(f), None) == -1
+    f.q_sl, f.L, f.bs = 128, 4096 * 32 + 1, 32                   # 4097 blocks
+    assert lib.fs_flex(ctypes.byref(f), None) == -2
+    assert lib.fs_flex_work_bytes(4, 1, 4096, 64) > 4 * 4096 * 4 * 2
     a = _lib.AttnArgs(q=16, k=16, v=16, out=16, dtype=1, B=1, Hq=3, Hk=2, Lq=10, Lk=10, D=128, bs=128)
     assert lib.fs_bsattn(ctypes.byref(a), None) == -1
     a = _lib.AttnArgs(q=16, k=16, v=16, out=16, work=16, dtype=1, B=1, Hq=4, Hk=2, Lq=10, Lk=10, D=96, bs=128)
