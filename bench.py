@@ -41,10 +41,14 @@ def parse():
     ap.add_argument("--config", default="c2")
     ap.add_argument("--threshold", type=float, default=0.9)
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--selector", choices=("fftsparse", "xattn"), default="fftsparse",
-                    help="block selection: FFTSparse v7 (default) or XAttention (the reference's comparison "
-                         "selector, attn_src/xattn), both attending with the same block-sparse kernel")
+    ap.add_argument("--selector", choices=("fftsparse", "xattn", "flex"), default="fftsparse",
+                    help="block selection: FFTSparse v7 (default), XAttention (attn_src/xattn) or FlexPrefill "
+                         "(attn_src/Flexprefill.py), the reference's comparison selectors, all attending with "
+                         "the same block-sparse kernel")
     ap.add_argument("--xattn-stride", type=int, default=8, help="XAttention's antidiagonal stride")
+    ap.add_argument("--flex-gamma", type=float, default=0.95,
+                    help="FlexPrefill's gamma (the reference benchmark's default)")
+    ap.add_argument("--flex-tau", type=float, default=0.1, help="FlexPrefill's tau (the reference benchmark's default)")
     ap.add_argument("--no-dense", action="store_true", help="skip the dense comparators")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--select-groups", type=int, default=None,
@@ -163,6 +167,42 @@ def _cpu_model():
     return "unknown"
 
 
+def cpu_baseline_flex(q, k, v, args, bs, nnz_total, sel, sample_heads=None):
+    """The FlexPrefill oracle (oracle/flex.py) on this host's cores: the
+    selection of the first ``sample_heads`` query heads (all by default; whole
+    KV groups) over the full length, scaled by the head count (heads are
+    independent), and fp32 block-sparse attention over the first query head's
+    selected tiles, scaled by the tile count."""
+    import torch
+    from oracle import flex as fo, v7
+    threads = torch.get_num_threads()
+    Hq, Hk = q.shape[1], k.shape[1]
+    g = Hq // Hk
+    hs = max(g, (min(sample_heads or Hq, Hq) // g) * g)
+    qs = q[:, :hs].cpu().transpose(1, 2).contiguous()
+    ks = k[:, :hs // g].cpu().transpose(1, 2).contiguous()
+    t0 = time.perf_counter()
+    fo.active_blocks(qs, ks, bs, args.flex_gamma, args.flex_tau)
+    t_s = time.perf_counter() - t0
+    t_sel = t_s * Hq / hs
+    mask = sel.dense_mask().cpu()
+    heads = [0]
+    tiles = int(mask[heads].sum())
+    qc, kc, vc = q.cpu(), k.cpu(), v.cpu()
+    t0 = time.perf_counter()
+    v7.block_sparse_attention(qc, kc, vc, mask, bs, heads=heads)
+    t_a = time.perf_counter() - t0
+    t_att = t_a * nnz_total / max(1, tiles)
+    return {
+        "value": round((t_sel + t_att) * 1e3, 1), "unit": "ms", "cores": threads, "kind": "port",
+        "sample": (f"oracle/flex.py on this host ({threads} torch threads): selection of query heads 0..{hs - 1} "
+                   f"({t_s:.1f} s) scaled x{Hq / hs:.0f} to all heads; fp32 block-sparse attention over head 0 "
+                   f"({tiles} tiles, {t_a:.1f} s) scaled x{nnz_total / max(1, tiles):.1f} to {nnz_total} tiles"),
+        "select_ms": round(t_sel * 1e3, 1), "attn_ms_scaled": round(t_att * 1e3, 1),
+        "cpu_model": _cpu_model(), "os_cpu_count": os.cpu_count(),
+    }
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -201,14 +241,20 @@ def main():
     # pre-pass, then order + attention kernel), all on torch's current stream,
     # which is the stream the events below are recorded on.
     xattn = args.selector == "xattn"
+    flex = args.selector == "flex"
     if xattn:
         from fftsparse_amd.xattn import xattn_select
+    if flex:
+        from fftsparse_amd.flex import flex_select
+        q_blhd, k_blhd = q.transpose(1, 2), k.transpose(1, 2)      # the reference's [B, L, H, D] views
 
     def step(ev=None):
         if ev:
             ev[0].record()
         if xattn:
             sel = xattn_select(q, k, stride=args.xattn_stride, threshold=args.threshold, block_size=bs)
+        elif flex:
+            sel = flex_select(q_blhd, k_blhd, gamma=args.flex_gamma, tau=args.flex_tau, block_size=bs)
         else:
             sel = select_blocks(q, k, pipeline_groups=args.select_groups, **kw)
         if ev:
@@ -248,7 +294,7 @@ def main():
     esz = q.element_size()
     sel_bytes = L * Hq * D * esz + L * Hk * D * esz
     t_sel = statistics.mean(sel_ms)
-    stripe = int(sel.is_stripe.sum().item()) if not xattn and sel.is_stripe is not None else None
+    stripe = (int(sel.is_stripe.sum().item()) if not (xattn or flex) and sel.is_stripe is not None else None)
 
     dense = {}
     if not args.no_dense:
@@ -285,6 +331,8 @@ def main():
         torch.cuda.synchronize()
         if xattn:
             cpu = cpu_baseline_xattn(q, k, v, args, bs, nnz, sel)
+        elif flex:
+            cpu = cpu_baseline_flex(q, k, v, args, bs, nnz, sel)
         else:
             cpu = cpu_baseline(q, k, v, kw, bs, nnz, args.cpu_heads)
 
@@ -298,6 +346,18 @@ def main():
                            "frac": round(est_flops / (t_sel * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4), "traffic": None,
                            "work": f"2 passes x 2*S*D flop per causal reshaped score (S={S}, {Lr} reshaped rows per head)",
                            "timed": "xattn_select: scores pass 1 (row stats), pass 2 (block sums), selection"}
+    elif flex:
+        # K read by the two last-block score passes and by the block means; the
+        # sparse heads' Q read for their block means; the fp32 profiles written once
+        n_sparse = int(sel.head_info[:, 2].sum().item())
+        flex_bytes = 3 * L * Hk * D * esz + n_sparse * L * D * esz + 2 * Hq * L * 4
+        roofline_select = {"bound": "hbm", "achieved": round(flex_bytes / (t_sel * 1e-3) / 1e9, 1),
+                           "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                           "frac": round(flex_bytes / (t_sel * 1e-3) / 1e9 / PEAK_HBM_GBS, 4), "traffic": None,
+                           "work": ("K read 3x (2 score passes + block means: 3*L*Hkv*D*2 bytes), the sparse heads' Q "
+                                    f"({n_sparse} heads), vertical/slash profiles written (2*Hq*L*4 bytes)"),
+                           "timed": "flex_select: last-block scores (2 passes), K block means, per-head budgets / "
+                                    "JS test / top-k, sparse-head cover (2 launches), block lists"}
     else:
         roofline_select = {"bound": "hbm", "achieved": round(sel_bytes / (t_sel * 1e-3) / 1e9, 1),
                            "peak": PEAK_HBM_GBS, "unit": "GB/s",
@@ -307,6 +367,9 @@ def main():
                            "timed": "select_blocks: pool, block-score tiles + statistics (2 launches), block lists "
                                     "(2 launches)"}
     sel_desc = (f"XAttention selection (stride {args.xattn_stride}, threshold {args.threshold})" if xattn
+                else f"FlexPrefill selection (gamma {args.flex_gamma}, tau {args.flex_tau}, {bs}-token blocks; the "
+                     f"reference benchmark runs FlexPrefill at 32-token blocks, which this attention kernel does "
+                     f"not take)" if flex
                 else f"corr_threshold {args.threshold}, production kwargs")
     line = {
         "metric": METRIC,
@@ -324,7 +387,8 @@ def main():
         "config": {"workload": f"{cfg.name}: one layer, L={L}, Hq={Hq}, Hkv={Hk}, D={D}, block {bs}, {sel_desc}",
                    "selector": args.selector,
                    "seq_len": L, "global_batch": 1, "block_size": bs,
-                   ("xattn_threshold" if xattn else "corr_threshold"): args.threshold,
+                   **({"flex_gamma": args.flex_gamma, "flex_tau": args.flex_tau} if flex else
+                      {("xattn_threshold" if xattn else "corr_threshold"): args.threshold}),
                    "parallelism": "none (1 GPU)"},
         "speedup_vs_dense": round(dense_ms / ms, 3) if dense_ms == dense_ms else None,
         "dense_ms": round(dense_ms, 3) if dense_ms == dense_ms else None,
@@ -340,7 +404,7 @@ def main():
         "stripe_heads": stripe,
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": None if xattn else pmc_traffic("bsattn", cfg.name),
+                     "traffic": None if (xattn or flex) else pmc_traffic("bsattn", cfg.name),
                      "kernel": f"fs::bsattn_kernel<{bs},{'bf16' if q.dtype == torch.bfloat16 else 'f16'}>",
                      "work": f"4*D*bs^2 flop per selected (query block, key block) tile x {nnz} tiles",
                      "timed": "fs_bsattn_run (order pass + attention kernel), HIP events on the launch stream"},

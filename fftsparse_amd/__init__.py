@@ -10,10 +10,15 @@ attn_src/fix_mask_attn/my_attn.py):
     block_sparse_attention(q, k, v, cnt, idx, ...)  stage 2 only
     rope_pool(q, k, cos, sin, ...)                  the rotary embedding before the call, fused
                                                     with the block pooling (select_blocks(pooled=...))
+
+The reference's comparison selectors on the same attention kernel:
+
+    xattn.Xattention_prefill(q, k, v, ...)          attn_src/xattn/src/Xattention.py
+    flex.Flexprefill_prefill(q, k, v, ...)          attn_src/Flexprefill.py
 """
 from .attn import (AttentionCall, BlockSelection, block_sparse_attention, myattn_prefill, rope_pool,  # noqa: F401
                    select_blocks)
-from . import fix_mask  # noqa: F401
+from . import fix_mask, flex, xattn  # noqa: F401
 
 __all__ = ["myattn_prefill", "select_blocks", "block_sparse_attention", "rope_pool", "AttentionCall",
-           "BlockSelection", "fix_mask"]
+           "BlockSelection", "fix_mask", "flex", "xattn"]

@@ -68,6 +68,16 @@ template <> struct FMma<f16_t> {
   }
 };
 
+constexpr float kLog2e = 1.4426950408889634f;
+
+// floats of the region shared by the K tile and PASS 2's p tile [bs][kFTile + 4]
+__host__ __device__ constexpr int flex_tile_floats(int bs) {
+  return bs * (kFTile + 4) > kFTile * kFD / 2 ? bs * (kFTile + 4) : kFTile * kFD / 2;
+}
+
+// 2^x by the hardware exponential (v_exp_f32); exp(y) is taken as 2^(y log2 e)
+__device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 struct FlexK {
   const uint16_t* q;            // [Hq][L][D] view (strides q_sh, q_sl)
   const uint16_t* k;
@@ -85,8 +95,11 @@ __device__ __forceinline__ int kv_head(int h, int Hq, int Hk, int interleave) {
 
 template <typename T, int PASS, int BS>
 __global__ __launch_bounds__(kFThreads) void flex_lastq_kernel(FlexK a) {
-  __shared__ __attribute__((aligned(16))) uint16_t lk[kFTile * kFD];        // 32 KiB
-  extern __shared__ float ptile[];                                           // PASS 2: [bs][kFTile] + carry
+  // dynamic LDS: the K tile (32 KiB), which in PASS 2 shares its region with
+  // the p tile (formed after the MFMAs have read K), then PASS 2's carry, row
+  // statistics and column half sums (PASS 1: the lane partials after the loop)
+  extern __shared__ __attribute__((aligned(16))) float dyn[];
+  uint16_t* lk = reinterpret_cast<uint16_t*>(dyn);
   const int h = blockIdx.x / a.nchunk, chunk = blockIdx.x % a.nchunk;
   const int kvh = kv_head(h, a.Hq, a.Hk, a.gqa_interleave);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, hi = lane >> 5;
@@ -121,14 +134,17 @@ __global__ __launch_bounds__(kFThreads) void flex_lastq_kernel(FlexK a) {
   const int c_end = min(L, c_begin + kFChunk);
   // PASS 2 starts one tile early (carry of the diagonals that cross into the chunk)
   const int t_first = (PASS == 2 && chunk > 0) ? c_begin - kFTile : c_begin;
-  float m_run = -INFINITY, l_run = 0.f;           // PASS 1, per lane (partial over its columns)
-  float M = 0.f, inv_s = 0.f;
-  float* ptl = ptile;                              // [bs][kFTile]
-  float* carry = ptile + bs * kFTile;              // [kFTile + bs] diagonal partials in flight
+  const int lim_causal = L - bs + row;            // the last block: key <= query
+  const int c_valid = PASS == 1 ? c_end : L;      // PASS 2 also forms the carry tile before the chunk
+  float m_run = -INFINITY, l_run = 0.f;           // PASS 1, per lane, log2 domain (partial over its columns)
+  float M2 = 0.f, inv_s = 0.f;                    // PASS 2: the row's max (log2 domain) and 1 / sum
+  constexpr int PS = kFTile + 4;                  // p-tile row stride: 16-byte row chunks spread over the banks
+  float* ptl = dyn;                               // [bs][PS], over the K tile
+  float* carry = dyn + flex_tile_floats(bs);      // [kFTile + bs] diagonal partials in flight
+  float* rowstat = carry + kFTile + bs;           // [bs][2]
+  float* vpart = rowstat + 2 * bs;                // [kFThreads] column sums of the two row halves
   if (PASS == 2) {
-    // combine the chunk partials of this thread's rows in a fixed order
-    // (threads tid < bs each own row tid; the tile code reads them from LDS)
-    float* rowstat = carry + kFTile + bs;          // [bs][2]
+    // combine the chunk partials of each row in a fixed order
     if (tid < bs) {
       const float* pp = a.part + ((int64_t)h * a.nchunk) * bs * 2;
       float mx = -INFINITY;
@@ -136,14 +152,14 @@ __global__ __launch_bounds__(kFThreads) void flex_lastq_kernel(FlexK a) {
       float s = 0.f;
       for (int c = 0; c < a.nchunk; ++c) {
         const float mc = pp[((int64_t)c * bs + tid) * 2], lc = pp[((int64_t)c * bs + tid) * 2 + 1];
-        if (mc > -INFINITY) s += lc * expf(mc - mx);
+        if (mc > -INFINITY) s += lc * fexp2(mc - mx);
       }
       rowstat[tid * 2] = mx;
       rowstat[tid * 2 + 1] = 1.0f / s;
     }
     for (int e = tid; e < kFTile + bs; e += kFThreads) carry[e] = 0.f;
     __syncthreads();
-    M = rowstat[row * 2];
+    M2 = rowstat[row * 2];
     inv_s = rowstat[row * 2 + 1];
   }
 
@@ -164,110 +180,118 @@ __global__ __launch_bounds__(kFThreads) void flex_lastq_kernel(FlexK a) {
       }
     }
     __syncthreads();
-    f32x16_t acc[4];
+    f32x16_t acc[nsub];
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
+    for (int s = 0; s < nsub; ++s)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[s][r] = 0.f;
 #pragma unroll
     for (int st = 0; st < kFD / 16; ++st) {
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        if (s >= nsub) break;
+      for (int s = 0; s < nsub; ++s) {
         const int kr = (cg * nsub + s) * 32 + l32;
         const uint4 ak = *reinterpret_cast<const uint4*>(lk + kr * kFD + (((2 * st + hi) ^ (kr & 15)) << 3));
         acc[s] = FMma<T>::mma(ak, qf[st], acc[s]);
       }
     }
-    // lane: keys t0 + (cg nsub + s) 32 + (r/4) 8 + hi 4 + r%4 of query row `row`
-    const int lim_causal = L - bs + row;           // the last block: key <= query
+    // lane: keys t0 + (cg nsub + s) 32 + (r/4) 8 + hi 4 + r%4 of query row `row`; the
+    // scores rounded to T (the reference's einsum output), then to the log2 domain
+    float x[nsub][16];
+#pragma unroll
+    for (int s = 0; s < nsub; ++s)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) x[s][r] = Conv<T>::round(acc[s][r]) * kLog2e;
+    if (PASS == 2) __syncthreads();                // every wave has read the K tile: the p tile overwrites it
+    // every column of the tile valid and causal for every row
+    const bool interior = t0 + kFTile <= c_valid && t0 + kFTile - 1 <= L - bs;
+    auto valid = [&](int c) { return interior || (c < c_valid && c <= lim_causal); };
     if (PASS == 1) {
       float mx = -INFINITY;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        if (s >= nsub) break;
+      for (int s = 0; s < nsub; ++s)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int c = t0 + (cg * nsub + s) * 32 + (r >> 2) * 8 + hi * 4 + (r & 3);
-          if (c < c_end && c <= lim_causal) mx = fmaxf(mx, Conv<T>::round(acc[s][r]));
+          if (valid(c)) mx = fmaxf(mx, x[s][r]);
         }
-      }
       const float m_new = fmaxf(m_run, mx);
       if (m_new > -INFINITY) {
         float sum = 0.f;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          if (s >= nsub) break;
+        for (int s = 0; s < nsub; ++s)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int c = t0 + (cg * nsub + s) * 32 + (r >> 2) * 8 + hi * 4 + (r & 3);
-            if (c < c_end && c <= lim_causal) sum += expf(Conv<T>::round(acc[s][r]) - m_new);
+            if (valid(c)) sum += fexp2(x[s][r] - m_new);
           }
-        }
-        l_run = l_run * expf(m_run - m_new) + sum;
+        l_run = l_run * fexp2(m_run - m_new) + sum;
         m_run = m_new;
       }
     } else {
-      // p tile [bs][kFTile] in LDS
+      // p tile [bs][PS] in LDS, four consecutive columns per 16-byte write
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        if (s >= nsub) break;
+      for (int s = 0; s < nsub; ++s)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int cl = (cg * nsub + s) * 32 + (r >> 2) * 8 + hi * 4 + (r & 3);
-          const int c = t0 + cl;
-          const float p = (c < L && c <= lim_causal) ? expf(Conv<T>::round(acc[s][r]) - M) * inv_s : 0.f;
-          ptl[row * kFTile + cl] = p;
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const int cl = (cg * nsub + s) * 32 + g4 * 8 + hi * 4;
+          float4 v;
+          v.x = valid(t0 + cl + 0) ? fexp2(x[s][g4 * 4 + 0] - M2) * inv_s : 0.f;
+          v.y = valid(t0 + cl + 1) ? fexp2(x[s][g4 * 4 + 1] - M2) * inv_s : 0.f;
+          v.z = valid(t0 + cl + 2) ? fexp2(x[s][g4 * 4 + 2] - M2) * inv_s : 0.f;
+          v.w = valid(t0 + cl + 3) ? fexp2(x[s][g4 * 4 + 3] - M2) * inv_s : 0.f;
+          *reinterpret_cast<float4*>(ptl + row * PS + cl) = v;
         }
-      }
       __syncthreads();
-      // vertical: column sums over the bs rows, in row order
+      // vertical: each column's rows in two halves (threads tid and tid + kFTile), four running sums each
       if (t0 >= c_begin) {
-        for (int cl = tid; cl < kFTile; cl += kFThreads) {
-          const int c = t0 + cl;
-          if (c >= c_end) continue;
-          float s = 0.f;
-          for (int i = 0; i < bs; ++i) s += ptl[i * kFTile + cl];
-          a.vert[(int64_t)h * L + c] = s / (float)bs;
+        const int cl = tid & (kFTile - 1), half = tid / kFTile;
+        const float* col = ptl + half * (bs / 2) * PS + cl;
+        float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll
+        for (int i = 0; i < bs / 2; i += 4) {
+          s0 += col[(i + 0) * PS];
+          s1 += col[(i + 1) * PS];
+          s2 += col[(i + 2) * PS];
+          s3 += col[(i + 3) * PS];
         }
+        vpart[tid] = (s0 + s1) + (s2 + s3);
       }
-      // slash: diagonal x (ending at column x of the last row) takes p[i][x + i - (bs-1)];
+      // slash: diagonal x = t0 + j (ending at column x of the last row) takes
+      // p[i][j + i - (bs-1)] for the rows whose column falls in this tile;
       // this tile adds to the diagonals x in [t0, t0 + kFTile + bs - 1)
-      float dpart[2];
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int j = tid + u * kFThreads;       // x = t0 + j
-        float s = 0.f;
-        if (j < kFTile + bs - 1) {
-          for (int i = 0; i < bs; ++i) {
-            const int cl = j + i - (bs - 1);
-            if (cl >= 0 && cl < kFTile) s += ptl[i * kFTile + cl];
-          }
+      float dsum = 0.f;
+      if (tid < kFTile + bs - 1) {
+        const int j = tid;
+        const int ilo = max(0, bs - 1 - j), ihi = min(bs, kFTile + bs - 1 - j);
+        const int base = j - (bs - 1);             // row i's element sits at i (PS + 1) + base
+        float d0 = 0.f, d1 = 0.f, d2 = 0.f, d3 = 0.f;
+        int i = ilo;
+        for (; i + 4 <= ihi; i += 4) {
+          d0 += ptl[(i + 0) * (PS + 1) + base];
+          d1 += ptl[(i + 1) * (PS + 1) + base];
+          d2 += ptl[(i + 2) * (PS + 1) + base];
+          d3 += ptl[(i + 3) * (PS + 1) + base];
         }
-        dpart[u] = s;
+        for (; i < ihi; ++i) d0 += ptl[i * (PS + 1) + base];
+        dsum = (d0 + d1) + (d2 + d3);
       }
-      __syncthreads();                             // carry read below is rewritten after
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int j = tid + u * kFThreads;
-        if (j < kFTile) {
-          const int x = t0 + j;
-          const float v = carry[j] + dpart[u];     // complete: no later column reaches x
-          if (t0 >= c_begin && x < c_end) a.slash[(int64_t)h * L + x] = v / (float)bs;
+      __syncthreads();                             // vpart written; carry read below is rewritten after
+      if (tid < kFTile) {
+        const int xcol = t0 + tid;
+        if (t0 >= c_begin && xcol < c_end) {
+          a.vert[(int64_t)h * L + xcol] = (vpart[tid] + vpart[tid + kFTile]) / (float)bs;
+          a.slash[(int64_t)h * L + xcol] = (carry[tid] + dsum) / (float)bs;   // complete: no later column reaches x
         }
       }
       __syncthreads();
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int j = tid + u * kFThreads;
-        if (j >= kFTile && j < kFTile + bs - 1) carry[j - kFTile] = dpart[u];
-      }
+      if (tid >= kFTile && tid < kFTile + bs - 1) carry[tid - kFTile] = dsum;
       for (int e = bs - 1 + tid; e < kFTile + bs; e += kFThreads) carry[e] = 0.f;
     }
   }
   if (PASS == 1) {
     // combine the row's columns held by the lanes of all column groups and both halves
-    float* red = ptile;                            // [4 waves][64 lanes][2]
+    __syncthreads();                               // the K tile is dead
+    float* red = dyn;                              // [4 waves][64 lanes][2]
     red[(wave * 64 + lane) * 2] = m_run;
     red[(wave * 64 + lane) * 2 + 1] = l_run;
     __syncthreads();
@@ -280,7 +304,7 @@ __global__ __launch_bounds__(kFThreads) void flex_lastq_kernel(FlexK a) {
       for (int c = 0; c < CG; ++c)
         for (int hh = 0; hh < 2; ++hh) {
           const int idx = (((c * RG + rgi) * 64) + hh * 32 + li) * 2;
-          if (red[idx] > -INFINITY) s += red[idx + 1] * expf(red[idx] - mx);
+          if (red[idx] > -INFINITY) s += red[idx + 1] * fexp2(red[idx] - mx);
         }
       float* pp = a.part + (((int64_t)h * a.nchunk + chunk) * bs + tid) * 2;
       pp[0] = mx;
@@ -333,49 +357,167 @@ __device__ __forceinline__ float block_max_f(float v, double* red) {
   return r;
 }
 
-// Count of the descending prefix sums of x[0 .. n) that are <= g (score_cover_topk
-// minus its + 1): the largest key t with sum(x >= t) <= g by bisection on the
-// order-preserving key, then the equal-valued elements just below t that still fit.
-__device__ int cover_count_dev(const float* x, int n, double g, double* red) {
+// ---- radix cuts over order-preserving keys (one 1024-thread workgroup) -----
+// Four passes over the data, one 8-bit digit of the key per pass (most
+// significant first): a histogram of the digit among the elements that share
+// the digits found so far, then one wave scans it from the largest digit down.
+// Masses are summed as integers x * 2^scale_exp, so the sums are exact and do
+// not depend on the order of the atomics.  The values of a profile fall in a
+// few top digits: the histogram is kept in kCutCopies copies, one per lane
+// residue, so that at most 64 / kCutCopies lanes of a wave add to one address.
+constexpr int kCutCopies = 8;                    // histogram copies: lane l adds to copy l % 8
+
+struct CutScratch {
+  uint64_t hm[kCutCopies][256]; // mass per digit
+  uint32_t hc[kCutCopies][256]; // count per digit
+  uint64_t mass;                // crossing: mass / count of the elements above its digit
+  int cnt;
+  int digit;                    // crossing digit, -1: none
+};
+
+struct CutResult {
+  int count;                    // elements in the cut
+  uint32_t key;                 // boundary key: every larger key is in the cut
+  int take_eq;                  // elements equal to the boundary key in the cut (lowest index first)
+};
+
+// BY_MASS: the descending prefix-sum cut of x >= 0 at g (score_cover_topk
+// without its + 1): the elements, largest first, while the running mass stays
+// <= g.  Otherwise: the `want` largest elements (want >= 1).
+template <bool BY_MASS>
+__device__ CutResult radix_cut(const float* x, int n, double g, int scale_exp, int want, CutScratch* cs) {
   const int tid = threadIdx.x;
-  auto mass_ge = [&](uint32_t key, int* cnt) -> double {
-    double s = 0.0;
-    int c = 0;
-    for (int i = tid; i < n; i += kFHeadThreads)
-      if (order_key(x[i]) >= key) {
-        s += (double)x[i];
-        ++c;
+  const double sc = ldexp(1.0, scale_exp);
+  const uint64_t G = BY_MASS ? (uint64_t)(g * sc) : 0;
+  uint32_t prefix = 0;
+  uint64_t above = 0;
+  int cnt_above = 0;
+  for (int pass = 0; pass < 4; ++pass) {
+    const int shift = 24 - 8 * pass;
+    for (int e = tid; e < kCutCopies * 256; e += kFHeadThreads) {
+      (&cs->hm[0][0])[e] = 0;
+      (&cs->hc[0][0])[e] = 0;
+    }
+    if (tid == 0) cs->digit = -1;
+    __syncthreads();
+    const int copy = tid % kCutCopies;
+    for (int i = tid; i < n; i += kFHeadThreads) {
+      const float v = x[i];
+      const uint32_t key = order_key(v);
+      if (pass == 0 || (key >> (shift + 8)) == prefix) {
+        const uint32_t d = (key >> shift) & 255u;
+        if (BY_MASS) {
+          const uint64_t m = (uint64_t)((double)v * sc);
+          if (m) atomicAdd(reinterpret_cast<unsigned long long*>(&cs->hm[copy][d]), (unsigned long long)m);
+        }
+        atomicAdd(&cs->hc[copy][d], 1u);
       }
-    if (cnt) *cnt = (int)block_sum_d((double)c, red);
-    return block_sum_d(s, red);
+    }
+    __syncthreads();
+    if (tid < 64) {
+      // lane l: digits 255 - 4l .. 252 - 4l, largest first
+      uint64_t lm[4], sm = 0;
+      uint32_t lc[4], scn = 0;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int d = 255 - 4 * tid - t;
+        lm[t] = 0;
+        lc[t] = 0;
+#pragma unroll
+        for (int r = 0; r < kCutCopies; ++r) {
+          if (BY_MASS) lm[t] += cs->hm[r][d];
+          lc[t] += cs->hc[r][d];
+        }
+        sm += lm[t];
+        scn += lc[t];
+      }
+      uint64_t im = sm;
+      uint32_t ic = scn;
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint64_t vm = __shfl_up(im, o, 64);
+        const uint32_t vc = __shfl_up(ic, o, 64);
+        if (tid >= o) {
+          im += vm;
+          ic += vc;
+        }
+      }
+      uint64_t run = above + (im - sm);
+      uint32_t runc = (uint32_t)cnt_above + (ic - scn);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const uint64_t prev = run;
+        const uint32_t prevc = runc;
+        run += lm[t];
+        runc += lc[t];
+        const bool cross = BY_MASS ? (prev <= G && run > G) : (prevc < (uint32_t)want && runc >= (uint32_t)want);
+        if (cross) {
+          cs->digit = 255 - 4 * tid - t;
+          cs->mass = prev;
+          cs->cnt = (int)prevc;
+        }
+      }
+    }
+    __syncthreads();
+    const int d = cs->digit;
+    if (d < 0) {                                   // everything is in the cut (first pass only)
+      __syncthreads();
+      return {n, 0u, 0};
+    }
+    prefix = (prefix << 8) | (uint32_t)d;
+    above = cs->mass;
+    cnt_above = cs->cnt;
+    uint32_t eq = 0;
+    for (int r = 0; r < kCutCopies; ++r) eq += cs->hc[r][d];
+    __syncthreads();                               // cs is rewritten by the next pass / call
+    if (pass == 3) {
+      int take;
+      if (BY_MASS) {
+        const uint64_t mv = (uint64_t)((double)key_to_f32(prefix) * sc);   // > 0: it pushed the sum past G
+        const uint64_t fit = mv ? (G - above) / mv : (uint64_t)eq;
+        take = (int)(fit < (uint64_t)eq ? fit : (uint64_t)eq);
+      } else {
+        take = want - cnt_above;
+      }
+      return {cnt_above + take, prefix, take};
+    }
+  }
+  return {n, 0u, 0};                               // not reached
+}
+
+// Sets, in out, the bits of the elements of a cut: every key above cut.key and
+// the first cut.take_eq elements equal to it in index order.  Element i of a
+// row of row_len elements goes to bit (i % row_len) of row i / row_len, rows
+// kFWords words apart.  Each thread owns a contiguous index range; a fixed-order
+// scan of the per-thread tie counts ranks the ties.
+__device__ void emit_cut(const float* x, int n, int row_len, const CutResult& cut, uint64_t* out, int* scan) {
+  const int tid = threadIdx.x;
+  const int per = (n + kFHeadThreads - 1) / kFHeadThreads;
+  const int i0 = min(n, tid * per), i1 = min(n, i0 + per);
+  auto set = [&](int i) {
+    const int r = i / row_len, c = i - r * row_len;
+    atomicOr(reinterpret_cast<unsigned long long*>(&out[(int64_t)r * kFWords + (c >> 6)]), 1ull << (c & 63));
   };
-  // t* = smallest key with mass(>= t) <= g  (mass is nonincreasing in t)
-  uint32_t lo = 0, hi = 0xffffffffu;               // mass(>= hi) <= g for hi = max key (only +inf/nan above)
-  if (mass_ge(hi, nullptr) > g) return 0;
-  while (lo < hi) {
-    const uint32_t mid = lo + (hi - lo) / 2;
-    if (mass_ge(mid, nullptr) <= g) hi = mid;
-    else lo = mid + 1;
+  int mine = 0;
+  for (int i = i0; i < i1; ++i) {
+    const uint32_t k = order_key(x[i]);
+    if (k > cut.key) set(i);
+    else if (k == cut.key) ++mine;
   }
-  int cnt = 0;
-  const double m = mass_ge(hi, &cnt);
-  // elements just below t: the largest value u < t and how many equal it
-  float u = -INFINITY;
-  for (int i = tid; i < n; i += kFHeadThreads)
-    if (order_key(x[i]) < hi) u = fmaxf(u, x[i]);
-  u = block_max_f(u, red);
-  if (u == -INFINITY) return cnt;                 // nothing below
-  int mu = 0;
-  for (int i = tid; i < n; i += kFHeadThreads) mu += x[i] == u;
-  mu = (int)block_sum_d((double)mu, red);
-  if (u == 0.f) return cnt + mu;                   // zeros keep every prefix sum <= g
-  int extra = 0;
-  double s = m;
-  while (extra < mu && s + (double)u <= g) {
-    s += (double)u;
-    ++extra;
+  scan[tid] = mine;
+  __syncthreads();
+  for (int off = 1; off < kFHeadThreads; off <<= 1) {
+    const int v = tid >= off ? scan[tid - off] : 0;
+    __syncthreads();
+    scan[tid] += v;
+    __syncthreads();
   }
-  return cnt + extra;
+  int rank = scan[tid] - mine;
+  __syncthreads();                                 // scan is reused by the caller
+  for (int i = i0; i < i1 && rank < cut.take_eq; ++i)
+    if (order_key(x[i]) == cut.key) {
+      set(i);
+      ++rank;
+    }
 }
 
 struct FlexHeadK {
@@ -392,51 +534,27 @@ struct FlexHeadK {
   float* js;                    // [Hq]
 };
 
-// the upper midpoint of [lo, hi], lo < hi, in (lo, hi]: the 64-bit sum keeps
-// hi - lo + 1 from wrapping to 0 on the full key range
-__device__ __forceinline__ uint32_t upper_mid(uint32_t lo, uint32_t hi) {
-  return lo + (uint32_t)(((uint64_t)hi - lo + 1) >> 1);
-}
-
 // the K largest of v[0 .. n) (ties: lower index first) as bits of out[kFWords]
-__device__ void topk_bits(const float* v, int n, int K, uint64_t* out, double* red) {
+__device__ void topk_bits(const float* v, int n, int K, uint64_t* out, CutScratch* cs, int* scan) {
   const int tid = threadIdx.x;
   for (int w = tid; w < kFWords; w += kFHeadThreads) out[w] = 0;
   __syncthreads();
   if (K <= 0) return;
-  // smallest key t with count(>= t) <= K ... find the K-th largest key by bisection
-  auto count_ge = [&](uint32_t key) -> int {
-    int c = 0;
-    for (int i = tid; i < n; i += kFHeadThreads) c += order_key(v[i]) >= key;
-    return (int)block_sum_d((double)c, red);
-  };
-  uint32_t lo = 0, hi = 0xffffffffu;               // largest t with count(>= t) >= K
-  while (lo < hi) {
-    const uint32_t mid = upper_mid(lo, hi);
-    if (count_ge(mid) >= K) lo = mid;
-    else hi = mid - 1;
-  }
-  const uint32_t kth = lo;
-  const int above = count_ge(kth == 0xffffffffu ? kth : kth + 1);
-  int need = K - above;                            // equal-keyed elements to take, lowest index first
-  // serial pass in index order for the ties (n <= 4096)
-  if (tid == 0) {
-    for (int i = 0; i < n; ++i) {
-      const uint32_t ki = order_key(v[i]);
-      if (ki > kth || (ki == kth && need > 0)) {
-        if (ki == kth) --need;
-        out[i >> 6] |= 1ull << (i & 63);
-      }
-    }
-  }
+  const CutResult cut = radix_cut<false>(v, n, 0.0, 0, K, cs);
+  emit_cut(v, n, n, cut, out, scan);
   __syncthreads();
 }
 
 template <typename T>
 __global__ __launch_bounds__(kFHeadThreads) void flex_head_kernel(FlexHeadK a) {
   __shared__ double red[kFHeadThreads];
-  __shared__ float pv[kFMaxBlocks], ps[kFMaxBlocks], pk[kFMaxBlocks];
   __shared__ float lqm[kFD];
+  __shared__ CutScratch cs;
+  extern __shared__ float pooled[];                // pv, ps, pk: [nb] each
+  float* pv = pooled;
+  float* ps = pooled + a.nb;
+  float* pk = pooled + 2 * a.nb;
+  int* scan = reinterpret_cast<int*>(red);         // the tie ranks reuse the reduction buffer
   const int h = blockIdx.x, tid = threadIdx.x;
   const int L = a.L, bs = a.bs, nb = a.nb;
   const float* vt = a.vert + (int64_t)h * L;
@@ -444,8 +562,9 @@ __global__ __launch_bounds__(kFHeadThreads) void flex_head_kernel(FlexHeadK a) {
   const int kvh = kv_head(h, a.Hq, a.Hk, a.gqa_interleave);
 
   // cover counts (score_cover_topk) -> block budgets
-  int nv = cover_count_dev(vt, L, (double)a.gamma, red) + 1;
-  int ns = cover_count_dev(st, L, (double)a.gamma, red) + 1;
+  // (the profiles each add to one: masses as integers x 2^58)
+  int nv = radix_cut<true>(vt, L, (double)a.gamma, 58, 0, &cs).count + 1;
+  int ns = radix_cut<true>(st, L, (double)a.gamma, 58, 0, &cs).count + 1;
   nv = nv / 128 + 1;
   ns = ns / 128 + 1;
   nv = min(max(nv, a.min_b), a.max_b);
@@ -506,10 +625,10 @@ __global__ __launch_bounds__(kFHeadThreads) void flex_head_kernel(FlexHeadK a) {
     ps[nb - 1] = INFINITY;
   }
   __syncthreads();
-  topk_bits(pv, nb, min(nv, nb), a.vmask + (int64_t)h * kFWords, red);
+  topk_bits(pv, nb, min(nv, nb), a.vmask + (int64_t)h * kFWords, &cs, scan);
   // slash: top ns pooled entries j -> offsets nb - 1 - j
   __shared__ uint64_t sb[kFWords];
-  topk_bits(ps, nb, min(ns, nb), sb, red);
+  topk_bits(ps, nb, min(ns, nb), sb, &cs, scan);
   for (int w = tid; w < kFWords; w += kFHeadThreads) a.smask[(int64_t)h * kFWords + w] = 0;
   __syncthreads();
   if (tid == 0) {
@@ -597,61 +716,22 @@ __global__ __launch_bounds__(kFThreads) void flex_cover_rows_kernel(FlexCoverK a
 
 // the cover of gamma * N over a sparse head's N x N probabilities (score_cover_idx)
 __global__ __launch_bounds__(kFHeadThreads) void flex_cover_select_kernel(FlexCoverK a) {
-  __shared__ double red[kFHeadThreads];
+  __shared__ CutScratch cs;
+  __shared__ int scan[kFHeadThreads];
   const int h = blockIdx.x, tid = threadIdx.x, nb = a.nb;
   if (a.info[h * 4 + 2] == 0) return;
   const float* x = a.attn + (int64_t)h * nb * nb;
   const int n = nb * nb;
-  const int cnt = cover_count_dev(x, n, (double)a.gamma * nb, red);   // entries kept (no + 1)
-  // the cnt largest, ties by the lower flat index: bisection for the cnt-th largest key
   uint64_t* cov = a.cover + (int64_t)h * nb * kFWords;
   for (int e = tid; e < nb * kFWords; e += kFHeadThreads) cov[e] = 0;
   __syncthreads();
-  if (cnt > 0) {
-    auto count_ge = [&](uint32_t key) -> int {
-      int c = 0;
-      for (int i = tid; i < n; i += kFHeadThreads) c += order_key(x[i]) >= key;
-      return (int)block_sum_d((double)c, red);
-    };
-    uint32_t lo = 0, hi = 0xffffffffu;
-    while (lo < hi) {
-      const uint32_t mid = upper_mid(lo, hi);
-      if (count_ge(mid) >= cnt) lo = mid;
-      else hi = mid - 1;
-    }
-    const uint32_t kth = lo;
-    const int above = kth == 0xffffffffu ? 0 : count_ge(kth + 1);
-    int need = cnt - above;
-    // strictly larger ones in parallel; equal ones in index order by one thread
-    for (int i = tid; i < n; i += kFHeadThreads)
-      if (order_key(x[i]) > kth) atomicOr(reinterpret_cast<unsigned long long*>(&cov[(i / nb) * kFWords + ((i % nb) >> 6)]),
-                                          1ull << ((i % nb) & 63));
-    __syncthreads();
-    // equal keys in flat index order: each thread owns a contiguous range, a
-    // fixed-order scan of the per-thread counts gives each element its rank
-    const int per = (n + kFHeadThreads - 1) / kFHeadThreads;
-    const int i0 = tid * per, i1 = min(n, i0 + per);
-    int mine = 0;
-    for (int i = i0; i < i1; ++i) mine += order_key(x[i]) == kth;
-    __shared__ int scan[kFHeadThreads];
-    scan[tid] = mine;
-    __syncthreads();
-    for (int off = 1; off < kFHeadThreads; off <<= 1) {
-      const int v = tid >= off ? scan[tid - off] : 0;
-      __syncthreads();
-      scan[tid] += v;
-      __syncthreads();
-    }
-    int rank = scan[tid] - mine;
-    for (int i = i0; i < i1 && rank < need; ++i)
-      if (order_key(x[i]) == kth) {
-        atomicOr(reinterpret_cast<unsigned long long*>(&cov[(i / nb) * kFWords + ((i % nb) >> 6)]),
-                 1ull << ((i % nb) & 63));
-        ++rank;
-      }
-  }
+  // every row adds to one, so the total is nb <= 2^12: masses as integers x 2^(58 - ceil(log2 nb))
+  int scale = 58;
+  for (int t = 1; t < nb; t <<= 1) --scale;
+  const CutResult cut = radix_cut<true>(x, n, (double)a.gamma * nb, scale, 0, &cs);
+  if (cut.count > 0) emit_cut(x, n, nb, cut, cov, scan);
   __syncthreads();
-  if (tid == 0) cov[0] |= 1ull;                    // entry 0 (the padding value of score_cover_idx)
+  if (tid == 0) atomicOr(reinterpret_cast<unsigned long long*>(&cov[0]), 1ull);   // entry 0 (score_cover_idx's padding value)
 }
 
 struct FlexListK {
@@ -738,6 +818,7 @@ static size_t flex_work(int Hq, int Hk, int L, int bs, size_t* o_vert, size_t* o
 
 template <typename T, int BS>
 static int launch_lastq(const FlexK& k, unsigned grid, size_t smem1, size_t smem2, hipStream_t s) {
+  if (int rc = fs_host::allow_dynamic_lds(flex_lastq_kernel<T, 1, BS>, smem1, "fs_flex")) return rc;
   if (int rc = fs_host::allow_dynamic_lds(flex_lastq_kernel<T, 2, BS>, smem2, "fs_flex")) return rc;
   flex_lastq_kernel<T, 1, BS><<<grid, kFThreads, smem1, s>>>(k);
   flex_lastq_kernel<T, 2, BS><<<grid, kFThreads, smem2, s>>>(k);
@@ -762,8 +843,8 @@ static int launch_flex(const fs_flex_args& a, hipStream_t s) {
   k.vert = a.vertical ? a.vertical : reinterpret_cast<float*>(w + o_v);
   k.slash = a.slash ? a.slash : reinterpret_cast<float*>(w + o_s);
   const unsigned grid = (unsigned)(a.Hq * nchunk);
-  const size_t smem1 = (size_t)4 * 64 * 2 * sizeof(float);
-  const size_t smem2 = ((size_t)a.bs * kFTile + kFTile + a.bs + (size_t)a.bs * 2) * sizeof(float);
+  const size_t smem1 = (size_t)kFTile * kFD * sizeof(uint16_t);
+  const size_t smem2 = ((size_t)flex_tile_floats(a.bs) + kFTile + a.bs + (size_t)a.bs * 2 + kFThreads) * sizeof(float);
   if (int rc = a.bs == 32    ? launch_lastq<T, 32>(k, grid, smem1, smem2, s)
                : a.bs == 64 ? launch_lastq<T, 64>(k, grid, smem1, smem2, s)
                             : launch_lastq<T, 128>(k, grid, smem1, smem2, s))
@@ -781,7 +862,12 @@ static int launch_flex(const fs_flex_args& a, hipStream_t s) {
   hk.smask = reinterpret_cast<uint64_t*>(w + o_sm);
   hk.info = a.head_info ? a.head_info : reinterpret_cast<int32_t*>(w + o_in);
   hk.js = a.head_js ? a.head_js : reinterpret_cast<float*>(w + o_in + (size_t)a.Hq * 4 * sizeof(int32_t));
-  flex_head_kernel<T><<<(unsigned)a.Hq, kFHeadThreads, 0, s>>>(hk);
+  const size_t smem_head = (size_t)3 * nb * sizeof(float);
+  // the limit covers the kernel's static LDS as well
+  const size_t static_head = sizeof(double) * kFHeadThreads + sizeof(float) * kFD + sizeof(CutScratch) +
+                             sizeof(uint64_t) * kFWords;
+  if (int rc = fs_host::allow_dynamic_lds(flex_head_kernel<T>, smem_head + static_head, "fs_flex")) return rc;
+  flex_head_kernel<T><<<(unsigned)a.Hq, kFHeadThreads, smem_head, s>>>(hk);
   FlexCoverK ck{};
   ck.q = k.q; ck.q_sh = a.q_sh; ck.q_sl = a.q_sl; ck.avg_k = avg_k; ck.info = hk.info;
   ck.attn = reinterpret_cast<float*>(w + o_at);
