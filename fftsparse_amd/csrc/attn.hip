@@ -3,7 +3,7 @@
 // list, flash_attn_func(causal=True) (my_attn_v7.py:509-519).
 //
 // Pre-pass (vt_kernel): V [Lk][D] of every KV head is rewritten once per call
-// as V^T [D][Lp] (Lp = Nk * BS, zero padded) with the keys of every group of
+// as V^T [D][Lp] (Lp = Nk * BS rounded up to 64, zero padded) with the keys of every group of
 // 16 stored in the order 0-3, 8-11, 4-7, 12-15.  That order is exactly the
 // key order in which an S^T accumulator of v_mfma_f32_32x32x16 hands P to the
 // next MFMA (lane half hi owns keys hi*4..hi*4+3 and 8+hi*4..8+hi*4+3 of each
@@ -23,6 +23,8 @@
 //    wait overlaps the other's MFMAs).
 //  - BS = 64 uses TK = 64 split between two key groups (4 waves), merged
 //    through LDS at the end.
+//  - BS = 32 uses TK = 64 holding two listed key blocks, one per key group
+//    (2 waves of the same 32 queries), merged the same way.
 // LDS rows are 256 B with the 16-byte chunk c of row r stored at c ^ (r & 15)
 // so the 8 lanes of a ds_read_b128 phase hit distinct banks.
 //
@@ -145,17 +147,24 @@ __global__ __launch_bounds__(256) void vt_kernel(const uint16_t* __restrict__ v,
 template <int BS, int TK>
 struct AttnCfg {
   static constexpr int QW = BS / 32;          // query waves (32 queries each)
-  static constexpr int KG = 2 * TK / BS;      // key groups: waves sharing the keys of a tile (2 or 1)
+  // key groups: waves sharing the keys of a tile (2 or 1); at BS = 32 a tile
+  // holds two listed key blocks, one per key group
+  static constexpr int KG = BS == 32 ? 2 : 2 * TK / BS;
   static constexpr int NW = QW * KG;          // waves
   static constexpr int NT = NW * 64;          // threads
   static constexpr int KH = TK / KG;          // keys per wave per tile
   static constexpr int KT = KH / 32;          // 32-key sub-tiles per wave
-  static constexpr int TPB = BS / TK;         // tiles per key block
+  static constexpr int TPB = BS >= TK ? BS / TK : 1;   // tiles per key block
+  static constexpr int BPT = TK > BS ? TK / BS : 1;    // key blocks per tile (BS = 32)
   static constexpr int TILE = TK * kD;        // elements of one K (or V^T) tile
   static constexpr int REGIONS = TILE * 2 / 1024;   // 1 KiB DMA regions per tile
   static constexpr int DMA_PER_WAVE = 2 * REGIONS / NW;
   static_assert(KG == 1 || KG == 2, "tile is a block or half a block");
+  static_assert(BS != 32 || (TK == 64 && KH == 32), "32-token blocks: two blocks per 64-key tile");
 };
+
+// V^T row length: the key blocks, zero padded to whole 64-key slabs
+__host__ __device__ inline int vt_len(int Nk, int bs) { return (Nk * bs + 63) / 64 * 64; }
 
 // element offset of 16-byte chunk c of 256-byte row r, swizzled
 __device__ __forceinline__ int swz(int r, int c) { return r * kD + ((c ^ (r & 15)) << 3); }
@@ -268,6 +277,7 @@ void bsattn_kernel(AttnKArgs a) {
     return (int)((gi & 1) ? (w >> 16) : (w & 0xffffu));
   };
   int cnt;                                         // key tiles of this query block
+  int nb_listed = 0;                               // listed key blocks after the causal trim
   if (listed) {
     int nb = (int)((cptr32)(uintptr_t)a.blk_cnt)[(int64_t)h * a.Nq + qb];
     lbase = ((int64_t)h * a.Nq + qb) * a.Nk;
@@ -275,16 +285,31 @@ void bsattn_kernel(AttnKArgs a) {
     if (a.is_causal) {
       while (nb > 0 && block_at(nb - 1) * BS > q0 + BS - 1 + off) --nb;
     }
-    cnt = nb * C::TPB;
+    cnt = C::BPT > 1 ? (nb + C::BPT - 1) / C::BPT : nb * C::TPB;
+    nb_listed = nb;
   } else {
     const int last_key = a.is_causal ? min(a.Lk - 1, q0 + BS - 1 + off) : a.Lk - 1;
     cnt = last_key < 0 ? 0 : last_key / TK + 1;
   }
-  // first key of tile t (-1: an out-of-range list entry, skipped)
+  // first key of tile t (-1: an out-of-range list entry, skipped).  At BS = 32
+  // (two key blocks per tile) it is the first key of this wave's block of the
+  // tile, and block_key gives either block's.
+  const int nlisted = nb_listed;
+  auto block_key = [&](int t, int half) -> int {   // BS = 32
+    if (!listed) return t * TK + half * BS;
+    const int i = t * C::BPT + half;
+    if (i >= nlisted) return -1;
+    const int kb = block_at(i);
+    return kb < a.Nk ? kb * BS : -1;
+  };
   auto key_of = [&](int t) -> int {
-    if (!listed) return t * TK;
-    const int kb = block_at(t / C::TPB);
-    return kb < a.Nk ? kb * BS + (t % C::TPB) * TK : -1;
+    if constexpr (C::BPT > 1) {
+      return block_key(t, kh);
+    } else {
+      if (!listed) return t * TK;
+      const int kb = block_at(t / C::TPB);
+      return kb < a.Nk ? kb * BS + (t % C::TPB) * TK : -1;
+    }
   };
 
   // ---- tile DMA: wave w copies 1 KiB regions w*NR .. w*NR+NR-1 of the K tile
@@ -298,14 +323,41 @@ void bsattn_kernel(AttnKArgs a) {
     const int R = wave * NR + i;                   // region: LDS rows 4R .. 4R+3
     const int r = 4 * R + (lane >> 4);
     const int c = (lane & 15) ^ (r & 15);
-    koff[i] = (uint32_t)(r * a.k_sl + c * 8) * 2u;
-    voff[i] = (TK == 128 ? (uint32_t)(r * a.Lp + c * 8)                          // d = r
-                         : (uint32_t)((2 * r + (c >> 3)) * a.Lp + (c & 7) * 8))  // two d rows per LDS row
-              * 2u;
+    if constexpr (C::BPT > 1) {
+      // K rows relative to this wave's key block (its 32 rows of the tile);
+      // V^T chunks (c & 7) < 4 hold the first block's keys, the others the second's
+      koff[i] = (uint32_t)((r - wave * 4 * NR) * a.k_sl + c * 8) * 2u;
+      voff[i] = (uint32_t)((2 * r + (c >> 3)) * a.Lp + (c & 3) * 8) * 2u;
+    } else {
+      koff[i] = (uint32_t)(r * a.k_sl + c * 8) * 2u;
+      voff[i] = (TK == 128 ? (uint32_t)(r * a.Lp + c * 8)                          // d = r
+                           : (uint32_t)((2 * r + (c >> 3)) * a.Lp + (c & 7) * 8))  // two d rows per LDS row
+                * 2u;
+    }
   }
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&lds[0][0][0]);
   auto issue_k = [&](int key0, int buf) {
     const uint32_t lk = lds0 + (uint32_t)(buf * C::TILE * 2 + wave * NR * 1024);
+    if constexpr (C::BPT > 1) {
+      // this wave's key block: 32 rows from key0
+      const int kc = min(max(key0, 0), a.Lk - 1);
+      const uint16_t* base = kp + (int64_t)kc * a.k_sl;
+      if (key0 >= 0 && key0 + 4 * NR <= a.Lk) {
+#pragma unroll
+        for (int i = 0; i < NR; ++i) dma16s(lk + i * 1024, base, koff[i]);
+      } else {
+        // rows past Lk (or of a missing block) read row Lk-1 instead (their scores are masked)
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+#pragma unroll
+        for (int i = 0; i < NR; ++i) {
+          const int rr = 4 * i + (ln >> 4);          // row within this wave's block
+          const int c = (ln & 15) ^ ((4 * (wave * NR + i) + (ln >> 4)) & 15);
+          dma16s(lk + i * 1024, base, (uint32_t)(min(rr, a.Lk - 1 - kc) * a.k_sl + c * 8) * 2u);
+        }
+      }
+      return;
+    }
     if (key0 >= 0 && key0 + TK <= a.Lk) {
       const uint16_t* base = kp + (int64_t)key0 * a.k_sl;
 #pragma unroll
@@ -326,8 +378,20 @@ void bsattn_kernel(AttnKArgs a) {
     }
   };
   auto issue_v = [&](int key0, int buf) {
-    const uint16_t* base = vtp + max(key0, 0);     // V^T is zero padded to Lp = Nk * BS
     const uint32_t lv = lds0 + (uint32_t)((2 + buf) * C::TILE * 2 + wave * NR * 1024);
+    if constexpr (C::BPT > 1) {
+      // key0 is the tile index here: the two key blocks' V^T columns
+      const uint32_t kA = (uint32_t)max(block_key(key0, 0), 0) * 2u;
+      const uint32_t kB = (uint32_t)max(block_key(key0, 1), 0) * 2u;
+#pragma unroll
+      for (int i = 0; i < NR; ++i) {
+        const int r = 4 * (wave * NR + i) + (lane >> 4);
+        const int c = (lane & 15) ^ (r & 15);
+        dma16s(lv + i * 1024, vtp, voff[i] + ((c & 4) ? kB : kA));
+      }
+      return;
+    }
+    const uint16_t* base = vtp + max(key0, 0);     // V^T is zero padded to Lp
 #pragma unroll
     for (int i = 0; i < NR; ++i) dma16s(lv + i * 1024, base, voff[i]);
   };
@@ -377,7 +441,7 @@ void bsattn_kernel(AttnKArgs a) {
   };
   // whether any key of this wave's half of tile kb is visible to its queries
   auto active_for = [&](int key0) {
-    const int kw0 = key0 + kbase;
+    const int kw0 = C::BPT > 1 ? key0 : key0 + kbase;
     return key0 >= 0 && kw0 < a.Lk && !(a.is_causal && kw0 > qw0 + 31 + off);
   };
 
@@ -385,7 +449,7 @@ void bsattn_kernel(AttnKArgs a) {
   // whose scores are in s; the running max is taken later, beside the
   // exponentials of that tile.
   auto mask_only = [&](int key0, f32x16_t* s) {
-    const int kw0 = key0 + kbase;
+    const int kw0 = C::BPT > 1 ? key0 : key0 + kbase;
     const bool act = active_for(key0);
     if (!act || (kw0 + C::KH > a.Lk) || (a.is_causal && kw0 + C::KH - 1 > qw0 + off)) {
       int lim = a.Lk - kw0 - hi * 4;
@@ -475,7 +539,7 @@ void bsattn_kernel(AttnKArgs a) {
       kb2 = key_of(t + 2);
       issue_k(kb2, t & 1);
     }
-    if (t < cnt) issue_v(kb0, t & 1);
+    if (t < cnt) issue_v(C::BPT > 1 ? t : kb0, t & 1);
     __builtin_amdgcn_s_setprio(2);
     // The row max of tile t, the raise of the running max and the
     // exponentials of tile t are VALU work independent of the MFMAs of S(t+1)
@@ -654,14 +718,14 @@ __global__ __launch_bounds__(kOrderThreads) void order_kernel(const int32_t* __r
 }
 
 static size_t vt_bytes(const fs_attn_args& a) {
-  const int64_t Nk = (a.Lk + a.bs - 1) / a.bs;
-  return ((size_t)a.B * a.Hk * a.D * Nk * a.bs * 2 + 255) & ~(size_t)255;
+  const int Nk = (a.Lk + a.bs - 1) / a.bs;
+  return ((size_t)a.B * a.Hk * a.D * vt_len(Nk, a.bs) * 2 + 255) & ~(size_t)255;
 }
 
 // order pass (block lists only) and the main kernel, reading V^T from the workspace
 template <int BS, int TK, typename T>
 static int launch_run(const fs_attn_args& a, int Nq, int Nk, hipStream_t s) {
-  const int Lp = Nk * BS;
+  const int Lp = vt_len(Nk, BS);
   const uint16_t* vt = static_cast<const uint16_t*>(a.work);
   int32_t* order = nullptr;
   int total;
@@ -718,7 +782,7 @@ static int check_attn(const fs_attn_args* a, const char* fn) {
                "%s: Hq=%d must be a multiple of Hk=%d", fn, a->Hq, a->Hk);
   FS_CHECK_ARG(a->Lq >= 1 && a->Lk >= 1, "%s: empty sequence", fn);
   FS_CHECK_SUPPORTED(a->D == kD, "%s: head_dim %d unsupported (128 only)", fn, a->D);
-  FS_CHECK_SUPPORTED(a->bs == 64 || a->bs == 128, "%s: block size %d unsupported", fn, a->bs);
+  FS_CHECK_SUPPORTED(a->bs == 32 || a->bs == 64 || a->bs == 128, "%s: block size %d unsupported", fn, a->bs);
   FS_CHECK_SUPPORTED(a->dtype == FS_DTYPE_BF16 || a->dtype == FS_DTYPE_F16,
                      "%s: dtype %d unsupported (bf16/f16)", fn, a->dtype);
   FS_CHECK_ARG(a->blk_cnt == nullptr || (a->blk_idx != nullptr && a->B == 1),
@@ -734,7 +798,7 @@ static int check_attn(const fs_attn_args* a, const char* fn) {
   FS_CHECK_SUPPORTED((int64_t)a->B * a->Hq * Nq < (1ll << 30) && (int64_t)a->B * a->Hk * Nk * a->bs / 64 < (1ll << 31),
                      "%s: grid too large", fn);
   // per-lane tile-copy offsets are 32-bit byte offsets: 128 rows of a row stride, 128 d rows of V^T
-  FS_CHECK_SUPPORTED(a->q_sl < (1 << 23) && a->k_sl < (1 << 23) && a->o_sl < (1 << 23) && Nk * a->bs < (1 << 23),
+  FS_CHECK_SUPPORTED(a->q_sl < (1 << 23) && a->k_sl < (1 << 23) && a->o_sl < (1 << 23) && vt_len((int)Nk, a->bs) < (1 << 23),
                      "%s: row stride or sequence too large", fn);
   return FS_OK;
 }
@@ -742,7 +806,7 @@ static int check_attn(const fs_attn_args* a, const char* fn) {
 extern "C" int fs_bsattn_prepare(const fs_attn_args* a, void* stream) {
   if (int rc = check_attn(a, "fs_bsattn_prepare")) return rc;
   const int Nk = (a->Lk + a->bs - 1) / a->bs;
-  const int Lp = Nk * a->bs;
+  const int Lp = vt_len(Nk, a->bs);
   vt_kernel<<<a->B * a->Hk * (Lp / 64), 256, 0, (hipStream_t)stream>>>(
       static_cast<const uint16_t*>(a->v), a->v_sb, a->v_sh, a->v_sl, static_cast<uint16_t*>(a->work), a->Hk, a->Lk,
       Lp);
@@ -757,6 +821,10 @@ extern "C" int fs_bsattn_run(const fs_attn_args* a, void* stream) {
   if (a->bs == 128) {
     return a->dtype == FS_DTYPE_BF16 ? launch_run<128, 64, bf16_t>(*a, Nq, Nk, s)
                                      : launch_run<128, 64, f16_t>(*a, Nq, Nk, s);
+  }
+  if (a->bs == 32) {
+    return a->dtype == FS_DTYPE_BF16 ? launch_run<32, 64, bf16_t>(*a, Nq, Nk, s)
+                                     : launch_run<32, 64, f16_t>(*a, Nq, Nk, s);
   }
   return a->dtype == FS_DTYPE_BF16 ? launch_run<64, 64, bf16_t>(*a, Nq, Nk, s) : launch_run<64, 64, f16_t>(*a, Nq, Nk, s);
 }

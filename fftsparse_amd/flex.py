@@ -101,9 +101,8 @@ def Flexprefill_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gamma
     """Flexprefill.py:1063-1098: q/k/v [B, L, H, D] -> [B, L, H, D].  Sequences
     of at most max(2 bs, ceil(min_budget / bs) bs) tokens take dense causal
     attention (:1084-1085), the others the FlexPrefill selection and the
-    block-sparse attention.  The attention kernel runs blocks of 64 and 128:
-    the selection of smaller blocks is available from ``flex_select``, their
-    attention is not built (NotImplementedError)."""
+    block-sparse attention.  The attention kernel runs blocks of 32, 64 and
+    128; 16-token blocks raise NotImplementedError."""
     assert q.is_cuda, "input tensors must be on the GPU"
     B, L, H, D = q.shape
     assert q.shape[1] == k.shape[1]
@@ -113,8 +112,8 @@ def Flexprefill_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gamma
     qv, kv, vv = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
     if L <= max(2 * block_size, math.ceil(mn / block_size) * block_size):
         return block_sparse_attention(qv, kv, vv, block_size=128, is_causal=True, softmax_scale=softmax_scale)
-    if block_size not in (64, 128):
-        raise NotImplementedError(f"block-sparse attention over {block_size}-token blocks is not built (64, 128)")
+    if block_size not in (32, 64, 128):
+        raise NotImplementedError(f"block-sparse attention over {block_size}-token blocks is not built (32, 64, 128)")
     if gqa_interleave:
         raise NotImplementedError("the attention kernel maps query head h to key head h // (H / Hk); "
                                   "interleaved GQA is not built")

@@ -281,7 +281,8 @@ FS_API int fs_flex(const fs_flex_args* a, void* stream);
  * key tokens s of the selected key blocks of query block t / bs (and s <= t +
  * Lk - Lq when is_causal).  blk_cnt == NULL selects every key block up to the
  * causal limit (dense causal attention).  Supported: dtype bf16/f16, D == 128,
- * bs in {64, 128}.  All tensors are strided views with d contiguous.
+ * bs in {32, 64, 128} (32: FlexPrefill's default block size).  All tensors are
+ * strided views with d contiguous.
  * work: fs_bsattn_work_bytes(a) bytes of device scratch (V is staged there
  * transposed, and the work items' longest-first order is computed there,
  * before the attention kernel runs). */

@@ -212,9 +212,27 @@ def test_flex_prefill_attention_parity():
     assert err.max().item() <= 2e-2 and err.mean().item() <= 1e-3
 
 
+def test_flex_prefill_reference_call_32_token_blocks():
+    """The reference's own call (eval/LongBench/pred.py:269-275: gamma 0.9,
+    tau 0.1, the default 32-token blocks): attention under the kernel's lists
+    against fp32 attention under the same mask."""
+    _case(L=6000, prefill=True, bs=32)
+    q, k, v = make_qkv(6000, 4, 2, dtype=torch.bfloat16, seed=47)
+    ql, kl, vl = _blhd(q, k, v)
+    out = Flexprefill_prefill(ql.to(DEV), kl.to(DEV), vl.to(DEV), gamma=0.9, tau=0.1)
+    torch.cuda.synchronize()
+    assert out.shape == (1, 6000, 4, 128)
+    sel = flex_select(ql.to(DEV), kl.to(DEV), gamma=0.9, tau=0.1, block_size=32)
+    mask = sel.dense_mask().cpu()
+    ref = v7.block_sparse_attention(q, k, v, mask, 32)
+    err = (out[0].float().cpu() - ref).abs()
+    print(f"  density {density(sel):.4f} max_abs={err.max().item():.3e} mean_abs={err.mean().item():.3e}")
+    assert err.max().item() <= 2e-2 and err.mean().item() <= 1e-3
+
+
 def test_flex_prefill_short_sequence_is_dense_and_small_blocks_raise():
     """L <= max(2 bs, ceil(min_budget / bs) bs) takes dense causal attention
-    (Flexprefill.py:1084-1085); 32-token attention blocks are not built."""
+    (Flexprefill.py:1084-1085); 16-token attention blocks are not built."""
     _case(L=256, dense=True)
     q, k, v = make_qkv(256, 2, 1, dtype=torch.bfloat16, seed=45)
     ql, kl, vl = _blhd(q, k, v)
@@ -225,7 +243,7 @@ def test_flex_prefill_short_sequence_is_dense_and_small_blocks_raise():
     q, k, v = make_qkv(1024, 2, 1, dtype=torch.bfloat16, seed=46)
     ql, kl, vl = _blhd(q, k, v)
     with pytest.raises(NotImplementedError):
-        Flexprefill_prefill(ql.to(DEV), kl.to(DEV), vl.to(DEV), block_size=32)
+        Flexprefill_prefill(ql.to(DEV), kl.to(DEV), vl.to(DEV), block_size=16)
     # min_budget of the whole sequence: dense as well
     out = Flexprefill_prefill(ql.to(DEV), kl.to(DEV), vl.to(DEV), block_size=32, min_budget=1024)
     ref = v7.block_sparse_attention(q, k, v, torch.ones(2, 8, 8, dtype=torch.bool), 128)

@@ -293,6 +293,7 @@ def _attn_check(out, ref, rows=None):
     (6000, 4, 2, 128, torch.bfloat16),
     (4096, 4, 1, 64, torch.bfloat16),
     (8192, 4, 4, 128, torch.float16),
+    (4000, 4, 2, 32, torch.bfloat16),        # 32-token blocks: 125 key blocks (odd), ragged L
 ])
 def test_attention_parity_reference_mask(L, Hq, Hk, bs, dtype):
     """Stage 2 alone, under the oracle's mask."""
@@ -326,7 +327,7 @@ def test_attention_running_max_raises(growth):
     shared direction): the running max is raised on nearly every tile, and at
     growth 3000 the exponentials taken against the stale max overflow to inf
     before the check replaces them.  Dense causal and listed (every causal
-    block, ascending) paths, both block sizes."""
+    block, ascending) paths, every block size."""
     _print_case("attention-raise", growth=growth)
     L, D = 2048, 128
     g = torch.Generator().manual_seed(11)
@@ -340,12 +341,42 @@ def test_attention_running_max_raises(growth):
     ref = v7.dense_causal_attention(q, k, v)[0]
     out = block_sparse_attention(*_gpu(q, k, v), block_size=128, is_causal=True)
     _attn_check(out[0], ref)
-    for bs in (128, 64):
+    for bs in (128, 64, 32):
         N = L // bs
         mask = torch.tril(torch.ones(2, N, N, dtype=torch.bool))
         cnt, idx = lists_from_mask(mask, DEV)
         out = block_sparse_attention(*_gpu(q, k, v), cnt, idx, block_size=bs)
         _attn_check(out[0], ref)
+
+
+@pytest.mark.parametrize("L,Hq,Hk,dtype,density,causal", [
+    (4000, 4, 2, torch.bfloat16, 0.3, True),      # 125 key blocks: a tile's second block missing in odd rows
+    (2048, 2, 1, torch.float16, 0.5, True),
+    (1000, 2, 2, torch.bfloat16, 0.4, False),     # non-causal, ragged
+])
+def test_attention_32_token_blocks(L, Hq, Hk, dtype, density, causal):
+    """32-token blocks (two listed key blocks per 64-key tile, one per key
+    group) under random block lists of odd and even lengths, against fp32
+    attention under the same mask; and the dense causal path at 32."""
+    _print_case("attention-bs32", L=L, Hq=Hq, Hk=Hk, dtype=dtype, density=density, causal=causal)
+    q, k, v = make_qkv(L, Hq, Hk, dtype=dtype, seed=12)
+    N = (L + 31) // 32
+    g = torch.Generator().manual_seed(13)
+    mask = torch.rand(Hq, N, N, generator=g) < density
+    mask |= torch.eye(N, dtype=torch.bool)
+    mask[:, :, 0] = True
+    if causal:
+        mask &= torch.ones(N, N, dtype=torch.bool).tril()
+    mask[0, 5] = False                          # a row holding only ...
+    mask[0, 5, 5] = True                        # ... its diagonal block
+    cnt, idx = lists_from_mask(mask, DEV)
+    out = block_sparse_attention(*_gpu(q, k, v), cnt, idx, block_size=32, is_causal=causal)
+    torch.cuda.synchronize()
+    ref = v7.block_sparse_attention(q, k, v, mask, 32, is_causal=causal)
+    _attn_check(out[0], ref)
+    if causal:
+        out = block_sparse_attention(*_gpu(q, k, v), block_size=32, is_causal=True)
+        _attn_check(out[0], v7.dense_causal_attention(q, k, v)[0])
 
 
 def test_attention_prepare_run_equals_single_call():
