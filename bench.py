@@ -49,6 +49,8 @@ def parse():
     ap.add_argument("--flex-gamma", type=float, default=0.95,
                     help="FlexPrefill's gamma (the reference benchmark's default)")
     ap.add_argument("--flex-tau", type=float, default=0.1, help="FlexPrefill's tau (the reference benchmark's default)")
+    ap.add_argument("--flex-block", type=int, default=32, choices=(32, 64, 128),
+                    help="FlexPrefill's block size (the reference benchmark calls it with its default, 32)")
     ap.add_argument("--no-dense", action="store_true", help="skip the dense comparators")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--select-groups", type=int, default=None,
@@ -227,13 +229,14 @@ def main():
 
     cfg = CONFIGS[args.config]
     dev = torch.device("cuda:0")
+    flex = args.selector == "flex"
     t_gen = time.perf_counter()
     q, k, v = make_config(cfg, seed=args.seed)
     q, k, v = q.to(dev), k.to(dev), v.to(dev)
     torch.cuda.synchronize()
     t_gen = time.perf_counter() - t_gen
     kw = dict(PROD, block_size=cfg.block_size, corr_threshold=args.threshold)
-    bs = cfg.block_size
+    bs = args.flex_block if flex else cfg.block_size
     Hq, L, D = q.shape[1], q.shape[2], q.shape[3]
     Hk = k.shape[1]
 
@@ -241,7 +244,6 @@ def main():
     # pre-pass, then order + attention kernel), all on torch's current stream,
     # which is the stream the events below are recorded on.
     xattn = args.selector == "xattn"
-    flex = args.selector == "flex"
     if xattn:
         from fftsparse_amd.xattn import xattn_select
     if flex:
@@ -300,10 +302,10 @@ def main():
     if not args.no_dense:
         # our kernel on the full causal block set
         e = [(_ev(), _ev()) for _ in range(3)]
-        block_sparse_attention(q, k, v, block_size=bs)
+        block_sparse_attention(q, k, v, block_size=cfg.block_size)
         for a, b in e:
             a.record()
-            block_sparse_attention(q, k, v, block_size=bs)
+            block_sparse_attention(q, k, v, block_size=cfg.block_size)
             b.record()
         torch.cuda.synchronize()
         dense["own_dense_ms"] = statistics.mean(a.elapsed_time(b) for a, b in e)
@@ -367,9 +369,8 @@ def main():
                            "timed": "select_blocks: pool, block-score tiles + statistics (2 launches), block lists "
                                     "(2 launches)"}
     sel_desc = (f"XAttention selection (stride {args.xattn_stride}, threshold {args.threshold})" if xattn
-                else f"FlexPrefill selection (gamma {args.flex_gamma}, tau {args.flex_tau}, {bs}-token blocks; the "
-                     f"reference benchmark runs FlexPrefill at 32-token blocks, which this attention kernel does "
-                     f"not take)" if flex
+                else f"FlexPrefill selection and attention at {bs}-token blocks (gamma {args.flex_gamma}, tau "
+                     f"{args.flex_tau}; the reference benchmark's call uses the default block size, 32)" if flex
                 else f"corr_threshold {args.threshold}, production kwargs")
     line = {
         "metric": METRIC,

@@ -19,10 +19,15 @@
 //  32x32x16 the compiler's wait before reading that result's last accumulator
 //  register was found too short (the read saw the value before the last MFMA).
 // flex_kpool_kernel: block means of K over each block's real rows, in T.
+// cut_pass_kernel<P> (four launches per cut): the mass cut of the descending
+//   prefix sums at gamma (score_cover_topk / score_cover_idx) over many
+//   workgroups: pass P histograms the P-th 8-bit digit of the order-preserving
+//   key among the elements carrying the digits found so far, with exact
+//   integer masses; jobs are the heads' vertical and slash profiles (budgets)
+//   and, later, the sparse heads' block attention (covers).
 // flex_head_kernel: one workgroup (1024 threads) per head:
-//   cover counts  n = #(descending prefix sums <= gamma) + 1 of vertical and
-//                 slash (a bisection on the value, fp64 fixed-order sums),
-//                 // 128 + 1, clamped to the block budgets;
+//   budgets       the profiles' cover counts n + 1 (replayed from their cut
+//                 histograms), // 128 + 1, clamped to the block budgets;
 //   pooled        block sums of vertical / slash; the bs-row mean of the
 //                 scaled last queries against the K block means (T), softmax;
 //   js            square-root Jensen-Shannon divergence to the pooled vertical
@@ -31,13 +36,15 @@
 //   choice        the top budgets of pooled vertical (block 0 forced) and
 //                 pooled slash (offset 0 forced), ties by the lower index, as
 //                 bit masks.
-// flex_cover_kernel: for each sparse head, the block-level causal attention
-//   softmax(avg_q / sqrt(D) avg_k^T) (block means of q, the last one rescaled
-//   to its real rows), and the entries whose descending prefix sum is at most
-//   gamma * N, as an N x N bit mask.
+// flex_cover_rows_kernel: for each sparse head, the block-level causal
+//   attention softmax(avg_q / sqrt(D) avg_k^T) (block means of q, the last one
+//   rescaled to its real rows); its cut at gamma * N by cut_pass_kernel, and
+//   flex_cover_emit_kernel writes the kept entries as an N x N bit mask.
 // flex_lists_kernel: per (head, block row r): the vertical columns <= r, the
 //   diagonals r - s of the chosen slash offsets, the sparse cover's row, as an
 //   ascending list (64-bit words, popcount offsets).
+#include <algorithm>
+
 #include "common.h"
 
 namespace fs {
@@ -87,6 +94,10 @@ struct FlexK {
   float* part;                  // [Hq][nchunk][bs][2] (max, sum) per chunk
   float* vert;                  // [Hq][L]
   float* slash;                 // [Hq][L]
+  uint64_t* p_hm;               // the cut histograms, zeroed here (PASS 1, chunk 0 of each head):
+  uint32_t* p_hc;               //   profiles [4][2 Hq][256]
+  uint64_t* c_hm;               //   covers [4][Hq][256]
+  uint32_t* c_hc;
 };
 
 __device__ __forceinline__ int kv_head(int h, int Hq, int Hk, int interleave) {
@@ -143,6 +154,21 @@ __global__ __launch_bounds__(kFThreads) void flex_lastq_kernel(FlexK a) {
   float* carry = dyn + flex_tile_floats(bs);      // [kFTile + bs] diagonal partials in flight
   float* rowstat = carry + kFTile + bs;           // [bs][2]
   float* vpart = rowstat + 2 * bs;                // [kFThreads] column sums of the two row halves
+  if (PASS == 1 && chunk == 0) {
+    // this head's cut histograms (profiles 2 h, 2 h + 1 and cover h, four passes)
+    for (int e = tid; e < 4 * 3 * 256; e += kFThreads) {
+      const int p = e / (3 * 256), r = e - p * 3 * 256, jj = r >> 8, d = r & 255;
+      if (jj < 2) {
+        const int64_t i = ((int64_t)p * 2 * a.Hq + 2 * h + jj) * 256 + d;
+        a.p_hm[i] = 0;
+        a.p_hc[i] = 0;
+      } else {
+        const int64_t i = ((int64_t)p * a.Hq + h) * 256 + d;
+        a.c_hm[i] = 0;
+        a.c_hc[i] = 0;
+      }
+    }
+  }
   if (PASS == 2) {
     // combine the chunk partials of each row in a fixed order
     if (tid < bs) {
@@ -379,6 +405,7 @@ struct CutResult {
   int count;                    // elements in the cut
   uint32_t key;                 // boundary key: every larger key is in the cut
   int take_eq;                  // elements equal to the boundary key in the cut (lowest index first)
+  int eq_total;                 // elements equal to the boundary key
 };
 
 // BY_MASS: the descending prefix-sum cut of x >= 0 at g (score_cover_topk
@@ -461,7 +488,7 @@ __device__ CutResult radix_cut(const float* x, int n, double g, int scale_exp, i
     const int d = cs->digit;
     if (d < 0) {                                   // everything is in the cut (first pass only)
       __syncthreads();
-      return {n, 0u, 0};
+      return {n, 0u, 0, 0};
     }
     prefix = (prefix << 8) | (uint32_t)d;
     above = cs->mass;
@@ -478,46 +505,230 @@ __device__ CutResult radix_cut(const float* x, int n, double g, int scale_exp, i
       } else {
         take = want - cnt_above;
       }
-      return {cnt_above + take, prefix, take};
+      return {cnt_above + take, prefix, take, (int)eq};
     }
   }
-  return {n, 0u, 0};                               // not reached
+  return {n, 0u, 0, 0};                            // not reached
 }
 
-// Sets, in out, the bits of the elements of a cut: every key above cut.key and
-// the first cut.take_eq elements equal to it in index order.  Element i of a
-// row of row_len elements goes to bit (i % row_len) of row i / row_len, rows
-// kFWords words apart.  Each thread owns a contiguous index range; a fixed-order
-// scan of the per-thread tie counts ranks the ties.
-__device__ void emit_cut(const float* x, int n, int row_len, const CutResult& cut, uint64_t* out, int* scan) {
-  const int tid = threadIdx.x;
-  const int per = (n + kFHeadThreads - 1) / kFHeadThreads;
-  const int i0 = min(n, tid * per), i1 = min(n, i0 + per);
-  auto set = [&](int i) {
-    const int r = i / row_len, c = i - r * row_len;
-    atomicOr(reinterpret_cast<unsigned long long*>(&out[(int64_t)r * kFWords + (c >> 6)]), 1ull << (c & 63));
-  };
-  int mine = 0;
-  for (int i = i0; i < i1; ++i) {
-    const uint32_t k = order_key(x[i]);
-    if (k > cut.key) set(i);
-    else if (k == cut.key) ++mine;
-  }
-  scan[tid] = mine;
-  __syncthreads();
-  for (int off = 1; off < kFHeadThreads; off <<= 1) {
-    const int v = tid >= off ? scan[tid - off] : 0;
-    __syncthreads();
-    scan[tid] += v;
-    __syncthreads();
-  }
-  int rank = scan[tid] - mine;
-  __syncthreads();                                 // scan is reused by the caller
-  for (int i = i0; i < i1 && rank < cut.take_eq; ++i)
-    if (order_key(x[i]) == cut.key) {
-      set(i);
-      ++rank;
+// Writes, in out, the bits of the elements of a cut: every key above cut.key
+// and the first cut.take_eq elements equal to it in index order.  Element i of
+// a row of row_len elements is bit i % row_len of row i / row_len, rows kFWords
+// words apart; every word of the rows' first ceil(row_len / 64) is written (one
+// ballot per word, no atomics).  Each wave owns a contiguous range of words;
+// when the cut splits the elements equal to its key, a fixed-order prefix of
+// the waves' tie counts ranks them.
+// Words wb .. we-1 only, with base_rank ties before them, when given.
+__device__ void emit_cut(const float* x, int rows, int row_len, const CutResult& cut, uint64_t* out, int* scan,
+                         int wb = 0, int we = -1, int base_rank = 0) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  constexpr int kWaves = kFHeadThreads / 64;
+  const int wpr = (row_len + 63) >> 6;             // words per row
+  if (we < 0) we = rows * wpr;
+  const int per = (we - wb + kWaves - 1) / kWaves;
+  const int w0 = min(we, wb + wave * per), w1 = min(we, w0 + per);
+  const bool ranked = cut.take_eq > 0 && cut.take_eq < cut.eq_total;
+  const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;   // lanes under this one
+  int rank = base_rank;
+  if (ranked) {
+    int cnt = 0;
+    for (int w = w0; w < w1; ++w) {
+      const int r = w / wpr, c = (w - r * wpr) * 64 + lane;
+      const bool eq = c < row_len && order_key(x[(int64_t)r * row_len + c]) == cut.key;
+      cnt += __popcll(__ballot(eq));
     }
+    if (lane == 0) scan[wave] = cnt;
+    __syncthreads();
+    for (int v = 0; v < wave; ++v) rank += scan[v];
+    __syncthreads();                               // scan is reused by the caller
+  }
+  for (int w = w0; w < w1; ++w) {
+    const int r = w / wpr, c = (w - r * wpr) * 64 + lane;
+    bool in = false, eq = false;
+    if (c < row_len) {
+      const uint32_t k = order_key(x[(int64_t)r * row_len + c]);
+      in = k > cut.key;
+      eq = k == cut.key;
+    }
+    if (ranked) {
+      const uint64_t eqm = __ballot(eq);
+      in = in || (eq && rank + __popcll(eqm & below) < cut.take_eq);
+      rank += __popcll(eqm);
+    } else {
+      in = in || (eq && cut.take_eq > 0);
+    }
+    const uint64_t word = __ballot(in);
+    if (lane == 0) out[(int64_t)r * kFWords + (w - r * wpr)] = word;
+  }
+}
+
+// ---- the same mass cuts over many workgroups -----------------------------
+// A job is one array to cut: a head's vertical or slash profile (the budgets)
+// or a sparse head's N x N block attention (its cover).  Pass p is one launch
+// over (job, slice) workgroups: each histograms the p-th key digit of its
+// slice's elements that carry the digits found by passes < p (replayed from
+// those passes' global histograms by one wave) and adds its histogram to the
+// job's global one with integer atomics (exact, so independent of order).
+constexpr int kCutSliceThreads = 256;
+
+struct CutJobs {
+  const float* x0;              // kind 0 data of head h at x0 + h * stride
+  const float* x1;              // kind 1 data (kinds == 2)
+  int64_t stride;
+  int n;                        // elements per job
+  int kinds;                    // jobs per head (1 or 2)
+  int jobs, slices;
+  int scale_exp;                // masses as integers x * 2^scale_exp
+  double g;                     // mass bound of the cut
+  const int32_t* info;          // [Hq][4]: only the jobs of sparse heads run (null: every job)
+  uint64_t* hm;                 // [4][jobs][256] mass per digit (zeroed before pass 0)
+  uint32_t* hc;                 // [4][jobs][256] count per digit
+};
+
+__device__ __forceinline__ const float* job_data(const CutJobs& c, int j) {
+  const int h = j / c.kinds, kind = j - h * c.kinds;
+  return (kind ? c.x1 : c.x0) + (int64_t)h * c.stride;
+}
+__device__ __forceinline__ bool job_live(const CutJobs& c, int j) {
+  return c.info == nullptr || c.info[(j / c.kinds) * 4 + 2] != 0;
+}
+
+struct CutState {
+  uint64_t above, mass;         // mass above the digits found so far; crossing scratch
+  uint32_t prefix, eq;          // digits found so far; elements equal to the boundary key
+  int cnt_above, cnt, digit;
+  int all;                      // 1: everything is in the cut
+};
+
+// Replays passes 0 .. npass-1 of job j from the global histograms into st (LDS);
+// every thread of the workgroup calls it, lanes 0-63 scan.
+__device__ void cut_replay(const CutJobs& c, int j, int npass, CutState* st) {
+  const int tid = threadIdx.x;
+  const uint64_t G = (uint64_t)(c.g * ldexp(1.0, c.scale_exp));
+  __syncthreads();                                 // st of an earlier call has been read
+  if (tid == 0) {
+    st->prefix = 0;
+    st->above = 0;
+    st->cnt_above = 0;
+    st->all = 0;
+    st->eq = 0;
+  }
+  __syncthreads();
+  for (int p = 0; p < npass; ++p) {
+    if (tid == 0) st->digit = -1;
+    __syncthreads();
+    if (tid < 64 && !st->all) {
+      const uint64_t* hm = c.hm + ((int64_t)p * c.jobs + j) * 256;
+      const uint32_t* hc = c.hc + ((int64_t)p * c.jobs + j) * 256;
+      uint64_t lm[4], sm = 0;
+      uint32_t lc[4], scn = 0;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int d = 255 - 4 * tid - t;
+        lm[t] = hm[d];
+        lc[t] = hc[d];
+        sm += lm[t];
+        scn += lc[t];
+      }
+      uint64_t im = sm;
+      uint32_t ic = scn;
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint64_t vm = __shfl_up(im, o, 64);
+        const uint32_t vc = __shfl_up(ic, o, 64);
+        if (tid >= o) {
+          im += vm;
+          ic += vc;
+        }
+      }
+      uint64_t run = st->above + (im - sm);
+      uint32_t runc = (uint32_t)st->cnt_above + (ic - scn);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const uint64_t prev = run;
+        const uint32_t prevc = runc;
+        run += lm[t];
+        runc += lc[t];
+        if (prev <= G && run > G) {
+          st->digit = 255 - 4 * tid - t;
+          st->mass = prev;
+          st->cnt = (int)prevc;
+          st->eq = lc[t];
+        }
+      }
+    }
+    __syncthreads();
+    if (tid == 0 && !st->all) {
+      if (st->digit < 0) {
+        st->all = 1;
+      } else {
+        st->prefix = (st->prefix << 8) | (uint32_t)st->digit;
+        st->above = st->mass;
+        st->cnt_above = st->cnt;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// the cut after the four passes
+__device__ CutResult cut_result(const CutJobs& c, const CutState& st) {
+  if (st.all) return {c.n, 0u, 0, 0};
+  const double sc = ldexp(1.0, c.scale_exp);
+  const uint64_t G = (uint64_t)(c.g * sc);
+  const uint64_t mv = (uint64_t)((double)key_to_f32(st.prefix) * sc);   // > 0: it pushed the sum past G
+  const uint64_t fit = mv ? (G - st.above) / mv : (uint64_t)st.eq;
+  const int take = (int)(fit < (uint64_t)st.eq ? fit : (uint64_t)st.eq);
+  return {st.cnt_above + take, st.prefix, take, (int)st.eq};
+}
+
+template <int PASS>
+__global__ __launch_bounds__(kCutSliceThreads) void cut_pass_kernel(CutJobs c) {
+  __shared__ uint64_t lhm[kCutCopies][256];
+  __shared__ uint32_t lhc[kCutCopies][256];
+  __shared__ CutState st;
+  const int j = blockIdx.x / c.slices, sl = blockIdx.x - j * c.slices;
+  if (!job_live(c, j)) return;
+  const int tid = threadIdx.x;
+  cut_replay(c, j, PASS, &st);
+  if (st.all) return;
+  for (int e = tid; e < kCutCopies * 256; e += kCutSliceThreads) {
+    (&lhm[0][0])[e] = 0;
+    (&lhc[0][0])[e] = 0;
+  }
+  __syncthreads();
+  const float* x = job_data(c, j);
+  const int per = (c.n + c.slices - 1) / c.slices;
+  const int i0 = sl * per, i1 = min(c.n, i0 + per);
+  const double sc = ldexp(1.0, c.scale_exp);
+  constexpr int shift = 24 - 8 * PASS;
+  const uint32_t prefix = st.prefix;
+  const int copy = tid % kCutCopies;
+  for (int i = i0 + tid; i < i1; i += kCutSliceThreads) {
+    const float v = x[i];
+    const uint32_t key = order_key(v);
+    if (PASS == 0 || (key >> (shift + 8)) == prefix) {
+      const uint32_t d = (key >> shift) & 255u;
+      const uint64_t m = (uint64_t)((double)v * sc);
+      if (m) atomicAdd(reinterpret_cast<unsigned long long*>(&lhm[copy][d]), (unsigned long long)m);
+      atomicAdd(&lhc[copy][d], 1u);
+    }
+  }
+  __syncthreads();
+  uint64_t* hm = c.hm + ((int64_t)PASS * c.jobs + j) * 256;
+  uint32_t* hc = c.hc + ((int64_t)PASS * c.jobs + j) * 256;
+  for (int d = tid; d < 256; d += kCutSliceThreads) {
+    uint64_t m = 0;
+    uint32_t k = 0;
+#pragma unroll
+    for (int r = 0; r < kCutCopies; ++r) {
+      m += lhm[r][d];
+      k += lhc[r][d];
+    }
+    if (k) {
+      atomicAdd(reinterpret_cast<unsigned long long*>(&hm[d]), (unsigned long long)m);
+      atomicAdd(&hc[d], k);
+    }
+  }
 }
 
 struct FlexHeadK {
@@ -532,6 +743,7 @@ struct FlexHeadK {
   uint64_t* smask;              // [Hq][kFWords] chosen slash offsets
   int32_t* info;                // [Hq][4]: num_vertical, num_slash, sparse, cover counts packed below
   float* js;                    // [Hq]
+  CutJobs pcut;                 // the profiles' cuts (jobs 2 h, 2 h + 1), histograms complete
 };
 
 // the K largest of v[0 .. n) (ties: lower index first) as bits of out[kFWords]
@@ -541,7 +753,7 @@ __device__ void topk_bits(const float* v, int n, int K, uint64_t* out, CutScratc
   __syncthreads();
   if (K <= 0) return;
   const CutResult cut = radix_cut<false>(v, n, 0.0, 0, K, cs);
-  emit_cut(v, n, n, cut, out, scan);
+  emit_cut(v, 1, n, cut, out, scan);
   __syncthreads();
 }
 
@@ -562,9 +774,11 @@ __global__ __launch_bounds__(kFHeadThreads) void flex_head_kernel(FlexHeadK a) {
   const int kvh = kv_head(h, a.Hq, a.Hk, a.gqa_interleave);
 
   // cover counts (score_cover_topk) -> block budgets
-  // (the profiles each add to one: masses as integers x 2^58)
-  int nv = radix_cut<true>(vt, L, (double)a.gamma, 58, 0, &cs).count + 1;
-  int ns = radix_cut<true>(st, L, (double)a.gamma, 58, 0, &cs).count + 1;
+  __shared__ CutState cst;
+  cut_replay(a.pcut, 2 * h, 4, &cst);
+  int nv = cut_result(a.pcut, cst).count + 1;
+  cut_replay(a.pcut, 2 * h + 1, 4, &cst);
+  int ns = cut_result(a.pcut, cst).count + 1;
   nv = nv / 128 + 1;
   ns = ns / 128 + 1;
   nv = min(max(nv, a.min_b), a.max_b);
@@ -714,24 +928,82 @@ __global__ __launch_bounds__(kFThreads) void flex_cover_rows_kernel(FlexCoverK a
   for (int j = tid; j < nb; j += kFThreads) out[j] = j <= i ? rowv[j] / se : 0.f;
 }
 
-// the cover of gamma * N over a sparse head's N x N probabilities (score_cover_idx)
-__global__ __launch_bounds__(kFHeadThreads) void flex_cover_select_kernel(FlexCoverK a) {
-  __shared__ CutScratch cs;
-  __shared__ int scan[kFHeadThreads];
-  const int h = blockIdx.x, tid = threadIdx.x, nb = a.nb;
-  if (a.info[h * 4 + 2] == 0) return;
+// the cover of gamma * N over a sparse head's N x N probabilities
+// (score_cover_idx) from its finished cut: one launch over (head, slice)
+// workgroups, one ballot per 64-entry word; when the cut splits the entries
+// equal to its boundary value, the head's first workgroup writes every word,
+// ranking those entries in flat index order
+// the words of slice sl of a head's cover: a contiguous range, in index order
+__device__ __forceinline__ void cover_slice_words(int nb, int slices, int sl, int* wb, int* we) {
+  const int nwords = nb * ((nb + 63) >> 6);
+  const int per = (nwords + slices - 1) / slices;
+  *wb = min(nwords, sl * per);
+  *we = min(nwords, *wb + per);
+}
+
+// when a sparse head's cut splits the entries equal to its boundary value:
+// their number in each slice's words (ties [Hq][slices])
+__global__ __launch_bounds__(kFHeadThreads) void flex_cover_ties_kernel(FlexCoverK a, CutJobs c, int* ties) {
+  __shared__ CutState st;
+  __shared__ int wsum[kFHeadThreads / 64];
+  const int h = blockIdx.x / c.slices, sl = blockIdx.x - h * c.slices;
+  if (!job_live(c, h)) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nb = a.nb;
+  cut_replay(c, h, 4, &st);
+  const CutResult cut = cut_result(c, st);
+  if (!(cut.take_eq > 0 && cut.take_eq < cut.eq_total)) return;
   const float* x = a.attn + (int64_t)h * nb * nb;
-  const int n = nb * nb;
+  const int wpr = (nb + 63) >> 6;
+  int wb, we;
+  cover_slice_words(nb, c.slices, sl, &wb, &we);
+  int cnt = 0;
+  for (int w = wb + wave; w < we; w += kFHeadThreads / 64) {
+    const int r = w / wpr, col = (w - r * wpr) * 64 + lane;
+    const bool eq = col < nb && order_key(x[(int64_t)r * nb + col]) == cut.key;
+    cnt += __popcll(__ballot(eq));
+  }
+  if (lane == 0) wsum[wave] = cnt;
+  __syncthreads();
+  if (tid == 0) {
+    int t = 0;
+    for (int v = 0; v < kFHeadThreads / 64; ++v) t += wsum[v];
+    ties[h * c.slices + sl] = t;
+  }
+}
+
+__global__ __launch_bounds__(kFHeadThreads) void flex_cover_emit_kernel(FlexCoverK a, CutJobs c, const int* ties) {
+  __shared__ CutState st;
+  __shared__ int scan[kFHeadThreads];
+  const int h = blockIdx.x / c.slices, sl = blockIdx.x - h * c.slices;
+  if (!job_live(c, h)) return;
+  const int tid = threadIdx.x, lane = tid & 63, nb = a.nb;
+  cut_replay(c, h, 4, &st);
+  const CutResult cut = cut_result(c, st);
+  const float* x = a.attn + (int64_t)h * nb * nb;
   uint64_t* cov = a.cover + (int64_t)h * nb * kFWords;
-  for (int e = tid; e < nb * kFWords; e += kFHeadThreads) cov[e] = 0;
+  if (cut.take_eq > 0 && cut.take_eq < cut.eq_total) {
+    // ties ranked in flat index order: this slice's words, after the earlier slices' ties
+    int base = 0;
+    for (int v = 0; v < sl; ++v) base += ties[h * c.slices + v];
+    int wb, we;
+    cover_slice_words(nb, c.slices, sl, &wb, &we);
+    emit_cut(x, nb, nb, cut, cov, scan, wb, we, base);
+  } else {
+    const int wpr = (nb + 63) >> 6, nwords = nb * wpr;
+    const int step = c.slices * (kFHeadThreads / 64);
+    for (int w = sl * (kFHeadThreads / 64) + (tid >> 6); w < nwords; w += step) {
+      const int r = w / wpr, col = (w - r * wpr) * 64 + lane;
+      bool in = false;
+      if (col < nb) {
+        const uint32_t k = order_key(x[(int64_t)r * nb + col]);
+        in = k > cut.key || (k == cut.key && cut.take_eq > 0);
+      }
+      const uint64_t word = __ballot(in);
+      if (lane == 0) cov[(int64_t)r * kFWords + (w - r * wpr)] = word;
+    }
+  }
   __syncthreads();
-  // every row adds to one, so the total is nb <= 2^12: masses as integers x 2^(58 - ceil(log2 nb))
-  int scale = 58;
-  for (int t = 1; t < nb; t <<= 1) --scale;
-  const CutResult cut = radix_cut<true>(x, n, (double)a.gamma * nb, scale, 0, &cs);
-  if (cut.count > 0) emit_cut(x, n, nb, cut, cov, scan);
-  __syncthreads();
-  if (tid == 0) atomicOr(reinterpret_cast<unsigned long long*>(&cov[0]), 1ull);   // entry 0 (score_cover_idx's padding value)
+  if (sl == 0 && tid == 0) atomicOr(reinterpret_cast<unsigned long long*>(&cov[0]), 1ull);   // entry 0 (the padding value)
 }
 
 struct FlexListK {
@@ -786,8 +1058,11 @@ __global__ __launch_bounds__(64) void flex_lists_kernel(FlexListK a) {
   if (lane == 0) a.blk_cnt[(int64_t)h * nb + r] = total;
 }
 
-static size_t flex_work(int Hq, int Hk, int L, int bs, size_t* o_vert, size_t* o_slash, size_t* o_avgk,
-                        size_t* o_vmask, size_t* o_smask, size_t* o_info, size_t* o_attn, size_t* o_cover) {
+struct FlexLayout {
+  size_t part, vert, slash, avgk, vmask, smask, info, attn, cover, p_hm, p_hc, c_hm, c_hc, ties, total;
+};
+
+static FlexLayout flex_work(int Hq, int Hk, int L, int bs) {
   const int nb = (L + bs - 1) / bs;
   const int nchunk = (L + kFChunk - 1) / kFChunk;
   size_t off = 0;
@@ -796,24 +1071,23 @@ static size_t flex_work(int Hq, int Hk, int L, int bs, size_t* o_vert, size_t* o
     off = (off + bytes + 255) & ~(size_t)255;
     return at;
   };
-  take((size_t)Hq * nchunk * bs * 2 * sizeof(float));                 // part at 0
-  const size_t v = take((size_t)Hq * L * sizeof(float));
-  const size_t s = take((size_t)Hq * L * sizeof(float));
-  const size_t k = take((size_t)Hk * nb * kFD * sizeof(uint16_t));
-  const size_t vm = take((size_t)Hq * kFWords * sizeof(uint64_t));
-  const size_t sm = take((size_t)Hq * kFWords * sizeof(uint64_t));
-  const size_t in = take((size_t)Hq * 4 * sizeof(int32_t) + (size_t)Hq * sizeof(float));
-  const size_t at = take((size_t)Hq * nb * nb * sizeof(float));
-  const size_t cv = take((size_t)Hq * nb * kFWords * sizeof(uint64_t));
-  if (o_vert) *o_vert = v;
-  if (o_slash) *o_slash = s;
-  if (o_avgk) *o_avgk = k;
-  if (o_vmask) *o_vmask = vm;
-  if (o_smask) *o_smask = sm;
-  if (o_info) *o_info = in;
-  if (o_attn) *o_attn = at;
-  if (o_cover) *o_cover = cv;
-  return off;
+  FlexLayout w;
+  w.part = take((size_t)Hq * nchunk * bs * 2 * sizeof(float));
+  w.vert = take((size_t)Hq * L * sizeof(float));
+  w.slash = take((size_t)Hq * L * sizeof(float));
+  w.avgk = take((size_t)Hk * nb * kFD * sizeof(uint16_t));
+  w.vmask = take((size_t)Hq * kFWords * sizeof(uint64_t));
+  w.smask = take((size_t)Hq * kFWords * sizeof(uint64_t));
+  w.info = take((size_t)Hq * 4 * sizeof(int32_t) + (size_t)Hq * sizeof(float));
+  w.attn = take((size_t)Hq * nb * nb * sizeof(float));
+  w.cover = take((size_t)Hq * nb * kFWords * sizeof(uint64_t));
+  w.p_hm = take((size_t)4 * 2 * Hq * 256 * sizeof(uint64_t));
+  w.p_hc = take((size_t)4 * 2 * Hq * 256 * sizeof(uint32_t));
+  w.c_hm = take((size_t)4 * Hq * 256 * sizeof(uint64_t));
+  w.c_hc = take((size_t)4 * Hq * 256 * sizeof(uint32_t));
+  w.ties = take((size_t)Hq * 256 * sizeof(int));     // [Hq][cover slices <= 256]
+  w.total = off;
+  return w;
 }
 
 template <typename T, int BS>
@@ -825,12 +1099,19 @@ static int launch_lastq(const FlexK& k, unsigned grid, size_t smem1, size_t smem
   return 0;
 }
 
+static void launch_cut_passes(const CutJobs& c, hipStream_t s) {
+  const unsigned grid = (unsigned)(c.jobs * c.slices);
+  cut_pass_kernel<0><<<grid, kCutSliceThreads, 0, s>>>(c);
+  cut_pass_kernel<1><<<grid, kCutSliceThreads, 0, s>>>(c);
+  cut_pass_kernel<2><<<grid, kCutSliceThreads, 0, s>>>(c);
+  cut_pass_kernel<3><<<grid, kCutSliceThreads, 0, s>>>(c);
+}
+
 template <typename T>
 static int launch_flex(const fs_flex_args& a, hipStream_t s) {
   const int nb = (a.L + a.bs - 1) / a.bs;
   const int nchunk = (a.L + kFChunk - 1) / kFChunk;
-  size_t o_v, o_s, o_k, o_vm, o_sm, o_in, o_at, o_cv;
-  flex_work(a.Hq, a.Hk, a.L, a.bs, &o_v, &o_s, &o_k, &o_vm, &o_sm, &o_in, &o_at, &o_cv);
+  const FlexLayout lay = flex_work(a.Hq, a.Hk, a.L, a.bs);
   char* w = static_cast<char*>(a.work);
   FlexK k{};
   k.q = static_cast<const uint16_t*>(a.q);
@@ -839,9 +1120,13 @@ static int launch_flex(const fs_flex_args& a, hipStream_t s) {
   k.Hq = a.Hq; k.Hk = a.Hk; k.L = a.L; k.bs = a.bs; k.nb = nb; k.gqa_interleave = a.gqa_interleave;
   k.nchunk = nchunk;
   k.sqrt_d = (float)sqrt((double)a.D);
-  k.part = reinterpret_cast<float*>(w);
-  k.vert = a.vertical ? a.vertical : reinterpret_cast<float*>(w + o_v);
-  k.slash = a.slash ? a.slash : reinterpret_cast<float*>(w + o_s);
+  k.part = reinterpret_cast<float*>(w + lay.part);
+  k.vert = a.vertical ? a.vertical : reinterpret_cast<float*>(w + lay.vert);
+  k.slash = a.slash ? a.slash : reinterpret_cast<float*>(w + lay.slash);
+  k.p_hm = reinterpret_cast<uint64_t*>(w + lay.p_hm);
+  k.p_hc = reinterpret_cast<uint32_t*>(w + lay.p_hc);
+  k.c_hm = reinterpret_cast<uint64_t*>(w + lay.c_hm);
+  k.c_hc = reinterpret_cast<uint32_t*>(w + lay.c_hc);
   const unsigned grid = (unsigned)(a.Hq * nchunk);
   const size_t smem1 = (size_t)kFTile * kFD * sizeof(uint16_t);
   const size_t smem2 = ((size_t)flex_tile_floats(a.bs) + kFTile + a.bs + (size_t)a.bs * 2 + kFThreads) * sizeof(float);
@@ -849,19 +1134,35 @@ static int launch_flex(const fs_flex_args& a, hipStream_t s) {
                : a.bs == 64 ? launch_lastq<T, 64>(k, grid, smem1, smem2, s)
                             : launch_lastq<T, 128>(k, grid, smem1, smem2, s))
     return rc;
-  uint16_t* avg_k = reinterpret_cast<uint16_t*>(w + o_k);
+  uint16_t* avg_k = reinterpret_cast<uint16_t*>(w + lay.avgk);
   flex_kpool_kernel<T><<<(unsigned)(a.Hk * nb), kFThreads, 0, s>>>(k.k, a.k_sh, a.k_sl, a.L, a.bs, nb, avg_k);
   if (int rc = fs_host::launch_status("fs_flex (scores)")) return rc;
+  // the profiles' mass cuts at gamma (each profile adds to one: masses x 2^58)
+  CutJobs pc{};
+  pc.x0 = k.vert;
+  pc.x1 = k.slash;
+  pc.stride = a.L;
+  pc.n = a.L;
+  pc.kinds = 2;
+  pc.jobs = 2 * a.Hq;
+  pc.slices = std::max(1, std::min(64, (a.L + 8191) / 8192));
+  pc.scale_exp = 58;
+  pc.g = (double)a.gamma;
+  pc.info = nullptr;
+  pc.hm = k.p_hm;
+  pc.hc = k.p_hc;
+  launch_cut_passes(pc, s);
   FlexHeadK hk{};
   hk.q = k.q; hk.q_sh = a.q_sh; hk.q_sl = a.q_sl;
   hk.avg_k = avg_k; hk.vert = k.vert; hk.slash = k.slash;
   hk.Hq = a.Hq; hk.Hk = a.Hk; hk.L = a.L; hk.bs = a.bs; hk.nb = nb; hk.gqa_interleave = a.gqa_interleave;
   hk.min_b = a.min_blocks; hk.max_b = a.max_blocks;
   hk.sqrt_d = k.sqrt_d; hk.gamma = a.gamma; hk.tau = a.tau;
-  hk.vmask = reinterpret_cast<uint64_t*>(w + o_vm);
-  hk.smask = reinterpret_cast<uint64_t*>(w + o_sm);
-  hk.info = a.head_info ? a.head_info : reinterpret_cast<int32_t*>(w + o_in);
-  hk.js = a.head_js ? a.head_js : reinterpret_cast<float*>(w + o_in + (size_t)a.Hq * 4 * sizeof(int32_t));
+  hk.vmask = reinterpret_cast<uint64_t*>(w + lay.vmask);
+  hk.smask = reinterpret_cast<uint64_t*>(w + lay.smask);
+  hk.info = a.head_info ? a.head_info : reinterpret_cast<int32_t*>(w + lay.info);
+  hk.js = a.head_js ? a.head_js : reinterpret_cast<float*>(w + lay.info + (size_t)a.Hq * 4 * sizeof(int32_t));
+  hk.pcut = pc;
   const size_t smem_head = (size_t)3 * nb * sizeof(float);
   // the limit covers the kernel's static LDS as well
   const size_t static_head = sizeof(double) * kFHeadThreads + sizeof(float) * kFD + sizeof(CutScratch) +
@@ -870,12 +1171,31 @@ static int launch_flex(const fs_flex_args& a, hipStream_t s) {
   flex_head_kernel<T><<<(unsigned)a.Hq, kFHeadThreads, smem_head, s>>>(hk);
   FlexCoverK ck{};
   ck.q = k.q; ck.q_sh = a.q_sh; ck.q_sl = a.q_sl; ck.avg_k = avg_k; ck.info = hk.info;
-  ck.attn = reinterpret_cast<float*>(w + o_at);
-  ck.cover = reinterpret_cast<uint64_t*>(w + o_cv);
+  ck.attn = reinterpret_cast<float*>(w + lay.attn);
+  ck.cover = reinterpret_cast<uint64_t*>(w + lay.cover);
   ck.Hq = a.Hq; ck.Hk = a.Hk; ck.L = a.L; ck.bs = a.bs; ck.nb = nb; ck.gqa_interleave = a.gqa_interleave;
   ck.sqrt_d = k.sqrt_d; ck.gamma = a.gamma;
   flex_cover_rows_kernel<T><<<(unsigned)(a.Hq * nb), kFThreads, 0, s>>>(ck);
-  flex_cover_select_kernel<<<(unsigned)a.Hq, kFHeadThreads, 0, s>>>(ck);
+  // the sparse heads' covers: mass cut at gamma N of N^2 entries (rows add to one,
+  // total nb <= 2^12: masses x 2^(58 - ceil(log2 nb)))
+  CutJobs cc{};
+  cc.x0 = ck.attn;
+  cc.x1 = nullptr;
+  cc.stride = (int64_t)nb * nb;
+  cc.n = nb * nb;
+  cc.kinds = 1;
+  cc.jobs = a.Hq;
+  cc.slices = std::max(1, std::min(256, (nb * nb + 16383) / 16384));
+  cc.scale_exp = 58;
+  for (int t = 1; t < nb; t <<= 1) --cc.scale_exp;
+  cc.g = (double)a.gamma * nb;
+  cc.info = hk.info;
+  cc.hm = k.c_hm;
+  cc.hc = k.c_hc;
+  launch_cut_passes(cc, s);
+  int* ties = reinterpret_cast<int*>(w + lay.ties);
+  flex_cover_ties_kernel<<<(unsigned)(a.Hq * cc.slices), kFHeadThreads, 0, s>>>(ck, cc, ties);
+  flex_cover_emit_kernel<<<(unsigned)(a.Hq * cc.slices), kFHeadThreads, 0, s>>>(ck, cc, ties);
   if (int rc = fs_host::launch_status("fs_flex (heads)")) return rc;
   FlexListK lk{};
   lk.vmask = hk.vmask; lk.smask = hk.smask; lk.cover = ck.cover; lk.info = hk.info;
@@ -890,7 +1210,7 @@ using namespace fs;
 
 extern "C" size_t fs_flex_work_bytes(int Hq, int Hk, int L, int bs) {
   if (Hq <= 0 || Hk <= 0 || L <= 0 || bs <= 0) return 0;
-  return flex_work(Hq, Hk, L, bs, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr);
+  return flex_work(Hq, Hk, L, bs).total;
 }
 
 extern "C" int fs_flex(const fs_flex_args* a, void* stream) {
