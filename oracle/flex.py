@@ -32,9 +32,12 @@ sums and cumsums) run here in torch's CPU order; torch.topk / torch.sort's
 order among equal values is unspecified, and ties are broken here by the lower
 index.
 
-Parity pins (tests/test_oracle_flex.py): diagonal sums and pooling by brute
-force; the cover count against a direct greedy count; the vertical / slash
-block sets against a direct construction; JS divergence against scipy.
+Parity pins (tests/test_oracle_flex.py): the last-block probabilities element
+by element in Python floats; diagonal sums and pooling by brute force; the
+cover count against a direct greedy count; the top-k with ties against
+Python's sort; the sparse heads' block cover against a greedy walk over
+sorted entries in float64; the vertical / slash block sets against a direct
+construction; JS divergence against scipy.
 """
 from __future__ import annotations
 

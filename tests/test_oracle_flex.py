@@ -112,3 +112,68 @@ def test_budgets_follow_the_reference_arithmetic():
     assert fo.budgets(4096, 128) == (1, 32)
     assert fo.budgets(4096, 32, min_budget=1024, max_budget=2048) == (32, 64)
     assert fo.budgets(100, 32, max_budget=10 ** 9) == (1, 4)
+
+
+def test_last_block_probs_brute_force():
+    """Flexprefill.py:958-984 element by element in Python floats: scores of the
+    scaled last queries (rounded to bf16 at each step the reference rounds),
+    the last bs columns causal, softmax per row."""
+    L, H, Hk, D, bs = 10, 2, 1, 8, 4
+    q = _rand(1, L, H, D, dtype=torch.bfloat16)
+    k = _rand(1, L, Hk, D, dtype=torch.bfloat16)
+    p, _ = fo.last_block_probs(q, k, bs)
+    for h in range(H):
+        for i in range(bs):
+            t = L - bs + i
+            lq = [float(torch.tensor(float(q[0, t, h, d]) / math.sqrt(D)).to(torch.bfloat16)) for d in range(D)]
+            s = []
+            for c in range(L):
+                if c > t:
+                    s.append(-math.inf)
+                    continue
+                dot = sum(lq[d] * float(k[0, c, 0, d]) for d in range(D))
+                s.append(float(torch.tensor(dot, dtype=torch.float64).to(torch.bfloat16)))
+            m = max(s)
+            e = [math.exp(x - m) for x in s]
+            z = sum(e)
+            for c in range(L):
+                assert abs(p[h, i, c].item() - e[c] / z) < 1e-6, (h, i, c)
+
+
+def test_topk_lower_first_brute_force():
+    """The K largest by value, equal values by the lower index: against
+    Python's sort of (-value, index) on rows full of ties."""
+    x = torch.tensor([[3.0, 1.0, 3.0, 2.0, 3.0, 1.0], [0.5, 0.5, 0.5, 0.5, 0.1, 0.9]])
+    assert fo.topk_lower_first(x, 3).tolist() == [[0, 2, 4], [5, 0, 1]]
+    y = torch.randint(0, 4, (3, 40), generator=G).float()
+    for K in (1, 7, 40):
+        got = fo.topk_lower_first(y, K)
+        for h in range(3):
+            want = sorted(range(40), key=lambda j: (-float(y[h, j]), j))[:K]
+            assert got[h].tolist() == want
+
+
+def test_sparse_cover_rule_brute_force():
+    """Flexprefill.py:1038-1060 / score_cover_idx (:879-883): the kept entries
+    of the N x N block attention are those whose descending prefix sum (ties by
+    the lower flat index) stays <= gamma * N, plus entry 0 -- checked by a
+    direct greedy walk over Python-sorted entries in float64."""
+    L, H, D, bs, gamma = 96, 1, 16, 16, 0.7
+    q = _rand(1, L, H, D, dtype=torch.bfloat16)
+    k = _rand(1, L, H, D, dtype=torch.bfloat16)
+    avg_k = fo.mean_pool_k(k, bs)
+    cov, attn, boundary = fo._sparse_cover(q, avg_k[:, 0], 0, bs, gamma)
+    nb = L // bs
+    flat = attn.reshape(-1).tolist()
+    order = sorted(range(nb * nb), key=lambda j: (-flat[j], j))
+    want = set([0])
+    run = 0.0
+    for j in order:
+        run += flat[j]
+        if run <= gamma * nb + 1e-6:
+            want.add(j)
+    got = set(torch.nonzero(cov.reshape(-1)).flatten().tolist())
+    assert got == want
+    # rows of the block attention are causal softmaxes
+    assert torch.allclose(attn.sum(-1), torch.ones(nb), atol=1e-6)
+    assert not (attn.triu(1) != 0).any()
