@@ -19,7 +19,7 @@ import torch  # noqa: F401  (must precede the library load, see module docstring
 LIB_PATH = Path(os.environ.get("FFTSPARSE_AMD_LIB") or Path(__file__).resolve().with_name("libfftsparse_amd.so"))
 
 FS_DTYPE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 
 class PoolArgs(ctypes.Structure):
@@ -110,7 +110,7 @@ class AttnArgs(ctypes.Structure):
                 ("out", c_void_p), ("o_sb", c_int64), ("o_sh", c_int64), ("o_sl", c_int64),
                 ("dtype", c_int), ("B", c_int), ("Hq", c_int), ("Hk", c_int), ("Lq", c_int), ("Lk", c_int),
                 ("D", c_int), ("bs", c_int),
-                ("is_causal", c_int), ("softmax_scale", c_float),
+                ("is_causal", c_int), ("softmax_scale", c_float), ("gqa_interleave", c_int),
                 ("blk_cnt", c_void_p), ("blk_idx", c_void_p), ("work", c_void_p)]
 
 

@@ -325,7 +325,7 @@ class AttentionCall:
     torch's current stream."""
 
     def __init__(self, query_states, key_states, value_states, blk_cnt=None, blk_idx=None, *,
-                 block_size=128, is_causal=True, softmax_scale=None, out=None):
+                 block_size=128, is_causal=True, softmax_scale=None, out=None, gqa_interleave=False):
         q = _check_layout(query_states)
         k = _check_layout(key_states)
         v = _check_layout(value_states)
@@ -346,7 +346,7 @@ class AttentionCall:
             v=v.data_ptr(), v_sb=v.stride(0), v_sh=v.stride(1), v_sl=v.stride(2),
             out=out.data_ptr(), o_sb=out.stride(0), o_sh=out.stride(2), o_sl=out.stride(1),
             dtype=_lib.FS_DTYPE[q.dtype], B=B, Hq=Hq, Hk=Hk, Lq=Lq, Lk=Lk, D=D, bs=block_size,
-            is_causal=int(bool(is_causal)), softmax_scale=scale,
+            is_causal=int(bool(is_causal)), softmax_scale=scale, gqa_interleave=int(bool(gqa_interleave)),
             blk_cnt=ptr(blk_cnt), blk_idx=ptr(blk_idx))
         self.work = torch.empty(_lib.load().fs_bsattn_work_bytes(ctypes.byref(args)), dtype=torch.uint8,
                                 device=q.device)
@@ -368,12 +368,15 @@ class AttentionCall:
 
 
 def block_sparse_attention(query_states, key_states, value_states, blk_cnt=None, blk_idx=None, *,
-                           block_size=128, is_causal=True, softmax_scale=None, out=None) -> torch.Tensor:
+                           block_size=128, is_causal=True, softmax_scale=None, out=None,
+                           gqa_interleave=False) -> torch.Tensor:
     """Block-sparse (or, with no block lists, dense causal) attention.
 
-    q [B,Hq,Lq,D], k/v [B,Hk,Lk,D] -> out [B, Lq, Hq, D] in the input dtype."""
+    q [B,Hq,Lq,D], k/v [B,Hk,Lk,D] -> out [B, Lq, Hq, D] in the input dtype.
+    Query head h reads KV head h // (Hq / Hk), or h % Hk with ``gqa_interleave``."""
     return AttentionCall(query_states, key_states, value_states, blk_cnt, blk_idx, block_size=block_size,
-                         is_causal=is_causal, softmax_scale=softmax_scale, out=out)()
+                         is_causal=is_causal, softmax_scale=softmax_scale, out=out,
+                         gqa_interleave=gqa_interleave)()
 
 
 def myattn_prefill(

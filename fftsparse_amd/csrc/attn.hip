@@ -195,6 +195,7 @@ struct AttnKArgs {
   int Hq, Hk, Lq, Lk, Nq, Nk, Lp, total, is_causal;
   int run;                      // query blocks per scheduling unit (block lists)
   float scale;
+  int gqa_interleave;           // KV head h % Hk (else h / (Hq / Hk))
 };
 
 // 16-byte LDS operand at byte offset off of base
@@ -242,7 +243,7 @@ void bsattn_kernel(AttnKArgs a) {
     b = r / a.Nq;
     qb = a.Nq - 1 - (r - b * a.Nq);
   }
-  const int hk = h / g;
+  const int hk = a.gqa_interleave ? h % a.Hk : h / g;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (scalar register)
@@ -760,6 +761,7 @@ static int launch_run(const fs_attn_args& a, int Nq, int Nk, hipStream_t s) {
   k.Nq = Nq; k.Nk = Nk; k.Lp = Lp; k.total = total; k.is_causal = a.is_causal;
   k.run = run;
   k.scale = a.softmax_scale;
+  k.gqa_interleave = a.gqa_interleave ? 1 : 0;
   bsattn_kernel<BS, TK, T><<<grid, AttnCfg<BS, TK>::NT, 0, s>>>(k);
   return fs_host::launch_status("fs_bsattn");
 }

@@ -102,7 +102,9 @@ def Flexprefill_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gamma
     of at most max(2 bs, ceil(min_budget / bs) bs) tokens take dense causal
     attention (:1084-1085), the others the FlexPrefill selection and the
     block-sparse attention.  The attention kernel runs blocks of 32, 64 and
-    128; 16-token blocks raise NotImplementedError."""
+    128; 16-token blocks raise NotImplementedError.  With ``gqa_interleave``
+    query head h reads KV head h % Hk in the selection and the sparse attention
+    (the dense branch keeps flash_attn_func's grouped heads, as the reference)."""
     assert q.is_cuda, "input tensors must be on the GPU"
     B, L, H, D = q.shape
     assert q.shape[1] == k.shape[1]
@@ -114,13 +116,10 @@ def Flexprefill_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gamma
         return block_sparse_attention(qv, kv, vv, block_size=128, is_causal=True, softmax_scale=softmax_scale)
     if block_size not in (32, 64, 128):
         raise NotImplementedError(f"block-sparse attention over {block_size}-token blocks is not built (32, 64, 128)")
-    if gqa_interleave:
-        raise NotImplementedError("the attention kernel maps query head h to key head h // (H / Hk); "
-                                  "interleaved GQA is not built")
     sel = flex_select(q, k, gamma=gamma, tau=tau, min_budget=min_budget, max_budget=max_budget,
                       gqa_interleave=gqa_interleave, block_size=block_size)
     return block_sparse_attention(qv, kv, vv, sel.blk_cnt, sel.blk_idx, block_size=block_size, is_causal=True,
-                                  softmax_scale=softmax_scale)
+                                  softmax_scale=softmax_scale, gqa_interleave=gqa_interleave)
 
 
 def density(sel: FlexSelection) -> float:

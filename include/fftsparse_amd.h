@@ -294,6 +294,7 @@ typedef struct {
   int dtype, B, Hq, Hk, Lq, Lk, D, bs;
   int is_causal;
   float softmax_scale;
+  int gqa_interleave;           /* query head h reads KV head h % Hk (else h / (Hq / Hk)) */
   const int32_t* blk_cnt;       /* [Hq][Nq] or NULL (B must be 1 when non-NULL) */
   const uint16_t* blk_idx;      /* [Hq][Nq][Nk] */
   void* work;

@@ -230,6 +230,35 @@ def test_flex_prefill_reference_call_32_token_blocks():
     assert err.max().item() <= 2e-2 and err.mean().item() <= 1e-3
 
 
+def test_flex_prefill_gqa_interleave():
+    """gqa_interleave=True: query head h reads KV head h % Hk in the selection
+    and the attention.  The reference output is the grouped fp32 attention on
+    the query heads (and their masks) reordered so that slot (h % Hk) * G + h // Hk
+    holds head h."""
+    _case(L=4096, prefill=True, gqa_interleave=True)
+    Hq, Hk, bs = 4, 2, 64
+    G = Hq // Hk
+    q, k, v = make_qkv(4096, Hq, Hk, dtype=torch.bfloat16, seed=48)
+    ql, kl, vl = _blhd(q, k, v)
+    out = Flexprefill_prefill(ql.to(DEV), kl.to(DEV), vl.to(DEV), gamma=0.9, tau=0.1, gqa_interleave=True,
+                              block_size=bs)
+    torch.cuda.synchronize()
+    sel = flex_select(ql.to(DEV), kl.to(DEV), gamma=0.9, tau=0.1, gqa_interleave=True, block_size=bs)
+    mask = sel.dense_mask().cpu()
+    slot = [(h % Hk) * G + h // Hk for h in range(Hq)]
+    qp, mp = torch.empty_like(q), torch.empty_like(mask)
+    for h in range(Hq):
+        qp[0, slot[h]] = q[0, h]
+        mp[slot[h]] = mask[h]
+    ref = v7.block_sparse_attention(qp, k, v, mp, bs)[:, slot]        # back to head order
+    err = (out[0].float().cpu() - ref).abs()
+    print(f"  max_abs={err.max().item():.3e} mean_abs={err.mean().item():.3e}")
+    assert err.max().item() <= 2e-2 and err.mean().item() <= 1e-3
+    # the grouped mapping gives a different result on these heads
+    grouped = Flexprefill_prefill(ql.to(DEV), kl.to(DEV), vl.to(DEV), gamma=0.9, tau=0.1, block_size=bs)
+    assert (grouped[0].float().cpu() - ref).abs().max().item() > 0.1
+
+
 def test_flex_prefill_short_sequence_is_dense_and_small_blocks_raise():
     """L <= max(2 bs, ceil(min_budget / bs) bs) takes dense causal attention
     (Flexprefill.py:1084-1085); 16-token attention blocks are not built."""
