@@ -383,21 +383,18 @@ __device__ __forceinline__ float block_max_f(float v, double* red) {
   return r;
 }
 
-// ---- radix cuts over order-preserving keys (one 1024-thread workgroup) -----
+// ---- the K largest by a radix cut on order-preserving keys (one 1024-thread workgroup)
 // Four passes over the data, one 8-bit digit of the key per pass (most
 // significant first): a histogram of the digit among the elements that share
-// the digits found so far, then one wave scans it from the largest digit down.
-// Masses are summed as integers x * 2^scale_exp, so the sums are exact and do
-// not depend on the order of the atomics.  The values of a profile fall in a
-// few top digits: the histogram is kept in kCutCopies copies, one per lane
-// residue, so that at most 64 / kCutCopies lanes of a wave add to one address.
+// the digits found so far, then one wave scans it from the largest digit down
+// for the digit where the count of larger elements reaches K.  The histogram is
+// kept in kCutCopies copies, one per lane residue, so that at most
+// 64 / kCutCopies lanes of a wave add to one address.
 constexpr int kCutCopies = 8;                    // histogram copies: lane l adds to copy l % 8
 
 struct CutScratch {
-  uint64_t hm[kCutCopies][256]; // mass per digit
   uint32_t hc[kCutCopies][256]; // count per digit
-  uint64_t mass;                // crossing: mass / count of the elements above its digit
-  int cnt;
+  int cnt;                      // crossing: count of the elements above its digit
   int digit;                    // crossing digit, -1: none
 };
 
@@ -408,105 +405,61 @@ struct CutResult {
   int eq_total;                 // elements equal to the boundary key
 };
 
-// BY_MASS: the descending prefix-sum cut of x >= 0 at g (score_cover_topk
-// without its + 1): the elements, largest first, while the running mass stays
-// <= g.  Otherwise: the `want` largest elements (want >= 1).
-template <bool BY_MASS>
-__device__ CutResult radix_cut(const float* x, int n, double g, int scale_exp, int want, CutScratch* cs) {
+// the `want` largest of x[0 .. n) (1 <= want; all of them when want >= n)
+__device__ CutResult radix_topk(const float* x, int n, int want, CutScratch* cs) {
   const int tid = threadIdx.x;
-  const double sc = ldexp(1.0, scale_exp);
-  const uint64_t G = BY_MASS ? (uint64_t)(g * sc) : 0;
   uint32_t prefix = 0;
-  uint64_t above = 0;
   int cnt_above = 0;
   for (int pass = 0; pass < 4; ++pass) {
     const int shift = 24 - 8 * pass;
-    for (int e = tid; e < kCutCopies * 256; e += kFHeadThreads) {
-      (&cs->hm[0][0])[e] = 0;
-      (&cs->hc[0][0])[e] = 0;
-    }
+    for (int e = tid; e < kCutCopies * 256; e += kFHeadThreads) (&cs->hc[0][0])[e] = 0;
     if (tid == 0) cs->digit = -1;
     __syncthreads();
     const int copy = tid % kCutCopies;
     for (int i = tid; i < n; i += kFHeadThreads) {
-      const float v = x[i];
-      const uint32_t key = order_key(v);
-      if (pass == 0 || (key >> (shift + 8)) == prefix) {
-        const uint32_t d = (key >> shift) & 255u;
-        if (BY_MASS) {
-          const uint64_t m = (uint64_t)((double)v * sc);
-          if (m) atomicAdd(reinterpret_cast<unsigned long long*>(&cs->hm[copy][d]), (unsigned long long)m);
-        }
-        atomicAdd(&cs->hc[copy][d], 1u);
-      }
+      const uint32_t key = order_key(x[i]);
+      if (pass == 0 || (key >> (shift + 8)) == prefix) atomicAdd(&cs->hc[copy][(key >> shift) & 255u], 1u);
     }
     __syncthreads();
     if (tid < 64) {
       // lane l: digits 255 - 4l .. 252 - 4l, largest first
-      uint64_t lm[4], sm = 0;
       uint32_t lc[4], scn = 0;
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const int d = 255 - 4 * tid - t;
-        lm[t] = 0;
         lc[t] = 0;
 #pragma unroll
-        for (int r = 0; r < kCutCopies; ++r) {
-          if (BY_MASS) lm[t] += cs->hm[r][d];
-          lc[t] += cs->hc[r][d];
-        }
-        sm += lm[t];
+        for (int r = 0; r < kCutCopies; ++r) lc[t] += cs->hc[r][d];
         scn += lc[t];
       }
-      uint64_t im = sm;
       uint32_t ic = scn;
       for (int o = 1; o < 64; o <<= 1) {
-        const uint64_t vm = __shfl_up(im, o, 64);
         const uint32_t vc = __shfl_up(ic, o, 64);
-        if (tid >= o) {
-          im += vm;
-          ic += vc;
-        }
+        if (tid >= o) ic += vc;
       }
-      uint64_t run = above + (im - sm);
       uint32_t runc = (uint32_t)cnt_above + (ic - scn);
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        const uint64_t prev = run;
         const uint32_t prevc = runc;
-        run += lm[t];
         runc += lc[t];
-        const bool cross = BY_MASS ? (prev <= G && run > G) : (prevc < (uint32_t)want && runc >= (uint32_t)want);
-        if (cross) {
+        if (prevc < (uint32_t)want && runc >= (uint32_t)want) {
           cs->digit = 255 - 4 * tid - t;
-          cs->mass = prev;
           cs->cnt = (int)prevc;
         }
       }
     }
     __syncthreads();
     const int d = cs->digit;
-    if (d < 0) {                                   // everything is in the cut (first pass only)
+    if (d < 0) {                                   // want >= n: everything (first pass only)
       __syncthreads();
       return {n, 0u, 0, 0};
     }
     prefix = (prefix << 8) | (uint32_t)d;
-    above = cs->mass;
     cnt_above = cs->cnt;
     uint32_t eq = 0;
     for (int r = 0; r < kCutCopies; ++r) eq += cs->hc[r][d];
     __syncthreads();                               // cs is rewritten by the next pass / call
-    if (pass == 3) {
-      int take;
-      if (BY_MASS) {
-        const uint64_t mv = (uint64_t)((double)key_to_f32(prefix) * sc);   // > 0: it pushed the sum past G
-        const uint64_t fit = mv ? (G - above) / mv : (uint64_t)eq;
-        take = (int)(fit < (uint64_t)eq ? fit : (uint64_t)eq);
-      } else {
-        take = want - cnt_above;
-      }
-      return {cnt_above + take, prefix, take, (int)eq};
-    }
+    if (pass == 3) return {want, prefix, want - cnt_above, (int)eq};
   }
   return {n, 0u, 0, 0};                            // not reached
 }
@@ -752,7 +705,7 @@ __device__ void topk_bits(const float* v, int n, int K, uint64_t* out, CutScratc
   for (int w = tid; w < kFWords; w += kFHeadThreads) out[w] = 0;
   __syncthreads();
   if (K <= 0) return;
-  const CutResult cut = radix_cut<false>(v, n, 0.0, 0, K, cs);
+  const CutResult cut = radix_topk(v, n, K, cs);
   emit_cut(v, 1, n, cut, out, scan);
   __syncthreads();
 }
@@ -1166,7 +1119,7 @@ static int launch_flex(const fs_flex_args& a, hipStream_t s) {
   const size_t smem_head = (size_t)3 * nb * sizeof(float);
   // the limit covers the kernel's static LDS as well
   const size_t static_head = sizeof(double) * kFHeadThreads + sizeof(float) * kFD + sizeof(CutScratch) +
-                             sizeof(uint64_t) * kFWords;
+                             sizeof(CutState) + sizeof(uint64_t) * kFWords;
   if (int rc = fs_host::allow_dynamic_lds(flex_head_kernel<T>, smem_head + static_head, "fs_flex")) return rc;
   flex_head_kernel<T><<<(unsigned)a.Hq, kFHeadThreads, smem_head, s>>>(hk);
   FlexCoverK ck{};
