@@ -12,15 +12,20 @@
 // over its causal keys n <= r, and the probabilities are summed over
 // (bs/S) x (bs/S) squares: the block sums, rounded to the input dtype.
 //
-// xattn_scores_kernel<T, PASS>: one workgroup (4 waves, 32 reshaped rows
-// each) per (head, 128 reshaped rows), longest rows first; key tiles of 64
-// reshaped keys up to the diagonal.  For each tile and each j < S the
-// workgroup stages the 128 query token rows rS + S-1-j and the 64 key token
-// rows nS + j in LDS (zero past L; 256-byte rows, 16-byte chunk c of row r at
-// c ^ (r & 15)) and accumulates S^T = K' Q'^T with v_mfma_f32_32x32x16.  Pass 1
-// keeps each row's running max and exp2 sum (the reference's first loop);
-// pass 2 recomputes the tile, forms p = exp2(x - max) / sum and reduces the
-// lanes of each block with xor shuffles (the second loop).
+// xattn_scores_kernel<T>: one workgroup (4 waves, 32 reshaped rows each) per
+// (head, 128 reshaped rows), longest rows first; key tiles of 64 reshaped keys
+// up to the diagonal.  For each tile and each j < S the workgroup stages the
+// 128 query token rows rS + S-1-j and the 64 key token rows nS + j in LDS (zero
+// past L; 256-byte rows, 16-byte chunk c of row r at c ^ (r & 15)) and
+// accumulates S^T = K' Q'^T with v_mfma_f32_32x32x16.  It keeps each row's
+// running max and exp2 sum (the reference's first loop) and stores the scores,
+// rounded to the input dtype, as the reference's GEMM kernel stores its
+// output: the causal part only, row tile by row tile (tile rt holds its 128
+// rows x 128 (rt + 1) keys, so it starts 16384 rt (rt + 1) / 2 values in).
+// xattn_sums_kernel<T>: one workgroup per (head, 128 reshaped rows) streams
+// the stored scores (threads along the keys, rows in order), forms
+// p = exp2(x - max) / sum and adds it over each block's rows and, by xor
+// shuffles, its keys (the reference's second loop).
 //
 // xattn_select_kernel: one workgroup per (head, block row I): the causal
 // block sums of the row, the forced first and diagonal blocks, the others in
@@ -67,9 +72,19 @@ struct XScoreK {
   float* m;                     // [Hq][Lr] row max (exp2 domain)
   float* l;                     // [Hq][Lr] row sum
   float* sums;                  // [Hq][Nb][Nb] block sums (values of T), causal part
+  uint16_t* scores;             // [Hq][head_stride] the rounded scores, causal row tiles
+  int64_t head_stride;
 };
 
-template <typename T, int PASS>
+// first stored score of row tile rt (every earlier tile is whole)
+__host__ __device__ inline int64_t xtile_offset(int rt) { return (int64_t)kXRows * 128 * rt * (rt + 1) / 2; }
+// keys stored per row of tile rt: its key tiles up to the diagonal
+__host__ __device__ inline int xtile_keys(int rt, int Lr) {
+  const int last_row = (rt + 1) * kXRows < Lr ? (rt + 1) * kXRows - 1 : Lr - 1;
+  return (last_row / kXKeys + 1) * kXKeys;
+}
+
+template <typename T>
 __global__ __launch_bounds__(kXThreads) void xattn_scores_kernel(XScoreK a) {
   __shared__ __attribute__((aligned(16))) uint16_t lq[kXRows * kXD];   // Q'_j rows, 32 KiB
   __shared__ __attribute__((aligned(16))) uint16_t lk[kXKeys * kXD];   // K'_j rows, 16 KiB
@@ -87,13 +102,7 @@ __global__ __launch_bounds__(kXThreads) void xattn_scores_kernel(XScoreK a) {
   const int nct = last_row / kXKeys + 1;           // key tiles up to the diagonal
   const bool row_ok = row < a.Lr;
 
-  float m_run = -INFINITY, l_run = 0.f, inv_l = 0.f;
-  if (PASS == 2 && row_ok) {
-    m_run = a.m[(int64_t)h * a.Lr + row];
-    inv_l = 1.0f / a.l[(int64_t)h * a.Lr + row];
-  }
-  const int rbs = a.rbs;                           // reshaped rows / keys per block: 8, 16 or 32
-  const int cbh = 32 / rbs;                        // blocks per 32-key half
+  float m_run = -INFINITY, l_run = 0.f;
 
   for (int ct = 0; ct < nct; ++ct) {
     const int n0 = ct * kXKeys;
@@ -152,7 +161,23 @@ __global__ __launch_bounds__(kXThreads) void xattn_scores_kernel(XScoreK a) {
         valid[kk][r] = row_ok && n <= row;
         x[kk][r] = Conv<T>::round(acc[kk][r]) * a.scale;
       }
-    if (PASS == 1) {
+    if (row_ok) {
+      // the rounded scores of this lane's row: four consecutive keys per 8-byte store
+      const int NK = xtile_keys(rt, a.Lr);
+      uint16_t* dst = a.scores + (int64_t)h * a.head_stride + xtile_offset(rt) + (int64_t)(row - r0) * NK;
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          uint32_t w[2];
+#pragma unroll
+          for (int e = 0; e < 2; ++e)
+            w[e] = (uint32_t)__builtin_bit_cast(uint16_t, Conv<T>::store(acc[kk][g * 4 + 2 * e])) |
+                   ((uint32_t)__builtin_bit_cast(uint16_t, Conv<T>::store(acc[kk][g * 4 + 2 * e + 1])) << 16);
+          *reinterpret_cast<uint2*>(dst + n0 + kk * 32 + g * 8 + hi * 4) = make_uint2(w[0], w[1]);
+        }
+    }
+    {
       float mx = -INFINITY;
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk)
@@ -171,55 +196,58 @@ __global__ __launch_bounds__(kXThreads) void xattn_scores_kernel(XScoreK a) {
         l_run = l_run * __builtin_amdgcn_exp2f(m_run - m_new) + s;
         m_run = m_new;
       }
-    } else {
-      // block partials of this lane: block cb of half kk holds r with (r/4) / (rbs/8) == cb
-      const bool real_row = row_ok && row < a.real;
-      float part[2][4];
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-        for (int cb = 0; cb < 4; ++cb) part[kk][cb] = 0.f;
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float p = (real_row && valid[kk][r]) ? __builtin_amdgcn_exp2f(x[kk][r] - m_run) * inv_l : 0.f;
-          const int cb = (r >> 2) / (rbs >> 3);
-#pragma unroll
-          for (int c = 0; c < 4; ++c)
-            if (c == cb) part[kk][c] += p;
-        }
-      // sum over the rbs rows of the lane's block row and the two lane halves
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-        for (int cb = 0; cb < 4; ++cb) {
-          if (cb >= cbh) continue;
-          float v = part[kk][cb];
-          for (int o = 1; o < rbs; o <<= 1) v += __shfl_xor(v, o, 64);
-          v += __shfl_xor(v, 32, 64);
-          part[kk][cb] = v;
-        }
-      if (hi == 0 && (l32 % rbs) == 0) {
-        const int I = (r0 + wave * 32 + l32) / rbs;
-        if (I < a.Nb) {
-#pragma unroll
-          for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-            for (int cb = 0; cb < 4; ++cb) {
-              if (cb >= cbh) continue;
-              const int J = (n0 + kk * 32) / rbs + cb;
-              if (J <= I) a.sums[((int64_t)h * a.Nb + I) * a.Nb + J] = Conv<T>::round(part[kk][cb]);
-            }
-        }
-      }
     }
   }
-  if (PASS == 1) {
-    const float lt = l_run + __shfl_xor(l_run, 32, 64);
-    if (row_ok && hi == 0) {
-      a.m[(int64_t)h * a.Lr + row] = m_run;
-      a.l[(int64_t)h * a.Lr + row] = lt;
+  const float lt = l_run + __shfl_xor(l_run, 32, 64);
+  if (row_ok && hi == 0) {
+    a.m[(int64_t)h * a.Lr + row] = m_run;
+    a.l[(int64_t)h * a.Lr + row] = lt;
+  }
+}
+
+// pass 2 over the stored scores
+template <typename T>
+__global__ __launch_bounds__(kXThreads) void xattn_sums_kernel(XScoreK a) {
+  __shared__ float rm[kXRows], rinv[kXRows];
+  const int nrt = (a.Lr + kXRows - 1) / kXRows;
+  const int rt = nrt - 1 - (int)(blockIdx.x / a.Hq);
+  const int h = (int)(blockIdx.x % a.Hq);
+  const int r0 = rt * kXRows;
+  const int nr = min(a.Lr, r0 + kXRows) - r0;       // a multiple of rbs
+  const int NK = xtile_keys(rt, a.Lr);
+  const int tid = threadIdx.x, rbs = a.rbs;
+  if (tid < kXRows) {
+    const int row = r0 + tid;
+    const bool real = row < a.real;                  // padding rows add nothing
+    rm[tid] = row < a.Lr ? a.m[(int64_t)h * a.Lr + row] : 0.f;
+    rinv[tid] = real ? 1.0f / a.l[(int64_t)h * a.Lr + row] : 0.f;
+  }
+  __syncthreads();
+  const uint16_t* src = a.scores + (int64_t)h * a.head_stride + xtile_offset(rt);
+  // four consecutive keys per thread (one 8-byte load a row): a key block of
+  // rbs >= 8 keys spans rbs / 4 neighbouring lanes
+  const int gl = rbs / 4;
+  for (int c0 = 0; c0 < NK; c0 += 4 * kXThreads) {
+    const int n = c0 + 4 * tid;
+    const bool key_ok = n < NK;                      // NK and n are multiples of 4
+    float acc = 0.f;
+    for (int i = 0; i < nr; ++i) {
+      const int row = r0 + i;
+      if (key_ok && n <= row && rinv[i] > 0.f) {
+        const uint2 w = *reinterpret_cast<const uint2*>(src + (int64_t)i * NK + n);
+        const uint32_t e[4] = {w.x & 0xffffu, w.x >> 16, w.y & 0xffffu, w.y >> 16};
+        const float mi = rm[i], li = rinv[i];
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          if (n + t <= row) acc += __builtin_amdgcn_exp2f(to_f32(T{(uint16_t)e[t]}) * a.scale - mi) * li;
+      }
+      if ((i + 1) % rbs == 0) {                      // the end of a block row: add over the block's keys
+        float v = acc;
+        for (int o = 1; o < gl; o <<= 1) v += __shfl_xor(v, o, 64);
+        const int I = row / rbs, J = n / rbs;
+        if (key_ok && (tid % gl) == 0 && J <= I && I < a.Nb) a.sums[((int64_t)h * a.Nb + I) * a.Nb + J] = Conv<T>::round(v);
+        acc = 0.f;
+      }
     }
   }
 }
@@ -330,10 +358,19 @@ __global__ __launch_bounds__(kXSelThreads) void xattn_select_kernel(XSelK a) {
   }
 }
 
+// stored scores per head: every row tile's rows x keys up to its diagonal
+static int64_t xattn_head_stride(int Lr) {
+  const int nrt = (Lr + kXRows - 1) / kXRows;
+  return xtile_offset(nrt - 1) + (int64_t)kXRows * xtile_keys(nrt - 1, Lr);
+}
+
+// workspace: row max and sum [Hq][Lr] each, then the stored scores
+static size_t xattn_stats_bytes(int Hq, int Lr) { return ((size_t)Hq * Lr * 2 * sizeof(float) + 255) & ~(size_t)255; }
+
 static size_t xattn_work(int Hq, int L, int stride, int bs) {
   const int64_t Lp = ((int64_t)L + bs - 1) / bs * bs;
-  const int64_t Lr = Lp / stride;
-  return ((size_t)Hq * Lr * 2 * sizeof(float) + 255) & ~(size_t)255;
+  const int Lr = (int)(Lp / stride);
+  return xattn_stats_bytes(Hq, Lr) + (size_t)Hq * xattn_head_stride(Lr) * sizeof(uint16_t);
 }
 
 }  // namespace fs
@@ -378,14 +415,16 @@ extern "C" int fs_xattn(const fs_xattn_args* a, void* stream) {
   k.m = static_cast<float*>(a->work);
   k.l = k.m + (size_t)a->Hq * k.Lr;
   k.sums = a->sums;
+  k.scores = reinterpret_cast<uint16_t*>(static_cast<char*>(a->work) + xattn_stats_bytes(a->Hq, k.Lr));
+  k.head_stride = xattn_head_stride(k.Lr);
   const unsigned grid = (unsigned)(a->Hq * ((k.Lr + kXRows - 1) / kXRows));
   hipStream_t s = (hipStream_t)stream;
   if (a->dtype == FS_DTYPE_BF16) {
-    xattn_scores_kernel<bf16_t, 1><<<grid, kXThreads, 0, s>>>(k);
-    xattn_scores_kernel<bf16_t, 2><<<grid, kXThreads, 0, s>>>(k);
+    xattn_scores_kernel<bf16_t><<<grid, kXThreads, 0, s>>>(k);
+    xattn_sums_kernel<bf16_t><<<grid, kXThreads, 0, s>>>(k);
   } else {
-    xattn_scores_kernel<f16_t, 1><<<grid, kXThreads, 0, s>>>(k);
-    xattn_scores_kernel<f16_t, 2><<<grid, kXThreads, 0, s>>>(k);
+    xattn_scores_kernel<f16_t><<<grid, kXThreads, 0, s>>>(k);
+    xattn_sums_kernel<f16_t><<<grid, kXThreads, 0, s>>>(k);
   }
   if (int rc = fs_host::launch_status("fs_xattn (scores)")) return rc;
   XSelK sk{};

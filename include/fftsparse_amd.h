@@ -222,7 +222,9 @@ FS_API int fs_select(const fs_select_args* a, void* stream);
  * ascending block lists blk_cnt [Hq][N], blk_idx [Hq][N][N] (N = ceil(L/bs),
  * causal; keep_sink: row 0 lists every block) and the causal part of sums
  * [Hq][N][N].  threshold: device array of Hq float64 values.  work:
- * fs_xattn_work_bytes(Hq, L, stride, bs) bytes of device scratch.
+ * fs_xattn_work_bytes(Hq, L, stride, bs) bytes of device scratch: the row
+ * statistics and the rounded scores A of the causal part (about
+ * Hq (L/S)^2 bytes: 8.7 GB at L = 131072, S = 8, 32 heads).
  * bf16/f16, D = 128, bs = 128, stride 4, 8 or 16, N <= 4096. */
 typedef struct {
   const void* q; int64_t q_sh, q_sl;
