@@ -41,6 +41,7 @@ namespace fs {
 constexpr int kXD = 128;          // head dim
 constexpr int kXRows = 128;       // reshaped rows per workgroup: 4 waves x 32
 constexpr int kXKeys = 64;        // reshaped keys per tile
+constexpr int kXKK = kXKeys / 32; // 32-key MFMA sub-tiles per tile
 constexpr int kXThreads = 256;
 constexpr int kXSelThreads = 256;
 constexpr int kXMaxBlocks = 4096;
@@ -87,7 +88,7 @@ __host__ __device__ inline int xtile_keys(int rt, int Lr) {
 template <typename T>
 __global__ __launch_bounds__(kXThreads) void xattn_scores_kernel(XScoreK a) {
   __shared__ __attribute__((aligned(16))) uint16_t lq[kXRows * kXD];   // Q'_j rows, 32 KiB
-  __shared__ __attribute__((aligned(16))) uint16_t lk[kXKeys * kXD];   // K'_j rows, 16 KiB
+  __shared__ __attribute__((aligned(16))) uint16_t lk[kXKeys * kXD];   // K'_j rows
   const int nrt = (a.Lr + kXRows - 1) / kXRows;
   const int rt = nrt - 1 - (int)(blockIdx.x / a.Hq);                 // longest rows first
   const int h = (int)(blockIdx.x % a.Hq);
@@ -106,9 +107,9 @@ __global__ __launch_bounds__(kXThreads) void xattn_scores_kernel(XScoreK a) {
 
   for (int ct = 0; ct < nct; ++ct) {
     const int n0 = ct * kXKeys;
-    f32x16_t acc[2];
+    f32x16_t acc[kXKK];
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
+    for (int kk = 0; kk < kXKK; ++kk)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[kk][r] = 0.f;
     for (int j = 0; j < S; ++j) {
@@ -142,7 +143,7 @@ __global__ __launch_bounds__(kXThreads) void xattn_scores_kernel(XScoreK a) {
       for (int st = 0; st < kXD / 16; ++st) {
         const uint4 bq = *reinterpret_cast<const uint4*>(lq + qr * kXD + (((2 * st + hi) ^ (qr & 15)) << 3));
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
+        for (int kk = 0; kk < kXKK; ++kk) {
           const int kr = kk * 32 + l32;
           const uint4 ak = *reinterpret_cast<const uint4*>(lk + kr * kXD + (((2 * st + hi) ^ (kr & 15)) << 3));
           acc[kk] = XMma<T>::mma(ak, bq, acc[kk]);
@@ -151,10 +152,10 @@ __global__ __launch_bounds__(kXThreads) void xattn_scores_kernel(XScoreK a) {
     }
 
     // ---- epilogue: lane holds keys n0 + 32 kk + (r/4) 8 + hi 4 + r%4 of its row
-    float x[2][16];
-    bool valid[2][16];
+    float x[kXKK][16];
+    bool valid[kXKK][16];
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
+    for (int kk = 0; kk < kXKK; ++kk)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int n = n0 + kk * 32 + (r >> 2) * 8 + hi * 4 + (r & 3);
@@ -166,7 +167,7 @@ __global__ __launch_bounds__(kXThreads) void xattn_scores_kernel(XScoreK a) {
       const int NK = xtile_keys(rt, a.Lr);
       uint16_t* dst = a.scores + (int64_t)h * a.head_stride + xtile_offset(rt) + (int64_t)(row - r0) * NK;
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
+      for (int kk = 0; kk < kXKK; ++kk)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           uint32_t w[2];
@@ -180,7 +181,7 @@ __global__ __launch_bounds__(kXThreads) void xattn_scores_kernel(XScoreK a) {
     {
       float mx = -INFINITY;
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
+      for (int kk = 0; kk < kXKK; ++kk)
 #pragma unroll
         for (int r = 0; r < 16; ++r)
           if (valid[kk][r]) mx = fmaxf(mx, x[kk][r]);
@@ -189,7 +190,7 @@ __global__ __launch_bounds__(kXThreads) void xattn_scores_kernel(XScoreK a) {
       if (m_new > -INFINITY) {
         float s = 0.f;
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk)
+        for (int kk = 0; kk < kXKK; ++kk)
 #pragma unroll
           for (int r = 0; r < 16; ++r)
             if (valid[kk][r]) s += __builtin_amdgcn_exp2f(x[kk][r] - m_new);
