@@ -314,3 +314,43 @@ def test_flex_full_length_properties():
             assert int(a.blk_cnt[h].max()) <= int(info[h, 0]) + int(info[h, 1])
     print(f"  density {density(a):.4f} sparse heads {int(info[:, 2].sum())}")
     assert not math.isnan(a.js.float().cpu().sum().item())
+
+
+def test_flex_full_length_32_token_blocks():
+    """Config-2 shape at FlexPrefill's default 32-token blocks: 4096 blocks, the
+    maximum block count, and sparse heads whose covers are cut over 16.7M
+    entries each (the many-workgroup cut, ties ranked across slices).  Lists
+    ascending and causal with block 0 and the diagonal, deterministic across
+    calls; every non-sparse row holds at most its budgets; some head sparse."""
+    _case(L=131072, full=True, bs=32)
+    from fftsparse_amd.synth import make_config
+    q, k, _ = make_config("c2")
+    qg, kg = q.to(DEV).transpose(1, 2), k.to(DEV).transpose(1, 2)
+    del q, k
+    a = flex_select(qg, kg, gamma=0.95, tau=0.1, block_size=32)
+    b = flex_select(qg, kg, gamma=0.95, tau=0.1, block_size=32)
+    torch.cuda.synchronize()
+    assert torch.equal(a.blk_cnt, b.blk_cnt) and torch.equal(a.head_info, b.head_info)
+    H, N = a.blk_cnt.shape
+    assert N == 4096
+    cnt = a.blk_cnt.to(torch.int64)
+    idx = a.blk_idx.view(torch.int16).to(torch.int64) & 0xFFFF
+    for h0 in range(0, H, 8):                                  # in head groups: [8, 4096, 4096] at a time
+        sl = slice(h0, h0 + 8)
+        ia, ib = idx[sl], b.blk_idx[sl].view(torch.int16).to(torch.int64) & 0xFFFF
+        pos = torch.arange(N, device=DEV)
+        valid = pos[None, None, :] < cnt[sl, :, None]
+        assert bool(((ia == ib) | ~valid).all())               # deterministic lists
+        assert bool(((ia <= pos[None, :, None]) | ~valid).all())
+        assert bool(((ia[:, :, 1:] > ia[:, :, :-1]) | ~valid[:, :, 1:]).all())
+        assert bool((ia[:, :, 0] == 0).all())
+        last = ia.gather(2, (cnt[sl] - 1).clamp(min=0)[:, :, None])[:, :, 0]
+        assert bool((last == pos[None, :]).all())
+        del ia, ib, valid
+    info = a.head_info.cpu()
+    for h in range(H):
+        if not info[h, 2]:
+            assert int(a.blk_cnt[h].max()) <= int(info[h, 0]) + int(info[h, 1])
+    n_sparse = int(info[:, 2].sum())
+    print(f"  density {density(a):.4f} sparse heads {n_sparse}")
+    assert n_sparse > 0
