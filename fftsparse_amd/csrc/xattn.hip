@@ -13,11 +13,12 @@
 // (bs/S) x (bs/S) squares: the block sums, rounded to the input dtype.
 //
 // xattn_scores_kernel<T>: one workgroup (4 waves, 32 reshaped rows each) per
-// (head, 128 reshaped rows), longest rows first; key tiles of 64 reshaped keys
-// up to the diagonal.  For each tile and each j < S the workgroup stages the
-// 128 query token rows rS + S-1-j and the 64 key token rows nS + j in LDS (zero
-// past L; 256-byte rows, 16-byte chunk c of row r at c ^ (r & 15)) and
-// accumulates S^T = K' Q'^T with v_mfma_f32_32x32x16.  It keeps each row's
+// (head, 128 reshaped rows), longest rows first; key tiles of 128 reshaped keys
+// up to the diagonal.  For each tile and each j < S the workgroup copies the
+// 128 query token rows rS + S-1-j and the 128 key token rows nS + j into LDS
+// with global -> LDS copies (no register staging; rows past L zeroed after;
+// 256-byte rows, 16-byte chunk c of row r at c ^ (r & 15)) and accumulates
+// S^T = K' Q'^T with v_mfma_f32_32x32x16.  It keeps each row's
 // running max and exp2 sum (the reference's first loop) and stores the scores,
 // rounded to the input dtype, as the reference's GEMM kernel stores its
 // output: the causal part only, row tile by row tile (tile rt holds its 128
@@ -40,8 +41,15 @@ namespace fs {
 
 constexpr int kXD = 128;          // head dim
 constexpr int kXRows = 128;       // reshaped rows per workgroup: 4 waves x 32
-constexpr int kXKeys = 64;        // reshaped keys per tile
+constexpr int kXKeys = 128;       // reshaped keys per tile
 constexpr int kXKK = kXKeys / 32; // 32-key MFMA sub-tiles per tile
+
+// One 1 KiB global -> LDS copy per wave: lane l's 16 bytes, from the
+// wave-uniform base plus the lane's byte offset, land at lds_base + 16 l.
+__device__ __forceinline__ void xdma16(uint32_t lds_base, const void* sbase, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :: "s"(lds_base), "v"(voff), "s"(sbase) : "memory");
+}
 constexpr int kXThreads = 256;
 constexpr int kXSelThreads = 256;
 constexpr int kXMaxBlocks = 4096;
@@ -114,30 +122,41 @@ __global__ __launch_bounds__(kXThreads) void xattn_scores_kernel(XScoreK a) {
       for (int r = 0; r < 16; ++r) acc[kk][r] = 0.f;
     for (int j = 0; j < S; ++j) {
       __syncthreads();                             // previous stage consumed
-      uint4 kv[kXKeys * 16 / kXThreads], qv[kXRows * 16 / kXThreads];
+      // 1 KiB regions of 4 LDS rows: lane l fills slot l % 16 of row 4R + l / 16
+      // with the token row's chunk (l % 16) ^ (row & 15); rows past L read row
+      // L-1 here and are zeroed below
+      const uint32_t lq0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lq);
+      const uint32_t lk0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lk);
+      const int wv = __builtin_amdgcn_readfirstlane(wave);   // wave-uniform: the copies' LDS bases
+      constexpr int QR = kXRows / 4 / 4, KR = kXKeys / 4 / 4;   // regions per wave
 #pragma unroll
-      for (int u = 0; u < kXKeys * 16 / kXThreads; ++u) {
-        const int e = tid + u * kXThreads, c = e >> 4, ch = e & 15;
-        const int t = (n0 + c) * S + j;
-        kv[u] = t < a.L ? *reinterpret_cast<const uint4*>(kh + (int64_t)t * a.k_sl + ch * 8) : make_uint4(0, 0, 0, 0);
+      for (int i = 0; i < QR; ++i) {
+        const int R = wv * QR + i, rr = 4 * R + (lane >> 4), c = (lane & 15) ^ (rr & 15);
+        const int t = min((r0 + rr) * S + S - 1 - j, a.L - 1);
+        xdma16(lq0 + R * 1024, qh, (uint32_t)(t * a.q_sl + c * 8) * 2u);
       }
 #pragma unroll
-      for (int u = 0; u < kXRows * 16 / kXThreads; ++u) {
-        const int e = tid + u * kXThreads, rr = e >> 4, ch = e & 15;
-        const int t = (r0 + rr) * S + S - 1 - j;
-        qv[u] = t < a.L ? *reinterpret_cast<const uint4*>(qh + (int64_t)t * a.q_sl + ch * 8) : make_uint4(0, 0, 0, 0);
+      for (int i = 0; i < KR; ++i) {
+        const int R = wv * KR + i, cr = 4 * R + (lane >> 4), c = (lane & 15) ^ (cr & 15);
+        const int t = min((n0 + cr) * S + j, a.L - 1);
+        xdma16(lk0 + R * 1024, kh, (uint32_t)(t * a.k_sl + c * 8) * 2u);
       }
-#pragma unroll
-      for (int u = 0; u < kXKeys * 16 / kXThreads; ++u) {
-        const int e = tid + u * kXThreads, c = e >> 4, ch = e & 15;
-        *reinterpret_cast<uint4*>(lk + c * kXD + ((ch ^ (c & 15)) << 3)) = kv[u];
-      }
-#pragma unroll
-      for (int u = 0; u < kXRows * 16 / kXThreads; ++u) {
-        const int e = tid + u * kXThreads, rr = e >> 4, ch = e & 15;
-        *reinterpret_cast<uint4*>(lq + rr * kXD + ((ch ^ (rr & 15)) << 3)) = qv[u];
-      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
+      if ((r0 + kXRows - 1) * S + S - 1 - j >= a.L || (n0 + kXKeys - 1) * S + j >= a.L) {
+        // this stage reaches past L: those rows are zero
+        for (int e = tid; e < (kXRows + kXKeys) * 16; e += kXThreads) {
+          const int r = e >> 4, ch = e & 15;
+          if (r < kXRows) {
+            if ((r0 + r) * S + S - 1 - j >= a.L) *reinterpret_cast<uint4*>(lq + r * kXD + ch * 8) = make_uint4(0, 0, 0, 0);
+          } else {
+            const int cr = r - kXRows;
+            if ((n0 + cr) * S + j >= a.L) *reinterpret_cast<uint4*>(lk + cr * kXD + ch * 8) = make_uint4(0, 0, 0, 0);
+          }
+        }
+        __syncthreads();
+      }
+
       const int qr = wave * 32 + l32;
 #pragma unroll
       for (int st = 0; st < kXD / 16; ++st) {
@@ -403,6 +422,9 @@ extern "C" int fs_xattn(const fs_xattn_args* a, void* stream) {
                "fs_xattn: q/k must be 16-byte aligned with strides of whole 16-byte chunks");
   const int N = (a->L + a->bs - 1) / a->bs;
   FS_CHECK_SUPPORTED(N <= kXMaxBlocks, "fs_xattn: %d blocks > %d", N, kXMaxBlocks);
+  // the tile copies address a token row by a 32-bit byte offset from the head's base
+  FS_CHECK_SUPPORTED((int64_t)a->L * (a->q_sl > a->k_sl ? a->q_sl : a->k_sl) * 2 < ((int64_t)1 << 32),
+                     "fs_xattn: sequence x row stride too large");
   XScoreK k{};
   k.q = static_cast<const uint16_t*>(a->q);
   k.k = static_cast<const uint16_t*>(a->k);
