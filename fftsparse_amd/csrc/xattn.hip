@@ -171,16 +171,10 @@ __global__ __launch_bounds__(kXThreads) void xattn_scores_kernel(XScoreK a) {
     }
 
     // ---- epilogue: lane holds keys n0 + 32 kk + (r/4) 8 + hi 4 + r%4 of its row
-    float x[kXKK][16];
-    bool valid[kXKK][16];
-#pragma unroll
-    for (int kk = 0; kk < kXKK; ++kk)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int n = n0 + kk * 32 + (r >> 2) * 8 + hi * 4 + (r & 3);
-        valid[kk][r] = row_ok && n <= row;
-        x[kk][r] = Conv<T>::round(acc[kk][r]) * a.scale;
-      }
+    // a key of this lane's row is causal; its score in the exp2 domain, from the
+    // accumulator (recomputed where used, so no tile-sized arrays stay live)
+    auto valid = [&](int kk, int r) { return row_ok && n0 + kk * 32 + (r >> 2) * 8 + hi * 4 + (r & 3) <= row; };
+    auto xval = [&](int kk, int r) { return Conv<T>::round(acc[kk][r]) * a.scale; };
     if (row_ok) {
       // the rounded scores of this lane's row: four consecutive keys per 8-byte store
       const int NK = xtile_keys(rt, a.Lr);
@@ -203,7 +197,7 @@ __global__ __launch_bounds__(kXThreads) void xattn_scores_kernel(XScoreK a) {
       for (int kk = 0; kk < kXKK; ++kk)
 #pragma unroll
         for (int r = 0; r < 16; ++r)
-          if (valid[kk][r]) mx = fmaxf(mx, x[kk][r]);
+          if (valid(kk, r)) mx = fmaxf(mx, xval(kk, r));
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));      // the row's other keys sit in lane ^ 32
       const float m_new = fmaxf(m_run, mx);
       if (m_new > -INFINITY) {
@@ -212,7 +206,7 @@ __global__ __launch_bounds__(kXThreads) void xattn_scores_kernel(XScoreK a) {
         for (int kk = 0; kk < kXKK; ++kk)
 #pragma unroll
           for (int r = 0; r < 16; ++r)
-            if (valid[kk][r]) s += __builtin_amdgcn_exp2f(x[kk][r] - m_new);
+            if (valid(kk, r)) s += __builtin_amdgcn_exp2f(xval(kk, r) - m_new);
         l_run = l_run * __builtin_amdgcn_exp2f(m_run - m_new) + s;
         m_run = m_new;
       }
