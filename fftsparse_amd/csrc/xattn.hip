@@ -238,22 +238,24 @@ __global__ __launch_bounds__(kXThreads) void xattn_sums_kernel(XScoreK a) {
   }
   __syncthreads();
   const uint16_t* src = a.scores + (int64_t)h * a.head_stride + xtile_offset(rt);
-  // four consecutive keys per thread (one 8-byte load a row): a key block of
-  // rbs >= 8 keys spans rbs / 4 neighbouring lanes
-  const int gl = rbs / 4;
-  for (int c0 = 0; c0 < NK; c0 += 4 * kXThreads) {
-    const int n = c0 + 4 * tid;
-    const bool key_ok = n < NK;                      // NK and n are multiples of 4
+  // eight consecutive keys per thread (one 16-byte load a row): a key block of
+  // rbs >= 8 keys spans rbs / 8 neighbouring lanes
+  const int gl = rbs / 8;
+  for (int c0 = 0; c0 < NK; c0 += 8 * kXThreads) {
+    const int n = c0 + 8 * tid;
+    const bool key_ok = n < NK;                      // NK and n are multiples of 8
     float acc = 0.f;
     for (int i = 0; i < nr; ++i) {
       const int row = r0 + i;
       if (key_ok && n <= row && rinv[i] > 0.f) {
-        const uint2 w = *reinterpret_cast<const uint2*>(src + (int64_t)i * NK + n);
-        const uint32_t e[4] = {w.x & 0xffffu, w.x >> 16, w.y & 0xffffu, w.y >> 16};
+        const uint4 w = *reinterpret_cast<const uint4*>(src + (int64_t)i * NK + n);
+        const uint32_t pr[4] = {w.x, w.y, w.z, w.w};
         const float mi = rm[i], li = rinv[i];
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
-          if (n + t <= row) acc += __builtin_amdgcn_exp2f(to_f32(T{(uint16_t)e[t]}) * a.scale - mi) * li;
+        for (int t = 0; t < 8; ++t) {
+          const uint16_t e = (uint16_t)((t & 1) ? (pr[t >> 1] >> 16) : (pr[t >> 1] & 0xffffu));
+          if (n + t <= row) acc += __builtin_amdgcn_exp2f(to_f32(T{e}) * a.scale - mi) * li;
+        }
       }
       if ((i + 1) % rbs == 0) {                      // the end of a block row: add over the block's keys
         float v = acc;
