@@ -208,8 +208,9 @@ def cpu_baseline_flex(q, k, v, args, bs, nnz_total, sel, sample_heads=None):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; multi-GPU sharding is a design "
-                                   "note (DESIGN.md), not a code path", "n_gpus": args.gpus}))
+        print(json.dumps({"error": "this build runs on one GPU only: the path would shard by KV-head group "
+                                   "(one KV head and its query heads per GPU, no exchange), which is not a "
+                                   "code path here", "n_gpus": args.gpus}))
         sys.exit(2)
     import torch
     if args.copy_calib:

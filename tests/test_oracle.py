@@ -20,9 +20,10 @@ def _rand(*shape, dtype=torch.float32):
 
 
 # --------------------------------------------------------------------------- parameters
-# Derived integers for the BASELINE configs (config table of the hot-path survey,
-# computed there from the reference formulas).
-SURVEY_TABLE = [
+# Derived integers for the five benchmark shapes (production kwargs of
+# eval/efficiency/1_run_eval_multilayer.sh:46-62), worked out by hand from the
+# reference formulas (my_attn_v7.py:533-585) independently of oracle/v7.py.
+CONFIG_TABLE = [
     # L, bs, N, keep_sink, lw, rs, n_samples, first tau, last tau, cs, ce, n_cols, k_max, last_k
     (8192, 128, 64, 1, 1, 2, 5, 2, 33, 6, 52, 9, 19, 64),
     (32768, 128, 256, 2, 2, 3, 19, 3, 129, 25, 205, 25, 76, 128),
@@ -32,7 +33,7 @@ SURVEY_TABLE = [
 ]
 
 
-@pytest.mark.parametrize("row", SURVEY_TABLE)
+@pytest.mark.parametrize("row", CONFIG_TABLE)
 def test_derived_params_match_config_table(row):
     L, bs, N, ks, lw, rs, ns, t0, t1, cs, ce, nc, kmax, lk = row
     p = v7.derive_params(L, L, bs, sink_ratio=0.01, recent_ratio=0.0, local_span_ratio=0.02,
