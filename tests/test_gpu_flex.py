@@ -354,3 +354,15 @@ def test_flex_full_length_32_token_blocks():
     n_sparse = int(info[:, 2].sum())
     print(f"  density {density(a):.4f} sparse heads {n_sparse}")
     assert n_sparse > 0
+
+
+@pytest.mark.parametrize("L,bs", [(65, 32), (100, 32), (129, 64), (2049, 32), (2049, 128), (4097, 64)])
+def test_flex_edge_lengths(L, bs):
+    """Few blocks (a single 64-bit word per row), one key past a 2048-column
+    chunk, one token past a whole block: exact against the oracle, tau
+    between the heads' divergences."""
+    _case(L=L, bs=bs, edge=True)
+    q, k, _ = make_qkv(L, 4, 2, dtype=torch.bfloat16, seed=49)
+    q, k = _blhd(q, k)
+    tau = _pick_tau(q, k, bs, 0.9)
+    _check(q, k, bs=bs, gamma=0.9, tau=tau)
