@@ -508,3 +508,16 @@ def test_block_count_above_the_limit_is_rejected():
     with pytest.raises(RuntimeError, match="exceed the selection kernels' maximum of 4096"):
         select_blocks(q, k, **PROD)
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("bs", [32, 64, 128])
+def test_dense_causal_fewer_queries_than_keys(bs):
+    """Dense causal attention with L_q < L_k (bottom-right aligned, as
+    flash_attn_func(causal=True) with a key prefix), every block size."""
+    _print_case("attention-offset", bs=bs)
+    q, _, _ = make_qkv(1000, 4, 2, seed=14)
+    _, k, v = make_qkv(1500, 4, 2, seed=15)
+    out = block_sparse_attention(*_gpu(q, k, v), block_size=bs, is_causal=True)
+    torch.cuda.synchronize()
+    ref = v7.dense_causal_attention(q, k, v)[0]
+    _attn_check(out[0], ref)
