@@ -166,3 +166,16 @@ def test_xattn_full_length_properties():
     row_mass = a.sums.sum(-1)                                        # [H, N]
     assert bool(((row_mass - 16.0).abs() <= 16.0 * 2 ** -7).all())
     print(f"  density {density(a):.4f}")
+
+
+@pytest.mark.parametrize("L,Hq,Hk,stride", [
+    (16, 1, 1, 8),            # shorter than one block: one partial row tile of 16 rows
+    (100, 2, 1, 8),           # one block, ragged
+    (129, 2, 1, 8),           # one token past a block
+    (1025, 2, 2, 16),         # one token past 8 blocks
+    (2049, 2, 1, 4),          # 513 reshaped rows: one row past 4 row tiles
+])
+def test_xattn_edge_lengths(L, Hq, Hk, stride):
+    _case(L=L, Hq=Hq, Hk=Hk, stride=stride, edge=True)
+    q, k, _ = make_qkv(L, Hq, Hk, dtype=torch.bfloat16, seed=32)
+    _check(q, k, stride, 0.9, torch.bfloat16)
