@@ -75,11 +75,28 @@ def _ev():
     return torch.cuda.Event(enable_timing=True)
 
 
-def cpu_baseline(q, k, v, kw, bs, nnz_total, sample_heads):
+def _block_match(got, ref, excusable):
+    """(exact-or-excused fraction, exact fraction, unexcused count) of the
+    causal (head, query block, key block) decisions of two [H, N, Nk] masks."""
+    import torch
+    H, N, Nk = ref.shape
+    dom = (torch.arange(N)[:, None] >= torch.arange(Nk)[None, :]).unsqueeze(0).expand(H, N, Nk)
+    total = int(dom.sum())
+    diff = (got != ref) & dom
+    unexc = int((diff & ~excusable).sum())
+    return (total - unexc) / total, (total - int(diff.sum())) / total, unexc
+
+
+def cpu_baseline(q, k, v, kw, bs, nnz_total, sample_heads, sel=None, out=None):
     """Oracle restatement of the reference path on this host's cores: full
     selection, and fp32 block-sparse attention over every query block of the
     first sample_heads query heads, scaled to the whole layer by the
-    selected-tile count (heads are independent)."""
+    selected-tile count (heads are independent).
+
+    The oracle's selection also checks the timed step: the block match of the
+    GPU's lists (sel) against it, and the GPU's output (out) against fp32
+    attention under those lists on the first, middle and last query block of
+    every head.  Returns (baseline, parity)."""
     import torch
     from oracle import v7
     threads = torch.get_num_threads()
@@ -87,6 +104,20 @@ def cpu_baseline(q, k, v, kw, bs, nnz_total, sample_heads):
     t0 = time.perf_counter()
     ref = v7.select_mask(qc, kc, **kw)
     t_sel = time.perf_counter() - t0
+    parity = None
+    if sel is not None and out is not None:
+        got = sel.dense_mask().cpu()
+        frac, exact, unexc = _block_match(got, ref.mask, ref.excusable)
+        N, L = ref.params.N, q.shape[2]
+        qblocks = sorted({0, N // 2, N - 1})
+        want = v7.block_sparse_attention(qc, kc, vc, got, bs, qblocks=qblocks)
+        rows = torch.cat([torch.arange(i * bs, min(L, (i + 1) * bs)) for i in qblocks])
+        err = (out[0].float().cpu()[rows] - want[rows]).abs()
+        parity = {"block_match": round(frac, 6), "block_exact": round(exact, 6), "unexcused": unexc,
+                  "bar": "exact or within 1e-3 of the threshold >= 0.999; attention max-abs <= 2e-2, mean-abs <= 1e-3",
+                  "attn_max_abs": float(f"{err.max().item():.3e}"), "attn_mean_abs": float(f"{err.mean().item():.3e}"),
+                  "attn_sample": f"query blocks {qblocks} of all {q.shape[1]} heads, fp32 oracle under the timed lists",
+                  "pass": bool(frac >= 0.999 and err.max().item() <= 2e-2 and err.mean().item() <= 1e-3)}
     heads = list(range(min(sample_heads, q.shape[1])))
     tiles = int(ref.mask[heads].sum())
     t0 = time.perf_counter()
@@ -106,7 +137,7 @@ def cpu_baseline(q, k, v, kw, bs, nnz_total, sample_heads):
         "attn_ms_scaled": round(t_att * 1e3, 1),
         "cpu_model": _cpu_model(),
         "os_cpu_count": os.cpu_count(),
-    }
+    }, parity
 
 
 def cpu_baseline_xattn(q, k, v, args, bs, nnz_total, sel):
@@ -278,7 +309,7 @@ def main():
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        sel, _ = step(events[i])
+        sel, out = step(events[i])
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) * 1e3 / args.steps
     sel_ms = [e[0].elapsed_time(e[1]) for e in events]
@@ -329,7 +360,7 @@ def main():
             dense["sdpa_flash_error"] = f"{type(ex).__name__}: {ex}"[:200]
     dense_ms = min([x for x in (dense.get("sdpa_flash_ms"), dense.get("own_dense_ms")) if x] or [float("nan")])
 
-    cpu = None
+    cpu = parity = None
     if not args.no_cpu:
         torch.cuda.synchronize()
         if xattn:
@@ -337,7 +368,7 @@ def main():
         elif flex:
             cpu = cpu_baseline_flex(q, k, v, args, bs, nnz, sel)
         else:
-            cpu = cpu_baseline(q, k, v, kw, bs, nnz, args.cpu_heads)
+            cpu, parity = cpu_baseline(q, k, v, kw, bs, nnz, args.cpu_heads, sel=sel, out=out)
 
     if xattn:
         # the two MFMA passes over the causal reshaped scores: 2 * S*D MACs per entry per pass
@@ -412,6 +443,7 @@ def main():
                      "timed": "fs_bsattn_run (order pass + attention kernel), HIP events on the launch stream"},
         "roofline_select": roofline_select,
         "cpu_baseline": cpu,
+        "parity": parity,
         "input_gen_s": round(t_gen, 1),
     }
     print(json.dumps(line), flush=True)

@@ -19,7 +19,7 @@ import torch  # noqa: F401  (must precede the library load, see module docstring
 LIB_PATH = Path(os.environ.get("FFTSPARSE_AMD_LIB") or Path(__file__).resolve().with_name("libfftsparse_amd.so"))
 
 FS_DTYPE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 
 class PoolArgs(ctypes.Structure):
@@ -144,7 +144,7 @@ def load() -> ctypes.CDLL:
     lib.fs_scores_work_bytes.restype = c_size_t
     lib.fs_scores_work_bytes.argtypes = [c_int, c_int, c_int]
     lib.fs_flex_work_bytes.restype = c_size_t
-    lib.fs_flex_work_bytes.argtypes = [c_int, c_int, c_int, c_int]
+    lib.fs_flex_work_bytes.argtypes = [c_int, c_int, c_int, c_int, c_float]
     lib.fs_xattn_work_bytes.restype = c_size_t
     lib.fs_xattn_work_bytes.argtypes = [c_int, c_int, c_int, c_int]
     lib.fs_bsattn_work_bytes.restype = c_size_t

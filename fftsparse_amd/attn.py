@@ -337,6 +337,19 @@ class AttentionCall:
             # flash-attention kernels accept fp16/bf16 only, as does the reference's
             # block_sparse_attn_func.
             raise RuntimeError("FlashAttention only supports fp16 and bf16 data type")
+        if (blk_cnt is None) != (blk_idx is None):
+            raise ValueError("blk_cnt and blk_idx go together")
+        if blk_cnt is not None:
+            Nq, Nk = -(-Lq // block_size), -(-Lk // block_size)
+            if blk_cnt.dtype != torch.int32 or tuple(blk_cnt.shape) != (Hq, Nq) or not blk_cnt.is_contiguous():
+                raise ValueError(f"blk_cnt must be a contiguous int32 [{Hq}, {Nq}] tensor, got "
+                                 f"{blk_cnt.dtype} {tuple(blk_cnt.shape)}")
+            if (blk_idx.dtype not in (torch.uint16, torch.int16) or tuple(blk_idx.shape) != (Hq, Nq, Nk)
+                    or not blk_idx.is_contiguous()):
+                raise ValueError(f"blk_idx must be a contiguous uint16 [{Hq}, {Nq}, {Nk}] tensor, got "
+                                 f"{blk_idx.dtype} {tuple(blk_idx.shape)}")
+            if blk_cnt.device != q.device or blk_idx.device != q.device:
+                raise ValueError("block lists must be on the device of the queries")
         if out is None:
             out = torch.empty(B, Lq, Hq, D, dtype=q.dtype, device=q.device)
         scale = 1.0 / math.sqrt(D) if softmax_scale is None else float(softmax_scale)

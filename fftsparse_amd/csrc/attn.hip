@@ -280,7 +280,8 @@ void bsattn_kernel(AttnKArgs a) {
   int cnt;                                         // key tiles of this query block
   int nb_listed = 0;                               // listed key blocks after the causal trim
   if (listed) {
-    int nb = (int)((cptr32)(uintptr_t)a.blk_cnt)[(int64_t)h * a.Nq + qb];
+    // a count past the row's Nk entries (or negative) is clamped to the row
+    int nb = min(max((int)((cptr32)(uintptr_t)a.blk_cnt)[(int64_t)h * a.Nq + qb], 0), a.Nk);
     lbase = ((int64_t)h * a.Nq + qb) * a.Nk;
     // drop trailing blocks entirely above the diagonal (lists are ascending)
     if (a.is_causal) {
@@ -797,6 +798,9 @@ static int check_attn(const fs_attn_args* a, const char* fn) {
   const uintptr_t ptrs[] = {(uintptr_t)a->q, (uintptr_t)a->k, (uintptr_t)a->v, (uintptr_t)a->out,
                             (uintptr_t)a->work};
   for (uintptr_t p : ptrs) FS_CHECK_ARG(p % 16 == 0, "%s: tensors must be 16-byte aligned", fn);
+  // the kernel reads the lists as 32-bit words
+  FS_CHECK_ARG((uintptr_t)a->blk_cnt % 4 == 0 && (uintptr_t)a->blk_idx % 4 == 0,
+               "%s: blk_cnt / blk_idx must be 4-byte aligned", fn);
   const int64_t Nq = (a->Lq + a->bs - 1) / a->bs;
   const int64_t Nk = (a->Lk + a->bs - 1) / a->bs;
   FS_CHECK_SUPPORTED((int64_t)a->B * a->Hq * Nq < (1ll << 30) && (int64_t)a->B * a->Hk * Nk * a->bs / 64 < (1ll << 31),

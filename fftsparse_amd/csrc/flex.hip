@@ -1015,7 +1015,9 @@ struct FlexLayout {
   size_t part, vert, slash, avgk, vmask, smask, info, attn, cover, p_hm, p_hc, c_hm, c_hc, ties, total;
 };
 
-static FlexLayout flex_work(int Hq, int Hk, int L, int bs) {
+// sparse: whether any head can take the block-level cover (tau > 0; the
+// square-root JS divergence is >= 0, or nan, so js < tau never holds otherwise)
+static FlexLayout flex_work(int Hq, int Hk, int L, int bs, bool sparse) {
   const int nb = (L + bs - 1) / bs;
   const int nchunk = (L + kFChunk - 1) / kFChunk;
   size_t off = 0;
@@ -1032,8 +1034,8 @@ static FlexLayout flex_work(int Hq, int Hk, int L, int bs) {
   w.vmask = take((size_t)Hq * kFWords * sizeof(uint64_t));
   w.smask = take((size_t)Hq * kFWords * sizeof(uint64_t));
   w.info = take((size_t)Hq * 4 * sizeof(int32_t) + (size_t)Hq * sizeof(float));
-  w.attn = take((size_t)Hq * nb * nb * sizeof(float));
-  w.cover = take((size_t)Hq * nb * kFWords * sizeof(uint64_t));
+  w.attn = take(sparse ? (size_t)Hq * nb * nb * sizeof(float) : 0);
+  w.cover = take(sparse ? (size_t)Hq * nb * kFWords * sizeof(uint64_t) : 0);
   w.p_hm = take((size_t)4 * 2 * Hq * 256 * sizeof(uint64_t));
   w.p_hc = take((size_t)4 * 2 * Hq * 256 * sizeof(uint32_t));
   w.c_hm = take((size_t)4 * Hq * 256 * sizeof(uint64_t));
@@ -1064,7 +1066,8 @@ template <typename T>
 static int launch_flex(const fs_flex_args& a, hipStream_t s) {
   const int nb = (a.L + a.bs - 1) / a.bs;
   const int nchunk = (a.L + kFChunk - 1) / kFChunk;
-  const FlexLayout lay = flex_work(a.Hq, a.Hk, a.L, a.bs);
+  const bool sparse = a.tau > 0.f;
+  const FlexLayout lay = flex_work(a.Hq, a.Hk, a.L, a.bs, sparse);
   char* w = static_cast<char*>(a.work);
   FlexK k{};
   k.q = static_cast<const uint16_t*>(a.q);
@@ -1128,7 +1131,7 @@ static int launch_flex(const fs_flex_args& a, hipStream_t s) {
   ck.cover = reinterpret_cast<uint64_t*>(w + lay.cover);
   ck.Hq = a.Hq; ck.Hk = a.Hk; ck.L = a.L; ck.bs = a.bs; ck.nb = nb; ck.gqa_interleave = a.gqa_interleave;
   ck.sqrt_d = k.sqrt_d; ck.gamma = a.gamma;
-  flex_cover_rows_kernel<T><<<(unsigned)(a.Hq * nb), kFThreads, 0, s>>>(ck);
+  if (sparse) flex_cover_rows_kernel<T><<<(unsigned)(a.Hq * nb), kFThreads, 0, s>>>(ck);
   // the sparse heads' covers: mass cut at gamma N of N^2 entries (rows add to one,
   // total nb <= 2^12: masses x 2^(58 - ceil(log2 nb)))
   CutJobs cc{};
@@ -1145,10 +1148,12 @@ static int launch_flex(const fs_flex_args& a, hipStream_t s) {
   cc.info = hk.info;
   cc.hm = k.c_hm;
   cc.hc = k.c_hc;
-  launch_cut_passes(cc, s);
-  int* ties = reinterpret_cast<int*>(w + lay.ties);
-  flex_cover_ties_kernel<<<(unsigned)(a.Hq * cc.slices), kFHeadThreads, 0, s>>>(ck, cc, ties);
-  flex_cover_emit_kernel<<<(unsigned)(a.Hq * cc.slices), kFHeadThreads, 0, s>>>(ck, cc, ties);
+  if (sparse) {
+    launch_cut_passes(cc, s);
+    int* ties = reinterpret_cast<int*>(w + lay.ties);
+    flex_cover_ties_kernel<<<(unsigned)(a.Hq * cc.slices), kFHeadThreads, 0, s>>>(ck, cc, ties);
+    flex_cover_emit_kernel<<<(unsigned)(a.Hq * cc.slices), kFHeadThreads, 0, s>>>(ck, cc, ties);
+  }
   if (int rc = fs_host::launch_status("fs_flex (heads)")) return rc;
   FlexListK lk{};
   lk.vmask = hk.vmask; lk.smask = hk.smask; lk.cover = ck.cover; lk.info = hk.info;
@@ -1161,9 +1166,9 @@ static int launch_flex(const fs_flex_args& a, hipStream_t s) {
 
 using namespace fs;
 
-extern "C" size_t fs_flex_work_bytes(int Hq, int Hk, int L, int bs) {
+extern "C" size_t fs_flex_work_bytes(int Hq, int Hk, int L, int bs, float tau) {
   if (Hq <= 0 || Hk <= 0 || L <= 0 || bs <= 0) return 0;
-  return flex_work(Hq, Hk, L, bs).total;
+  return flex_work(Hq, Hk, L, bs, tau > 0.f).total;
 }
 
 extern "C" int fs_flex(const fs_flex_args* a, void* stream) {

@@ -83,7 +83,7 @@ def flex_select(q: torch.Tensor, k: torch.Tensor, *, gamma: float = 0.9, tau: fl
                         slash=torch.empty(Hq, L, dtype=torch.float32, device=dev),
                         block_size=block_size)
     lib = _lib.load()
-    work = torch.empty(max(1, lib.fs_flex_work_bytes(Hq, Hk, L, block_size)), dtype=torch.uint8, device=dev)
+    work = torch.empty(max(1, lib.fs_flex_work_bytes(Hq, Hk, L, block_size, float(tau))), dtype=torch.uint8, device=dev)
     _lib.call("fs_flex", FlexArgs(
         q=qv.data_ptr(), q_sh=qv.stride(1), q_sl=qv.stride(2), k=kv.data_ptr(), k_sh=kv.stride(1),
         k_sl=kv.stride(2), dtype=_lib.FS_DTYPE[q.dtype], Hq=Hq, Hk=Hk, L=L, D=D, bs=block_size,

@@ -120,10 +120,18 @@ def fused_attention_forward(self, hidden_states, position_embeddings=None, atten
         e0 = _event() if _state["events"] is not None else None
         q, k, q_b, k_b = rope_pool(q, k, cos, sin, block_size=bs)
         if past_key_values is not None:
+            # transformers 5.x's LlamaAttention.forward passes no cache kwargs either
             k, v = past_key_values.update(k, v, self.layer_idx)
-        out, sel = v7_prefill(q, k, v, softmax_scale=self.scaling, return_selection=True, pooled=(q_b, k_b), **kw)
-        if e0 is not None:
-            _record(self, e0, sel, q.shape[1], q_len)
+        if k.shape[2] == q_len:
+            out, sel = v7_prefill(q, k, v, softmax_scale=self.scaling, return_selection=True, pooled=(q_b, k_b),
+                                  **kw)
+            if e0 is not None:
+                _record(self, e0, sel, q.shape[1], q_len)
+        else:
+            # a cache that hands back more keys than this prefill wrote (a
+            # preallocated static cache): the registered attention's path for
+            # L_q != L_k, as the unpatched forward would take
+            out, _ = fftsparse_attention(self, q, k, v, attention_mask, dropout=0.0, scaling=self.scaling, **kwargs)
     else:
         q, k = apply_rotary_pos_emb(q, k, cos, sin)
         if past_key_values is not None:

@@ -258,7 +258,9 @@ FS_API int fs_xattn(const fs_xattn_args* a, void* stream);
  * block lists blk_cnt [Hq][N], blk_idx [Hq][N][N] (N = ceil(L/bs)), optionally
  * head_info [Hq][4] (vertical budget, slash budget, sparse, 0), head_js [Hq]
  * and the per-token vertical / slash profiles [Hq][L] (fp32).
- * work: fs_flex_work_bytes(Hq, Hk, L, bs) bytes.  bf16/f16, D = 128,
+ * work: fs_flex_work_bytes(Hq, Hk, L, bs, tau) bytes, with the tau of the
+ * call (tau <= 0, the reference's default, makes no head sparse and needs no
+ * room for the block-level attention and covers).  bf16/f16, D = 128,
  * bs 32, 64 or 128, L > bs, N <= 4096. */
 typedef struct {
   const void* q; int64_t q_sh, q_sl;
@@ -275,7 +277,7 @@ typedef struct {
   float* slash;
   void* work;
 } fs_flex_args;
-FS_API size_t fs_flex_work_bytes(int Hq, int Hk, int L, int bs);
+FS_API size_t fs_flex_work_bytes(int Hq, int Hk, int L, int bs, float tau);
 FS_API int fs_flex(const fs_flex_args* a, void* stream);
 
 /* ---- block-sparse attention prefill --------------------------------------

@@ -70,7 +70,15 @@ def test_bad_shapes_rejected_without_gpu():
     assert lib.fs_flex(ctypes.byref(f), None) == -1
     f.q_sl, f.L, f.bs = 128, 4096 * 32 + 1, 32                   # 4097 blocks
     assert lib.fs_flex(ctypes.byref(f), None) == -2
-    assert lib.fs_flex_work_bytes(4, 1, 4096, 64) > 4 * 4096 * 4 * 2
+    assert lib.fs_flex_work_bytes(4, 1, 4096, 64, 0.1) > 4 * 4096 * 4 * 2
+    # tau <= 0 (the reference's default) makes no head sparse: no room for the
+    # block-level attention [Hq][nb][nb] fp32 and the covers
+    nb = 4096 // 64
+    assert lib.fs_flex_work_bytes(4, 1, 4096, 64, 0.1) - lib.fs_flex_work_bytes(4, 1, 4096, 64, 0.0) >= 4 * nb * nb * 4
+    x = _lib.AttnArgs(q=16, k=16, v=16, out=16, work=16, dtype=1, B=1, Hq=4, Hk=2, Lq=1280, Lk=1280, D=128, bs=128,
+                      q_sl=128, k_sl=128, v_sl=128, o_sl=512, blk_cnt=18, blk_idx=16)
+    assert lib.fs_bsattn(ctypes.byref(x), None) == -1             # the lists are read as 32-bit words
+    assert b"4-byte aligned" in lib.fs_last_error()
     a = _lib.AttnArgs(q=16, k=16, v=16, out=16, dtype=1, B=1, Hq=3, Hk=2, Lq=10, Lk=10, D=128, bs=128)
     assert lib.fs_bsattn(ctypes.byref(a), None) == -1
     a = _lib.AttnArgs(q=16, k=16, v=16, out=16, work=16, dtype=1, B=1, Hq=4, Hk=2, Lq=10, Lk=10, D=96, bs=128)
@@ -123,3 +131,16 @@ def test_synthetic_inputs_are_pinned():
     q, k, v = make_qkv(2048, 4, 2, dtype=torch.bfloat16, seed=0, stripe_density=0.005, period=512)
     assert sha256_of(q, k, v) == want["small_bf16_seed0"]
     assert CONFIGS["c2"].period == 512 and CONFIGS["c3a"].theta == 1000000.0
+
+
+def test_block_lists_checked_before_any_launch():
+    """Lists of the wrong dtype, shape or layout raise ValueError on the host."""
+    q = torch.zeros(1, 4, 1280, 128, dtype=torch.bfloat16)
+    k = torch.zeros(1, 2, 1280, 128, dtype=torch.bfloat16)
+    cnt = torch.ones(4, 10, dtype=torch.int32)
+    idx = torch.zeros(4, 10, 10, dtype=torch.uint16)
+    bad = [(cnt.to(torch.int64), idx), (cnt[:, :9], idx), (cnt, idx[:, :, :9]), (cnt, idx.to(torch.int32)),
+           (cnt, idx.transpose(1, 2)), (cnt, None)]
+    for c, i in bad:
+        with pytest.raises(ValueError):
+            fftsparse_amd.AttentionCall(q, k, k, c, i)
