@@ -117,7 +117,7 @@ class AttnArgs(ctypes.Structure):
 STRUCTS = [PoolArgs, CorrArgs, StatsArgs, SelectArgs, AttnArgs, ScoresArgs, RopePoolArgs, XattnArgs, FlexArgs]
 
 ENTRY_POINTS = ["fs_pool", "fs_rope_pool", "fs_corr_work_bytes", "fs_corr", "fs_stats", "fs_scores_work_bytes",
-                "fs_scores", "fs_select", "fs_bsattn_work_bytes",
+                "fs_scores", "fs_scores_noalloc", "fs_select", "fs_bsattn_work_bytes",
                 "fs_bsattn", "fs_bsattn_prepare", "fs_bsattn_run", "fs_xattn_work_bytes", "fs_xattn",
                 "fs_flex_work_bytes", "fs_flex",
                 "fs_last_error", "fs_abi_version", "fs_sizeof_args"]
@@ -150,7 +150,8 @@ def load() -> ctypes.CDLL:
     lib.fs_bsattn_work_bytes.restype = c_size_t
     lib.fs_bsattn_work_bytes.argtypes = [POINTER(AttnArgs)]
     for name, st in [("fs_pool", PoolArgs), ("fs_rope_pool", RopePoolArgs), ("fs_corr", CorrArgs),
-                     ("fs_stats", StatsArgs), ("fs_scores", ScoresArgs), ("fs_select", SelectArgs), ("fs_bsattn", AttnArgs), ("fs_bsattn_prepare", AttnArgs),
+                     ("fs_stats", StatsArgs), ("fs_scores", ScoresArgs), ("fs_scores_noalloc", ScoresArgs),
+                     ("fs_select", SelectArgs), ("fs_bsattn", AttnArgs), ("fs_bsattn_prepare", AttnArgs),
                      ("fs_bsattn_run", AttnArgs), ("fs_xattn", XattnArgs),
                      ("fs_flex", FlexArgs)]:
         fn = getattr(lib, name)

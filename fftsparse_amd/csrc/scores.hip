@@ -21,6 +21,8 @@
 // selects the lags, 2 the column scores and their top-n, 3 the last-row
 // top-k, 4 .. 7 the diagonal statistics (one wave per sample; job 1 is
 // idle); every sum is in a fixed order (deterministic).
+#include <mutex>
+
 #include "common.h"
 
 namespace fs {
@@ -331,31 +333,96 @@ extern "C" size_t fs_scores_work_bytes(int Hq, int N, int n_samples) {
   return part_offsets(Hq, N, n_samples, nullptr, nullptr);
 }
 
-extern "C" int fs_scores(const fs_scores_args* a, void* stream) {
-  FS_CHECK_ARG(a != nullptr, "fs_scores: null args");
-  FS_CHECK_ARG(a->q_b && a->k_b && a->work, "fs_scores: null pointer");
-  FS_CHECK_ARG(a->Hq > 0 && a->Hk > 0 && a->Hq % a->Hk == 0, "fs_scores: Hq=%d must be a multiple of Hk=%d",
+// Argument checks of fs_scores and fs_scores_noalloc (fn: the caller's name;
+// with_work: the caller passes the workspace).
+static int check_scores(const fs_scores_args* a, const char* fn, bool with_work) {
+  FS_CHECK_ARG(a != nullptr, "%s: null args", fn);
+  FS_CHECK_ARG(a->q_b && a->k_b && (a->work || !with_work), "%s: null pointer", fn);
+  FS_CHECK_ARG(a->Hq > 0 && a->Hk > 0 && a->Hq % a->Hk == 0, "%s: Hq=%d must be a multiple of Hk=%d", fn,
                a->Hq, a->Hk);
-  FS_CHECK_ARG(a->N >= 1 && a->D >= 16, "fs_scores: bad sizes");
-  FS_CHECK_ARG(((uintptr_t)a->q_b % 16) == 0 && ((uintptr_t)a->k_b % 16) == 0, "fs_scores: unaligned pooled tensors");
+  FS_CHECK_ARG(a->N >= 1 && a->D >= 16, "%s: bad sizes", fn);
+  FS_CHECK_ARG(((uintptr_t)a->q_b % 16) == 0 && ((uintptr_t)a->k_b % 16) == 0, "%s: unaligned pooled tensors", fn);
   FS_CHECK_ARG(a->keep_tau == nullptr || (a->corr && a->remote_start >= 0 && a->local_window >= 0),
-               "fs_scores: bad correlation arguments");
+               "%s: bad correlation arguments", fn);
   FS_CHECK_ARG(a->keep_tau == nullptr || a->corr_mode == 0 ||
                    (a->corr_mode == 1 && a->remote_start < a->N && a->corr_quantile >= 0.f && a->corr_quantile <= 1.f),
-               "fs_scores: corr_mode must be 0 or 1; topk mode needs remote_start < N and a quantile in [0, 1]");
+               "%s: corr_mode must be 0 or 1; topk mode needs remote_start < N and a quantile in [0, 1]", fn);
   FS_CHECK_ARG(a->n_samples >= 0 && (a->n_samples == 0 || (a->sample_taus && a->diag_var)),
-               "fs_scores: sample arrays missing");
+               "%s: sample arrays missing", fn);
   FS_CHECK_ARG(a->n_cols <= 0 || (a->col_sel && a->col_start >= 0 && a->col_end <= a->N &&
                                   a->col_end > a->col_start && a->n_cols <= a->col_end - a->col_start),
-               "fs_scores: bad column range");
+               "%s: bad column range", fn);
   FS_CHECK_ARG(a->last_k <= 0 || (a->last_sel && a->last_scores && a->last_k <= a->N),
-               "fs_scores: bad last-row arguments");
+               "%s: bad last-row arguments", fn);
   FS_CHECK_SUPPORTED(a->dtype == FS_DTYPE_BF16 || a->dtype == FS_DTYPE_F16,
-                     "fs_scores: dtype %d unsupported (bf16/f16; fp32 uses fs_corr and fs_stats)", a->dtype);
+                     "%s: dtype %d unsupported (bf16/f16; fp32 uses fs_corr and fs_stats)", fn, a->dtype);
   // the staged K tile (128 * D 16-bit values) shares the S tile's LDS; D <= 128
-  FS_CHECK_SUPPORTED(a->D % 16 == 0 && a->D <= 128, "fs_scores: head_dim %d unsupported", a->D);
-  FS_CHECK_SUPPORTED(a->N <= 4096, "fs_scores: N=%d > 4096", a->N);
-  FS_CHECK_SUPPORTED(a->n_samples <= kMaxSamples, "fs_scores: %d diagonal samples > %d", a->n_samples, kMaxSamples);
+  FS_CHECK_SUPPORTED(a->D % 16 == 0 && a->D <= 128, "%s: head_dim %d unsupported", fn, a->D);
+  FS_CHECK_SUPPORTED(a->N <= 4096, "%s: N=%d > 4096", fn, a->N);
+  FS_CHECK_SUPPORTED(a->n_samples <= kMaxSamples, "%s: %d diagonal samples > %d", fn, a->n_samples, kMaxSamples);
+  return FS_OK;
+}
+
+extern "C" int fs_scores(const fs_scores_args* a, void* stream) {
+  if (int rc = check_scores(a, "fs_scores", true)) return rc;
   hipStream_t s = (hipStream_t)stream;
   return a->dtype == FS_DTYPE_BF16 ? launch_scores<bf16_t>(*a, s) : launch_scores<f16_t>(*a, s);
+}
+
+// ---- fs_scores without a workspace --------------------------------------
+// The per-tile partials go to `scratch`, a static device array that every GPU
+// the library runs on holds until the process ends.  In host code `scratch`
+// names a host-side stand-in, not device memory: its device address is taken
+// once per device with hipGetSymbolAddress (that device current) and only that
+// address is handed to the kernels.  Every call on a GPU shares its array:
+// calls that overlap on one GPU race.  Nothing in it must start at zero: each
+// call's tile kernel writes every partial its final kernel reads.
+constexpr size_t kScoresStaticBytes = (size_t)32 << 20;   // FS_SCORES_STATIC_BYTES
+static __device__ __align__(256) unsigned char scratch[kScoresStaticBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices];                 // device address of `scratch`, per device
+
+int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    fs_host::set_error("fs_scores_noalloc: hipGetDevice failed: %s", hipGetErrorString(e));
+    return FS_ERR_LAUNCH;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    fs_host::set_error("fs_scores_noalloc: device %d out of range (< %d)", dev, kMaxDevices);
+    return FS_ERR_UNSUPPORTED;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_dev[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      fs_host::set_error("fs_scores_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                         hipGetErrorString(e));
+      return FS_ERR_LAUNCH;
+    }
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return FS_OK;
+}
+}  // namespace
+
+extern "C" int fs_scores_noalloc(const fs_scores_args* a, void* stream) {
+  if (int rc = check_scores(a, "fs_scores_noalloc", false)) return rc;
+  const size_t need = part_offsets(a->Hq, a->N, a->n_samples, nullptr, nullptr);
+  FS_CHECK_SUPPORTED(need <= kScoresStaticBytes,
+                     "fs_scores_noalloc: %zu bytes of partials (Hq=%d, N=%d, n_samples=%d) exceed the static "
+                     "buffer of %zu bytes; use fs_scores with a workspace",
+                     need, a->Hq, a->N, a->n_samples, kScoresStaticBytes);
+  void* ptr = nullptr;
+  if (int rc = scratch_address(&ptr)) return rc;
+  fs_scores_args b = *a;
+  b.work = ptr;
+  hipStream_t s = (hipStream_t)stream;
+  return b.dtype == FS_DTYPE_BF16 ? launch_scores<bf16_t>(b, s) : launch_scores<f16_t>(b, s);
 }

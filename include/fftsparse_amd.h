@@ -176,6 +176,21 @@ typedef struct {
 FS_API size_t fs_scores_work_bytes(int Hq, int N, int n_samples);
 FS_API int fs_scores(const fs_scores_args* a, void* stream);
 
+/* ---- fs_scores without a workspace ---------------------------------------
+ * No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops or harnesses that forbid
+ * hipMalloc): fs_scores with its per-tile partials in a static device array of
+ * FS_SCORES_STATIC_BYTES (32 MiB) that each GPU the library runs on holds
+ * until the process ends; a->work is ignored (may be NULL).  Same outputs as
+ * fs_scores, bit for bit.  A call whose fs_scores_work_bytes(Hq, N, n_samples)
+ * exceeds the array is rejected with FS_ERR_UNSUPPORTED before any launch
+ * (BASELINE shapes need <= 10 MiB: Hq = 32, N = 1024, 64 samples).  Calls
+ * on one GPU share its array: calls that overlap on one GPU (several streams
+ * or threads) race; order them on one stream.  The first call on a device
+ * looks the array's device address up (no allocation). */
+#define FS_SCORES_STATIC_BYTES ((size_t)32 << 20)
+FS_API int fs_scores_noalloc(const fs_scores_args* a, void* stream);
+
 /* ---- mask composition -> per-row block lists ----------------------------
  * Row i of head h selects key block j (0 <= j < Nk, and j <= i if mask_causal) iff
  *   prior:  j < keep_sink || j >= Nk - keep_recent || (local_window > 0 && |i-j| <= local_window)

@@ -144,3 +144,17 @@ def test_block_lists_checked_before_any_launch():
     for c, i in bad:
         with pytest.raises(ValueError):
             fftsparse_amd.AttentionCall(q, k, k, c, i)
+
+
+def test_noalloc_scores_rejects_sizes_past_its_static_buffer_without_gpu():
+    """fs_scores_noalloc checks its size against the static buffer before any
+    HIP call: 32 heads at N = 4096 with 64 sampled diagonals need 56.75 MiB."""
+    lib = _lib.load()
+    a = _lib.ScoresArgs(q_b=16, k_b=16, dtype=1, Hq=32, Hk=8, N=4096, D=128, n_samples=64, sample_taus=16,
+                        diag_var=16, n_cols=0, last_k=0)
+    assert lib.fs_scores_work_bytes(32, 4096, 64) > 32 << 20
+    assert lib.fs_scores_noalloc(ctypes.byref(a), None) == -2
+    assert b"exceed the static buffer" in lib.fs_last_error()
+    a.Hq, a.Hk = 3, 2
+    assert lib.fs_scores_noalloc(ctypes.byref(a), None) == -1
+    assert b"fs_scores_noalloc: Hq=3" in lib.fs_last_error()
