@@ -30,10 +30,12 @@
 //
 // Scheduling: workgroup w runs on XCD w % 8.  With block lists, the query
 // blocks of a head are grouped in runs of consecutive blocks; a counting sort
-// (order_kernel) ranks the runs by tile count, and the runs are dealt
-// round-robin to the XCDs, longest first, the blocks of a run in consecutive
-// slots of one XCD (neighbouring query blocks select shifted copies of the
-// same lag diagonals and the same columns, which then hit that XCD's L2).
+// (order_kernel) ranks the runs KV group by KV group (one KV head's K and V^T
+// then stay in the last-level cache while its query heads run) and, inside a
+// group, by decreasing tile count; the runs are dealt round-robin to the XCDs
+// in that order, the blocks of a run in consecutive slots of one XCD
+// (neighbouring query blocks select shifted copies of the same lag diagonals
+// and the same columns, which then hit that XCD's L2).
 // The dense path gives XCD x every 8th query-block row (last rows first) of
 // every head.
 #include <climits>
@@ -665,36 +667,41 @@ void bsattn_kernel(AttnKArgs a) {
     }
 }
 
-// ---- longest-first order of the scheduling units (run consecutive query
-// blocks of one head): counting sort of their total tile count, in bins of 2^shift
+// ---- order of the scheduling units (run consecutive query blocks of one
+// head): KV group by KV group, and inside a group longest first.  One KV
+// head's K and V^T (64 MiB at L = 131072) then stay in the last-level cache
+// while its query heads run, instead of every KV head's streaming at once.
+// Counting sort of key = hk * nbc + (nbc - 1 - (tile count >> shift)).
 constexpr int kOrderThreads = 1024;
 constexpr int kOrderMaxBins = 8192;
-__global__ __launch_bounds__(kOrderThreads) void order_kernel(const int32_t* __restrict__ cnt, int Hq, int Nq, int run,
-                                                              int Nk, int shift, int32_t* __restrict__ order) {
+__global__ __launch_bounds__(kOrderThreads) void order_kernel(const int32_t* __restrict__ cnt, int Hq, int Hk,
+                                                              int gqa_interleave, int Nq, int run, int Nk, int shift,
+                                                              int32_t* __restrict__ order) {
   __shared__ int hist[kOrderMaxBins];
   __shared__ int part[kOrderThreads];
   const int tid = threadIdx.x;
   const int nc = (Nq + run - 1) / run;
   const int units = Hq * nc;
-  const int nb = ((run * Nk) >> shift) + 1;        // bins 0 .. (run Nk) >> shift
-  auto bin_of = [&](int u) {
+  const int g = Hq / Hk;
+  const int nbc = ((run * Nk) >> shift) + 1;       // count bins 0 .. (run Nk) >> shift
+  const int nb = Hk * nbc;                         // keys
+  auto key_of = [&](int u) {
     const int h = u / nc, q0 = (u - h * nc) * run;
     int c = 0;
     for (int j = 0; j < run && q0 + j < Nq; ++j) c += min(max(cnt[(int64_t)h * Nq + q0 + j], 0), Nk);
-    return c >> shift;
+    const int hk = gqa_interleave ? h % Hk : h / g;
+    return hk * nbc + (nbc - 1 - (c >> shift));
   };
   for (int i = tid; i < nb; i += kOrderThreads) hist[i] = 0;
   __syncthreads();
-  for (int u = tid; u < units; u += kOrderThreads) atomicAdd(&hist[bin_of(u)], 1);
+  for (int u = tid; u < units; u += kOrderThreads) atomicAdd(&hist[key_of(u)], 1);
   __syncthreads();
-  // start[c] = number of units in higher bins: scan bins from the top down
+  // start[k] = number of units with a smaller key: thread tid scans keys tid*per ..
   const int per = (nb + kOrderThreads - 1) / kOrderThreads;
-  const int c_hi = nb - 1 - tid * per;             // this thread scans bins c_hi, c_hi-1, ...
+  const int k0 = tid * per;
   int local = 0;
-  for (int k = 0; k < per; ++k) {
-    const int c = c_hi - k;
-    if (c >= 0) local += hist[c];
-  }
+  for (int k = 0; k < per; ++k)
+    if (k0 + k < nb) local += hist[k0 + k];
   part[tid] = local;
   __syncthreads();
   for (int off = 1; off < kOrderThreads; off <<= 1) {   // inclusive scan of chunk sums
@@ -705,16 +712,15 @@ __global__ __launch_bounds__(kOrderThreads) void order_kernel(const int32_t* __r
   }
   int acc = part[tid] - local;                     // exclusive prefix of this chunk
   for (int k = 0; k < per; ++k) {
-    const int c = c_hi - k;
-    if (c >= 0) {
-      const int h = hist[c];
-      hist[c] = acc;
+    if (k0 + k < nb) {
+      const int h = hist[k0 + k];
+      hist[k0 + k] = acc;
       acc += h;
     }
   }
   __syncthreads();
   for (int u = tid; u < units; u += kOrderThreads) {
-    const int pos = atomicAdd(&hist[bin_of(u)], 1);
+    const int pos = atomicAdd(&hist[key_of(u)], 1);
     order[pos] = u;
   }
 }
@@ -740,10 +746,11 @@ static int launch_run(const fs_attn_args& a, int Nq, int Nk, hipStream_t s) {
   const int run = BS == 32 ? min(64, max(1, Nq / 64)) : min(16, max(1, Nq / 64));
   if (a.blk_cnt) {
     int shift = 0;
-    while (((run * Nk) >> shift) + 1 > kOrderMaxBins) ++shift;
+    while ((int64_t)a.Hk * (((run * Nk) >> shift) + 1) > kOrderMaxBins) ++shift;
     order = reinterpret_cast<int32_t*>(static_cast<char*>(a.work) + vt_bytes(a));
     total = a.Hq * ((Nq + run - 1) / run);
-    order_kernel<<<1, kOrderThreads, 0, s>>>(a.blk_cnt, a.Hq, Nq, run, Nk, shift, order);
+    order_kernel<<<1, kOrderThreads, 0, s>>>(a.blk_cnt, a.Hq, a.Hk, a.gqa_interleave ? 1 : 0, Nq, run, Nk, shift,
+                                             order);
     if (int rc = fs_host::launch_status("fs_bsattn (order)")) return rc;
     grid = (unsigned)((total + 7) / 8 * 8 * run);
   } else {
@@ -790,6 +797,7 @@ static int check_attn(const fs_attn_args* a, const char* fn) {
   FS_CHECK_SUPPORTED(a->bs == 32 || a->bs == 64 || a->bs == 128, "%s: block size %d unsupported", fn, a->bs);
   FS_CHECK_SUPPORTED(a->dtype == FS_DTYPE_BF16 || a->dtype == FS_DTYPE_F16,
                      "%s: dtype %d unsupported (bf16/f16)", fn, a->dtype);
+  FS_CHECK_SUPPORTED(a->Hk <= 4096, "%s: %d KV heads > 4096", fn, a->Hk);
   FS_CHECK_ARG(a->blk_cnt == nullptr || (a->blk_idx != nullptr && a->B == 1),
                "%s: block lists need blk_idx and B == 1", fn);
   const int64_t strides[] = {a->q_sb, a->q_sh, a->q_sl, a->k_sb, a->k_sh, a->k_sl,
