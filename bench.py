@@ -64,6 +64,9 @@ def parse():
                          "or the model's own RoPE before the registered attention")
     ap.add_argument("--c4-compare-rope", action="store_true",
                     help="config c4: also time the other --c4-rope variant (same steps)")
+    ap.add_argument("--gemm-ceiling", action="store_true",
+                    help="only time a bf16 8192^3 torch.matmul (hipBLASLt) 3 + 60 times, the practical MFMA ceiling "
+                         "the attention kernel is compared with in the profiles, then exit")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (5 times) to calibrate "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE, then exit")
@@ -244,6 +247,23 @@ def main():
                                    "code path here", "n_gpus": args.gpus}))
         sys.exit(2)
     import torch
+    if args.gemm_ceiling:
+        n = 8192
+        a = torch.randn(n, n, device="cuda:0", dtype=torch.bfloat16)
+        b = torch.randn(n, n, device="cuda:0", dtype=torch.bfloat16)
+        for _ in range(3):
+            a @ b
+        torch.cuda.synchronize()
+        e0, e1 = _ev(), _ev()
+        e0.record()
+        for _ in range(60):
+            a @ b
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / 60
+        print(json.dumps({"gemm_ceiling": f"bf16 {n}^3 torch.matmul", "ms": round(ms, 4),
+                          "tflops": round(2 * n ** 3 / ms / 1e9, 1), "launches": 60}))
+        return
     if args.copy_calib:
         n = args.copy_calib * (1 << 20)
         x = torch.ones(n, dtype=torch.uint8, device="cuda:0")
