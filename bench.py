@@ -483,16 +483,12 @@ def run_c4(args):
     with the fused RoPE, around the rotary embedding + pooling pass and the
     attention) over the forward time."""
     import torch
-    from transformers import LlamaConfig, LlamaForCausalLM
+    from transformers import LlamaForCausalLM
     import fftsparse_amd.hf as fh
+    from fftsparse_amd.synth import c4_model_config
 
     L = args.c4_len
-    cfg = LlamaConfig(hidden_size=4096, intermediate_size=14336, num_hidden_layers=32, num_attention_heads=32,
-                      num_key_value_heads=8, head_dim=128, vocab_size=128256, max_position_embeddings=131072,
-                      rms_norm_eps=1e-5, tie_word_embeddings=False,
-                      rope_parameters={"rope_type": "llama3", "rope_theta": 500000.0, "factor": 8.0,
-                                       "low_freq_factor": 1.0, "high_freq_factor": 4.0,
-                                       "original_max_position_embeddings": 8192})
+    cfg = c4_model_config()
     dev = torch.device("cuda:0")
     t0 = time.perf_counter()
     torch.manual_seed(args.seed)

@@ -121,3 +121,17 @@ def sha256_of(*tensors) -> str:
         h.update(str(tuple(t.shape)).encode())
         h.update(t.view(torch.uint8).numpy().tobytes())
     return h.hexdigest()
+
+
+def c4_model_config(num_hidden_layers: int = 32, max_position_embeddings: int = 131072):
+    """BASELINE config 4's model: a Llama-3.1-8B-shaped transformers
+    LlamaConfig (hidden 4096, 32 query / 8 KV heads, head_dim 128, MLP 14336,
+    vocabulary 128256, llama3 RoPE scaling with theta 500000), for random-init
+    weights (no checkpoint is available offline)."""
+    from transformers import LlamaConfig
+    return LlamaConfig(hidden_size=4096, intermediate_size=14336, num_hidden_layers=num_hidden_layers,
+                       num_attention_heads=32, num_key_value_heads=8, head_dim=128, vocab_size=128256,
+                       max_position_embeddings=max_position_embeddings, rms_norm_eps=1e-5, tie_word_embeddings=False,
+                       rope_parameters={"rope_type": "llama3", "rope_theta": 500000.0, "factor": 8.0,
+                                        "low_freq_factor": 1.0, "high_freq_factor": 4.0,
+                                        "original_max_position_embeddings": 8192})
