@@ -52,6 +52,11 @@ def parse():
     ap.add_argument("--flex-block", type=int, default=32, choices=(32, 64, 128),
                     help="FlexPrefill's block size (the reference benchmark calls it with its default, 32)")
     ap.add_argument("--no-dense", action="store_true", help="skip the dense comparators")
+    ap.add_argument("--selection-only", action="store_true",
+                    help="time only the block selection (select_blocks) and print its own JSON line; with "
+                         "--dtype float32 this is the fp32 path (LDS radix-FFT lag correlation, fs_corr + fs_stats)")
+    ap.add_argument("--dtype", choices=("bfloat16", "float16", "float32"), default=None,
+                    help="cast the config's synthetic Q/K/V to this dtype (default: the config's own)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--select-groups", type=int, default=None,
                     help="KV-head groups of the selection pipeline (default: the library's choice)")
@@ -284,6 +289,8 @@ def main():
     flex = args.selector == "flex"
     t_gen = time.perf_counter()
     q, k, v = make_config(cfg, seed=args.seed)
+    if args.dtype:
+        q, k, v = (x.to(getattr(torch, args.dtype)) for x in (q, k, v))
     q, k, v = q.to(dev), k.to(dev), v.to(dev)
     torch.cuda.synchronize()
     t_gen = time.perf_counter() - t_gen
@@ -291,6 +298,9 @@ def main():
     bs = args.flex_block if flex else cfg.block_size
     Hq, L, D = q.shape[1], q.shape[2], q.shape[3]
     Hk = k.shape[1]
+
+    if args.selection_only:
+        return run_selection_only(args, cfg, q, k, kw)
 
     # One step = selection (pool, corr, stats, select) + attention (V^T
     # pre-pass, then order + attention kernel), all on torch's current stream,
@@ -467,6 +477,41 @@ def main():
         "input_gen_s": round(t_gen, 1),
     }
     print(json.dumps(line), flush=True)
+
+
+def run_selection_only(args, cfg, q, k, kw):
+    """The v7 block selection alone (select_blocks: pool, lag correlation and
+    statistics, block lists) on the config's inputs in their dtype, HIP events
+    on torch's current stream; one JSON line with its time and HBM roofline."""
+    import torch
+    from fftsparse_amd import select_blocks
+    for _ in range(args.warmup):
+        select_blocks(q, k, **kw)
+    torch.cuda.synchronize()
+    ev = [(_ev(), _ev()) for _ in range(args.steps)]
+    for a, b in ev:
+        a.record()
+        sel = select_blocks(q, k, **kw)
+        b.record()
+    torch.cuda.synchronize()
+    ms = [a.elapsed_time(b) for a, b in ev]
+    L, Hq, Hk, D = q.shape[2], q.shape[1], k.shape[1], q.shape[3]
+    nbytes = L * (Hq + Hk) * D * q.element_size()
+    t = statistics.mean(ms)
+    N = -(-L // kw["block_size"])
+    print(json.dumps({
+        "metric": "block selection ms (select_blocks)", "value": round(t, 4), "unit": "ms",
+        "higher_is_better": False, "steps": args.steps, "warmup": args.warmup,
+        "dtype": str(q.dtype).replace("torch.", ""),
+        "config": {"workload": f"{cfg.name} shape: L={L}, Hq={Hq}, Hkv={Hk}, D={D}, block {kw['block_size']}, "
+                               f"corr_threshold {kw['corr_threshold']}, production kwargs, selection only",
+                   "seq_len": L},
+        "median_ms": round(statistics.median(ms), 4),
+        "density": round(sel.nnz() / (Hq * N * (N + 1) / 2), 5),
+        "roofline_select": {"bound": "hbm", "achieved": round(nbytes / (t * 1e-3) / 1e9, 1), "peak": PEAK_HBM_GBS,
+                            "unit": "GB/s", "frac": round(nbytes / (t * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                            "work": "Q and K read once (L*(Hq+Hkv)*D*element bytes)"},
+    }), flush=True)
 
 
 C4_METRIC = "end-to-end prefill ms, 32-layer random-init Llama-3.1-8B at 128K, attention share, 1 GPU"
