@@ -674,6 +674,7 @@ void bsattn_kernel(AttnKArgs a) {
 // Counting sort of key = hk * nbc + (nbc - 1 - (tile count >> shift)).
 constexpr int kOrderThreads = 1024;
 constexpr int kOrderMaxBins = 8192;
+constexpr int kOrderKeysPerThread = 8;           // keys kept in registers between the two passes
 __global__ __launch_bounds__(kOrderThreads) void order_kernel(const int32_t* __restrict__ cnt, int Hq, int Hk,
                                                               int gqa_interleave, int Nq, int run, int Nk, int shift,
                                                               int32_t* __restrict__ order) {
@@ -687,14 +688,38 @@ __global__ __launch_bounds__(kOrderThreads) void order_kernel(const int32_t* __r
   const int nb = Hk * nbc;                         // keys
   auto key_of = [&](int u) {
     const int h = u / nc, q0 = (u - h * nc) * run;
+    const int32_t* c0 = cnt + (int64_t)h * Nq + q0;
+    const int n = min(run, Nq - q0);
+    // the count loads of a unit are issued together (16 at a time), then added
     int c = 0;
-    for (int j = 0; j < run && q0 + j < Nq; ++j) c += min(max(cnt[(int64_t)h * Nq + q0 + j], 0), Nk);
+    for (int j0 = 0; j0 < n; j0 += 16) {
+      int v[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) v[j] = j0 + j < n ? c0[j0 + j] : 0;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) c += min(max(v[j], 0), Nk);
+    }
     const int hk = gqa_interleave ? h % Hk : h / g;
     return hk * nbc + (nbc - 1 - (c >> shift));
   };
+  // this thread's units u = tid + k * kOrderThreads; their keys stay in registers
+  // when there are at most kOrderKeysPerThread of them, else they are formed again
+  const bool held = units <= kOrderKeysPerThread * kOrderThreads;
+  int keys[kOrderKeysPerThread];
+#pragma unroll
+  for (int k = 0; k < kOrderKeysPerThread; ++k) {
+    const int u = tid + k * kOrderThreads;
+    keys[k] = (held && u < units) ? key_of(u) : 0;
+  }
   for (int i = tid; i < nb; i += kOrderThreads) hist[i] = 0;
   __syncthreads();
-  for (int u = tid; u < units; u += kOrderThreads) atomicAdd(&hist[key_of(u)], 1);
+  if (held) {
+#pragma unroll
+    for (int k = 0; k < kOrderKeysPerThread; ++k)
+      if (tid + k * kOrderThreads < units) atomicAdd(&hist[keys[k]], 1);
+  } else {
+    for (int u = tid; u < units; u += kOrderThreads) atomicAdd(&hist[key_of(u)], 1);
+  }
   __syncthreads();
   // start[k] = number of units with a smaller key: thread tid scans keys tid*per ..
   const int per = (nb + kOrderThreads - 1) / kOrderThreads;
@@ -719,9 +744,14 @@ __global__ __launch_bounds__(kOrderThreads) void order_kernel(const int32_t* __r
     }
   }
   __syncthreads();
-  for (int u = tid; u < units; u += kOrderThreads) {
-    const int pos = atomicAdd(&hist[key_of(u)], 1);
-    order[pos] = u;
+  if (held) {
+#pragma unroll
+    for (int k = 0; k < kOrderKeysPerThread; ++k) {
+      const int u = tid + k * kOrderThreads;
+      if (u < units) order[atomicAdd(&hist[keys[k]], 1)] = u;
+    }
+  } else {
+    for (int u = tid; u < units; u += kOrderThreads) order[atomicAdd(&hist[key_of(u)], 1)] = u;
   }
 }
 
