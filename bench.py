@@ -468,7 +468,8 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": None if (xattn or flex) else pmc_traffic("bsattn", cfg.name),
-                     "kernel": f"fs::bsattn_kernel<{bs},{'bf16' if q.dtype == torch.bfloat16 else 'f16'}>",
+                     "kernel": (f"fs::bsattn_kernel<128, 64, {'bf16' if q.dtype == torch.bfloat16 else 'f16'}, {bs}>"
+                                + (" (union of 128 / bs rows' lists per workgroup)" if bs < 64 else "")),
                      "work": f"4*D*bs^2 flop per selected (query block, key block) tile x {nnz} tiles",
                      "timed": "fs_bsattn_run (order pass + attention kernel), HIP events on the launch stream"},
         "roofline_select": roofline_select,

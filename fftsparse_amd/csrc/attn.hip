@@ -23,8 +23,9 @@
 //    wait overlaps the other's MFMAs).
 //  - BS = 64 uses TK = 64 split between two key groups (4 waves), merged
 //    through LDS at the end.
-//  - BS = 32 uses TK = 64 holding two listed key blocks, one per key group
-//    (2 waves of the same 32 queries), merged the same way.
+//  - 16- and 32-token block lists run in union mode: a workgroup of 128
+//    queries walks the union of its 128 / bs rows' lists (see below), with the
+//    BS = 128 layout.  Dense calls at those block sizes take the BS = 128 kernel.
 // LDS rows are 256 B with the 16-byte chunk c of row r stored at c ^ (r & 15)
 // so the 8 lanes of a ds_read_b128 phase hit distinct banks.
 //
@@ -149,20 +150,17 @@ __global__ __launch_bounds__(256) void vt_kernel(const uint16_t* __restrict__ v,
 template <int BS, int TK>
 struct AttnCfg {
   static constexpr int QW = BS / 32;          // query waves (32 queries each)
-  // key groups: waves sharing the keys of a tile (2 or 1); at BS = 32 a tile
-  // holds two listed key blocks, one per key group
-  static constexpr int KG = BS == 32 ? 2 : 2 * TK / BS;
+  // key groups: waves sharing the keys of a tile (2 or 1)
+  static constexpr int KG = 2 * TK / BS;
   static constexpr int NW = QW * KG;          // waves
   static constexpr int NT = NW * 64;          // threads
   static constexpr int KH = TK / KG;          // keys per wave per tile
   static constexpr int KT = KH / 32;          // 32-key sub-tiles per wave
   static constexpr int TPB = BS >= TK ? BS / TK : 1;   // tiles per key block
-  static constexpr int BPT = TK > BS ? TK / BS : 1;    // key blocks per tile (BS = 32)
   static constexpr int TILE = TK * kD;        // elements of one K (or V^T) tile
   static constexpr int REGIONS = TILE * 2 / 1024;   // 1 KiB DMA regions per tile
   static constexpr int DMA_PER_WAVE = 2 * REGIONS / NW;
   static_assert(KG == 1 || KG == 2, "tile is a block or half a block");
-  static_assert(BS != 32 || (TK == 64 && KH == 32), "32-token blocks: two blocks per 64-key tile");
 };
 
 // V^T row length: the key blocks, zero padded to whole 64-key slabs
@@ -205,10 +203,20 @@ __device__ __forceinline__ uint4 lds16(const char* base, uint32_t off) {
   return *reinterpret_cast<const uint4*>(base + off);
 }
 
-template <int BS, int TK, typename T>
+// LB < BS (union mode, BS = 128): the block lists are at LB-token granularity
+// and a workgroup covers BS / LB consecutive list rows (128 queries).  It walks
+// the ascending union of their lists (union_kernel), each entry a key block
+// with the set of the group's rows that selected it; a lane's scores of a key
+// block its row did not select are masked.  A tile of TK keys holds TK / LB
+// union entries, so every K / V^T tile copy serves 128 queries and every wave
+// does 32 x TK per barrier, as with 128-token blocks.
+template <int BS, int TK, typename T, int LB = BS>
 __global__ __launch_bounds__((AttnCfg<BS, TK>::NT)) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void bsattn_kernel(AttnKArgs a) {
   using C = AttnCfg<BS, TK>;
+  constexpr bool UNION = LB < BS;
+  constexpr int EPT = UNION ? TK / LB : 1;         // union entries per tile
+  static_assert(!UNION || (BS == 128 && TK == 64 && (LB == 16 || LB == 32)), "union mode: 16- or 32-token lists");
   using Ops = MfmaOps<T>;
   using V8 = typename Ops::V8;
   // [K | V^T][buffer] tiles; 256-byte rows with swizzled 16-byte chunks
@@ -281,7 +289,13 @@ void bsattn_kernel(AttnKArgs a) {
   };
   int cnt;                                         // key tiles of this query block
   int nb_listed = 0;                               // listed key blocks after the causal trim
-  if (listed) {
+  if (UNION && listed) {
+    // the group's union list: 32-bit entries (block | rows << 16), no trim
+    const int nb = min(max((int)((cptr32)(uintptr_t)a.blk_cnt)[(int64_t)h * a.Nq + qb], 0), a.Nk);
+    lbase = ((int64_t)h * a.Nq + qb) * a.Nk;
+    cnt = (nb + EPT - 1) / EPT;
+    nb_listed = nb;
+  } else if (listed) {
     // a count past the row's Nk entries (or negative) is clamped to the row
     int nb = min(max((int)((cptr32)(uintptr_t)a.blk_cnt)[(int64_t)h * a.Nq + qb], 0), a.Nk);
     lbase = ((int64_t)h * a.Nq + qb) * a.Nk;
@@ -289,31 +303,25 @@ void bsattn_kernel(AttnKArgs a) {
     if (a.is_causal) {
       while (nb > 0 && block_at(nb - 1) * BS > q0 + BS - 1 + off) --nb;
     }
-    cnt = C::BPT > 1 ? (nb + C::BPT - 1) / C::BPT : nb * C::TPB;
+    cnt = nb * C::TPB;
     nb_listed = nb;
   } else {
     const int last_key = a.is_causal ? min(a.Lk - 1, q0 + BS - 1 + off) : a.Lk - 1;
     cnt = last_key < 0 ? 0 : last_key / TK + 1;
   }
-  // first key of tile t (-1: an out-of-range list entry, skipped).  At BS = 32
-  // (two key blocks per tile) it is the first key of this wave's block of the
-  // tile, and block_key gives either block's.
+  // first key of tile t (-1: an out-of-range list entry, skipped)
   const int nlisted = nb_listed;
-  auto block_key = [&](int t, int half) -> int {   // BS = 32
-    if (!listed) return t * TK + half * BS;
-    const int i = t * C::BPT + half;
-    if (i >= nlisted) return -1;
-    const int kb = block_at(i);
-    return kb < a.Nk ? kb * BS : -1;
+  auto uent = [&](int i) -> uint32_t {            // union entry i, all ones past the end
+    if (i >= nlisted) return 0xffffffffu;
+    return ((cptr32)(uintptr_t)a.blk_idx)[lbase + i];
   };
   auto key_of = [&](int t) -> int {
-    if constexpr (C::BPT > 1) {
-      return block_key(t, kh);
-    } else {
-      if (!listed) return t * TK;
-      const int kb = block_at(t / C::TPB);
-      return kb < a.Nk ? kb * BS + (t % C::TPB) * TK : -1;
+    if constexpr (UNION) {
+      if (listed) return t;                        // union mode: copies and masks look the tile's entries up
     }
+    if (!listed) return t * TK;
+    const int kb = block_at(t / C::TPB);
+    return kb < a.Nk ? kb * BS + (t % C::TPB) * TK : -1;
   };
 
   // ---- tile DMA: wave w copies 1 KiB regions w*NR .. w*NR+NR-1 of the K tile
@@ -327,11 +335,11 @@ void bsattn_kernel(AttnKArgs a) {
     const int R = wave * NR + i;                   // region: LDS rows 4R .. 4R+3
     const int r = 4 * R + (lane >> 4);
     const int c = (lane & 15) ^ (r & 15);
-    if constexpr (C::BPT > 1) {
-      // K rows relative to this wave's key block (its 32 rows of the tile);
-      // V^T chunks (c & 7) < 4 hold the first block's keys, the others the second's
+    if constexpr (UNION) {
+      // K rows relative to this wave's 16 rows of the tile; V^T: the key
+      // offset of the lane's 8 keys inside their union entry
       koff[i] = (uint32_t)((r - wave * 4 * NR) * a.k_sl + c * 8) * 2u;
-      voff[i] = (uint32_t)((2 * r + (c >> 3)) * a.Lp + (c & 3) * 8) * 2u;
+      voff[i] = (uint32_t)((2 * r + (c >> 3)) * a.Lp + (((c & 7) * 8) % LB)) * 2u;
     } else {
       koff[i] = (uint32_t)(r * a.k_sl + c * 8) * 2u;
       voff[i] = (TK == 128 ? (uint32_t)(r * a.Lp + c * 8)                          // d = r
@@ -342,8 +350,16 @@ void bsattn_kernel(AttnKArgs a) {
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&lds[0][0][0]);
   auto issue_k = [&](int key0, int buf) {
     const uint32_t lk = lds0 + (uint32_t)(buf * C::TILE * 2 + wave * NR * 1024);
-    if constexpr (C::BPT > 1) {
-      // this wave's key block: 32 rows from key0
+    if constexpr (UNION) {
+      if (listed) {
+        // key0 is the tile index: this wave's 16 rows belong to entry 16 wave / LB
+        const uint32_t e = uent(key0 * EPT + (16 * wave) / LB);
+        const int blk = (int)(e & 0xffffu);
+        key0 = blk < a.Nk ? blk * LB + (16 * wave) % LB : -1;
+      }
+    }
+    if constexpr (UNION) {
+      // this wave's 16 rows of the tile from key0
       const int kc = min(max(key0, 0), a.Lk - 1);
       const uint16_t* base = kp + (int64_t)kc * a.k_sl;
       if (key0 >= 0 && key0 + 4 * NR <= a.Lk) {
@@ -383,17 +399,27 @@ void bsattn_kernel(AttnKArgs a) {
   };
   auto issue_v = [&](int key0, int buf) {
     const uint32_t lv = lds0 + (uint32_t)((2 + buf) * C::TILE * 2 + wave * NR * 1024);
-    if constexpr (C::BPT > 1) {
-      // key0 is the tile index here: the two key blocks' V^T columns
-      const uint32_t kA = (uint32_t)max(block_key(key0, 0), 0) * 2u;
-      const uint32_t kB = (uint32_t)max(block_key(key0, 1), 0) * 2u;
+    if constexpr (UNION) {
+      if (listed) {
+        // key0 is the tile index; lane chunk c holds keys of entry ((c & 7) * 8) / LB
+        uint32_t ek[EPT];
 #pragma unroll
-      for (int i = 0; i < NR; ++i) {
-        const int r = 4 * (wave * NR + i) + (lane >> 4);
-        const int c = (lane & 15) ^ (r & 15);
-        dma16s(lv + i * 1024, vtp, voff[i] + ((c & 4) ? kB : kA));
+        for (int ie = 0; ie < EPT; ++ie) {
+          const int blk = (int)(uent(key0 * EPT + ie) & 0xffffu);
+          ek[ie] = (uint32_t)(blk < a.Nk ? blk * LB : 0) * 2u;
+        }
+#pragma unroll
+        for (int i = 0; i < NR; ++i) {
+          const int r = 4 * (wave * NR + i) + (lane >> 4);
+          const int c = (lane & 15) ^ (r & 15);
+          const int sel = ((c & 7) * 8) / LB;
+          uint32_t k = ek[0];
+#pragma unroll
+          for (int ie = 1; ie < EPT; ++ie) k = sel == ie ? ek[ie] : k;
+          dma16s(lv + i * 1024, vtp, voff[i] + k);
+        }
+        return;
       }
-      return;
     }
     const uint16_t* base = vtp + max(key0, 0);     // V^T is zero padded to Lp
 #pragma unroll
@@ -445,7 +471,7 @@ void bsattn_kernel(AttnKArgs a) {
   };
   // whether any key of this wave's half of tile kb is visible to its queries
   auto active_for = [&](int key0) {
-    const int kw0 = C::BPT > 1 ? key0 : key0 + kbase;
+    const int kw0 = key0 + kbase;
     return key0 >= 0 && kw0 < a.Lk && !(a.is_causal && kw0 > qw0 + 31 + off);
   };
 
@@ -453,7 +479,47 @@ void bsattn_kernel(AttnKArgs a) {
   // whose scores are in s; the running max is taken later, beside the
   // exponentials of that tile.
   auto mask_only = [&](int key0, f32x16_t* s) {
-    const int kw0 = C::BPT > 1 ? key0 : key0 + kbase;
+    if constexpr (UNION) {
+      if (listed) {
+        // key0 is the tile index.  Lane row jq of the group; a key of entry ie
+        // is kept iff the entry is real, row jq selected it, and it is below Lk
+        // and (causal) at or before the lane's query.  Fast path: every row of
+        // this wave selected every entry and no key needs the causal / Lk cut.
+        const int jq = (qq * 32 + l32) / LB;
+        constexpr uint32_t kWaveRows = (1u << (32 / LB)) - 1;
+        const uint32_t wrows = kWaveRows << ((qq * 32) / LB);
+        uint32_t ents[EPT];
+        bool full = true;
+#pragma unroll
+        for (int ie = 0; ie < EPT; ++ie) {
+          ents[ie] = uent(key0 * EPT + ie);
+          const int blk = (int)(ents[ie] & 0xffffu);
+          if (blk >= a.Nk || ((ents[ie] >> 16) & wrows) != wrows || blk * LB + LB > a.Lk ||
+              (a.is_causal && blk * LB + LB - 1 > qw0 + off))
+            full = false;
+        }
+        if (!full) {
+#pragma unroll
+          for (int ie = 0; ie < EPT; ++ie) {
+            const int blk = (int)(ents[ie] & 0xffffu);
+            const bool mine = blk < a.Nk && ((ents[ie] >> (16 + jq)) & 1u);
+            int lim = a.Lk - blk * LB;
+            if (a.is_causal) lim = min(lim, qrow + off - blk * LB + 1);
+            lim = mine ? lim - hi * 4 : INT_MIN;
+            // registers of entry ie: sub-tile kt = ie * LB / 32, and at LB = 16 the half r >> 3
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int kt = (ie * LB) / 32;
+              if (LB == 16 && (r >> 3) != (ie & 1)) continue;
+              const int local = (((r >> 2) * 8) % LB) + (r & 3);
+              if (local >= lim) s[kt][r] = -INFINITY;
+            }
+          }
+        }
+        return;
+      }
+    }
+    const int kw0 = key0 + kbase;
     const bool act = active_for(key0);
     if (!act || (kw0 + C::KH > a.Lk) || (a.is_causal && kw0 + C::KH - 1 > qw0 + off)) {
       int lim = a.Lk - kw0 - hi * 4;
@@ -543,7 +609,7 @@ void bsattn_kernel(AttnKArgs a) {
       kb2 = key_of(t + 2);
       issue_k(kb2, t & 1);
     }
-    if (t < cnt) issue_v(C::BPT > 1 ? t : kb0, t & 1);
+    if (t < cnt) issue_v((UNION && listed) ? t : kb0, t & 1);
     __builtin_amdgcn_s_setprio(2);
     // The row max of tile t, the raise of the running max and the
     // exponentials of tile t are VALU work independent of the MFMAs of S(t+1)
@@ -755,25 +821,82 @@ __global__ __launch_bounds__(kOrderThreads) void order_kernel(const int32_t* __r
   }
 }
 
+// ---- union lists of groups of R consecutive list rows (union mode) -------
+// One wave per (head, group): the rows' block lists as bit rows in LDS, their
+// OR word by word (lane w: blocks 64 w .. 64 w + 63), a prefix of the popcounts
+// over the lanes, and each lane writes its blocks in ascending order as
+// block | (rows that selected it) << 16.  Nk <= 4096, R <= 8.
+constexpr int kUnionMaxRows = 8;
+__global__ __launch_bounds__(64) void union_kernel(const int32_t* __restrict__ cnt, const uint16_t* __restrict__ idx,
+                                                   int Nq, int Nk, int R, int Ng, int32_t* __restrict__ u_cnt,
+                                                   uint32_t* __restrict__ u_idx) {
+  __shared__ unsigned long long bits[kUnionMaxRows][64];
+  const int h = blockIdx.x / Ng, grp = blockIdx.x - h * Ng;
+  const int lane = threadIdx.x;
+  for (int j = 0; j < kUnionMaxRows; ++j) bits[j][lane] = 0ull;
+  __syncthreads();
+  for (int j = 0; j < R; ++j) {
+    const int row = grp * R + j;
+    if (row >= Nq) break;
+    const int n = min(max(cnt[(int64_t)h * Nq + row], 0), Nk);
+    const uint16_t* li = idx + ((int64_t)h * Nq + row) * Nk;
+    for (int e = lane; e < n; e += 64) {
+      const int blk = li[e];
+      if (blk < Nk) atomicOr(&bits[j][blk >> 6], 1ull << (blk & 63));
+    }
+  }
+  __syncthreads();
+  unsigned long long any = 0ull;
+  for (int j = 0; j < R; ++j) any |= bits[j][lane];
+  const int c = __popcll(any);
+  int incl = c;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int v = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += v;
+  }
+  const int total = __shfl(incl, 63, 64);
+  uint32_t* out = u_idx + ((int64_t)h * Ng + grp) * Nk;
+  int pos = incl - c;
+  while (any) {
+    const int b = __builtin_ctzll(any);
+    any &= any - 1;
+    uint32_t rows = 0;
+    for (int j = 0; j < R; ++j) rows |= (uint32_t)((bits[j][lane] >> b) & 1ull) << j;
+    out[pos++] = (uint32_t)(64 * lane + b) | (rows << 16);
+  }
+  if (lane == 0) u_cnt[(int64_t)h * Ng + grp] = total;
+}
+
 static size_t vt_bytes(const fs_attn_args& a) {
   const int Nk = (a.Lk + a.bs - 1) / a.bs;
   return ((size_t)a.B * a.Hk * a.D * vt_len(Nk, a.bs) * 2 + 255) & ~(size_t)255;
 }
+static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+// workspace after V^T: the order [Hq * Nq] (+ union mode: u_cnt [Hq * Ng], u_idx [Hq * Ng * Nk])
+static size_t order_bytes(const fs_attn_args& a) {
+  const int64_t Nq = (a.Lq + a.bs - 1) / a.bs;
+  return align256((size_t)a.Hq * Nq * sizeof(int32_t));
+}
+static bool union_mode(const fs_attn_args& a) { return a.blk_cnt != nullptr && a.bs < 64; }
+static int union_groups(const fs_attn_args& a) {
+  const int Nq = (a.Lq + a.bs - 1) / a.bs;
+  const int R = 128 / a.bs;
+  return (Nq + R - 1) / R;
+}
 
 // order pass (block lists only) and the main kernel, reading V^T from the workspace
 template <int BS, int TK, typename T>
-static int launch_run(const fs_attn_args& a, int Nq, int Nk, hipStream_t s) {
-  const int Lp = vt_len(Nk, BS);
+static int launch_run(const fs_attn_args& a, int Nq, int Nk, hipStream_t s, int Lp = 0) {
+  if (Lp == 0) Lp = vt_len(Nk, BS);                // else: V^T laid out for another block size
   const uint16_t* vt = static_cast<const uint16_t*>(a.work);
   int32_t* order = nullptr;
   int total;
   unsigned grid;
   // Scheduling units of `run` consecutive query blocks: at C2 (Nq = 1024) a
   // run of 16 halves the K/V bytes fetched beyond L2 (166 -> 83 GB) and
-  // still leaves 2048 units for longest-first balance over 256 CUs.  32-token
-  // blocks take runs of 64 (2048 tokens, as 16 blocks of 128): 4% faster than
-  // 16 on FlexPrefill's lists at C2.
-  const int run = BS == 32 ? min(64, max(1, Nq / 64)) : min(16, max(1, Nq / 64));
+  // still leaves 2048 units for longest-first balance over 256 CUs.
+  const int run = min(16, max(1, Nq / 64));
   if (a.blk_cnt) {
     int shift = 0;
     while ((int64_t)a.Hk * (((run * Nk) >> shift) + 1) > kOrderMaxBins) ++shift;
@@ -806,14 +929,58 @@ static int launch_run(const fs_attn_args& a, int Nq, int Nk, hipStream_t s) {
   return fs_host::launch_status("fs_bsattn");
 }
 
+// union mode (16- and 32-token lists): union lists, order pass over the
+// groups, the 128-query kernel over the unions
+template <int LB, typename T>
+static int launch_run_union(const fs_attn_args& a, hipStream_t s) {
+  constexpr int R = 128 / LB;
+  const int NqL = (a.Lq + LB - 1) / LB, NkL = (a.Lk + LB - 1) / LB;
+  const int Ng = (NqL + R - 1) / R;
+  char* w = static_cast<char*>(a.work);
+  int32_t* order = reinterpret_cast<int32_t*>(w + vt_bytes(a));
+  int32_t* u_cnt = reinterpret_cast<int32_t*>(w + vt_bytes(a) + order_bytes(a));
+  uint32_t* u_idx = reinterpret_cast<uint32_t*>(w + vt_bytes(a) + order_bytes(a) +
+                                                align256((size_t)a.Hq * Ng * sizeof(int32_t)));
+  union_kernel<<<(unsigned)(a.Hq * Ng), 64, 0, s>>>(a.blk_cnt, a.blk_idx, NqL, NkL, R, Ng, u_cnt, u_idx);
+  if (int rc = fs_host::launch_status("fs_bsattn (union lists)")) return rc;
+  const int run = min(16, max(1, Ng / 64));
+  int shift = 0;
+  while ((int64_t)a.Hk * (((run * NkL) >> shift) + 1) > kOrderMaxBins) ++shift;
+  const int total = a.Hq * ((Ng + run - 1) / run);
+  order_kernel<<<1, kOrderThreads, 0, s>>>(u_cnt, a.Hq, a.Hk, a.gqa_interleave ? 1 : 0, Ng, run, NkL, shift, order);
+  if (int rc = fs_host::launch_status("fs_bsattn (order)")) return rc;
+  AttnKArgs k;
+  k.q = static_cast<const uint16_t*>(a.q);
+  k.k = static_cast<const uint16_t*>(a.k);
+  k.vt = static_cast<const uint16_t*>(a.work);
+  k.out = static_cast<uint16_t*>(a.out);
+  k.blk_cnt = u_cnt;
+  k.blk_idx = reinterpret_cast<const uint16_t*>(u_idx);   // read as 32-bit entries
+  k.order = order;
+  k.q_sb = a.q_sb; k.q_sh = a.q_sh; k.k_sb = a.k_sb; k.k_sh = a.k_sh; k.o_sb = a.o_sb; k.o_sh = a.o_sh;
+  k.q_sl = (int)a.q_sl; k.k_sl = (int)a.k_sl; k.o_sl = (int)a.o_sl;
+  k.Hq = a.Hq; k.Hk = a.Hk; k.Lq = a.Lq; k.Lk = a.Lk;
+  k.Nq = Ng; k.Nk = NkL; k.Lp = vt_len(NkL, LB); k.total = total; k.is_causal = a.is_causal;
+  k.run = run;
+  k.scale = a.softmax_scale;
+  k.gqa_interleave = a.gqa_interleave ? 1 : 0;
+  const unsigned grid = (unsigned)((total + 7) / 8 * 8 * run);
+  bsattn_kernel<128, 64, T, LB><<<grid, AttnCfg<128, 64>::NT, 0, s>>>(k);
+  return fs_host::launch_status("fs_bsattn");
+}
+
 }  // namespace fs
 
 using namespace fs;
 
 extern "C" size_t fs_bsattn_work_bytes(const fs_attn_args* a) {
   if (!a || a->B <= 0 || a->Hq <= 0 || a->Hk <= 0 || a->Lq <= 0 || a->Lk <= 0 || a->D <= 0 || a->bs <= 0) return 0;
-  const int64_t Nq = (a->Lq + a->bs - 1) / a->bs;
-  return vt_bytes(*a) + (size_t)a->Hq * Nq * sizeof(int32_t);
+  size_t n = vt_bytes(*a) + order_bytes(*a);
+  if (union_mode(*a)) {
+    const size_t Ng = (size_t)union_groups(*a), Nk = (size_t)(a->Lk + a->bs - 1) / a->bs;
+    n += align256((size_t)a->Hq * Ng * sizeof(int32_t)) + (size_t)a->Hq * Ng * Nk * sizeof(uint32_t);
+  }
+  return n;
 }
 
 // Argument checks shared by the three attention entry points.
@@ -824,7 +991,11 @@ static int check_attn(const fs_attn_args* a, const char* fn) {
                "%s: Hq=%d must be a multiple of Hk=%d", fn, a->Hq, a->Hk);
   FS_CHECK_ARG(a->Lq >= 1 && a->Lk >= 1, "%s: empty sequence", fn);
   FS_CHECK_SUPPORTED(a->D == kD, "%s: head_dim %d unsupported (128 only)", fn, a->D);
-  FS_CHECK_SUPPORTED(a->bs == 32 || a->bs == 64 || a->bs == 128, "%s: block size %d unsupported", fn, a->bs);
+  FS_CHECK_SUPPORTED(a->bs == 16 || a->bs == 32 || a->bs == 64 || a->bs == 128, "%s: block size %d unsupported", fn,
+                     a->bs);
+  // union mode (16- and 32-token lists): block indices and their rows packed in 32-bit entries
+  FS_CHECK_SUPPORTED(!(a->blk_cnt && a->bs < 64) || (a->Lk + a->bs - 1) / a->bs <= 4096,
+                     "%s: %d-token lists over more than 4096 key blocks unsupported", fn, a->bs);
   FS_CHECK_SUPPORTED(a->dtype == FS_DTYPE_BF16 || a->dtype == FS_DTYPE_F16,
                      "%s: dtype %d unsupported (bf16/f16)", fn, a->dtype);
   FS_CHECK_SUPPORTED(a->Hk <= 4096, "%s: %d KV heads > 4096", fn, a->Hk);
@@ -868,9 +1039,18 @@ extern "C" int fs_bsattn_run(const fs_attn_args* a, void* stream) {
     return a->dtype == FS_DTYPE_BF16 ? launch_run<128, 64, bf16_t>(*a, Nq, Nk, s)
                                      : launch_run<128, 64, f16_t>(*a, Nq, Nk, s);
   }
-  if (a->bs == 32) {
-    return a->dtype == FS_DTYPE_BF16 ? launch_run<32, 64, bf16_t>(*a, Nq, Nk, s)
-                                     : launch_run<32, 64, f16_t>(*a, Nq, Nk, s);
+  if (a->bs < 64) {
+    if (a->blk_cnt) {
+      // 16- and 32-token lists: unions over groups of 128 queries
+      if (a->bs == 32)
+        return a->dtype == FS_DTYPE_BF16 ? launch_run_union<32, bf16_t>(*a, s) : launch_run_union<32, f16_t>(*a, s);
+      return a->dtype == FS_DTYPE_BF16 ? launch_run_union<16, bf16_t>(*a, s) : launch_run_union<16, f16_t>(*a, s);
+    }
+    // dense causal attention does not depend on the block size: the 128-token
+    // kernel, reading V^T as it was laid out for this block size
+    const int Nq128 = (a->Lq + 127) / 128, Nk128 = (a->Lk + 127) / 128;
+    return a->dtype == FS_DTYPE_BF16 ? launch_run<128, 64, bf16_t>(*a, Nq128, Nk128, s, vt_len(Nk, a->bs))
+                                     : launch_run<128, 64, f16_t>(*a, Nq128, Nk128, s, vt_len(Nk, a->bs));
   }
   return a->dtype == FS_DTYPE_BF16 ? launch_run<64, 64, bf16_t>(*a, Nq, Nk, s) : launch_run<64, 64, f16_t>(*a, Nq, Nk, s);
 }

@@ -300,7 +300,9 @@ FS_API int fs_flex(const fs_flex_args* a, void* stream);
  * key tokens s of the selected key blocks of query block t / bs (and s <= t +
  * Lk - Lq when is_causal).  blk_cnt == NULL selects every key block up to the
  * causal limit (dense causal attention).  Supported: dtype bf16/f16, D == 128,
- * bs in {32, 64, 128} (32: FlexPrefill's default block size).  All tensors are
+ * bs in {16, 32, 64, 128} (16 and 32: FlexPrefill's block sizes; their lists
+ * are attended 128 queries at a time over the union of 128 / bs rows' lists,
+ * up to 4096 key blocks).  All tensors are
  * strided views with d contiguous.
  * work: fs_bsattn_work_bytes(a) bytes of device scratch (V is staged there
  * transposed, and the work items' longest-first order is computed there,

@@ -341,7 +341,7 @@ def test_attention_running_max_raises(growth):
     ref = v7.dense_causal_attention(q, k, v)[0]
     out = block_sparse_attention(*_gpu(q, k, v), block_size=128, is_causal=True)
     _attn_check(out[0], ref)
-    for bs in (128, 64, 32):
+    for bs in (128, 64, 32, 16):
         N = L // bs
         mask = torch.tril(torch.ones(2, N, N, dtype=torch.bool))
         cnt, idx = lists_from_mask(mask, DEV)
@@ -349,18 +349,21 @@ def test_attention_running_max_raises(growth):
         _attn_check(out[0], ref)
 
 
+@pytest.mark.parametrize("bs", [32, 16])
 @pytest.mark.parametrize("L,Hq,Hk,dtype,density,causal", [
-    (4000, 4, 2, torch.bfloat16, 0.3, True),      # 125 key blocks: a tile's second block missing in odd rows
+    (4000, 4, 2, torch.bfloat16, 0.3, True),      # 125 key blocks at 32 (250 at 16): odd union lengths
     (2048, 2, 1, torch.float16, 0.5, True),
     (1000, 2, 2, torch.bfloat16, 0.4, False),     # non-causal, ragged
+    (3000, 4, 1, torch.bfloat16, 0.05, True),     # sparse rows: union entries selected by one row only
 ])
-def test_attention_32_token_blocks(L, Hq, Hk, dtype, density, causal):
-    """32-token blocks (two listed key blocks per 64-key tile, one per key
-    group) under random block lists of odd and even lengths, against fp32
-    attention under the same mask; and the dense causal path at 32."""
-    _print_case("attention-bs32", L=L, Hq=Hq, Hk=Hk, dtype=dtype, density=density, causal=causal)
+def test_attention_short_blocks(bs, L, Hq, Hk, dtype, density, causal):
+    """16- and 32-token blocks (a workgroup of 128 queries walks the union of
+    its 128 / bs rows' lists, masking per row) under random block lists of odd
+    and even lengths, against fp32 attention under the same mask; and the
+    dense causal path at that block size."""
+    _print_case("attention-short-blocks", bs=bs, L=L, Hq=Hq, Hk=Hk, dtype=dtype, density=density, causal=causal)
     q, k, v = make_qkv(L, Hq, Hk, dtype=dtype, seed=12)
-    N = (L + 31) // 32
+    N = (L + bs - 1) // bs
     g = torch.Generator().manual_seed(13)
     mask = torch.rand(Hq, N, N, generator=g) < density
     mask |= torch.eye(N, dtype=torch.bool)
@@ -369,13 +372,14 @@ def test_attention_32_token_blocks(L, Hq, Hk, dtype, density, causal):
         mask &= torch.ones(N, N, dtype=torch.bool).tril()
     mask[0, 5] = False                          # a row holding only ...
     mask[0, 5, 5] = True                        # ... its diagonal block
+    mask[-1, 9] = False                         # a row with no block at all (output 0)
     cnt, idx = lists_from_mask(mask, DEV)
-    out = block_sparse_attention(*_gpu(q, k, v), cnt, idx, block_size=32, is_causal=causal)
+    out = block_sparse_attention(*_gpu(q, k, v), cnt, idx, block_size=bs, is_causal=causal)
     torch.cuda.synchronize()
-    ref = v7.block_sparse_attention(q, k, v, mask, 32, is_causal=causal)
+    ref = v7.block_sparse_attention(q, k, v, mask, bs, is_causal=causal)
     _attn_check(out[0], ref)
     if causal:
-        out = block_sparse_attention(*_gpu(q, k, v), block_size=32, is_causal=True)
+        out = block_sparse_attention(*_gpu(q, k, v), block_size=bs, is_causal=True)
         _attn_check(out[0], v7.dense_causal_attention(q, k, v)[0])
 
 
@@ -510,7 +514,7 @@ def test_block_count_above_the_limit_is_rejected():
         torch.cuda.synchronize()
 
 
-@pytest.mark.parametrize("bs", [32, 64, 128])
+@pytest.mark.parametrize("bs", [16, 32, 64, 128])
 def test_dense_causal_fewer_queries_than_keys(bs):
     """Dense causal attention with L_q < L_k (bottom-right aligned, as
     flash_attn_func(causal=True) with a key prefix), every block size."""
