@@ -116,11 +116,14 @@ __global__ __launch_bounds__(kFThreads) void flex_lastq_kernel(FlexK a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, hi = lane >> 5;
   constexpr int bs = BS;
   const int L = a.L;
-  constexpr int RG = bs / 32, CG = 4 / RG;        // row groups, column groups
+  // 32-row groups of the last block's queries; 16-token blocks fill half of
+  // one group (rows 16 .. 31 have no query: zero operands, no scores kept)
+  constexpr int RG = bs >= 32 ? bs / 32 : 1, CG = 4 / RG;   // row groups, column groups
   const int rg = wave % RG, cg = wave / RG;
   constexpr int nsub = (kFTile / CG) / 32;        // 32-column sub-tiles per wave: 4 / CG
   const int row = rg * 32 + l32;                  // this lane's query row (0 .. bs-1)
-  const int qtok = L - bs + row;
+  const bool row_ok = row < bs;
+  const int qtok = L - bs + (row_ok ? row : 0);
   const uint16_t* qh = a.q + (int64_t)h * a.q_sh;
   const uint16_t* kh = a.k + (int64_t)kvh * a.k_sh;
 
@@ -128,7 +131,8 @@ __global__ __launch_bounds__(kFThreads) void flex_lastq_kernel(FlexK a) {
   uint4 qf[kFD / 16];
 #pragma unroll
   for (int st = 0; st < kFD / 16; ++st) {
-    const uint4 raw = *reinterpret_cast<const uint4*>(qh + (int64_t)qtok * a.q_sl + st * 16 + hi * 8);
+    const uint4 raw = row_ok ? *reinterpret_cast<const uint4*>(qh + (int64_t)qtok * a.q_sl + st * 16 + hi * 8)
+                             : make_uint4(0, 0, 0, 0);
     const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
     uint32_t o[4];
 #pragma unroll
@@ -185,8 +189,8 @@ __global__ __launch_bounds__(kFThreads) void flex_lastq_kernel(FlexK a) {
     }
     for (int e = tid; e < kFTile + bs; e += kFThreads) carry[e] = 0.f;
     __syncthreads();
-    M2 = rowstat[row * 2];
-    inv_s = rowstat[row * 2 + 1];
+    M2 = row_ok ? rowstat[row * 2] : 0.f;
+    inv_s = row_ok ? rowstat[row * 2 + 1] : 0.f;
   }
 
   for (int t0 = t_first; t0 < c_end; t0 += kFTile) {
@@ -230,7 +234,7 @@ __global__ __launch_bounds__(kFThreads) void flex_lastq_kernel(FlexK a) {
     if (PASS == 2) __syncthreads();                // every wave has read the K tile: the p tile overwrites it
     // every column of the tile valid and causal for every row
     const bool interior = t0 + kFTile <= c_valid && t0 + kFTile - 1 <= L - bs;
-    auto valid = [&](int c) { return interior || (c < c_valid && c <= lim_causal); };
+    auto valid = [&](int c) { return row_ok && (interior || (c < c_valid && c <= lim_causal)); };
     if (PASS == 1) {
       float mx = -INFINITY;
 #pragma unroll
@@ -265,7 +269,7 @@ __global__ __launch_bounds__(kFThreads) void flex_lastq_kernel(FlexK a) {
           v.y = valid(t0 + cl + 1) ? fexp2(x[s][g4 * 4 + 1] - M2) * inv_s : 0.f;
           v.z = valid(t0 + cl + 2) ? fexp2(x[s][g4 * 4 + 2] - M2) * inv_s : 0.f;
           v.w = valid(t0 + cl + 3) ? fexp2(x[s][g4 * 4 + 3] - M2) * inv_s : 0.f;
-          *reinterpret_cast<float4*>(ptl + row * PS + cl) = v;
+          if (row_ok) *reinterpret_cast<float4*>(ptl + row * PS + cl) = v;
         }
       __syncthreads();
       // vertical: each column's rows in two halves (threads tid and tid + kFTile), four running sums each
@@ -1086,7 +1090,8 @@ static int launch_flex(const fs_flex_args& a, hipStream_t s) {
   const unsigned grid = (unsigned)(a.Hq * nchunk);
   const size_t smem1 = (size_t)kFTile * kFD * sizeof(uint16_t);
   const size_t smem2 = ((size_t)flex_tile_floats(a.bs) + kFTile + a.bs + (size_t)a.bs * 2 + kFThreads) * sizeof(float);
-  if (int rc = a.bs == 32    ? launch_lastq<T, 32>(k, grid, smem1, smem2, s)
+  if (int rc = a.bs == 16    ? launch_lastq<T, 16>(k, grid, smem1, smem2, s)
+               : a.bs == 32 ? launch_lastq<T, 32>(k, grid, smem1, smem2, s)
                : a.bs == 64 ? launch_lastq<T, 64>(k, grid, smem1, smem2, s)
                             : launch_lastq<T, 128>(k, grid, smem1, smem2, s))
     return rc;
@@ -1179,8 +1184,8 @@ extern "C" int fs_flex(const fs_flex_args* a, void* stream) {
   FS_CHECK_SUPPORTED(a->dtype == FS_DTYPE_BF16 || a->dtype == FS_DTYPE_F16, "fs_flex: dtype %d unsupported (bf16/f16)",
                      a->dtype);
   FS_CHECK_SUPPORTED(a->D == kFD, "fs_flex: head_dim %d unsupported (128 only)", a->D);
-  FS_CHECK_SUPPORTED(a->bs == 32 || a->bs == 64 || a->bs == 128, "fs_flex: block size %d unsupported (32, 64, 128)",
-                     a->bs);
+  FS_CHECK_SUPPORTED(a->bs == 16 || a->bs == 32 || a->bs == 64 || a->bs == 128,
+                     "fs_flex: block size %d unsupported (16, 32, 64, 128)", a->bs);
   FS_CHECK_ARG(a->L > a->bs, "fs_flex: the sequence must be longer than one block");
   FS_CHECK_ARG(a->min_blocks >= 1 && a->max_blocks >= 1, "fs_flex: bad budgets");
   FS_CHECK_ARG(((uintptr_t)a->q % 16) == 0 && ((uintptr_t)a->k % 16) == 0 && a->q_sl % 8 == 0 && a->k_sl % 8 == 0 &&

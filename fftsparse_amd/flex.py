@@ -101,8 +101,8 @@ def Flexprefill_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gamma
     """Flexprefill.py:1063-1098: q/k/v [B, L, H, D] -> [B, L, H, D].  Sequences
     of at most max(2 bs, ceil(min_budget / bs) bs) tokens take dense causal
     attention (:1084-1085), the others the FlexPrefill selection and the
-    block-sparse attention.  The attention kernel runs blocks of 32, 64 and
-    128; 16-token blocks raise NotImplementedError.  With ``gqa_interleave``
+    block-sparse attention, at 16-, 32-, 64- or 128-token blocks (at most 4096
+    blocks: 65536 tokens at 16, 131072 at 32).  With ``gqa_interleave``
     query head h reads KV head h % Hk in the selection and the sparse attention
     (the dense branch keeps flash_attn_func's grouped heads, as the reference)."""
     assert q.is_cuda, "input tensors must be on the GPU"
@@ -114,8 +114,6 @@ def Flexprefill_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gamma
     qv, kv, vv = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
     if L <= max(2 * block_size, math.ceil(mn / block_size) * block_size):
         return block_sparse_attention(qv, kv, vv, block_size=128, is_causal=True, softmax_scale=softmax_scale)
-    if block_size not in (32, 64, 128):
-        raise NotImplementedError(f"block-sparse attention over {block_size}-token blocks is not built (32, 64, 128)")
     sel = flex_select(q, k, gamma=gamma, tau=tau, min_budget=min_budget, max_budget=max_budget,
                       gqa_interleave=gqa_interleave, block_size=block_size)
     return block_sparse_attention(qv, kv, vv, sel.blk_cnt, sel.blk_idx, block_size=block_size, is_causal=True,

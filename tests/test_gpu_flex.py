@@ -158,6 +158,8 @@ def _check(q, k, *, bs, gamma, tau, min_budget=None, max_budget=None, gqa_interl
     (6000, 4, 1, 64, 0.95, torch.bfloat16, (256, 2048)),        # ragged: L % 64 != 0, token budgets
     (4100, 2, 2, 32, 0.9, torch.float16, (1024, None)),         # ragged, 32-token blocks
     (8192, 8, 8, 64, 0.99, torch.bfloat16, (None, 512)),        # MHA, max budget clamps
+    (4100, 4, 2, 16, 0.9, torch.bfloat16, (None, None)),         # 16-token blocks, ragged
+    (6000, 2, 1, 16, 0.95, torch.float16, (256, 1024)),          # 16-token blocks, token budgets
 ])
 def test_flex_selection_parity(L, Hq, Hk, bs, gamma, dtype, budget):
     _case(L=L, Hq=Hq, Hk=Hk, bs=bs, gamma=gamma, dtype=dtype, budget=budget)
@@ -230,6 +232,25 @@ def test_flex_prefill_reference_call_32_token_blocks():
     assert err.max().item() <= 2e-2 and err.mean().item() <= 1e-3
 
 
+@pytest.mark.parametrize("L,Hq,Hk,tau", [(5000, 4, 2, 0.1), (3000, 2, 2, 0.0)])
+def test_flex_prefill_16_token_blocks(L, Hq, Hk, tau):
+    """16-token blocks (Flexprefill.py:1079 accepts them): the selection at 16,
+    and the attention over the union of each 8 rows' lists, against fp32
+    attention under the kernel's lists."""
+    _case(L=L, prefill=True, bs=16, tau=tau)
+    q, k, v = make_qkv(L, Hq, Hk, dtype=torch.bfloat16, seed=50)
+    ql, kl, vl = _blhd(q, k, v)
+    out = Flexprefill_prefill(ql.to(DEV), kl.to(DEV), vl.to(DEV), gamma=0.9, tau=tau, block_size=16)
+    torch.cuda.synchronize()
+    assert out.shape == (1, L, Hq, 128)
+    sel = flex_select(ql.to(DEV), kl.to(DEV), gamma=0.9, tau=tau, block_size=16)
+    mask = sel.dense_mask().cpu()
+    ref = v7.block_sparse_attention(q, k, v, mask, 16)
+    err = (out[0].float().cpu() - ref).abs()
+    print(f"  density {density(sel):.4f} max_abs={err.max().item():.3e} mean_abs={err.mean().item():.3e}")
+    assert err.max().item() <= 2e-2 and err.mean().item() <= 1e-3
+
+
 def test_flex_prefill_gqa_interleave():
     """gqa_interleave=True: query head h reads KV head h % Hk in the selection
     and the attention.  The reference output is the grouped fp32 attention on
@@ -259,9 +280,9 @@ def test_flex_prefill_gqa_interleave():
     assert (grouped[0].float().cpu() - ref).abs().max().item() > 0.1
 
 
-def test_flex_prefill_short_sequence_is_dense_and_small_blocks_raise():
+def test_flex_prefill_short_sequence_is_dense():
     """L <= max(2 bs, ceil(min_budget / bs) bs) takes dense causal attention
-    (Flexprefill.py:1084-1085); 16-token attention blocks are not built."""
+    (Flexprefill.py:1084-1085)."""
     _case(L=256, dense=True)
     q, k, v = make_qkv(256, 2, 1, dtype=torch.bfloat16, seed=45)
     ql, kl, vl = _blhd(q, k, v)
@@ -271,8 +292,6 @@ def test_flex_prefill_short_sequence_is_dense_and_small_blocks_raise():
     assert err.max().item() <= 2e-2 and err.mean().item() <= 1e-3
     q, k, v = make_qkv(1024, 2, 1, dtype=torch.bfloat16, seed=46)
     ql, kl, vl = _blhd(q, k, v)
-    with pytest.raises(NotImplementedError):
-        Flexprefill_prefill(ql.to(DEV), kl.to(DEV), vl.to(DEV), block_size=16)
     # min_budget of the whole sequence: dense as well
     out = Flexprefill_prefill(ql.to(DEV), kl.to(DEV), vl.to(DEV), block_size=32, min_budget=1024)
     ref = v7.block_sparse_attention(q, k, v, torch.ones(2, 8, 8, dtype=torch.bool), 128)
@@ -356,7 +375,8 @@ def test_flex_full_length_32_token_blocks():
     assert n_sparse > 0
 
 
-@pytest.mark.parametrize("L,bs", [(65, 32), (100, 32), (129, 64), (2049, 32), (2049, 128), (4097, 64)])
+@pytest.mark.parametrize("L,bs", [(65, 32), (100, 32), (129, 64), (2049, 32), (2049, 128), (4097, 64), (33, 16),
+                                  (2049, 16)])
 def test_flex_edge_lengths(L, bs):
     """Few blocks (a single 64-bit word per row), one key past a 2048-column
     chunk, one token past a whole block: exact against the oracle, tau

@@ -58,9 +58,9 @@ def test_bad_shapes_rejected_without_gpu():
     assert lib.fs_xattn(ctypes.byref(x), None) == -2
     x.stride, x.Hk = 8, 3
     assert lib.fs_xattn(ctypes.byref(x), None) == -1
-    f = _lib.FlexArgs(q=16, k=16, blk_cnt=16, blk_idx=16, work=16, dtype=1, Hq=4, Hk=1, L=4096, D=128, bs=16,
+    f = _lib.FlexArgs(q=16, k=16, blk_cnt=16, blk_idx=16, work=16, dtype=1, Hq=4, Hk=1, L=4096, D=128, bs=8,
                       gamma=0.9, tau=0.1, min_blocks=1, max_blocks=64, q_sl=128, k_sl=128, q_sh=128, k_sh=128)
-    assert lib.fs_flex(ctypes.byref(f), None) == -2              # 16-token blocks: not built
+    assert lib.fs_flex(ctypes.byref(f), None) == -2              # the reference asserts 16, 32, 64 or 128
     assert b"block size" in lib.fs_last_error()
     f.bs, f.L = 64, 64                                           # one block: the reference attends densely
     assert lib.fs_flex(ctypes.byref(f), None) == -1
@@ -68,7 +68,7 @@ def test_bad_shapes_rejected_without_gpu():
     assert lib.fs_flex(ctypes.byref(f), None) == -1
     f.Hk, f.q_sl = 1, 100                                        # 200-byte row stride
     assert lib.fs_flex(ctypes.byref(f), None) == -1
-    f.q_sl, f.L, f.bs = 128, 4096 * 32 + 1, 32                   # 4097 blocks
+    f.q_sl, f.L, f.bs = 128, 4096 * 16 + 1, 16                   # 4097 blocks
     assert lib.fs_flex(ctypes.byref(f), None) == -2
     assert lib.fs_flex_work_bytes(4, 1, 4096, 64, 0.1) > 4 * 4096 * 4 * 2
     # tau <= 0 (the reference's default) makes no head sparse: no room for the
