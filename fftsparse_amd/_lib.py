@@ -19,7 +19,7 @@ import torch  # noqa: F401  (must precede the library load, see module docstring
 LIB_PATH = Path(os.environ.get("FFTSPARSE_AMD_LIB") or Path(__file__).resolve().with_name("libfftsparse_amd.so"))
 
 FS_DTYPE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 
 class PoolArgs(ctypes.Structure):
@@ -44,7 +44,9 @@ class XattnArgs(ctypes.Structure):
                 ("k", c_void_p), ("k_sh", c_int64), ("k_sl", c_int64),
                 ("dtype", c_int), ("Hq", c_int), ("Hk", c_int), ("L", c_int), ("D", c_int), ("stride", c_int),
                 ("bs", c_int), ("norm", c_float), ("threshold", c_void_p), ("keep_sink", c_int),
-                ("sums", c_void_p), ("blk_cnt", c_void_p), ("blk_idx", c_void_p), ("work", c_void_p)]
+                ("sums", c_void_p), ("blk_cnt", c_void_p), ("blk_idx", c_void_p), ("work", c_void_p),
+                ("non_causal", c_int), ("torch_path", c_int), ("select_mode", c_int), ("perm", c_int * 16),
+                ("kdb", c_int), ("no_softmax", c_int), ("chunk", c_int), ("keep_recent", c_int)]
 
 
 class FlexArgs(ctypes.Structure):
@@ -146,7 +148,7 @@ def load() -> ctypes.CDLL:
     lib.fs_flex_work_bytes.restype = c_size_t
     lib.fs_flex_work_bytes.argtypes = [c_int, c_int, c_int, c_int, c_float]
     lib.fs_xattn_work_bytes.restype = c_size_t
-    lib.fs_xattn_work_bytes.argtypes = [c_int, c_int, c_int, c_int]
+    lib.fs_xattn_work_bytes.argtypes = [ctypes.POINTER(XattnArgs)]
     lib.fs_bsattn_work_bytes.restype = c_size_t
     lib.fs_bsattn_work_bytes.argtypes = [POINTER(AttnArgs)]
     for name, st in [("fs_pool", PoolArgs), ("fs_rope_pool", RopePoolArgs), ("fs_corr", CorrArgs),

@@ -1,40 +1,52 @@
 // XAttention block selection on gfx950 -- the reference's other selector
 // (attn_src/xattn/src/Xattention.py:14-303 xattn_estimate + :306-406
-// Xattention_prefill; its Triton kernels attn_src/xattn/src/kernels.py:5-97 and
+// Xattention_prefill; its Triton kernels attn_src/xattn/src/kernels.py:5-156 and
 // :195-234; attn_src/xattn/src/utils.py:44-200 find_blocks_chunked), feeding
 // the same block-sparse attention kernel as the FFT selector.
 //
-// Reshaped scores (stride S, "inverse" mode): for reshaped query row r and key
-// n,  A[r][n] = sum_{j<S} q[rS + S-1-j] . k[nS + j]  -- a GEMM with an S*D
-// reduction whose operands are S token rows each; the fp32 result is rounded
-// to the input dtype, as the reference's kernel stores it.  Then, in the exp2
-// domain, x = A * log2(e) / sqrt(D) / S / norm, each real row is normalised
-// over its causal keys n <= r, and the probabilities are summed over
+// Reshaped scores (stride S): for reshaped query row m and key n,
+//   A[m][n] = sum_{j<S} q[m QS + o_j] . k'[nS + j]
+// -- a GEMM with an S*D reduction whose operands are S token rows each; the
+// fp32 result is rounded to the input dtype, as the reference's kernel (and
+// its torch matmul) stores it.  The Triton path the callers use has o_j =
+// S-1-j ("inverse"), QS = S and k' = k.  The torch path (use_triton=False)
+// has o_j = S-1-j (inverse, double, triple), j (slash) or perm[j] (random),
+// QS = S kdb for inverse (else S), and k' = k, or for double / triple the
+// neighbouring-chunk sums of k rounded to dtype (xattn_kaug_kernel).
+//
+// Triton path: in the exp2 domain, x = A log2(e) / sqrt(D) / S / norm, each
+// row is normalised over the keys it sees (causal: n <= m; non-causal: every
+// key of the chunk-padded sequence) and the probabilities are summed over
 // (bs/S) x (bs/S) squares: the block sums, rounded to the input dtype.
+// Torch path: x = A / sqrt(D) / S / norm with each division rounded to dtype,
+// causal rows m see keys n <= m kdb + kdb - 1 (the padding ones too), p is the
+// float32 softmax (or exp) rounded to dtype, and the block sums are two sums
+// rounded to dtype: over a block's keys, then over its rows.
 //
-// xattn_scores_kernel<T>: one workgroup (4 waves, 32 reshaped rows each) per
-// (head, 128 reshaped rows), longest rows first; key tiles of 128 reshaped keys
-// up to the diagonal.  For each tile and each j < S the workgroup copies the
-// 128 query token rows rS + S-1-j and the 128 key token rows nS + j into LDS
-// with global -> LDS copies (no register staging; rows past L zeroed after;
-// 256-byte rows, 16-byte chunk c of row r at c ^ (r & 15)) and accumulates
-// S^T = K' Q'^T with v_mfma_f32_32x32x16.  It keeps each row's
-// running max and exp2 sum (the reference's first loop) and stores the scores,
-// rounded to the input dtype, as the reference's GEMM kernel stores its
-// output: the causal part only, row tile by row tile (tile rt holds its 128
-// rows x 128 (rt + 1) keys, so it starts 16384 rt (rt + 1) / 2 values in).
-// xattn_sums_kernel<T>: one workgroup per (head, 128 reshaped rows) streams
-// the stored scores (threads along the keys, rows in order), forms
-// p = exp2(x - max) / sum and adds it over each block's rows and, by xor
-// shuffles, its keys (the reference's second loop).
+// xattn_scores_kernel<T, TP>: one workgroup (4 waves, 32 reshaped rows each)
+// per (head, 128 reshaped rows), longest rows first; key tiles of 128 reshaped
+// keys up to the last one the tile's rows see.  For each tile and each j < S
+// the workgroup copies the 128 query token rows and the 128 key token rows of
+// stage j into LDS with global -> LDS copies (no register staging; rows past
+// the sequence zeroed after; 256-byte rows, 16-byte chunk c of row r at
+// c ^ (r & 15)) and accumulates S^T = K' Q'^T with v_mfma_f32_32x32x16.  It
+// keeps each row's running max and exp sum (the reference's first loop) and
+// stores the scores, rounded to the input dtype, row tile by row tile (tile rt
+// holds its 128 rows x 128 nct(rt) keys).
+// xattn_sums_kernel<T, TP>: one workgroup per (head, 128 reshaped rows)
+// streams the stored scores (threads along the keys, rows in order), forms p
+// and adds it over each block's rows and, by xor shuffles, its keys (the
+// reference's second loop).  Non-causal: the keys of the chunk padding past
+// the last block score 0; their mass per block row is formed in closed form.
 //
-// xattn_select_kernel: one workgroup per (head, block row I): the causal
-// block sums of the row, the forced first and diagonal blocks, the others in
-// decreasing order (ties: lower index first) by a bitonic sort in LDS, their
-// exclusive prefix masses in fp64, and each other block kept iff
-// forced mass + prefix < row total * threshold.  Output: ascending per-row
-// block lists (the causal tril; keep_sink fills row 0, keep_recent the
-// diagonal).
+// xattn_select_kernel: one workgroup per (head, block row I), in float64.
+// Causal: the causal block sums of the row, the forced first and diagonal
+// blocks, the others in decreasing order (ties: lower index first) by a
+// bitonic sort in LDS, their exclusive prefix masses, and each other block
+// kept iff forced mass + prefix < row total * threshold.  Non-causal: every
+// block of the chunk-padded row sorted, none forced, and block 0 always kept.
+// Output: ascending per-row block lists of the N real blocks (keep_sink fills
+// row 0, keep_recent the diagonal).
 #include "common.h"
 
 namespace fs {
@@ -74,30 +86,63 @@ template <> struct XMma<f16_t> {
 
 struct XScoreK {
   const uint16_t* q;
-  const uint16_t* k;
+  const uint16_t* k;            // k, or the K' buffer (double / triple)
   int64_t q_sh, q_sl, k_sh, k_sl;
-  int Hq, Hk, L, S, Lr, real, rbs, Nb;
-  float scale;                  // log2(e) / sqrt(D) / S / norm
-  float* m;                     // [Hq][Lr] row max (exp2 domain)
-  float* l;                     // [Hq][Lr] row sum
-  float* sums;                  // [Hq][Nb][Nb] block sums (values of T), causal part
-  uint16_t* scores;             // [Hq][head_stride] the rounded scores, causal row tiles
+  int Hq, Hk, S, QS, Lq_tok, Lk_tok;
+  uint64_t qorder;              // 4 bits per stage j: o_j
+  int Lrq, Lrk, rbs, rpb, Nb;   // query rows, keys, keys per block, query rows per block, blocks
+  int causal, kdb, own_chunk;
+  int real_rows, npad, softmax;
+  float scale;                  // Triton path: log2(e) / sqrt(D) / S / norm
+  float inv_sqrt, inv_S, inv_norm;   // torch path: float32 reciprocals of the divisors
+  float* m;                     // [Hq][Lrq] row max (exp2 domain on the Triton path)
+  float* l;                     // [Hq][Lrq] row sum
+  float* sums;                  // [Hq][Nb][Nb] block sums (values of T)
+  float* pad_sum;               // [Hq][Nb] non-causal: the sum of every key block of the chunk padding
+  uint16_t* scores;             // [Hq][head_stride] the rounded scores, row tiles
   int64_t head_stride;
 };
 
+__host__ __device__ inline int ximin(int a, int b) { return a < b ? a : b; }
+// key tiles of row tile rt: up to the last key its rows see
+__host__ __device__ inline int xnct(int rt, int Lrq, int Lrk, int causal, int kdb) {
+  const int last_row = ximin(Lrq, (rt + 1) * kXRows) - 1;
+  int last_key = Lrk - 1;
+  if (causal) last_key = ximin(last_key, last_row * kdb + kdb - 1);
+  return last_key < 0 ? 1 : last_key / kXKeys + 1;
+}
 // first stored score of row tile rt (every earlier tile is whole)
-__host__ __device__ inline int64_t xtile_offset(int rt) { return (int64_t)kXRows * 128 * rt * (rt + 1) / 2; }
-// keys stored per row of tile rt: its key tiles up to the diagonal
-__host__ __device__ inline int xtile_keys(int rt, int Lr) {
-  const int last_row = (rt + 1) * kXRows < Lr ? (rt + 1) * kXRows - 1 : Lr - 1;
-  return (last_row / kXKeys + 1) * kXKeys;
+__host__ __device__ inline int64_t xoffset(int rt, int Lrq, int Lrk, int causal, int kdb) {
+  int64_t o = 0;
+  for (int t = 0; t < rt; ++t) o += (int64_t)kXRows * kXKeys * xnct(t, Lrq, Lrk, causal, kdb);
+  return o;
 }
 
-template <typename T>
+// whether row sees key (the keys past Lrk -- chunk padding -- are formed in closed form)
+__device__ __forceinline__ bool xkey_ok(const XScoreK& a, int row, int key) {
+  if (key >= a.Lrk) return false;
+  if (!a.causal) return true;
+  if (key > row * a.kdb + a.kdb - 1) return false;
+  return a.own_chunk == 0 || key >= (row * a.kdb / a.own_chunk) * a.own_chunk;
+}
+// the score in the softmax's domain from the fp32 accumulator (or a stored value)
+template <typename T, bool TP>
+__device__ __forceinline__ float xscaled(const XScoreK& a, float acc) {
+  const float r = Conv<T>::round(acc);
+  if constexpr (!TP) return r * a.scale;
+  return Conv<T>::round(Conv<T>::round(Conv<T>::round(r * a.inv_sqrt) * a.inv_S) * a.inv_norm);
+}
+template <bool TP>
+__device__ __forceinline__ float xexp(float x) {
+  if constexpr (TP) return expf(x);
+  return __builtin_amdgcn_exp2f(x);
+}
+
+template <typename T, bool TP>
 __global__ __launch_bounds__(kXThreads) void xattn_scores_kernel(XScoreK a) {
   __shared__ __attribute__((aligned(16))) uint16_t lq[kXRows * kXD];   // Q'_j rows, 32 KiB
   __shared__ __attribute__((aligned(16))) uint16_t lk[kXKeys * kXD];   // K'_j rows
-  const int nrt = (a.Lr + kXRows - 1) / kXRows;
+  const int nrt = (a.Lrq + kXRows - 1) / kXRows;
   const int rt = nrt - 1 - (int)(blockIdx.x / a.Hq);                 // longest rows first
   const int h = (int)(blockIdx.x % a.Hq);
   const int hk = h / (a.Hq / a.Hk);
@@ -106,10 +151,10 @@ __global__ __launch_bounds__(kXThreads) void xattn_scores_kernel(XScoreK a) {
   const int row = r0 + wave * 32 + l32;            // this lane's reshaped row (column of S^T)
   const uint16_t* qh = a.q + (int64_t)h * a.q_sh;
   const uint16_t* kh = a.k + (int64_t)hk * a.k_sh;
-  const int S = a.S;
-  const int last_row = min(a.Lr, r0 + kXRows) - 1;
-  const int nct = last_row / kXKeys + 1;           // key tiles up to the diagonal
-  const bool row_ok = row < a.Lr;
+  const int S = a.S, QS = a.QS;
+  const int nct = xnct(rt, a.Lrq, a.Lrk, a.causal, a.kdb);
+  const bool row_ok = row < a.Lrq;
+  const bool stats = !TP || a.softmax;
 
   float m_run = -INFINITY, l_run = 0.f;
 
@@ -121,10 +166,11 @@ __global__ __launch_bounds__(kXThreads) void xattn_scores_kernel(XScoreK a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[kk][r] = 0.f;
     for (int j = 0; j < S; ++j) {
+      const int oj = (int)((a.qorder >> (4 * j)) & 15);
       __syncthreads();                             // previous stage consumed
       // 1 KiB regions of 4 LDS rows: lane l fills slot l % 16 of row 4R + l / 16
-      // with the token row's chunk (l % 16) ^ (row & 15); rows past L read row
-      // L-1 here and are zeroed below
+      // with the token row's chunk (l % 16) ^ (row & 15); rows past the
+      // sequence read its last row here and are zeroed below
       const uint32_t lq0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lq);
       const uint32_t lk0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lk);
       const int wv = __builtin_amdgcn_readfirstlane(wave);   // wave-uniform: the copies' LDS bases
@@ -132,26 +178,26 @@ __global__ __launch_bounds__(kXThreads) void xattn_scores_kernel(XScoreK a) {
 #pragma unroll
       for (int i = 0; i < QR; ++i) {
         const int R = wv * QR + i, rr = 4 * R + (lane >> 4), c = (lane & 15) ^ (rr & 15);
-        const int t = min((r0 + rr) * S + S - 1 - j, a.L - 1);
+        const int t = min((r0 + rr) * QS + oj, a.Lq_tok - 1);
         xdma16(lq0 + R * 1024, qh, (uint32_t)(t * a.q_sl + c * 8) * 2u);
       }
 #pragma unroll
       for (int i = 0; i < KR; ++i) {
         const int R = wv * KR + i, cr = 4 * R + (lane >> 4), c = (lane & 15) ^ (cr & 15);
-        const int t = min((n0 + cr) * S + j, a.L - 1);
+        const int t = min((n0 + cr) * S + j, a.Lk_tok - 1);
         xdma16(lk0 + R * 1024, kh, (uint32_t)(t * a.k_sl + c * 8) * 2u);
       }
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
-      if ((r0 + kXRows - 1) * S + S - 1 - j >= a.L || (n0 + kXKeys - 1) * S + j >= a.L) {
-        // this stage reaches past L: those rows are zero
+      if ((r0 + kXRows - 1) * QS + oj >= a.Lq_tok || (n0 + kXKeys - 1) * S + j >= a.Lk_tok) {
+        // this stage reaches past the sequence: those rows are zero
         for (int e = tid; e < (kXRows + kXKeys) * 16; e += kXThreads) {
           const int r = e >> 4, ch = e & 15;
           if (r < kXRows) {
-            if ((r0 + r) * S + S - 1 - j >= a.L) *reinterpret_cast<uint4*>(lq + r * kXD + ch * 8) = make_uint4(0, 0, 0, 0);
+            if ((r0 + r) * QS + oj >= a.Lq_tok) *reinterpret_cast<uint4*>(lq + r * kXD + ch * 8) = make_uint4(0, 0, 0, 0);
           } else {
             const int cr = r - kXRows;
-            if ((n0 + cr) * S + j >= a.L) *reinterpret_cast<uint4*>(lk + cr * kXD + ch * 8) = make_uint4(0, 0, 0, 0);
+            if ((n0 + cr) * S + j >= a.Lk_tok) *reinterpret_cast<uint4*>(lk + cr * kXD + ch * 8) = make_uint4(0, 0, 0, 0);
           }
         }
         __syncthreads();
@@ -170,15 +216,16 @@ __global__ __launch_bounds__(kXThreads) void xattn_scores_kernel(XScoreK a) {
       }
     }
 
-    // ---- epilogue: lane holds keys n0 + 32 kk + (r/4) 8 + hi 4 + r%4 of its row
-    // a key of this lane's row is causal; its score in the exp2 domain, from the
-    // accumulator (recomputed where used, so no tile-sized arrays stay live)
-    auto valid = [&](int kk, int r) { return row_ok && n0 + kk * 32 + (r >> 2) * 8 + hi * 4 + (r & 3) <= row; };
-    auto xval = [&](int kk, int r) { return Conv<T>::round(acc[kk][r]) * a.scale; };
+    // ---- epilogue: lane holds keys n0 + 32 kk + (r/4) 8 + hi 4 + r%4 of its row;
+    // whether the row sees a key and its scaled score are recomputed from the
+    // accumulator where used, so no tile-sized arrays stay live
+    auto valid = [&](int kk, int r) { return row_ok && xkey_ok(a, row, n0 + kk * 32 + (r >> 2) * 8 + hi * 4 + (r & 3)); };
+    auto xval = [&](int kk, int r) { return xscaled<T, TP>(a, acc[kk][r]); };
     if (row_ok) {
       // the rounded scores of this lane's row: four consecutive keys per 8-byte store
-      const int NK = xtile_keys(rt, a.Lr);
-      uint16_t* dst = a.scores + (int64_t)h * a.head_stride + xtile_offset(rt) + (int64_t)(row - r0) * NK;
+      const int NK = nct * kXKeys;
+      uint16_t* dst = a.scores + (int64_t)h * a.head_stride + xoffset(rt, a.Lrq, a.Lrk, a.causal, a.kdb) +
+                      (int64_t)(row - r0) * NK;
 #pragma unroll
       for (int kk = 0; kk < kXKK; ++kk)
 #pragma unroll
@@ -191,7 +238,7 @@ __global__ __launch_bounds__(kXThreads) void xattn_scores_kernel(XScoreK a) {
           *reinterpret_cast<uint2*>(dst + n0 + kk * 32 + g * 8 + hi * 4) = make_uint2(w[0], w[1]);
         }
     }
-    {
+    if (stats) {
       float mx = -INFINITY;
 #pragma unroll
       for (int kk = 0; kk < kXKK; ++kk)
@@ -206,74 +253,152 @@ __global__ __launch_bounds__(kXThreads) void xattn_scores_kernel(XScoreK a) {
         for (int kk = 0; kk < kXKK; ++kk)
 #pragma unroll
           for (int r = 0; r < 16; ++r)
-            if (valid(kk, r)) s += __builtin_amdgcn_exp2f(xval(kk, r) - m_new);
-        l_run = l_run * __builtin_amdgcn_exp2f(m_run - m_new) + s;
+            if (valid(kk, r)) s += xexp<TP>(xval(kk, r) - m_new);
+        l_run = l_run * xexp<TP>(m_run - m_new) + s;
         m_run = m_new;
       }
     }
   }
-  const float lt = l_run + __shfl_xor(l_run, 32, 64);
+  float lt = l_run + __shfl_xor(l_run, 32, 64);
+  if (stats && a.npad > 0) {
+    // the chunk padding's keys (zero rows of K) score 0
+    const float m2 = fmaxf(m_run, 0.f);
+    lt = lt * xexp<TP>(m_run - m2) + (float)a.npad * xexp<TP>(-m2);
+    m_run = m2;
+  }
+  if (!stats) {
+    m_run = 0.f;
+    lt = 1.f;
+  }
   if (row_ok && hi == 0) {
-    a.m[(int64_t)h * a.Lr + row] = m_run;
-    a.l[(int64_t)h * a.Lr + row] = lt;
+    a.m[(int64_t)h * a.Lrq + row] = m_run;
+    a.l[(int64_t)h * a.Lrq + row] = lt;
   }
 }
 
 // pass 2 over the stored scores
-template <typename T>
+template <typename T, bool TP>
 __global__ __launch_bounds__(kXThreads) void xattn_sums_kernel(XScoreK a) {
-  __shared__ float rm[kXRows], rinv[kXRows];
-  const int nrt = (a.Lr + kXRows - 1) / kXRows;
+  __shared__ float rm[kXRows], rl[kXRows];
+  __shared__ int rok[kXRows];
+  const int nrt = (a.Lrq + kXRows - 1) / kXRows;
   const int rt = nrt - 1 - (int)(blockIdx.x / a.Hq);
   const int h = (int)(blockIdx.x % a.Hq);
   const int r0 = rt * kXRows;
-  const int nr = min(a.Lr, r0 + kXRows) - r0;       // a multiple of rbs
-  const int NK = xtile_keys(rt, a.Lr);
-  const int tid = threadIdx.x, rbs = a.rbs;
+  const int nr = min(a.Lrq, r0 + kXRows) - r0;       // a multiple of rpb
+  const int NK = xnct(rt, a.Lrq, a.Lrk, a.causal, a.kdb) * kXKeys;
+  const int tid = threadIdx.x, rbs = a.rbs, rpb = a.rpb;
   if (tid < kXRows) {
     const int row = r0 + tid;
-    const bool real = row < a.real;                  // padding rows add nothing
-    rm[tid] = row < a.Lr ? a.m[(int64_t)h * a.Lr + row] : 0.f;
-    rinv[tid] = real ? 1.0f / a.l[(int64_t)h * a.Lr + row] : 0.f;
+    const bool ok = row < a.Lrq && row < a.real_rows;   // padding rows add nothing
+    const float lv = ok ? a.l[(int64_t)h * a.Lrq + row] : 0.f;
+    rok[tid] = ok && lv > 0.f;
+    rm[tid] = ok ? a.m[(int64_t)h * a.Lrq + row] : 0.f;
+    rl[tid] = TP ? lv : (lv > 0.f ? 1.0f / lv : 0.f);   // torch path divides, Triton multiplies by 1 / l
   }
   __syncthreads();
-  const uint16_t* src = a.scores + (int64_t)h * a.head_stride + xtile_offset(rt);
+  // p of a key with scaled score x in row i: rounded to dtype on the torch path
+  auto prob = [&](int i, float x) -> float {
+    if constexpr (TP) {
+      if (!a.softmax) return Conv<T>::round(expf(x));
+      return Conv<T>::round(expf(x - rm[i]) / rl[i]);
+    }
+    return __builtin_amdgcn_exp2f(x - rm[i]) * rl[i];
+  };
+  const uint16_t* src = a.scores + (int64_t)h * a.head_stride + xoffset(rt, a.Lrq, a.Lrk, a.causal, a.kdb);
   // eight consecutive keys per thread (one 16-byte load a row): a key block of
   // rbs >= 8 keys spans rbs / 8 neighbouring lanes
   const int gl = rbs / 8;
   for (int c0 = 0; c0 < NK; c0 += 8 * kXThreads) {
     const int n = c0 + 8 * tid;
-    const bool key_ok = n < NK;                      // NK and n are multiples of 8
+    const bool key_in = n < NK;                      // NK and n are multiples of 8
     float acc = 0.f;
     for (int i = 0; i < nr; ++i) {
       const int row = r0 + i;
-      if (key_ok && n <= row && rinv[i] > 0.f) {
+      float v = 0.f;
+      // a row's visible keys start and end on multiples of 8 from below (chunk
+      // starts are multiples of bs / S >= 8), so n decides whether any is seen
+      if (key_in && rok[i] && xkey_ok(a, row, n)) {
         const uint4 w = *reinterpret_cast<const uint4*>(src + (int64_t)i * NK + n);
         const uint32_t pr[4] = {w.x, w.y, w.z, w.w};
-        const float mi = rm[i], li = rinv[i];
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
           const uint16_t e = (uint16_t)((t & 1) ? (pr[t >> 1] >> 16) : (pr[t >> 1] & 0xffffu));
-          if (n + t <= row) acc += __builtin_amdgcn_exp2f(to_f32(T{e}) * a.scale - mi) * li;
+          if (xkey_ok(a, row, n + t)) v += prob(i, xscaled<T, TP>(a, to_f32(T{e})));
         }
       }
-      if ((i + 1) % rbs == 0) {                      // the end of a block row: add over the block's keys
-        float v = acc;
+      if constexpr (TP) {
+        // the row's sum over the block's keys, rounded to dtype
         for (int o = 1; o < gl; o <<= 1) v += __shfl_xor(v, o, 64);
-        const int I = row / rbs, J = n / rbs;
-        if (key_ok && (tid % gl) == 0 && J <= I && I < a.Nb) a.sums[((int64_t)h * a.Nb + I) * a.Nb + J] = Conv<T>::round(v);
+        acc += Conv<T>::round(v);
+      } else {
+        acc += v;
+      }
+      if ((i + 1) % rpb == 0) {                      // the end of a block row
+        float tot = acc;
+        if constexpr (!TP) for (int o = 1; o < gl; o <<= 1) tot += __shfl_xor(tot, o, 64);
+        const int I = row / rpb, J = n / rbs;
+        if (key_in && (tid % gl) == 0 && I < a.Nb && J < a.Nb && (!a.causal || J <= I))
+          a.sums[((int64_t)h * a.Nb + I) * a.Nb + J] = Conv<T>::round(tot);
         acc = 0.f;
       }
     }
   }
+  if (a.npad > 0 && tid < nr / rpb) {
+    // non-causal: each key block of the chunk padding holds rbs keys scoring 0
+    float acc = 0.f;
+    for (int i = tid * rpb; i < (tid + 1) * rpb; ++i) {
+      if (!rok[i]) continue;
+      if constexpr (TP) acc += Conv<T>::round((float)rbs * prob(i, 0.f));
+      else acc += (float)rbs * prob(i, 0.f);
+    }
+    const int I = (r0 + tid * rpb) / rpb;
+    if (I < a.Nb) a.pad_sum[(int64_t)h * a.Nb + I] = Conv<T>::round(acc);
+  }
+}
+
+// torch path, double / triple: K' [Hk][Lp][D] with token nS + j holding
+// round(k[nS+j] + k[nS+(j+1)%S]) (double), then round(K'_j + K'_{(j-1)%S}) (triple)
+template <typename T>
+__global__ __launch_bounds__(256) void xattn_kaug_kernel(const uint16_t* __restrict__ k, int64_t k_sh, int64_t k_sl,
+                                                         int Hk, int L, int Lp, int S, int triple,
+                                                         uint16_t* __restrict__ out) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;   // (hk, token, 8-dim chunk)
+  if (idx >= (int64_t)Hk * Lp * (kXD / 8)) return;
+  const int c = (int)(idx % (kXD / 8));
+  const int64_t ht = idx / (kXD / 8);
+  const int t = (int)(ht % Lp), hk = (int)(ht / Lp);
+  const int n = t / S, j = t - n * S;
+  const uint16_t* kh = k + (int64_t)hk * k_sh;
+  float r[3][8];                                   // chunks j-1, j, j+1 (mod S)
+#pragma unroll
+  for (int d = 0; d < 3; ++d) {
+    const int tt = n * S + (j + d - 1 + S) % S;
+    uint4 w = make_uint4(0, 0, 0, 0);
+    if (tt < L) w = *reinterpret_cast<const uint4*>(kh + (int64_t)tt * k_sl + c * 8);
+    const uint32_t pr[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[d][e] = to_f32(T{(uint16_t)((e & 1) ? (pr[e >> 1] >> 16) : (pr[e >> 1] & 0xffffu))});
+  }
+  uint32_t o[4];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float v = Conv<T>::round(r[1][e] + r[2][e]);                         // chunk j of the doubled key
+    if (triple) v = Conv<T>::round(v + Conv<T>::round(r[0][e] + r[1][e]));   // + its chunk j-1
+    const uint16_t b = __builtin_bit_cast(uint16_t, Conv<T>::store(v));
+    if (e & 1) o[e >> 1] |= (uint32_t)b << 16;
+    else o[e >> 1] = b;
+  }
+  *reinterpret_cast<uint4*>(out + ((int64_t)hk * Lp + t) * kXD + c * 8) = make_uint4(o[0], o[1], o[2], o[3]);
 }
 
 struct XSelK {
   const float* sums;            // [Hq][Nb][Nb]
+  const float* pad_sum;         // [Hq][Nb] (non-causal)
   const double* thr;            // [Hq]
   int32_t* blk_cnt;             // [Hq][N]
   uint16_t* blk_idx;            // [Hq][N][Nk]
-  int Hq, Nb, N, Nk, keep_sink;
+  int Hq, Nb, N, Nk, Nbp, causal, keep_sink, keep_recent;
 };
 
 __global__ __launch_bounds__(kXSelThreads) void xattn_select_kernel(XSelK a) {
@@ -283,19 +408,21 @@ __global__ __launch_bounds__(kXSelThreads) void xattn_select_kernel(XSelK a) {
   const int h = (int)(blockIdx.x / a.N), I = (int)(blockIdx.x % a.N);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const float* row = a.sums + ((int64_t)h * a.Nb + I) * a.Nb;
-  const int n = I + 1;                              // causal blocks of the row
+  const int n = a.causal ? I + 1 : a.Nbp;           // blocks of the row
+  const float vpad = a.causal ? 0.f : a.pad_sum[(int64_t)h * a.Nb + I];
+  auto val = [&](int J) { return J < a.Nb ? row[J] : vpad; };
   int P = 1;
   while (P < n) P <<= 1;
 
-  // keys (the forced blocks enter the sorted list as zeros, as the
+  // keys (causal: the forced blocks enter the sorted list as zeros, as the
   // reference's masked_fill does) and the row total in a fixed order
   double tot = 0.0;
   for (int J = tid; J < P; J += kXSelThreads) {
     uint64_t kk = ~0ull;
     if (J < n) {
-      const float v = row[J];
+      const float v = val(J);
       tot += (double)v;
-      const float vo = (J == 0 || J == I) ? 0.f : v;
+      const float vo = (a.causal && (J == 0 || J == I)) ? 0.f : v;
       kk = ((uint64_t)(~__float_as_uint(vo)) << 32) | (uint32_t)J;
     }
     key[J] = kk;
@@ -308,7 +435,7 @@ __global__ __launch_bounds__(kXSelThreads) void xattn_select_kernel(XSelK a) {
     __syncthreads();
   }
   const double total = part[0];
-  const double forced = (double)row[0] + (I > 0 ? (double)row[I] : 0.0);
+  const double forced = a.causal ? (double)row[0] + (I > 0 ? (double)row[I] : 0.0) : 0.0;
   const double required = total * a.thr[h];
   __syncthreads();
 
@@ -357,15 +484,18 @@ __global__ __launch_bounds__(kXSelThreads) void xattn_select_kernel(XSelK a) {
   }
   __syncthreads();
 
-  // ascending list: forced blocks, chosen blocks, the causal tril; keep_sink fills row 0
+  // ascending list of the real blocks: the chosen ones, the forced ones (causal),
+  // block 0 (non-causal: the reference's unselected positions scatter to it),
+  // row 0 whole with keep_sink, the diagonal with keep_recent
   if (wave == 0) {
-    const int limit = (I == 0 && a.keep_sink) ? a.Nk : n;
+    const int limit = (I == 0 && a.keep_sink) || !a.causal ? a.Nk : n;
     uint16_t* out = a.blk_idx + ((int64_t)h * a.N + I) * a.Nk;
     int cnt = 0;
     for (int J0 = 0; J0 < limit; J0 += 64) {
       const int J = J0 + lane;
       bool in = false;
-      if (J < limit) in = J >= n || J == 0 || J == I || sel[J];
+      if (J < limit)
+        in = (I == 0 && a.keep_sink) || J == 0 || sel[J] || (a.causal && J == I) || (a.keep_recent && J == I);
       const uint64_t m = __ballot(in);
       if (in) out[cnt + rank_below(m)] = (uint16_t)J;
       cnt += __popcll(m);
@@ -374,34 +504,76 @@ __global__ __launch_bounds__(kXSelThreads) void xattn_select_kernel(XSelK a) {
   }
 }
 
-// stored scores per head: every row tile's rows x keys up to its diagonal
-static int64_t xattn_head_stride(int Lr) {
-  const int nrt = (Lr + kXRows - 1) / kXRows;
-  return xtile_offset(nrt - 1) + (int64_t)kXRows * xtile_keys(nrt - 1, Lr);
+// Geometry of one call (host)
+struct XGeom {
+  int N, S, rbs, kdb, QS, Lrq, Lrk, Lp_blk, Lpc, Nbp, real_rows, own_chunk, npad, causal, aug;
+  uint64_t qorder;
+  int64_t head_stride;
+};
+
+static int xgeom(const fs_xattn_args* a, XGeom& g) {
+  g.N = (a->L + a->bs - 1) / a->bs;
+  g.S = a->stride;
+  g.rbs = a->bs / a->stride;
+  g.kdb = a->torch_path && a->kdb > 1 ? a->kdb : 1;
+  g.causal = a->non_causal ? 0 : 1;
+  const bool inverse = !a->torch_path || a->select_mode == 0;
+  g.QS = inverse ? g.S * g.kdb : g.S;
+  g.aug = a->torch_path && (a->select_mode == 3 || a->select_mode == 4) ? a->select_mode - 2 : 0;
+  g.qorder = 0;
+  for (int j = 0; j < g.S; ++j) {
+    int o = g.S - 1 - j;                                           // inverse, double, triple
+    if (a->torch_path && a->select_mode == 1) o = j;               // slash
+    if (a->torch_path && a->select_mode == 2) o = a->perm[j];      // random
+    g.qorder |= (uint64_t)o << (4 * j);
+  }
+  g.Lp_blk = g.N * a->bs;
+  const int chunk = a->chunk > 0 ? a->chunk : g.Lp_blk;
+  g.Lpc = (int)(((int64_t)a->L + chunk - 1) / chunk * chunk);
+  g.Nbp = g.Lpc / a->bs;
+  g.Lrk = g.N * g.rbs;
+  g.Lrq = g.Lrk / g.kdb;
+  g.npad = g.causal ? 0 : g.Lpc / g.S - g.Lrk;
+  const int k_pad_r = (g.Lpc - a->L) / g.S;                       // k_num_to_pad // stride
+  if (a->torch_path) {
+    // rows zeroed at the end (Xattention.py:248-249): the last q_pad_r // kdb of
+    // the Lpc / (S kdb); when that is 0 with some padding, [-0:] zeroes the last chunk
+    int z = k_pad_r / g.kdb;
+    if (z == 0 && k_pad_r != 0) z = chunk / g.S / g.kdb;
+    g.real_rows = g.Lpc / (g.S * g.kdb) - z;
+    // the padding key columns' marks (Xattention.py:205) lie in the last chunk,
+    // whose own square (:206-217) is written over them: a row of that chunk sees
+    // a padding key at or before its mask row; with no padding the slice [-0:]
+    // marks every column first and only the row's own chunk is cleared again
+    g.own_chunk = (g.causal && k_pad_r == 0) ? chunk / g.S : 0;
+  } else {
+    g.real_rows = (a->L + g.S - 1) / g.S;
+    g.own_chunk = 0;
+  }
+  const int nrt = (g.Lrq + kXRows - 1) / kXRows;
+  g.head_stride = xoffset(nrt, g.Lrq, g.Lrk, g.causal, g.kdb);
+  return 0;
 }
 
-// workspace: row max and sum [Hq][Lr] each, then the stored scores
-static size_t xattn_stats_bytes(int Hq, int Lr) { return ((size_t)Hq * Lr * 2 * sizeof(float) + 255) & ~(size_t)255; }
-
-static size_t xattn_work(int Hq, int L, int stride, int bs) {
-  const int64_t Lp = ((int64_t)L + bs - 1) / bs * bs;
-  const int Lr = (int)(Lp / stride);
-  return xattn_stats_bytes(Hq, Lr) + (size_t)Hq * xattn_head_stride(Lr) * sizeof(uint16_t);
+// workspace: row max and sum [Hq][Lrq] each, pad sums [Hq][N], K' [Hk][Lp][D] (double / triple), the stored scores
+static size_t xalign(size_t n) { return (n + 255) & ~(size_t)255; }
+static size_t xattn_stats_bytes(int Hq, const XGeom& g) {
+  return xalign((size_t)Hq * g.Lrq * 2 * sizeof(float) + (size_t)Hq * g.N * sizeof(float));
+}
+static size_t xattn_kaug_bytes(int Hk, const XGeom& g) { return g.aug ? xalign((size_t)Hk * g.Lp_blk * kXD * 2) : 0; }
+static size_t xattn_work(const fs_xattn_args* a, const XGeom& g) {
+  return xattn_stats_bytes(a->Hq, g) + xattn_kaug_bytes(a->Hk, g) + (size_t)a->Hq * g.head_stride * sizeof(uint16_t);
 }
 
 }  // namespace fs
 
 using namespace fs;
 
-extern "C" size_t fs_xattn_work_bytes(int Hq, int L, int stride, int bs) {
-  if (Hq <= 0 || L <= 0 || stride <= 0 || bs <= 0) return 0;
-  return xattn_work(Hq, L, stride, bs);
-}
-
-extern "C" int fs_xattn(const fs_xattn_args* a, void* stream) {
+static int xattn_check(const fs_xattn_args* a, bool need_buffers) {
   FS_CHECK_ARG(a != nullptr, "fs_xattn: null args");
-  FS_CHECK_ARG(a->q && a->k && a->threshold && a->sums && a->blk_cnt && a->blk_idx && a->work,
-               "fs_xattn: null pointer");
+  if (need_buffers)
+    FS_CHECK_ARG(a->q && a->k && a->threshold && a->sums && a->blk_cnt && a->blk_idx && a->work,
+                 "fs_xattn: null pointer");
   FS_CHECK_ARG(a->Hq > 0 && a->Hk > 0 && a->Hq % a->Hk == 0, "fs_xattn: Hq=%d must be a multiple of Hk=%d", a->Hq,
                a->Hk);
   FS_CHECK_ARG(a->L > 0, "fs_xattn: empty sequence");
@@ -413,45 +585,117 @@ extern "C" int fs_xattn(const fs_xattn_args* a, void* stream) {
   FS_CHECK_SUPPORTED(a->stride == 4 || a->stride == 8 || a->stride == 16, "fs_xattn: stride %d unsupported (4, 8, 16)",
                      a->stride);
   FS_CHECK_ARG(a->norm > 0.f, "fs_xattn: norm must be positive");
+  FS_CHECK_ARG(a->select_mode >= 0 && a->select_mode <= 4, "fs_xattn: select_mode %d unknown", a->select_mode);
+  if (a->torch_path && a->select_mode == 2) {
+    unsigned seen = 0;
+    for (int j = 0; j < a->stride; ++j) {
+      FS_CHECK_ARG(a->perm[j] >= 0 && a->perm[j] < a->stride && !(seen >> a->perm[j] & 1u),
+                   "fs_xattn: perm is not a permutation of 0..%d", a->stride - 1);
+      seen |= 1u << a->perm[j];
+    }
+  }
+  const int kdb = a->kdb > 1 ? a->kdb : 1;
+  FS_CHECK_ARG(a->torch_path || kdb == 1, "use_triton and kdb cannot be used together");   // Xattention.py:144
+  FS_CHECK_ARG(a->chunk >= 0 && (a->chunk == 0 || (a->chunk % a->bs == 0 && (a->chunk / a->stride) % kdb == 0)),
+               "fs_xattn: chunk %d must be a multiple of the block size and of stride x kdb", a->chunk);
+  FS_CHECK_ARG((a->bs / a->stride) % kdb == 0, "fs_xattn: kdb %d must divide the reshaped block size %d", kdb,
+               a->bs / a->stride);
+  FS_CHECK_ARG(!(a->non_causal || a->torch_path) || a->chunk > 0,
+               "fs_xattn: the non-causal and torch paths need the chunk size");
+  const int N = (a->L + a->bs - 1) / a->bs;
+  FS_CHECK_SUPPORTED(N <= kXMaxBlocks, "fs_xattn: %d blocks > %d", N, kXMaxBlocks);
+  XGeom g;
+  xgeom(a, g);
+  FS_CHECK_SUPPORTED(g.Nbp <= kXMaxBlocks, "fs_xattn: %d chunk-padded blocks > %d", g.Nbp, kXMaxBlocks);
+  // the tile copies address a token row by a 32-bit byte offset from the head's base
+  FS_CHECK_SUPPORTED((int64_t)g.Lpc * (a->q_sl > a->k_sl ? a->q_sl : a->k_sl) * 2 < ((int64_t)1 << 32) &&
+                         (int64_t)g.Lp_blk * kXD * 2 < ((int64_t)1 << 32),
+                     "fs_xattn: sequence x row stride too large");
   FS_CHECK_ARG(((uintptr_t)a->q % 16) == 0 && ((uintptr_t)a->k % 16) == 0 && a->q_sl % 8 == 0 && a->k_sl % 8 == 0 &&
                    a->q_sh % 8 == 0 && a->k_sh % 8 == 0,
                "fs_xattn: q/k must be 16-byte aligned with strides of whole 16-byte chunks");
-  const int N = (a->L + a->bs - 1) / a->bs;
-  FS_CHECK_SUPPORTED(N <= kXMaxBlocks, "fs_xattn: %d blocks > %d", N, kXMaxBlocks);
-  // the tile copies address a token row by a 32-bit byte offset from the head's base
-  FS_CHECK_SUPPORTED((int64_t)a->L * (a->q_sl > a->k_sl ? a->q_sl : a->k_sl) * 2 < ((int64_t)1 << 32),
-                     "fs_xattn: sequence x row stride too large");
+  return FS_OK;
+}
+
+extern "C" size_t fs_xattn_work_bytes(const fs_xattn_args* a) {
+  if (!a || a->Hq <= 0 || a->Hk <= 0 || a->L <= 0 || a->stride <= 0 || a->bs <= 0 || a->bs % a->stride) return 0;
+  XGeom g;
+  xgeom(a, g);
+  return xattn_work(a, g);
+}
+
+extern "C" int fs_xattn(const fs_xattn_args* a, void* stream) {
+  if (int rc = xattn_check(a, true)) return rc;
+  XGeom g;
+  xgeom(a, g);
   XScoreK k{};
   k.q = static_cast<const uint16_t*>(a->q);
-  k.k = static_cast<const uint16_t*>(a->k);
-  k.q_sh = a->q_sh; k.q_sl = a->q_sl; k.k_sh = a->k_sh; k.k_sl = a->k_sl;
-  k.Hq = a->Hq; k.Hk = a->Hk; k.L = a->L; k.S = a->stride;
-  k.Lr = N * a->bs / a->stride;
-  k.real = (a->L + a->stride - 1) / a->stride;
-  k.rbs = a->bs / a->stride;
-  k.Nb = N;
+  k.q_sh = a->q_sh; k.q_sl = a->q_sl;
+  k.Hq = a->Hq; k.Hk = a->Hk; k.S = g.S; k.QS = g.QS;
+  k.Lq_tok = a->L;
+  k.qorder = g.qorder;
+  k.Lrq = g.Lrq; k.Lrk = g.Lrk; k.rbs = g.rbs; k.rpb = g.rbs / g.kdb; k.Nb = g.N;
+  k.causal = g.causal; k.kdb = g.kdb; k.own_chunk = g.own_chunk;
+  k.real_rows = g.real_rows; k.npad = g.npad; k.softmax = a->no_softmax ? 0 : 1;
   k.scale = (float)(1.4426950408889634 / sqrt((double)a->D) / a->stride / a->norm);
-  k.m = static_cast<float*>(a->work);
-  k.l = k.m + (size_t)a->Hq * k.Lr;
+  k.inv_sqrt = 1.0f / (float)sqrt((double)a->D);
+  k.inv_S = 1.0f / (float)a->stride;
+  k.inv_norm = 1.0f / a->norm;
+  char* w = static_cast<char*>(a->work);
+  k.m = reinterpret_cast<float*>(w);
+  k.l = k.m + (size_t)a->Hq * g.Lrq;
+  k.pad_sum = k.l + (size_t)a->Hq * g.Lrq;
   k.sums = a->sums;
-  k.scores = reinterpret_cast<uint16_t*>(static_cast<char*>(a->work) + xattn_stats_bytes(a->Hq, k.Lr));
-  k.head_stride = xattn_head_stride(k.Lr);
-  const unsigned grid = (unsigned)(a->Hq * ((k.Lr + kXRows - 1) / kXRows));
+  uint16_t* kaug = reinterpret_cast<uint16_t*>(w + xattn_stats_bytes(a->Hq, g));
+  k.scores = reinterpret_cast<uint16_t*>(w + xattn_stats_bytes(a->Hq, g) + xattn_kaug_bytes(a->Hk, g));
+  k.head_stride = g.head_stride;
   hipStream_t s = (hipStream_t)stream;
-  if (a->dtype == FS_DTYPE_BF16) {
-    xattn_scores_kernel<bf16_t><<<grid, kXThreads, 0, s>>>(k);
-    xattn_sums_kernel<bf16_t><<<grid, kXThreads, 0, s>>>(k);
+  const bool bf = a->dtype == FS_DTYPE_BF16;
+  if (g.aug) {
+    const int64_t n = (int64_t)a->Hk * g.Lp_blk * (kXD / 8);
+    const unsigned blocks = (unsigned)((n + 255) / 256);
+    const int triple = g.aug == 2;
+    if (bf) xattn_kaug_kernel<bf16_t><<<blocks, 256, 0, s>>>(static_cast<const uint16_t*>(a->k), a->k_sh, a->k_sl,
+                                                                a->Hk, a->L, g.Lp_blk, g.S, triple, kaug);
+    else xattn_kaug_kernel<f16_t><<<blocks, 256, 0, s>>>(static_cast<const uint16_t*>(a->k), a->k_sh, a->k_sl, a->Hk,
+                                                          a->L, g.Lp_blk, g.S, triple, kaug);
+    if (int rc = fs_host::launch_status("fs_xattn (keys)")) return rc;
+    k.k = kaug;
+    k.k_sh = (int64_t)g.Lp_blk * kXD;
+    k.k_sl = kXD;
+    k.Lk_tok = g.Lp_blk;
   } else {
-    xattn_scores_kernel<f16_t><<<grid, kXThreads, 0, s>>>(k);
-    xattn_sums_kernel<f16_t><<<grid, kXThreads, 0, s>>>(k);
+    k.k = static_cast<const uint16_t*>(a->k);
+    k.k_sh = a->k_sh; k.k_sl = a->k_sl;
+    k.Lk_tok = a->L;
+  }
+  const unsigned grid = (unsigned)(a->Hq * ((g.Lrq + kXRows - 1) / kXRows));
+  if (a->torch_path) {
+    if (bf) {
+      xattn_scores_kernel<bf16_t, true><<<grid, kXThreads, 0, s>>>(k);
+      xattn_sums_kernel<bf16_t, true><<<grid, kXThreads, 0, s>>>(k);
+    } else {
+      xattn_scores_kernel<f16_t, true><<<grid, kXThreads, 0, s>>>(k);
+      xattn_sums_kernel<f16_t, true><<<grid, kXThreads, 0, s>>>(k);
+    }
+  } else {
+    if (bf) {
+      xattn_scores_kernel<bf16_t, false><<<grid, kXThreads, 0, s>>>(k);
+      xattn_sums_kernel<bf16_t, false><<<grid, kXThreads, 0, s>>>(k);
+    } else {
+      xattn_scores_kernel<f16_t, false><<<grid, kXThreads, 0, s>>>(k);
+      xattn_sums_kernel<f16_t, false><<<grid, kXThreads, 0, s>>>(k);
+    }
   }
   if (int rc = fs_host::launch_status("fs_xattn (scores)")) return rc;
   XSelK sk{};
   sk.sums = a->sums;
+  sk.pad_sum = k.pad_sum;
   sk.thr = a->threshold;
   sk.blk_cnt = a->blk_cnt;
   sk.blk_idx = a->blk_idx;
-  sk.Hq = a->Hq; sk.Nb = N; sk.N = N; sk.Nk = N; sk.keep_sink = a->keep_sink;
-  xattn_select_kernel<<<(unsigned)(a->Hq * N), kXSelThreads, 0, s>>>(sk);
+  sk.Hq = a->Hq; sk.Nb = g.N; sk.N = g.N; sk.Nk = g.N; sk.Nbp = g.causal ? g.N : g.Nbp;
+  sk.causal = g.causal; sk.keep_sink = a->keep_sink; sk.keep_recent = a->keep_recent;
+  xattn_select_kernel<<<(unsigned)(a->Hq * g.N), kXSelThreads, 0, s>>>(sk);
   return fs_host::launch_status("fs_xattn (select)");
 }

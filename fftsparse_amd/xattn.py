@@ -2,18 +2,22 @@
 same block-sparse kernel as the FFT selector.
 
 Mirrors attn_src/xattn/src/Xattention.py: ``xattn_estimate`` (:14-303) and
-``Xattention_prefill`` (:306-406), whose callers use the Triton path
-(use_triton=True, "inverse" reshaping, kdb 1): reshaped antidiagonal scores,
-an exp2-domain causal softmax per reshaped row, block sums, and
-find_blocks_chunked's cumulative-mass choice per block row
-(attn_src/xattn/src/utils.py:44-200).  One C call (fs_xattn) runs all of it and
-emits the per-row block lists fs_bsattn reads.
+``Xattention_prefill`` (:306-406).  Its callers use the Triton path
+(use_triton=True: "inverse" reshaping, kdb 1): reshaped antidiagonal scores, an
+exp2-domain softmax per reshaped row (causal, or over the whole chunk-padded
+sequence), block sums, and find_blocks_chunked's cumulative-mass choice per
+block row (attn_src/xattn/src/utils.py:44-200).  use_triton=False selects the
+reference's torch path (Xattention.py:72-135, 170-258): the "inverse" (with
+kdb), "slash", "random", "double" and "triple" reshapings, its dtype
+roundings, and softmax=False.  One C call (fs_xattn) runs all of it and emits
+the per-row block lists fs_bsattn reads.
 
 K/V may carry Hq heads (the reference asserts that: its callers pass
 repeat_kv'd K/V) or Hkv heads with Hq % Hkv == 0 (native GQA, read as they are).
 """
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass
 
 import torch
@@ -72,13 +76,27 @@ def _thresholds(threshold, H: int, device) -> torch.Tensor:
     return d
 
 
+_MODES = {"inverse": 0, "": 0, "slash": 1, "random": 2, "double": 3, "triple": 4}
+
+
+def default_chunk_size(k_len: int) -> int:
+    """Xattention_prefill's chunk size when none is given (Xattention.py:326-335):
+    the next power of two of k_len, clamped to [2048, 2^28 / that power]."""
+    p = 1 << (k_len - 1).bit_length()
+    return int(max(min(max(2048, p), 128 * 1024 * 2048 // p), 2048))
+
+
 def xattn_select(query_states: torch.Tensor, key_states: torch.Tensor, *, stride: int = 8, threshold=0.9,
-                 norm: float = 1.0, block_size: int = 128, keep_sink: bool = False,
-                 keep_recent: bool = False) -> XSelection:
-    """The causal block selection of xattn_estimate (Xattention.py:14-303) as
-    block lists.  q [1,Hq,L,D], k [1,Hq or Hkv,L,D] on the GPU (bf16/f16,
-    D = 128).  ``keep_recent`` adds the diagonal, which the selection always
-    keeps, so it changes nothing."""
+                 norm: float = 1.0, block_size: int = 128, keep_sink: bool = False, keep_recent: bool = False,
+                 causal: bool = True, use_triton: bool = True, select_mode: str = "inverse", kdb: int = 1,
+                 softmax: bool = True, chunk_size: int | None = None, perm=None) -> XSelection:
+    """The block selection of xattn_estimate (Xattention.py:14-303) as block
+    lists.  q [1,Hq,L,D], k [1,Hq or Hkv,L,D] on the GPU (bf16/f16, D = 128).
+    ``chunk_size`` (tokens; default Xattention_prefill's) sets the zero padding
+    the non-causal softmax and the torch path's masks see.  ``perm``: the
+    "random" reshaping's permutation; by default torch.randperm(stride), drawn
+    where the reference draws it.  On the Triton path select_mode and softmax
+    are not used, as in the reference."""
     q = _check_layout(query_states)
     k = _check_layout(key_states)
     assert q.shape[0] == 1 and k.shape[0] == 1, "batch size 1 only"          # Xattention.py:361
@@ -89,6 +107,18 @@ def xattn_select(query_states: torch.Tensor, key_states: torch.Tensor, *, stride
         raise ValueError(f"query {tuple(q.shape)} and key {tuple(k.shape)} shapes do not match")
     if q.dtype != k.dtype or q.dtype not in (torch.bfloat16, torch.float16):
         raise TypeError(f"unsupported dtypes {q.dtype}, {k.dtype} (bf16/f16)")
+    if use_triton and kdb != 1:
+        raise ValueError("use_triton and kdb cannot be used together")           # Xattention.py:144
+    mode = 0
+    pm = list(range(16))
+    if not use_triton:
+        if select_mode not in _MODES:
+            raise ValueError(f"unknown select_mode {select_mode!r}")
+        mode = _MODES[select_mode]
+        if mode == 2:
+            pv = torch.randperm(stride) if perm is None else torch.as_tensor(perm)   # Xattention.py:76
+            pm[:stride] = [int(x) for x in pv.tolist()]
+    chunk = default_chunk_size(L) if chunk_size is None else int(chunk_size)
     N = -(-L // block_size)
     dev = q.device
     thr = _thresholds(threshold, Hq, dev)
@@ -96,13 +126,18 @@ def xattn_select(query_states: torch.Tensor, key_states: torch.Tensor, *, stride
                      blk_idx=torch.empty(Hq, N, N, dtype=torch.uint16, device=dev),
                      sums=torch.zeros(Hq, N, N, dtype=torch.float32, device=dev),
                      stride=stride, block_size=block_size)
-    lib = _lib.load()
-    work = torch.empty(max(1, lib.fs_xattn_work_bytes(Hq, L, stride, block_size)), dtype=torch.uint8, device=dev)
-    _lib.call("fs_xattn", XattnArgs(
+    args = XattnArgs(
         q=q.data_ptr(), q_sh=q.stride(1), q_sl=q.stride(2), k=k.data_ptr(), k_sh=k.stride(1), k_sl=k.stride(2),
         dtype=_lib.FS_DTYPE[q.dtype], Hq=Hq, Hk=Hk, L=L, D=D, stride=stride, bs=block_size, norm=float(norm),
         threshold=thr.data_ptr(), keep_sink=int(bool(keep_sink)), sums=sel.sums.data_ptr(),
-        blk_cnt=sel.blk_cnt.data_ptr(), blk_idx=sel.blk_idx.data_ptr(), work=work.data_ptr()))
+        blk_cnt=sel.blk_cnt.data_ptr(), blk_idx=sel.blk_idx.data_ptr(),
+        non_causal=int(not causal), torch_path=int(not use_triton), select_mode=mode, kdb=int(kdb),
+        no_softmax=int(not use_triton and not softmax), chunk=chunk, keep_recent=int(bool(keep_recent)))
+    args.perm[:] = pm
+    lib = _lib.load()
+    work = torch.empty(max(1, lib.fs_xattn_work_bytes(ctypes.byref(args))), dtype=torch.uint8, device=dev)
+    args.work = work.data_ptr()
+    _lib.call("fs_xattn", args)
     sel._keep = (thr, work)                          # alive until the stream has used them
     return sel
 
@@ -113,37 +148,27 @@ def xattn_estimate(query_states, key_states, block_size, stride, norm=1, softmax
     """Xattention.py:14-303 on the GPU kernels: returns (attn_sums, simple_masks),
     [1, H, N, N] in the input dtype and bool, N = ceil(L / block_size) (the
     reference pads both to whole chunks; its Xattention_prefill keeps this
-    N x N corner).  The Triton path is the one computed, whatever
-    ``use_triton`` says; ``chunk_size`` only sizes the reference's working
-    buffers and does not change the result."""
-    if kdb != 1:
-        raise ValueError("use_triton and kdb cannot be used together")           # Xattention.py:144
-    if not causal:
-        raise NotImplementedError("the non-causal XAttention selection is not built")
-    if not softmax:
-        raise NotImplementedError("softmax=False is not built")
-    if select_mode not in ("inverse", ""):
-        raise NotImplementedError(f"select_mode {select_mode!r} is not built (the Triton path is 'inverse')")
+    N x N corner).  Causal sums are zero above the diagonal."""
     sel = xattn_select(query_states, key_states, stride=stride, threshold=threshold, norm=norm,
-                       block_size=block_size, keep_sink=keep_sink, keep_recent=keep_recent)
+                       block_size=block_size, keep_sink=keep_sink, keep_recent=keep_recent, causal=causal,
+                       use_triton=use_triton, select_mode=select_mode, kdb=kdb, softmax=softmax,
+                       chunk_size=chunk_size)
     return sel.sums.to(query_states.dtype)[None], sel.dense_mask()[None]
 
 
 def Xattention_prefill(query_states: torch.Tensor, key_states: torch.Tensor, value_states: torch.Tensor, stride,
                        norm=1, threshold=0.8, block_size=128, use_triton=True, causal=True, kdb=1,
                        chunk_size=None, keep_sink=False, keep_recent=False):
-    """Xattention.py:306-406: the XAttention selection, then block-sparse
-    causal attention over the chosen blocks.  q [1,H,L,D], k/v [1,H or Hkv,L,D]
-    -> [1, H, L, D] (a view of [1, L, H, D] storage, as the reference returns)."""
+    """Xattention.py:306-406: the XAttention selection ("inverse" reshaping),
+    then block-sparse attention over the chosen blocks (causal or not).
+    q [1,H,L,D], k/v [1,H or Hkv,L,D] -> [1, H, L, D] (a view of [1, L, H, D]
+    storage, as the reference returns)."""
     assert query_states.is_cuda, "input tensors must be on the GPU"
-    if kdb != 1:
-        raise ValueError("use_triton and kdb cannot be used together")
-    if not causal:
-        raise NotImplementedError("the non-causal XAttention selection is not built")
     sel = xattn_select(query_states, key_states, stride=stride, threshold=threshold, norm=norm,
-                       block_size=block_size, keep_sink=keep_sink, keep_recent=keep_recent)
+                       block_size=block_size, keep_sink=keep_sink, keep_recent=keep_recent, causal=causal,
+                       use_triton=use_triton, kdb=kdb, chunk_size=chunk_size)
     out = block_sparse_attention(query_states, key_states, value_states, sel.blk_cnt, sel.blk_idx,
-                                 block_size=block_size, is_causal=True)
+                                 block_size=block_size, is_causal=causal)
     return out.transpose(1, 2)
 
 
@@ -154,4 +179,4 @@ def density(sel: XSelection) -> float:
     return min(1.0, sel.nnz() / (H * N * (N + 1) / 2))
 
 
-__all__ = ["XSelection", "xattn_select", "xattn_estimate", "Xattention_prefill", "density"]
+__all__ = ["XSelection", "xattn_select", "xattn_estimate", "Xattention_prefill", "default_chunk_size", "density"]

@@ -223,24 +223,39 @@ typedef struct {
 FS_API int fs_select(const fs_select_args* a, void* stream);
 
 /* ---- XAttention block selection ------------------------------------------
- * The reference's other selector (attn_src/xattn/src/Xattention.py:14-303,
- * Triton path: kernels.py:5-97, 195-234; find_blocks_chunked utils.py:44-200),
- * causal, "inverse" reshaping, kdb 1, block size 128.  For query head h (key
- * head h / (Hq/Hk)), stride S, reshaped row r and key n (tokens zero past L):
- *   A[r][n]  = sum_{j<S} q[rS+S-1-j] . k[nS+j]  rounded to dtype,
- *   p[r][n]  = exp2(x - max_r) / sum_r,  x = A log2(e) / sqrt(D) / S / norm, n <= r,
- *              rows r >= ceil(L/S) zero,
- *   sums[h][I][J] = sum of p over reshaped rows / keys of blocks I, J, rounded to dtype;
- * then per block row I the blocks 0 and I, and the other blocks in decreasing
- * order of sums while  sums(0) + sums(I) + (mass of the larger others) <
- * row total * threshold[h]  (float64; ties: lower index first).  Outputs the
- * ascending block lists blk_cnt [Hq][N], blk_idx [Hq][N][N] (N = ceil(L/bs),
- * causal; keep_sink: row 0 lists every block) and the causal part of sums
- * [Hq][N][N].  threshold: device array of Hq float64 values.  work:
- * fs_xattn_work_bytes(Hq, L, stride, bs) bytes of device scratch: the row
- * statistics and the rounded scores A of the causal part (about
- * Hq (L/S)^2 bytes: 8.7 GB at L = 131072, S = 8, 32 heads).
- * bf16/f16, D = 128, bs = 128, stride 4, 8 or 16, N <= 4096. */
+ * The reference's other selector (attn_src/xattn/src/Xattention.py:14-303
+ * xattn_estimate; Triton path kernels.py:5-156, 195-234; torch path
+ * Xattention.py:72-135, 170-258; find_blocks_chunked utils.py:44-200), block
+ * size 128.  For query head h (key head h / (Hq/Hk)), stride S, reshaped row m
+ * and key n (tokens zero past L):
+ *   A[m][n]  = sum_{j<S} q[m QS + o_j] . k'[nS+j]  rounded to dtype;
+ * Triton path (torch_path 0: the callers' use_triton=True): o_j = S-1-j,
+ * QS = S, k' = k, x = A log2(e) / sqrt(D) / S / norm, p = exp2(x - max_m) /
+ * sum_m over the keys row m sees (causal: n <= m; non_causal: every key of the
+ * sequence zero-padded to whole chunks of `chunk` tokens), rows m >= ceil(L/S)
+ * zero, sums[h][I][J] = sum of p over the reshaped rows / keys of blocks I, J,
+ * rounded to dtype.  Torch path (use_triton=False): select_mode 0 inverse
+ * (o_j = S-1-j, QS = S kdb), 1 slash (o_j = j), 2 random (o_j = perm[j]),
+ * 3 double / 4 triple (o_j = S-1-j; k' the neighbouring-chunk sums of k in
+ * dtype); x = A / sqrt(D) / S / norm, each division rounded to dtype; causal
+ * row m sees keys n <= m kdb + kdb - 1 (those of its own chunk only when the
+ * sequence needs no padding, as the reference's mask does); p = softmax (float32; or exp with no_softmax) rounded to dtype; the
+ * last padded rows zeroed; sums = two sums rounded to dtype (a block's keys,
+ * then its rows).  Then per block row I, in float64: causal: the blocks 0 and
+ * I, and the other blocks in decreasing order of sums while sums(0) + sums(I)
+ * + (mass of the larger others) < row total * threshold[h]; non_causal: every
+ * block of the chunk-padded row in decreasing order while the mass before it
+ * < row total * threshold[h], and block 0 (ties: lower index first).  Outputs
+ * the ascending block lists blk_cnt [Hq][N], blk_idx [Hq][N][N] of the
+ * N = ceil(L/bs) real blocks (causal: the tril; keep_sink: row 0 lists every
+ * block; keep_recent: the diagonal) and sums [Hq][N][N] (causal: its lower
+ * triangle).  threshold: device array of Hq float64 values.  work:
+ * fs_xattn_work_bytes(a) bytes of device scratch: the row statistics, K' for
+ * double / triple and the rounded scores A of the keys each row sees (about
+ * Hq (L/S)^2 bytes causal, twice that non-causal: 8.7 / 17.2 GB at
+ * L = 131072, S = 8, 32 heads).  Zero-initialised trailing fields give the
+ * Triton causal path.  bf16/f16, D = 128, bs = 128, stride 4, 8 or 16,
+ * N <= 4096 and chunk-padded blocks <= 4096. */
 typedef struct {
   const void* q; int64_t q_sh, q_sl;
   const void* k; int64_t k_sh, k_sl;
@@ -252,8 +267,16 @@ typedef struct {
   int32_t* blk_cnt;
   uint16_t* blk_idx;
   void* work;
+  int non_causal;       /* causal=False */
+  int torch_path;       /* use_triton=False */
+  int select_mode;      /* torch path: 0 inverse, 1 slash, 2 random, 3 double, 4 triple */
+  int perm[16];         /* random: the query token offset of chunk j (torch.randperm(stride) in the reference) */
+  int kdb;              /* torch path: every kdb-th reshaped query row (0 or 1: all) */
+  int no_softmax;       /* torch path: softmax=False */
+  int chunk;            /* chunk_size in tokens (non-causal and torch path; 0: none) */
+  int keep_recent;
 } fs_xattn_args;
-FS_API size_t fs_xattn_work_bytes(int Hq, int L, int stride, int bs);
+FS_API size_t fs_xattn_work_bytes(const fs_xattn_args* a);
 FS_API int fs_xattn(const fs_xattn_args* a, void* stream);
 
 /* ---- FlexPrefill block selection -----------------------------------------

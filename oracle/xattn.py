@@ -16,6 +16,22 @@ Restates, in torch on the CPU:
   while the mass before them is below threshold x row total, in float64), and
   Xattention.py:278-301 (causal tril, keep_sink, keep_recent).
 
+The other paths of xattn_estimate, restated in ``estimate``:
+  - causal=False on the Triton path: the softmax over every key of the
+    chunk-padded sequence (Xattention.py:36-55: Q and K zero-padded to whole
+    chunks; kernels.py:98-156 normalises over all of them), and
+    find_blocks_chunked's non-causal branch (utils.py:163-188: no forced
+    blocks, every block sorted, and block 0 always marked because unselected
+    positions scatter to index 0);
+  - use_triton=False (Xattention.py:72-135, 170-258): the reshapings
+    "inverse" (with kdb), "slash", "random", "double", "triple"; scores from a
+    matmul in the input dtype, divided by sqrt(D), S and norm in that dtype; the
+    causal mask (the kdb-subsampled rows take mask rows kdb-1, 2kdb-1, ...; the
+    padding-column marks are overwritten by each chunk's own square);
+    softmax in float32 (or exp when softmax=False) rounded to the input dtype;
+    padded query rows zeroed; block sums as two sums in the input dtype (over a
+    block's keys, then its rows).
+
 Accumulation orders the reference leaves to Triton (the GEMM's and the block
 sums' fp32 reductions) are done here in float64 and rounded once; torch.sort's
 order among equal values is unspecified, and ties are broken here by the lower
@@ -26,6 +42,15 @@ Parity pins (tests/test_oracle_xattn.py):
   block_sums        -- softmax rows sum to one; brute-force block sums
   select_blocks     -- hand-built rows with closed-form selections; the sorted
                        cumulative rule checked against a direct greedy loop
+  general_scores    -- every reshaping against sums of the token score matrix
+                       over the permutation's entries (double / triple: the
+                       neighbouring-key sums); kdb rows equal every kdb-th row
+  estimate          -- the Triton causal path equals xattn_mask; probabilities
+                       of every real row sum to one over the chunk-padded keys
+                       (non-causal) or its visible keys; softmax=False gives
+                       exp of the scaled scores; the non-causal selection on
+                       closed-form rows, block 0 kept; default_chunk_size's
+                       closed forms
 """
 from __future__ import annotations
 
@@ -159,3 +184,213 @@ def xattn_mask(q: torch.Tensor, k: torch.Tensor, *, stride: int, threshold, bloc
         mask |= torch.eye(Nb, dtype=torch.bool)
     N = -(-L // block_size)
     return mask[:, :N, :N], sums, margin
+
+
+# ---- the other paths of xattn_estimate ---------------------------------------
+
+def default_chunk_size(k_len: int) -> int:
+    """Xattention_prefill's chunk_size when none is given (Xattention.py:326-335):
+    the next power of two of k_len, clamped to [2048, 2^28 / that power]."""
+    p = 1 << (k_len - 1).bit_length()
+    return int(max(min(max(2048, p), 128 * 1024 * 2048 // p), 2048))
+
+
+def query_order(select_mode: str, stride: int, perm=None):
+    """The token offset within a stride group that query chunk i takes
+    (Xattention.py:74-135): "inverse" / "" and "double" / "triple" reverse the
+    group (S-1-i), "slash" keeps it (i), "random" takes perm[i]."""
+    if select_mode in ("inverse", "", "double", "triple"):
+        return [stride - 1 - i for i in range(stride)]
+    if select_mode == "slash":
+        return list(range(stride))
+    if select_mode == "random":
+        return [int(x) for x in perm]
+    raise ValueError(f"unknown select_mode {select_mode!r}")
+
+
+def reshaped_keys(k: torch.Tensor, Lp: int, stride: int, select_mode: str) -> torch.Tensor:
+    """K' [Hk, Lp/S, S, D] (values of k's dtype, as float64): chunk j of
+    reshaped key n is k[nS + j] (zero past L); "double" adds chunk j + 1 (mod S),
+    "triple" then adds the doubled chunk j - 1 (mod S), each sum rounded to the
+    dtype as the reference's tensor additions are (Xattention.py:103-135)."""
+    _, Hk, L, D = k.shape
+    kp = torch.zeros(Hk, Lp, D, dtype=torch.float64)
+    kp[:, :L] = k[0].double()
+    R = kp.view(Hk, Lp // stride, stride, D)
+    if select_mode in ("double", "triple"):
+        R = round_to(R + R.roll(-1, dims=2), k.dtype).double()
+        if select_mode == "triple":
+            R = round_to(R + R.roll(1, dims=2), k.dtype).double()
+    return R
+
+
+def general_scores(q: torch.Tensor, k: torch.Tensor, *, stride: int, Lp: int, select_mode: str = "inverse",
+                   kdb: int = 1, perm=None) -> torch.Tensor:
+    """Reshaped scores A [H, Lp/(S kdb), Lp/S] rounded to the input dtype (as
+    float32).  Query row m takes the tokens m*QS + order[i], QS = S*kdb for
+    "inverse" (its reshaping strides by S*kdb) and S for the other modes (which
+    ignore kdb when reshaping; the kdb-th rows are then sliced by position,
+    Xattention.py:172-178); key n the chunks of reshaped_keys."""
+    _, H, L, D = q.shape
+    S = stride
+    g = H // k.shape[1]
+    order = query_order(select_mode, S, perm)
+    QS = S * kdb if select_mode in ("inverse", "") else S
+    nq = Lp // (S * kdb)
+    qp = torch.zeros(H, Lp + QS, D, dtype=torch.float64)
+    qp[:, :L] = q[0].double()
+    Qr = torch.stack([qp[:, torch.arange(nq) * QS + o] for o in order], dim=2)   # [H, nq, S, D]
+    Kr = reshaped_keys(k, Lp, S, select_mode).repeat_interleave(g, 0)             # [H, Lp/S, S, D]
+    A = torch.einsum("hmsd,hnsd->hmn", Qr, Kr)
+    return round_to(A, q.dtype)
+
+
+def _visible(nq: int, nk: int, *, causal: bool, kdb: int, own_chunk: int = 0) -> torch.Tensor:
+    """[nq, nk] keys a query row may attend: causal row m sees keys
+    n <= m*kdb + kdb - 1 (the mask row the kdb-th slice takes); own_chunk > 0:
+    only keys from the start of the row's chunk of own_chunk reshaped rows on
+    (see torch_sums)."""
+    if not causal:
+        return torch.ones(nq, nk, dtype=torch.bool)
+    m = torch.arange(nq)[:, None]
+    n = torch.arange(nk)[None, :]
+    vis = n <= m * kdb + kdb - 1
+    if own_chunk:
+        vis &= n >= (m * kdb // own_chunk) * own_chunk
+    return vis
+
+
+def triton_sums(A: torch.Tensor, L: int, *, stride: int, bs: int, norm: float, head_dim: int,
+                causal: bool) -> torch.Tensor:
+    """kernels.py:5-156 on A [H, Lr, Lk]: x = A log2(e) / sqrt(D) / S / norm,
+    per row the exp2-domain softmax over the keys it sees (causal: n <= r;
+    non-causal: every key of the padded sequence), rows at or past ceil(L/S)
+    zero, summed over (bs/S) x (bs/S) squares in float64, rounded to the
+    input dtype by the caller."""
+    H, Lr, Lk = A.shape
+    rbs = bs // stride
+    real = -(-L // stride)
+    x = A.double() * (LOG2E / math.sqrt(head_dim) / stride / norm)
+    vis = _visible(Lr, Lk, causal=causal, kdb=1)
+    x = x.masked_fill(~vis, float("-inf"))
+    e = torch.exp2(x - x.max(-1, keepdim=True).values)
+    p = e / e.sum(-1, keepdim=True)
+    p[:, real:] = 0
+    return p.view(H, Lr // rbs, rbs, Lk // rbs, rbs).sum((2, 4))
+
+
+def torch_zero_rows(L: int, Lp: int, *, stride: int, chunk_size: int, kdb: int) -> int:
+    """Query rows (of the Lp/(S kdb) the torch path keeps) zeroed at the end:
+    the last q_reshaped_num_to_pad // kdb (Xattention.py:248-249); when that is
+    0 but some reshaped rows are padding, the slice [-0:] zeroes the whole last
+    chunk (chunk_size / (S kdb) rows)."""
+    pad_r = (Lp - L) // stride
+    z = pad_r // kdb
+    if z == 0 and pad_r != 0:
+        z = chunk_size // stride // kdb
+    return z
+
+
+def torch_sums(A: torch.Tensor, L: int, Lp: int, *, stride: int, bs: int, norm: float, head_dim: int,
+               causal: bool, kdb: int, softmax: bool, dtype, chunk_size: int) -> torch.Tensor:
+    """Xattention.py:180-258 on A [H, nq, Lk] (the matmul's output in dtype):
+    the divisions by sqrt(D), S and norm each rounded to dtype (a division by a
+    Python number runs as a multiplication by its float32 reciprocal on the
+    GPU), the causal mask, softmax in float32 -- here float64 -- or exp,
+    rounded to dtype, the padded query rows zeroed (torch_zero_rows); then a
+    sum over each block's keys and one over its rows, each rounded to dtype.
+    The causal mask first marks the last k_num_to_pad // S key columns (:205),
+    then writes each query chunk's own square upper-triangular (:206-217) over
+    them: the padding columns lie in the last chunk, so a row of that chunk sees
+    a padding key at or before its mask row (with kdb > 1 some kept rows do).
+    When the padding count is 0 the slice [-0:] marks every column and only the
+    own square is cleared again, so each row then sees the keys of its own
+    chunk only.  Returns [H, Lp/bs, Lk*S/bs] block sums (float32)."""
+    H, nq, Lk = A.shape
+    S = stride
+    rbs = bs // S
+
+    def div(x, v):
+        inv = torch.tensor(1.0, dtype=torch.float32) / torch.tensor(v, dtype=torch.float32)
+        return round_to(x.float() * inv, dtype)
+    x = div(div(div(A, math.sqrt(head_dim)), S), norm).double()
+    k_pad_r = (Lp - L) // S                        # k_num_to_pad // stride
+    vis = _visible(nq, Lk, causal=causal, kdb=kdb, own_chunk=chunk_size // S if k_pad_r == 0 else 0)
+    x = x.masked_fill(~vis, float("-inf"))
+    if softmax:
+        mx = x.max(-1, keepdim=True).values
+        e = torch.exp(x - mx)
+        p = e / e.sum(-1, keepdim=True)
+    else:
+        p = torch.exp(x)
+    zero_rows = torch_zero_rows(L, Lp, stride=S, chunk_size=chunk_size, kdb=kdb)
+    if zero_rows:
+        p[:, nq - zero_rows:] = 0
+    p = torch.nan_to_num(round_to(p, dtype).double(), nan=0.0)
+    s1 = round_to(p.view(H, nq, Lk // rbs, rbs).sum(-1), dtype).double()          # over the block's keys
+    s = s1.view(H, nq // (rbs // kdb), rbs // kdb, Lk // rbs).sum(2)                # over its rows
+    return round_to(s, dtype)
+
+
+def select_rows_noncausal(sums: torch.Tensor, threshold):
+    """find_blocks_chunked's non-causal prefill branch (utils.py:163-188) on
+    [H, Nq, Nk] sums: every block in decreasing order (ties: lower index
+    first) is selected while the mass before it is below total * threshold
+    (float64); block 0 is always marked (the unselected positions scatter to
+    index 0).  Returns (mask, margin) as select_rows."""
+    H, Nq, Nk = sums.shape
+    thr = _head_thresholds(threshold, H)
+    v = sums.double()
+    mask = torch.zeros(H, Nq, Nk, dtype=torch.bool)
+    margin = torch.zeros(H, Nq, Nk, dtype=torch.float64)
+    for h in range(H):
+        for i in range(Nq):
+            row = v[h, i]
+            req = float(row.sum()) * thr[h]
+            order = sorted(range(Nk), key=lambda j: (-float(row[j]), j))
+            before = 0.0
+            for j in order:
+                margin[h, i, j] = (before / req - 1.0) if req > 0 else math.inf
+                if before < req:
+                    mask[h, i, j] = True
+                before += float(row[j])
+            mask[h, i, 0] = True
+            margin[h, i, 0] = -math.inf                # kept whatever the masses
+    return mask, margin
+
+
+def estimate(q: torch.Tensor, k: torch.Tensor, *, stride: int, threshold, block_size: int = 128,
+             norm: float = 1.0, softmax: bool = True, chunk_size: int = 16384, select_mode: str = "inverse",
+             use_triton: bool = True, causal: bool = True, kdb: int = 1, keep_sink: bool = False,
+             keep_recent: bool = False, perm=None):
+    """xattn_estimate (Xattention.py:14-303) with every path, for L_q == L_k:
+    returns (mask [H, N, N] bool, sums [H, N, N] float32 values of the input
+    dtype, margin [H, N, N], sums_padded [H, Nqp, Nkp]) with N = ceil(L / bs)
+    (the corner Xattention_prefill keeps) and the chunk-padded sums behind the
+    selection.  ``perm``: the random mode's permutation (torch.randperm(stride)
+    in the reference)."""
+    _, H, L, D = q.shape
+    if use_triton:
+        if kdb != 1:
+            raise ValueError("use_triton and kdb cannot be used together")
+        select_mode = "inverse"
+    Lp = -(-L // chunk_size) * chunk_size
+    A = general_scores(q, k, stride=stride, Lp=Lp, select_mode=select_mode, kdb=kdb, perm=perm)
+    if use_triton:
+        sums = round_to(triton_sums(A, L, stride=stride, bs=block_size, norm=norm, head_dim=D, causal=causal),
+                        q.dtype)
+    else:
+        sums = torch_sums(A, L, Lp, stride=stride, bs=block_size, norm=norm, head_dim=D, causal=causal,
+                          kdb=kdb, softmax=softmax, dtype=q.dtype, chunk_size=chunk_size)
+    Nb = sums.shape[1]
+    if causal:
+        mask, margin = select_rows(sums, threshold)
+        mask &= torch.tril(torch.ones(Nb, Nb, dtype=torch.bool))
+    else:
+        mask, margin = select_rows_noncausal(sums, threshold)
+    if keep_sink:
+        mask[:, 0, :] = True
+    if keep_recent:
+        mask[:, :, :Nb] |= torch.eye(Nb, dtype=torch.bool)
+    N = -(-L // block_size)
+    return mask[:, :N, :N], sums[:, :N, :N], margin[:, :N, :N], sums
