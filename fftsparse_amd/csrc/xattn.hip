@@ -118,10 +118,13 @@ __host__ __device__ inline int64_t xoffset(int rt, int Lrq, int Lrk, int causal,
   return o;
 }
 
-// whether row sees key (the keys past Lrk -- chunk padding -- are formed in closed form)
+// whether row sees key (the keys past Lrk -- chunk padding -- are formed in
+// closed form); the Triton path has kdb 1 and no own-chunk rule
+template <bool TP>
 __device__ __forceinline__ bool xkey_ok(const XScoreK& a, int row, int key) {
   if (key >= a.Lrk) return false;
   if (!a.causal) return true;
+  if constexpr (!TP) return key <= row;
   if (key > row * a.kdb + a.kdb - 1) return false;
   return a.own_chunk == 0 || key >= (row * a.kdb / a.own_chunk) * a.own_chunk;
 }
@@ -153,6 +156,7 @@ __global__ __launch_bounds__(kXThreads) void xattn_scores_kernel(XScoreK a) {
   const uint16_t* kh = a.k + (int64_t)hk * a.k_sh;
   const int S = a.S, QS = a.QS;
   const int nct = xnct(rt, a.Lrq, a.Lrk, a.causal, a.kdb);
+  const int64_t tile_off = xoffset(rt, a.Lrq, a.Lrk, a.causal, a.kdb);   // once, before the key loop
   const bool row_ok = row < a.Lrq;
   const bool stats = !TP || a.softmax;
 
@@ -219,13 +223,12 @@ __global__ __launch_bounds__(kXThreads) void xattn_scores_kernel(XScoreK a) {
     // ---- epilogue: lane holds keys n0 + 32 kk + (r/4) 8 + hi 4 + r%4 of its row;
     // whether the row sees a key and its scaled score are recomputed from the
     // accumulator where used, so no tile-sized arrays stay live
-    auto valid = [&](int kk, int r) { return row_ok && xkey_ok(a, row, n0 + kk * 32 + (r >> 2) * 8 + hi * 4 + (r & 3)); };
+    auto valid = [&](int kk, int r) { return row_ok && xkey_ok<TP>(a, row, n0 + kk * 32 + (r >> 2) * 8 + hi * 4 + (r & 3)); };
     auto xval = [&](int kk, int r) { return xscaled<T, TP>(a, acc[kk][r]); };
     if (row_ok) {
       // the rounded scores of this lane's row: four consecutive keys per 8-byte store
       const int NK = nct * kXKeys;
-      uint16_t* dst = a.scores + (int64_t)h * a.head_stride + xoffset(rt, a.Lrq, a.Lrk, a.causal, a.kdb) +
-                      (int64_t)(row - r0) * NK;
+      uint16_t* dst = a.scores + (int64_t)h * a.head_stride + tile_off + (int64_t)(row - r0) * NK;
 #pragma unroll
       for (int kk = 0; kk < kXKK; ++kk)
 #pragma unroll
@@ -318,13 +321,13 @@ __global__ __launch_bounds__(kXThreads) void xattn_sums_kernel(XScoreK a) {
       float v = 0.f;
       // a row's visible keys start and end on multiples of 8 from below (chunk
       // starts are multiples of bs / S >= 8), so n decides whether any is seen
-      if (key_in && rok[i] && xkey_ok(a, row, n)) {
+      if (key_in && rok[i] && xkey_ok<TP>(a, row, n)) {
         const uint4 w = *reinterpret_cast<const uint4*>(src + (int64_t)i * NK + n);
         const uint32_t pr[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
           const uint16_t e = (uint16_t)((t & 1) ? (pr[t >> 1] >> 16) : (pr[t >> 1] & 0xffffu));
-          if (xkey_ok(a, row, n + t)) v += prob(i, xscaled<T, TP>(a, to_f32(T{e})));
+          if (xkey_ok<TP>(a, row, n + t)) v += prob(i, xscaled<T, TP>(a, to_f32(T{e})));
         }
       }
       if constexpr (TP) {
