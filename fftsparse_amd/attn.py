@@ -64,8 +64,11 @@ class BlockSelection:
         return int(self.blk_cnt.sum().item())
 
 
-# largest block count of the selection kernels (LDS FFT length 8192, 64 membership words per row)
-MAX_SELECT_BLOCKS = 4096
+# largest block count of the selection kernels: 8192 on the 16-bit path (block
+# scores on MFMA; a diffuse head's 4-row score panel in LDS), 4096 on the fp32
+# path (LDS FFT length 8192)
+MAX_SELECT_BLOCKS = 8192
+MAX_FFT_BLOCKS = 4096
 
 _tau_cache: dict = {}
 
@@ -134,8 +137,11 @@ def select_blocks(query_states: torch.Tensor, key_states: torch.Tensor, *, block
     last_k = p.last_k if enable_last_block_mask else 0
     n_samples = 0 if (not p.corr_enabled or p.stripe_all_diffuse) else len(p.sample_taus)
     # 16-bit inputs: correlation and statistics in one call from MFMA block-score tiles
-    use_scores = (q.dtype in (torch.bfloat16, torch.float16) and D % 16 == 0 and D <= 128 and N <= 4096
+    use_scores = (q.dtype in (torch.bfloat16, torch.float16) and D % 16 == 0 and D <= 128
                   and (p.corr_enabled or n_cols or last_k))
+    if not use_scores and (p.corr_enabled or n_cols or last_k) and N > MAX_FFT_BLOCKS:
+        raise RuntimeError(f"{N} query blocks exceed the fp32 / D > 128 selection path's maximum of "
+                           f"{MAX_FFT_BLOCKS} (the 16-bit path with D <= 128 takes up to {MAX_SELECT_BLOCKS})")
     thr = f32(corr_threshold)
     corr_mode = 1 if correlation_selection_mode == "topk" else 0
     corr_q = f32(1.0 - correlation_topk_ratio)                  # torch.quantile's q in fp32 (:200-201)

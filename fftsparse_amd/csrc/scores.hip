@@ -33,6 +33,7 @@ constexpr int kFinalThreads = 1024;
 constexpr int kDiagSlots = 256;                 // 255 local diagonals per tile (+1 pad)
 constexpr int kMaxSamples = 1024;               // sampled diagonals per head
 constexpr int kDiagJobs = 4;                    // final-kernel workgroups per head for the diagonal statistics
+constexpr int kScoresMaxN = 8192;               // the final kernel's per-head row of N floats in LDS
 
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -358,7 +359,7 @@ static int check_scores(const fs_scores_args* a, const char* fn, bool with_work)
                      "%s: dtype %d unsupported (bf16/f16; fp32 uses fs_corr and fs_stats)", fn, a->dtype);
   // the staged K tile (128 * D 16-bit values) shares the S tile's LDS; D <= 128
   FS_CHECK_SUPPORTED(a->D % 16 == 0 && a->D <= 128, "%s: head_dim %d unsupported", fn, a->D);
-  FS_CHECK_SUPPORTED(a->N <= 4096, "%s: N=%d > 4096", fn, a->N);
+  FS_CHECK_SUPPORTED(a->N <= kScoresMaxN, "%s: N=%d > %d", fn, a->N, kScoresMaxN);
   FS_CHECK_SUPPORTED(a->n_samples <= kMaxSamples, "%s: %d diagonal samples > %d", fn, a->n_samples, kMaxSamples);
   return FS_OK;
 }

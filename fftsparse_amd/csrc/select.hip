@@ -6,7 +6,7 @@
 // One workgroup (4 waves) owns RPW consecutive query-block rows of one head.
 // Stripe heads (and the fixed mask) and diffuse heads are served by two
 // launches of the kernel, so only the diffuse launch reserves LDS for the
-// score panel.  Stripe / fixed rows (Nk <= 4096) are built word-parallel: a
+// score panel.  N <= 8192.  Stripe / fixed rows (Nk <= 4096) are built word-parallel: a
 // lane forms the 64-bit membership mask of 64 key blocks (range masks for
 // the prior, columns and causal limit; a funnel-shifted window of the
 // bit-reversed lag mask for the lag diagonals), and writes its set bits at
@@ -23,6 +23,7 @@ namespace fs {
 constexpr int kSelThreads = 256;
 constexpr int kSelWaves = kSelThreads / 64;
 constexpr int kMaxWords = 64;                       // word-parallel path: Nk <= 4096
+constexpr int kSelMaxN = 8192;                      // per-row path (a diffuse head's 4-row score panel fits LDS)
 
 // bits of word w (blocks 64w .. 64w+63) that lie in [lo, hi)
 __device__ __forceinline__ uint64_t range_bits(int w, int lo, int hi) {
@@ -216,7 +217,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(fs_select_args a, i
     return;
   }
   // ---- per-head lag / column / last-row flags, staged in LDS (bit 0 lag, 1 column, 2 last row)
-  __shared__ uint8_t flags[4096];
+  __shared__ uint8_t flags[kSelMaxN];
   for (int j = tid; j < N; j += kSelThreads) {
     uint8_t f = 0;
     if (a.keep_tau && a.keep_tau[(int64_t)h * N + j]) f |= 1;
@@ -321,7 +322,8 @@ extern "C" int fs_select(const fs_select_args* a, void* stream) {
   FS_CHECK_ARG(a->col_mode != 1 || a->dyn_mode == 1, "fs_select: col_mode 1 needs dyn_mode 1");
   FS_CHECK_ARG((a->dyn_mode == 0 && a->col_mode == 0 && a->last_sel == nullptr) || a->N == a->Nk,
                "fs_select: dynamic, column and last-row masks need N == Nk");
-  FS_CHECK_SUPPORTED(a->N <= 4096 && (a->dyn_mode == 0 || a->D <= 256), "fs_select: N=%d too large", a->N);
+  FS_CHECK_SUPPORTED(a->N <= kSelMaxN && (a->dyn_mode == 0 || a->D <= 256), "fs_select: N=%d > %d or D=%d > 256",
+                     a->N, kSelMaxN, a->D);
   const int rows_per_wave = a->N <= 1024 ? 4 : (a->N <= 2048 ? 2 : 1);
   const int RPW = rows_per_wave * kSelWaves;
   const int chunks = (a->N + RPW - 1) / RPW;

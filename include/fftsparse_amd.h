@@ -102,7 +102,8 @@ FS_API int fs_rope_pool(const fs_rope_pool_args* a, void* stream);
  *     0 "threshold" (:205-208): corr[h][t] / max(max_{t'>=rs} corr[h][t'], 1e-6) >= corr_threshold;
  *     1 "topk" (:196-203): corr[h][t] >= the corr_quantile quantile of corr[h][rs..N-1]
  *       (torch.quantile, linear interpolation; corr_quantile = 1 - correlation_topk_ratio in fp32).
- * work: fs_corr_work_bytes(Hq, N, D) bytes of device scratch. */
+ * work: fs_corr_work_bytes(Hq, N, D) bytes of device scratch.  N <= 4096
+ * (one LDS FFT of length 2N). */
 typedef struct {
   const void* q_b; const void* k_b;
   int dtype, Hq, Hk, N, D;
@@ -144,7 +145,7 @@ FS_API int fs_stats(const fs_stats_args* a, void* stream);
 
 /* ---- correlation + statistics from MFMA block-score tiles (16-bit inputs)
  * One call producing what fs_corr and fs_stats produce, for dtype bf16/f16,
- * D % 16 == 0, D <= 128, N <= 4096 (my_attn_v7.py:117-157, 190-208,
+ * D % 16 == 0, D <= 128, N <= 8192 (my_attn_v7.py:117-157, 190-208,
  * 301-363, 390-447, 54-72).  The tiles of S = q_b k_b^T (i >= j) are formed
  * on MFMA and every statistic is a fixed-order sum over them: the lag sums
  * corr_sum[h][t] = sum_i S[i][i-t] (the reference's FFT computes the same
@@ -201,7 +202,8 @@ FS_API int fs_scores_noalloc(const fs_scores_args* a, void* stream);
  *   column: col_mode 2, or col_mode 1 and stripe head: col_sel[h][j] && j <= i
  * with is_stripe[h] = mean_s(diag_var[h][s]) <= stripe_threshold (false when
  * stripe_all_diffuse or the mean is nan).  Output: blk_cnt[h][i] and the
- * selected j in ascending order at blk_idx[(h*N + i) * Nk ...]. */
+ * selected j in ascending order at blk_idx[(h*N + i) * Nk ...].  N <= 8192
+ * (D <= 256 with dyn_mode 1). */
 typedef struct {
   const void* q_b; const void* k_b;
   int dtype, Hq, Hk, N, Nk, D;

@@ -210,6 +210,8 @@ def test_selection_parity_c0(name, over):
     (16384, 4, 4, 128, torch.float16, dict(corr_threshold=0.5)),
     (32768, 8, 2, 128, torch.bfloat16, dict(correlation_selection_mode="topk")),
     (24000, 7, 1, 64, torch.bfloat16, dict(correlation_selection_mode="topk", correlation_topk_ratio=0.3)),
+    (300000, 4, 1, 64, torch.bfloat16, {}),                      # N = 4688 > 4096 blocks
+    (300000, 2, 1, 64, torch.bfloat16, dict(stripe_threshold=0.0)),   # diffuse heads' score panel at N = 4688
 ])
 def test_selection_parity_bf16(L, Hq, Hk, bs, dtype, over):
     _print_case("selection", L=L, Hq=Hq, Hk=Hk, bs=bs, dtype=dtype, over=over)
@@ -475,12 +477,12 @@ def test_full_length_c2_properties():
 
 
 def test_maximum_block_count_properties():
-    """The largest supported selection, N = 4096 blocks (L = 524288 at block
+    """The largest supported selection, N = 8192 blocks (L = 1048576 at block
     128): every row's list ascending, causal, with the sink block and the
     diagonal; selection deterministic; attention output finite."""
-    _print_case("max-blocks", L=4096 * 128, Hq=2, Hk=1)
+    _print_case("max-blocks", L=8192 * 128, Hq=2, Hk=1)
     g = torch.Generator(device=DEV).manual_seed(12)
-    L, Hq, Hk = 4096 * 128, 2, 1
+    L, Hq, Hk = 8192 * 128, 2, 1
     q = torch.randn(1, Hq, L, 128, device=DEV, generator=g, dtype=torch.bfloat16)
     k = torch.randn(1, Hk, L, 128, device=DEV, generator=g, dtype=torch.bfloat16)
     v = torch.randn(1, Hk, L, 128, device=DEV, generator=g, dtype=torch.bfloat16)
@@ -488,13 +490,13 @@ def test_maximum_block_count_properties():
     sel = select_blocks(q, k, **PROD)
     sel2 = select_blocks(q, k, **PROD)
     torch.cuda.synchronize()
-    assert sel.params.N == 4096
+    assert sel.params.N == 8192
     assert torch.equal(sel.blk_cnt, sel2.blk_cnt)
     cnt = sel.blk_cnt.cpu()
-    assert bool((cnt >= 1).all()) and bool((cnt <= torch.arange(1, 4097)[None, :]).all())
+    assert bool((cnt >= 1).all()) and bool((cnt <= torch.arange(1, 8193)[None, :]).all())
     idx = sel.blk_idx.view(torch.int16).cpu().to(torch.int64) & 0xFFFF
     for h in range(Hq):
-        for i in (0, 1, 2047, 4094, 4095):
+        for i in (0, 1, 4095, 4096, 8190, 8191):
             row = idx[h, i, : cnt[h, i]]
             assert int(row[0]) == 0 and int(row[-1]) == i and bool((row[1:] > row[:-1]).all())
     assert torch.equal(sel.dense_mask(), sel2.dense_mask())
@@ -504,12 +506,20 @@ def test_maximum_block_count_properties():
 
 
 def test_block_count_above_the_limit_is_rejected():
-    """N = 4097 blocks is past the selection kernels' limit: a clear error, no launch."""
-    _print_case("over-limit", L=4097 * 128)
-    L = 4097 * 128
+    """N = 8193 blocks is past the selection kernels' limit, and N = 4097 past
+    the fp32 path's (one LDS FFT of length 2N): clear errors, no launch."""
+    _print_case("over-limit", L=8193 * 128)
+    L = 8193 * 128
     q = torch.zeros(1, 1, L, 128, device=DEV, dtype=torch.bfloat16)
     k = torch.zeros(1, 1, L, 128, device=DEV, dtype=torch.bfloat16)
-    with pytest.raises(RuntimeError, match="exceed the selection kernels' maximum of 4096"):
+    with pytest.raises(RuntimeError, match="exceed the selection kernels' maximum of 8192"):
+        select_blocks(q, k, **PROD)
+        torch.cuda.synchronize()
+    del q, k
+    L = 4097 * 128
+    q = torch.zeros(1, 1, L, 128, device=DEV, dtype=torch.float32)
+    k = torch.zeros(1, 1, L, 128, device=DEV, dtype=torch.float32)
+    with pytest.raises(RuntimeError, match="maximum of 4096"):
         select_blocks(q, k, **PROD)
         torch.cuda.synchronize()
 

@@ -158,3 +158,20 @@ def test_noalloc_scores_rejects_sizes_past_its_static_buffer_without_gpu():
     a.Hq, a.Hk = 3, 2
     assert lib.fs_scores_noalloc(ctypes.byref(a), None) == -1
     assert b"fs_scores_noalloc: Hq=3" in lib.fs_last_error()
+
+
+def test_selection_block_limits_without_gpu():
+    """The 16-bit selection kernels take up to 8192 blocks (a diffuse head's
+    4-row score panel in LDS); the fp32 path's LDS FFT of length 2N up to 4096.
+    Past those, unsupported (-2) before any HIP call."""
+    lib = _lib.load()
+    sc = _lib.ScoresArgs(q_b=16, k_b=16, work=16, dtype=1, Hq=1, Hk=1, N=8193, D=128, n_cols=0, last_k=0)
+    assert lib.fs_scores(ctypes.byref(sc), None) == -2
+    assert b"N=8193 > 8192" in lib.fs_last_error()
+    se = _lib.SelectArgs(q_b=16, k_b=16, dtype=1, Hq=1, Hk=1, N=8193, Nk=8193, D=128, blk_cnt=16, blk_idx=16)
+    assert lib.fs_select(ctypes.byref(se), None) == -2
+    assert b"N=8193 > 8192" in lib.fs_last_error()
+    co = _lib.CorrArgs(q_b=16, k_b=16, dtype=0, Hq=1, Hk=1, N=4097, D=128, work=16, corr=16, corr_sum=16,
+                       keep_tau=16, corr_threshold=0.9)
+    assert lib.fs_corr(ctypes.byref(co), None) == -2
+    assert b"N=4097" in lib.fs_last_error()
