@@ -46,7 +46,8 @@ class XattnArgs(ctypes.Structure):
                 ("bs", c_int), ("norm", c_float), ("threshold", c_void_p), ("keep_sink", c_int),
                 ("sums", c_void_p), ("blk_cnt", c_void_p), ("blk_idx", c_void_p), ("work", c_void_p),
                 ("non_causal", c_int), ("torch_path", c_int), ("select_mode", c_int), ("perm", c_int * 16),
-                ("kdb", c_int), ("no_softmax", c_int), ("chunk", c_int), ("keep_recent", c_int)]
+                ("kdb", c_int), ("no_softmax", c_int), ("chunk", c_int), ("keep_recent", c_int),
+                ("head_group", c_int)]
 
 
 class FlexArgs(ctypes.Structure):

@@ -99,8 +99,9 @@ struct XScoreK {
   float* l;                     // [Hq][Lrq] row sum
   float* sums;                  // [Hq][Nb][Nb] block sums (values of T)
   float* pad_sum;               // [Hq][Nb] non-causal: the sum of every key block of the chunk padding
-  uint16_t* scores;             // [Hq][head_stride] the rounded scores, row tiles
+  uint16_t* scores;             // [hg][head_stride] the rounded scores of heads h0 .. h0+hg-1, row tiles
   int64_t head_stride;
+  int h0, hg;                   // the heads of this launch
 };
 
 __host__ __device__ inline int ximin(int a, int b) { return a < b ? a : b; }
@@ -146,8 +147,8 @@ __global__ __launch_bounds__(kXThreads) void xattn_scores_kernel(XScoreK a) {
   __shared__ __attribute__((aligned(16))) uint16_t lq[kXRows * kXD];   // Q'_j rows, 32 KiB
   __shared__ __attribute__((aligned(16))) uint16_t lk[kXKeys * kXD];   // K'_j rows
   const int nrt = (a.Lrq + kXRows - 1) / kXRows;
-  const int rt = nrt - 1 - (int)(blockIdx.x / a.Hq);                 // longest rows first
-  const int h = (int)(blockIdx.x % a.Hq);
+  const int rt = nrt - 1 - (int)(blockIdx.x / a.hg);                 // longest rows first
+  const int h = a.h0 + (int)(blockIdx.x % a.hg);
   const int hk = h / (a.Hq / a.Hk);
   const int r0 = rt * kXRows;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, hi = lane >> 5;
@@ -228,7 +229,7 @@ __global__ __launch_bounds__(kXThreads) void xattn_scores_kernel(XScoreK a) {
     if (row_ok) {
       // the rounded scores of this lane's row: four consecutive keys per 8-byte store
       const int NK = nct * kXKeys;
-      uint16_t* dst = a.scores + (int64_t)h * a.head_stride + tile_off + (int64_t)(row - r0) * NK;
+      uint16_t* dst = a.scores + (int64_t)(h - a.h0) * a.head_stride + tile_off + (int64_t)(row - r0) * NK;
 #pragma unroll
       for (int kk = 0; kk < kXKK; ++kk)
 #pragma unroll
@@ -285,8 +286,8 @@ __global__ __launch_bounds__(kXThreads) void xattn_sums_kernel(XScoreK a) {
   __shared__ float rm[kXRows], rl[kXRows];
   __shared__ int rok[kXRows];
   const int nrt = (a.Lrq + kXRows - 1) / kXRows;
-  const int rt = nrt - 1 - (int)(blockIdx.x / a.Hq);
-  const int h = (int)(blockIdx.x % a.Hq);
+  const int rt = nrt - 1 - (int)(blockIdx.x / a.hg);
+  const int h = a.h0 + (int)(blockIdx.x % a.hg);
   const int r0 = rt * kXRows;
   const int nr = min(a.Lrq, r0 + kXRows) - r0;       // a multiple of rpb
   const int NK = xnct(rt, a.Lrq, a.Lrk, a.causal, a.kdb) * kXKeys;
@@ -308,7 +309,8 @@ __global__ __launch_bounds__(kXThreads) void xattn_sums_kernel(XScoreK a) {
     }
     return __builtin_amdgcn_exp2f(x - rm[i]) * rl[i];
   };
-  const uint16_t* src = a.scores + (int64_t)h * a.head_stride + xoffset(rt, a.Lrq, a.Lrk, a.causal, a.kdb);
+  const uint16_t* src =
+      a.scores + (int64_t)(h - a.h0) * a.head_stride + xoffset(rt, a.Lrq, a.Lrk, a.causal, a.kdb);
   // eight consecutive keys per thread (one 16-byte load a row): a key block of
   // rbs >= 8 keys spans rbs / 8 neighbouring lanes
   const int gl = rbs / 8;
@@ -564,8 +566,13 @@ static size_t xattn_stats_bytes(int Hq, const XGeom& g) {
   return xalign((size_t)Hq * g.Lrq * 2 * sizeof(float) + (size_t)Hq * g.N * sizeof(float));
 }
 static size_t xattn_kaug_bytes(int Hk, const XGeom& g) { return g.aug ? xalign((size_t)Hk * g.Lp_blk * kXD * 2) : 0; }
+// heads whose scores the workspace holds at once (the passes run head group by head group)
+static int xattn_head_group(const fs_xattn_args* a) {
+  return a->head_group > 0 && a->head_group < a->Hq ? a->head_group : a->Hq;
+}
 static size_t xattn_work(const fs_xattn_args* a, const XGeom& g) {
-  return xattn_stats_bytes(a->Hq, g) + xattn_kaug_bytes(a->Hk, g) + (size_t)a->Hq * g.head_stride * sizeof(uint16_t);
+  return xattn_stats_bytes(a->Hq, g) + xattn_kaug_bytes(a->Hk, g) +
+         (size_t)xattn_head_group(a) * g.head_stride * sizeof(uint16_t);
 }
 
 }  // namespace fs
@@ -589,6 +596,7 @@ static int xattn_check(const fs_xattn_args* a, bool need_buffers) {
                      a->stride);
   FS_CHECK_ARG(a->norm > 0.f, "fs_xattn: norm must be positive");
   FS_CHECK_ARG(a->select_mode >= 0 && a->select_mode <= 4, "fs_xattn: select_mode %d unknown", a->select_mode);
+  FS_CHECK_ARG(a->head_group >= 0, "fs_xattn: negative head_group");
   if (a->torch_path && a->select_mode == 2) {
     unsigned seen = 0;
     for (int j = 0; j < a->stride; ++j) {
@@ -672,25 +680,31 @@ extern "C" int fs_xattn(const fs_xattn_args* a, void* stream) {
     k.k_sh = a->k_sh; k.k_sl = a->k_sl;
     k.Lk_tok = a->L;
   }
-  const unsigned grid = (unsigned)(a->Hq * ((g.Lrq + kXRows - 1) / kXRows));
-  if (a->torch_path) {
-    if (bf) {
-      xattn_scores_kernel<bf16_t, true><<<grid, kXThreads, 0, s>>>(k);
-      xattn_sums_kernel<bf16_t, true><<<grid, kXThreads, 0, s>>>(k);
+  // the score and block-sum passes, head group by head group through the same scores buffer
+  const int hg = xattn_head_group(a);
+  for (int h0 = 0; h0 < a->Hq; h0 += hg) {
+    k.h0 = h0;
+    k.hg = a->Hq - h0 < hg ? a->Hq - h0 : hg;
+    const unsigned grid = (unsigned)(k.hg * ((g.Lrq + kXRows - 1) / kXRows));
+    if (a->torch_path) {
+      if (bf) {
+        xattn_scores_kernel<bf16_t, true><<<grid, kXThreads, 0, s>>>(k);
+        xattn_sums_kernel<bf16_t, true><<<grid, kXThreads, 0, s>>>(k);
+      } else {
+        xattn_scores_kernel<f16_t, true><<<grid, kXThreads, 0, s>>>(k);
+        xattn_sums_kernel<f16_t, true><<<grid, kXThreads, 0, s>>>(k);
+      }
     } else {
-      xattn_scores_kernel<f16_t, true><<<grid, kXThreads, 0, s>>>(k);
-      xattn_sums_kernel<f16_t, true><<<grid, kXThreads, 0, s>>>(k);
+      if (bf) {
+        xattn_scores_kernel<bf16_t, false><<<grid, kXThreads, 0, s>>>(k);
+        xattn_sums_kernel<bf16_t, false><<<grid, kXThreads, 0, s>>>(k);
+      } else {
+        xattn_scores_kernel<f16_t, false><<<grid, kXThreads, 0, s>>>(k);
+        xattn_sums_kernel<f16_t, false><<<grid, kXThreads, 0, s>>>(k);
+      }
     }
-  } else {
-    if (bf) {
-      xattn_scores_kernel<bf16_t, false><<<grid, kXThreads, 0, s>>>(k);
-      xattn_sums_kernel<bf16_t, false><<<grid, kXThreads, 0, s>>>(k);
-    } else {
-      xattn_scores_kernel<f16_t, false><<<grid, kXThreads, 0, s>>>(k);
-      xattn_sums_kernel<f16_t, false><<<grid, kXThreads, 0, s>>>(k);
-    }
+    if (int rc = fs_host::launch_status("fs_xattn (scores)")) return rc;
   }
-  if (int rc = fs_host::launch_status("fs_xattn (scores)")) return rc;
   XSelK sk{};
   sk.sums = a->sums;
   sk.pad_sum = k.pad_sum;

@@ -89,14 +89,18 @@ def default_chunk_size(k_len: int) -> int:
 def xattn_select(query_states: torch.Tensor, key_states: torch.Tensor, *, stride: int = 8, threshold=0.9,
                  norm: float = 1.0, block_size: int = 128, keep_sink: bool = False, keep_recent: bool = False,
                  causal: bool = True, use_triton: bool = True, select_mode: str = "inverse", kdb: int = 1,
-                 softmax: bool = True, chunk_size: int | None = None, perm=None) -> XSelection:
+                 softmax: bool = True, chunk_size: int | None = None, perm=None,
+                 max_workspace_bytes: int = 16 << 30) -> XSelection:
     """The block selection of xattn_estimate (Xattention.py:14-303) as block
     lists.  q [1,Hq,L,D], k [1,Hq or Hkv,L,D] on the GPU (bf16/f16, D = 128).
     ``chunk_size`` (tokens; default Xattention_prefill's) sets the zero padding
     the non-causal softmax and the torch path's masks see.  ``perm``: the
     "random" reshaping's permutation; by default torch.randperm(stride), drawn
     where the reference draws it.  On the Triton path select_mode and softmax
-    are not used, as in the reference."""
+    are not used, as in the reference.  The stored scores (about (L/S)^2
+    bytes per head) are formed for as many heads at a time as fit
+    ``max_workspace_bytes`` (one head at least); the result does not depend
+    on the grouping."""
     q = _check_layout(query_states)
     k = _check_layout(key_states)
     assert q.shape[0] == 1 and k.shape[0] == 1, "batch size 1 only"          # Xattention.py:361
@@ -135,6 +139,14 @@ def xattn_select(query_states: torch.Tensor, key_states: torch.Tensor, *, stride
         no_softmax=int(not use_triton and not softmax), chunk=chunk, keep_recent=int(bool(keep_recent)))
     args.perm[:] = pm
     lib = _lib.load()
+    hg = Hq
+    while hg > 1:
+        args.head_group = hg
+        if lib.fs_xattn_work_bytes(ctypes.byref(args)) <= max_workspace_bytes:
+            break
+        hg -= 1
+    groups = -(-Hq // hg)
+    args.head_group = -(-Hq // groups)            # the same heads per group, as few groups as fit
     work = torch.empty(max(1, lib.fs_xattn_work_bytes(ctypes.byref(args))), dtype=torch.uint8, device=dev)
     args.work = work.data_ptr()
     _lib.call("fs_xattn", args)

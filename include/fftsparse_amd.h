@@ -253,9 +253,9 @@ FS_API int fs_select(const fs_select_args* a, void* stream);
  * block; keep_recent: the diagonal) and sums [Hq][N][N] (causal: its lower
  * triangle).  threshold: device array of Hq float64 values.  work:
  * fs_xattn_work_bytes(a) bytes of device scratch: the row statistics, K' for
- * double / triple and the rounded scores A of the keys each row sees (about
- * Hq (L/S)^2 bytes causal, twice that non-causal: 8.7 / 17.2 GB at
- * L = 131072, S = 8, 32 heads).  Zero-initialised trailing fields give the
+ * double / triple and the rounded scores A of the keys each row sees, for
+ * head_group heads at a time (about (L/S)^2 bytes per head causal, twice
+ * that non-causal: 8.7 / 17.2 GB for 32 heads at L = 131072, S = 8).  Zero-initialised trailing fields give the
  * Triton causal path.  bf16/f16, D = 128, bs = 128, stride 4, 8 or 16,
  * N <= 4096 and chunk-padded blocks <= 4096. */
 typedef struct {
@@ -277,6 +277,8 @@ typedef struct {
   int no_softmax;       /* torch path: softmax=False */
   int chunk;            /* chunk_size in tokens (non-causal and torch path; 0: none) */
   int keep_recent;
+  int head_group;       /* heads whose scores the workspace holds at once (0: all): the score
+                           and block-sum passes run group by group, bounding the workspace */
 } fs_xattn_args;
 FS_API size_t fs_xattn_work_bytes(const fs_xattn_args* a);
 FS_API int fs_xattn(const fs_xattn_args* a, void* stream);

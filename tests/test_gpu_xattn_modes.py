@@ -15,9 +15,12 @@ same mask.
 """
 from __future__ import annotations
 
+import ctypes
+
 import pytest
 import torch
 
+from fftsparse_amd import _lib
 from fftsparse_amd.synth import make_qkv
 from fftsparse_amd.xattn import Xattention_prefill, default_chunk_size, xattn_estimate, xattn_select
 from oracle import v7
@@ -172,3 +175,30 @@ def test_torch_path_prefill_kdb_attention():
     err = (out[0].transpose(0, 1).float().cpu() - ref).abs()
     print(f"  max_abs={err.max().item():.3e} mean_abs={err.mean().item():.3e}", flush=True)
     assert err.max().item() <= 2e-2 and err.mean().item() <= 1e-3
+
+
+@pytest.mark.parametrize("causal,use_triton", [(True, True), (False, True), (True, False)])
+def test_head_groups_give_the_same_lists(causal, use_triton):
+    """A workspace too small for every head's scores: the passes run head group
+    by head group (here 1 head, and 2 when 3 of the 4 fit) and give the lists,
+    sums and decisions of one pass over all heads."""
+    L = 5000
+    print(f"[case] xattn-mode head groups causal={causal} triton={use_triton} L={L}", flush=True)
+    q, k, _ = make_qkv(L, 4, 2, dtype=torch.bfloat16, seed=50)
+    qg, kg = q.to(DEV), k.to(DEV)
+    kw = dict(stride=8, threshold=0.9, causal=causal, use_triton=use_triton)
+    full = xattn_select(qg, kg, **kw)
+    one = xattn_select(qg, kg, max_workspace_bytes=1, **kw)
+    lib = _lib.load()
+
+    def work(hg):
+        a = _lib.XattnArgs(dtype=1, Hq=4, Hk=2, L=L, D=128, stride=8, bs=128, norm=1.0, non_causal=int(not causal),
+                           torch_path=int(not use_triton), chunk=default_chunk_size(L), head_group=hg)
+        return lib.fs_xattn_work_bytes(ctypes.byref(a))
+    assert work(1) < work(3) < work(4)
+    three = xattn_select(qg, kg, max_workspace_bytes=work(3), **kw)        # groups of 2 heads (3 do not divide 4)
+    torch.cuda.synchronize()
+    for x in (one, three):
+        assert torch.equal(full.blk_cnt, x.blk_cnt)
+        assert torch.equal(full.dense_mask(), x.dense_mask())
+        assert torch.equal(full.sums, x.sums)
