@@ -153,15 +153,29 @@ def cpu_baseline_xattn(q, k, v, args, bs, nnz_total, sel):
     bounded sample: the selection of one head over the first 16384 tokens,
     scaled by the reshaped-score count to all heads and the full length (the
     estimate is quadratic in L), and fp32 block-sparse attention over the first
-    query head's selected tiles, scaled by the tile count."""
+    query head's selected tiles, scaled by the tile count.  The same sample
+    checks the GPU's selection.  Returns (baseline, parity)."""
     import torch
     from oracle import v7, xattn as xo
     threads = torch.get_num_threads()
     Ls = min(16384, q.shape[2])
     qs, ks = q[:, :1, :Ls].cpu(), k[:, :1, :Ls].cpu()
     t0 = time.perf_counter()
-    xo.xattn_mask(qs, ks, stride=args.xattn_stride, threshold=args.threshold, block_size=bs)
+    ref_mask, _, margin = xo.xattn_mask(qs, ks, stride=args.xattn_stride, threshold=args.threshold, block_size=bs)
     t_s = time.perf_counter() - t0
+    # parity on the same sample: the GPU's selection of head 0 over the first Ls tokens
+    from fftsparse_amd.xattn import xattn_select
+    g = xattn_select(q[:, :1, :Ls], k[:, :1, :Ls], stride=args.xattn_stride, threshold=args.threshold,
+                     block_size=bs).dense_mask().cpu()
+    n = ref_mask.shape[1]
+    tril = torch.tril(torch.ones(n, n, dtype=torch.bool))
+    diff = (g != ref_mask) & tril
+    unexc = int((diff & ~(margin[:, :n, :n].abs() <= 1e-3)).sum())
+    total = int(tril.sum())
+    parity = {"block_match": round((total - unexc) / total, 6), "block_exact": round(1 - int(diff.sum()) / total, 6),
+              "unexcused": unexc, "sample": f"query head 0 over the first {Ls} tokens, oracle/xattn.py",
+              "bar": "exact or within 1e-3 of the required mass >= 0.999",
+              "pass": bool((total - unexc) / total >= 0.999)}
     L, Hq = q.shape[2], q.shape[1]
     t_sel = t_s * (L / Ls) ** 2 * Hq
     mask = sel.dense_mask().cpu()
@@ -180,7 +194,7 @@ def cpu_baseline_xattn(q, k, v, args, bs, nnz_total, sel):
                    f"{nnz_total / max(1, tiles):.1f} to {nnz_total} tiles"),
         "select_ms": round(t_sel * 1e3, 1), "attn_ms_scaled": round(t_att * 1e3, 1),
         "cpu_model": _cpu_model(), "os_cpu_count": os.cpu_count(),
-    }
+    }, parity
 
 
 def pmc_traffic(kernel, config):
@@ -213,7 +227,8 @@ def cpu_baseline_flex(q, k, v, args, bs, nnz_total, sel, sample_heads=None):
     selection of the first ``sample_heads`` query heads (all by default; whole
     KV groups) over the full length, scaled by the head count (heads are
     independent), and fp32 block-sparse attention over the first query head's
-    selected tiles, scaled by the tile count."""
+    selected tiles, scaled by the tile count.  The timed lists of the sampled
+    heads are checked against the oracle's.  Returns (baseline, parity)."""
     import torch
     from oracle import flex as fo, v7
     threads = torch.get_num_threads()
@@ -223,10 +238,20 @@ def cpu_baseline_flex(q, k, v, args, bs, nnz_total, sel, sample_heads=None):
     qs = q[:, :hs].cpu().transpose(1, 2).contiguous()
     ks = k[:, :hs // g].cpu().transpose(1, 2).contiguous()
     t0 = time.perf_counter()
-    fo.active_blocks(qs, ks, bs, args.flex_gamma, args.flex_tau)
+    ref = fo.active_blocks(qs, ks, bs, args.flex_gamma, args.flex_tau)
     t_s = time.perf_counter() - t0
     t_sel = t_s * Hq / hs
     mask = sel.dense_mask().cpu()
+    # parity of the timed lists on the sampled heads: exact block decisions (the
+    # GPU tests also excuse near ties of the profiles; here the exact share)
+    nb = mask.shape[1]
+    tril = torch.tril(torch.ones(nb, nb, dtype=torch.bool))
+    diff = (mask[:hs] != ref.mask) & tril
+    total = int(tril.sum()) * hs
+    exact = 1 - int(diff.sum()) / total
+    parity = {"block_exact": round(exact, 6), "differing": int(diff.sum()),
+              "sample": f"query heads 0..{hs - 1} at full length, oracle/flex.py",
+              "bar": "exact >= 0.99 (the GPU tests: exact or a near tie >= 0.999)", "pass": bool(exact >= 0.99)}
     heads = [0]
     tiles = int(mask[heads].sum())
     qc, kc, vc = q.cpu(), k.cpu(), v.cpu()
@@ -241,7 +266,7 @@ def cpu_baseline_flex(q, k, v, args, bs, nnz_total, sel, sample_heads=None):
                    f"({tiles} tiles, {t_a:.1f} s) scaled x{nnz_total / max(1, tiles):.1f} to {nnz_total} tiles"),
         "select_ms": round(t_sel * 1e3, 1), "attn_ms_scaled": round(t_att * 1e3, 1),
         "cpu_model": _cpu_model(), "os_cpu_count": os.cpu_count(),
-    }
+    }, parity
 
 
 def main():
@@ -394,9 +419,9 @@ def main():
     if not args.no_cpu:
         torch.cuda.synchronize()
         if xattn:
-            cpu = cpu_baseline_xattn(q, k, v, args, bs, nnz, sel)
+            cpu, parity = cpu_baseline_xattn(q, k, v, args, bs, nnz, sel)
         elif flex:
-            cpu = cpu_baseline_flex(q, k, v, args, bs, nnz, sel)
+            cpu, parity = cpu_baseline_flex(q, k, v, args, bs, nnz, sel)
         else:
             cpu, parity = cpu_baseline(q, k, v, kw, bs, nnz, args.cpu_heads, sel=sel, out=out)
 
