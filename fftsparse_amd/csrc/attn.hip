@@ -585,7 +585,6 @@ void bsattn_kernel(AttnKArgs a) {
         for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
     }
   };
-  __builtin_amdgcn_s_waitcnt(0);                   // retire the Q loads (see below)
   // Pipeline with P V deferred by one tile.  Iteration t: wait for K(t+1)
   // and V(t-1), one barrier, copy K(t+2) (into the buffer of K(t)) and V(t)
   // (into that of V(t-2)); then one straight-line block with S(t+1) and
@@ -653,6 +652,9 @@ void bsattn_kernel(AttnKArgs a) {
     kb0 = kb1;
     kb1 = kb2;
   };
+  // The first two K tiles are requested before the Q loads are waited for,
+  // so the two latencies overlap; one wait then retires both (the loop's own
+  // waits then find no register load of Q outstanding).
   if (cnt > 0) {
     kb0 = key_of(0);
     issue_k(kb0, 0);
@@ -660,7 +662,9 @@ void bsattn_kernel(AttnKArgs a) {
       kb1 = key_of(1);
       issue_k(kb1, 1);
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  if (cnt > 0) {
     __builtin_amdgcn_s_barrier();
     compute_s(0, sa);
     mask_only(kb0, sa);
