@@ -23,16 +23,18 @@
 // float32 softmax (or exp) rounded to dtype, and the block sums are two sums
 // rounded to dtype: over a block's keys, then over its rows.
 //
-// xattn_scores_kernel<T, TP>: one workgroup (4 waves, 32 reshaped rows each)
-// per (head, 128 reshaped rows), longest rows first; key tiles of 128 reshaped
-// keys up to the last one the tile's rows see.  For each tile and each j < S
-// the workgroup copies the 128 query token rows and the 128 key token rows of
-// stage j into LDS with global -> LDS copies (no register staging; rows past
-// the sequence zeroed after; 256-byte rows, 16-byte chunk c of row r at
-// c ^ (r & 15)) and accumulates S^T = K' Q'^T with v_mfma_f32_32x32x16.  It
-// keeps each row's running max and exp sum (the reference's first loop) and
-// stores the scores, rounded to the input dtype, row tile by row tile (tile rt
-// holds its 128 rows x 128 nct(rt) keys).
+// xattn_scores_wide_kernel<T, TP>: one workgroup (8 waves: 4 groups of 64
+// reshaped rows x 2 groups of 128 keys) per (head, 256 reshaped rows), longest
+// rows first; key tiles of 256 reshaped keys up to the last one the tile's rows
+// see.  For each tile, each j < S and each 64-dim half, the workgroup copies
+// the 256 query token rows and the 256 key token rows of that stage into LDS
+// with global -> LDS copies (two buffers: the next stage's copies land while
+// this stage's MFMAs run; rows past the sequence zeroed after; 128-byte rows,
+// 16-byte chunk c of row r at c ^ (r & 7)) and accumulates S^T = K' Q'^T with
+// v_mfma_f32_32x32x16.  It keeps each row's running max and exp sum (the
+// reference's first loop), merged over the two key halves at the end, and
+// stores the scores, rounded to the input dtype, in tiles of 128 rows (row
+// tile rt holds its 128 rows x 128 nct(rt) keys).
 // xattn_sums_kernel<T, TP>: one workgroup per (head, 128 reshaped rows)
 // streams the stored scores (threads along the keys, rows in order), forms p
 // and adds it over each block's rows and, by xor shuffles, its keys (the
@@ -142,141 +144,199 @@ __device__ __forceinline__ float xexp(float x) {
   return __builtin_amdgcn_exp2f(x);
 }
 
+// The score pass: one workgroup of 8 waves per (head, 256 reshaped rows), key
+// tiles of 256 reshaped keys up to the last key the rows see.  Wave w computes rows 64 (w % 4) .. +63 against keys 128 (w / 4) .. +127
+// of the tile (8 v_mfma_f32_32x32x16 tiles).  Each stage copies the 256 query
+// token rows and the 256 key token rows of one token offset j, one 64-dim half
+// at a time (128-byte LDS rows, chunk c of row r at c ^ (r & 7)), into one of
+// two buffers, so a stage's copies land while the previous stage's MFMAs run;
+// a 256 x 256 tile reads half the operand bytes per flop of a 128 x 128 one.
+// The scores are stored in tiles of 128 rows (the layout the block-sum pass
+// reads), and each row's running max / sum of the two key halves are merged at
+// the end.
+constexpr int kXWide = 256;
+constexpr int kXWideThreads = 512;
+constexpr int kXHalf = 64;
 template <typename T, bool TP>
-__global__ __launch_bounds__(kXThreads) void xattn_scores_kernel(XScoreK a) {
-  __shared__ __attribute__((aligned(16))) uint16_t lq[kXRows * kXD];   // Q'_j rows, 32 KiB
-  __shared__ __attribute__((aligned(16))) uint16_t lk[kXKeys * kXD];   // K'_j rows
-  const int nrt = (a.Lrq + kXRows - 1) / kXRows;
-  const int rt = nrt - 1 - (int)(blockIdx.x / a.hg);                 // longest rows first
+__global__ __launch_bounds__(kXWideThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void xattn_scores_wide_kernel(XScoreK a) {
+  // [buffer][Q' rows 0..255, then K' rows 0..255][64 dims]: 2 x 64 KiB
+  __shared__ __attribute__((aligned(1024))) uint16_t lds[2][2 * kXWide * kXHalf];
+  const int nrt = (a.Lrq + kXWide - 1) / kXWide;
+  const int R = nrt - 1 - (int)(blockIdx.x / a.hg);                  // longest rows first
   const int h = a.h0 + (int)(blockIdx.x % a.hg);
   const int hk = h / (a.Hq / a.Hk);
-  const int r0 = rt * kXRows;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, hi = lane >> 5;
-  const int row = r0 + wave * 32 + l32;            // this lane's reshaped row (column of S^T)
+  const int rg = wave & 3, kg = wave >> 2;          // 64-row group, 128-key group
+  const int r0 = R * kXWide, wr0 = r0 + rg * 64;
   const uint16_t* qh = a.q + (int64_t)h * a.q_sh;
   const uint16_t* kh = a.k + (int64_t)hk * a.k_sh;
   const int S = a.S, QS = a.QS;
-  const int nct = xnct(rt, a.Lrq, a.Lrk, a.causal, a.kdb);
-  const int64_t tile_off = xoffset(rt, a.Lrq, a.Lrk, a.causal, a.kdb);   // once, before the key loop
-  const bool row_ok = row < a.Lrq;
+  const int last_row = min(a.Lrq, r0 + kXWide) - 1;
+  int last_key = a.Lrk - 1;
+  if (a.causal) last_key = min(last_key, last_row * a.kdb + a.kdb - 1);
+  const int nct = last_key / kXWide + 1;           // 256-key tiles
+  // this wave's rows lie in one 128-row tile of the stored layout
+  const int rt = wr0 / kXRows;
+  const int NK = xnct(rt, a.Lrq, a.Lrk, a.causal, a.kdb) * kXKeys;
+  uint16_t* dst_base = a.scores + (int64_t)(h - a.h0) * a.head_stride + xoffset(rt, a.Lrq, a.Lrk, a.causal, a.kdb);
   const bool stats = !TP || a.softmax;
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&lds[0][0]);
 
-  float m_run = -INFINITY, l_run = 0.f;
+  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+  f32x16_t acc[kXKK][2];
+#pragma unroll
+  for (int kk = 0; kk < kXKK; ++kk)
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[kk][rr][r] = 0.f;
 
-  for (int ct = 0; ct < nct; ++ct) {
-    const int n0 = ct * kXKeys;
-    f32x16_t acc[kXKK];
+  // stage s = (ct S + j) 2 + dh: key tile ct, token offset j, dims 64 dh .. +63, buffer s & 1.
+  // 512 rows of 128 bytes = 64 regions of 1 KiB (8 rows); waves 0-3 copy Q', 4-7 K'
+  auto issue = [&](int s) {
+    const int dh = s & 1, sj = s >> 1, ct = sj / S, j = sj - ct * S;
+    const int oj = (int)((a.qorder >> (4 * j)) & 15);
+    const uint32_t lb = lds0 + (uint32_t)((s & 1) * 2 * kXWide * kXHalf * 2);
 #pragma unroll
-    for (int kk = 0; kk < kXKK; ++kk)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[kk][r] = 0.f;
-    for (int j = 0; j < S; ++j) {
-      const int oj = (int)((a.qorder >> (4 * j)) & 15);
-      __syncthreads();                             // previous stage consumed
-      // 1 KiB regions of 4 LDS rows: lane l fills slot l % 16 of row 4R + l / 16
-      // with the token row's chunk (l % 16) ^ (row & 15); rows past the
-      // sequence read its last row here and are zeroed below
-      const uint32_t lq0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lq);
-      const uint32_t lk0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lk);
-      const int wv = __builtin_amdgcn_readfirstlane(wave);   // wave-uniform: the copies' LDS bases
-      constexpr int QR = kXRows / 4 / 4, KR = kXKeys / 4 / 4;   // regions per wave
-#pragma unroll
-      for (int i = 0; i < QR; ++i) {
-        const int R = wv * QR + i, rr = 4 * R + (lane >> 4), c = (lane & 15) ^ (rr & 15);
+    for (int i = 0; i < 8; ++i) {
+      const int Rg = wv * 8 + i, rr = 8 * Rg + (lane >> 3), c = (lane & 7) ^ (rr & 7);
+      if (wv < 4) {
         const int t = min((r0 + rr) * QS + oj, a.Lq_tok - 1);
-        xdma16(lq0 + R * 1024, qh, (uint32_t)(t * a.q_sl + c * 8) * 2u);
+        xdma16(lb + Rg * 1024, qh, (uint32_t)(t * a.q_sl + dh * kXHalf + c * 8) * 2u);
+      } else {
+        const int t = min((ct * kXWide + rr - kXWide) * S + j, a.Lk_tok - 1);
+        xdma16(lb + Rg * 1024, kh, (uint32_t)(t * a.k_sl + dh * kXHalf + c * 8) * 2u);
       }
+    }
+  };
+  auto epilogue = [&](int ct) {
+    const int n0 = ct * kXWide + kg * kXKeys;        // this wave's first key
 #pragma unroll
-      for (int i = 0; i < KR; ++i) {
-        const int R = wv * KR + i, cr = 4 * R + (lane >> 4), c = (lane & 15) ^ (cr & 15);
-        const int t = min((n0 + cr) * S + j, a.Lk_tok - 1);
-        xdma16(lk0 + R * 1024, kh, (uint32_t)(t * a.k_sl + c * 8) * 2u);
-      }
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      __syncthreads();
-      if ((r0 + kXRows - 1) * QS + oj >= a.Lq_tok || (n0 + kXKeys - 1) * S + j >= a.Lk_tok) {
-        // this stage reaches past the sequence: those rows are zero
-        for (int e = tid; e < (kXRows + kXKeys) * 16; e += kXThreads) {
-          const int r = e >> 4, ch = e & 15;
-          if (r < kXRows) {
-            if ((r0 + r) * QS + oj >= a.Lq_tok) *reinterpret_cast<uint4*>(lq + r * kXD + ch * 8) = make_uint4(0, 0, 0, 0);
-          } else {
-            const int cr = r - kXRows;
-            if ((n0 + cr) * S + j >= a.Lk_tok) *reinterpret_cast<uint4*>(lk + cr * kXD + ch * 8) = make_uint4(0, 0, 0, 0);
+    for (int rr = 0; rr < 2; ++rr) {
+      const int row = wr0 + rr * 32 + l32;
+      const bool row_ok = row < a.Lrq;
+      auto valid = [&](int kk, int r) { return row_ok && xkey_ok<TP>(a, row, n0 + kk * 32 + (r >> 2) * 8 + hi * 4 + (r & 3)); };
+      auto xval = [&](int kk, int r) { return xscaled<T, TP>(a, acc[kk][rr][r]); };
+      if (row_ok && n0 < NK) {
+        uint16_t* dst = dst_base + (int64_t)(row - rt * kXRows) * NK;
+#pragma unroll
+        for (int kk = 0; kk < kXKK; ++kk)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            uint32_t w[2];
+#pragma unroll
+            for (int e = 0; e < 2; ++e)
+              w[e] = (uint32_t)__builtin_bit_cast(uint16_t, Conv<T>::store(acc[kk][rr][g * 4 + 2 * e])) |
+                     ((uint32_t)__builtin_bit_cast(uint16_t, Conv<T>::store(acc[kk][rr][g * 4 + 2 * e + 1])) << 16);
+            *reinterpret_cast<uint2*>(dst + n0 + kk * 32 + g * 8 + hi * 4) = make_uint2(w[0], w[1]);
           }
-        }
-        __syncthreads();
       }
-
-      const int qr = wave * 32 + l32;
-#pragma unroll
-      for (int st = 0; st < kXD / 16; ++st) {
-        const uint4 bq = *reinterpret_cast<const uint4*>(lq + qr * kXD + (((2 * st + hi) ^ (qr & 15)) << 3));
-#pragma unroll
-        for (int kk = 0; kk < kXKK; ++kk) {
-          const int kr = kk * 32 + l32;
-          const uint4 ak = *reinterpret_cast<const uint4*>(lk + kr * kXD + (((2 * st + hi) ^ (kr & 15)) << 3));
-          acc[kk] = XMma<T>::mma(ak, bq, acc[kk]);
-        }
-      }
-    }
-
-    // ---- epilogue: lane holds keys n0 + 32 kk + (r/4) 8 + hi 4 + r%4 of its row;
-    // whether the row sees a key and its scaled score are recomputed from the
-    // accumulator where used, so no tile-sized arrays stay live
-    auto valid = [&](int kk, int r) { return row_ok && xkey_ok<TP>(a, row, n0 + kk * 32 + (r >> 2) * 8 + hi * 4 + (r & 3)); };
-    auto xval = [&](int kk, int r) { return xscaled<T, TP>(a, acc[kk][r]); };
-    if (row_ok) {
-      // the rounded scores of this lane's row: four consecutive keys per 8-byte store
-      const int NK = nct * kXKeys;
-      uint16_t* dst = a.scores + (int64_t)(h - a.h0) * a.head_stride + tile_off + (int64_t)(row - r0) * NK;
-#pragma unroll
-      for (int kk = 0; kk < kXKK; ++kk)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          uint32_t w[2];
-#pragma unroll
-          for (int e = 0; e < 2; ++e)
-            w[e] = (uint32_t)__builtin_bit_cast(uint16_t, Conv<T>::store(acc[kk][g * 4 + 2 * e])) |
-                   ((uint32_t)__builtin_bit_cast(uint16_t, Conv<T>::store(acc[kk][g * 4 + 2 * e + 1])) << 16);
-          *reinterpret_cast<uint2*>(dst + n0 + kk * 32 + g * 8 + hi * 4) = make_uint2(w[0], w[1]);
-        }
-    }
-    if (stats) {
-      float mx = -INFINITY;
-#pragma unroll
-      for (int kk = 0; kk < kXKK; ++kk)
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          if (valid(kk, r)) mx = fmaxf(mx, xval(kk, r));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));      // the row's other keys sit in lane ^ 32
-      const float m_new = fmaxf(m_run, mx);
-      if (m_new > -INFINITY) {
-        float s = 0.f;
+      if (stats) {
+        float mx = -INFINITY;
 #pragma unroll
         for (int kk = 0; kk < kXKK; ++kk)
 #pragma unroll
           for (int r = 0; r < 16; ++r)
-            if (valid(kk, r)) s += xexp<TP>(xval(kk, r) - m_new);
-        l_run = l_run * xexp<TP>(m_run - m_new) + s;
-        m_run = m_new;
+            if (valid(kk, r)) mx = fmaxf(mx, xval(kk, r));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));    // the row's other keys sit in lane ^ 32
+        const float m_new = fmaxf(m_run[rr], mx);
+        if (m_new > -INFINITY) {
+          float sm = 0.f;
+#pragma unroll
+          for (int kk = 0; kk < kXKK; ++kk)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+              if (valid(kk, r)) sm += xexp<TP>(xval(kk, r) - m_new);
+          l_run[rr] = l_run[rr] * xexp<TP>(m_run[rr] - m_new) + sm;
+          m_run[rr] = m_new;
+        }
+      }
+#pragma unroll
+      for (int kk = 0; kk < kXKK; ++kk)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[kk][rr][r] = 0.f;
+    }
+  };
+
+  const int nst = nct * S * 2;
+  issue(0);
+  for (int s = 0; s < nst; ++s) {
+    const int dh = s & 1, sj = s >> 1, ct = sj / S, j = sj - ct * S;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's copies of stage s
+    __syncthreads();                               // every wave's copies landed; stage s-1 done
+    if (s + 1 < nst) issue(s + 1);                 // into the buffer stage s-1 used
+    const uint16_t* qb = lds[s & 1];
+    const uint16_t* kb = lds[s & 1] + kXWide * kXHalf;
+    const int oj = (int)((a.qorder >> (4 * j)) & 15);
+    if ((r0 + kXWide - 1) * QS + oj >= a.Lq_tok || (ct * kXWide + kXWide - 1) * S + j >= a.Lk_tok) {
+      // this stage reaches past the sequence: those rows are zero
+      uint16_t* w = lds[s & 1];
+      for (int e = tid; e < 2 * kXWide * 8; e += kXWideThreads) {
+        const int r = e >> 3, ch = e & 7;
+        const bool past = r < kXWide ? (r0 + r) * QS + oj >= a.Lq_tok
+                                     : (ct * kXWide + r - kXWide) * S + j >= a.Lk_tok;
+        if (past) *reinterpret_cast<uint4*>(w + r * kXHalf + ch * 8) = make_uint4(0, 0, 0, 0);
+      }
+      __syncthreads();
+    }
+#pragma unroll
+    for (int st = 0; st < kXHalf / 16; ++st) {
+      uint4 bq[2];
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr) {
+        const int row = rg * 64 + rr * 32 + l32;
+        bq[rr] = *reinterpret_cast<const uint4*>(qb + row * kXHalf + (((2 * st + hi) ^ (row & 7)) << 3));
+      }
+#pragma unroll
+      for (int kk = 0; kk < kXKK; ++kk) {
+        const int key = kg * kXKeys + kk * 32 + l32;
+        const uint4 ak = *reinterpret_cast<const uint4*>(kb + key * kXHalf + (((2 * st + hi) ^ (key & 7)) << 3));
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) acc[kk][rr] = XMma<T>::mma(ak, bq[rr], acc[kk][rr]);
       }
     }
+    if (dh == 1 && j == S - 1) epilogue(ct);
   }
-  float lt = l_run + __shfl_xor(l_run, 32, 64);
-  if (stats && a.npad > 0) {
-    // the chunk padding's keys (zero rows of K) score 0
-    const float m2 = fmaxf(m_run, 0.f);
-    lt = lt * xexp<TP>(m_run - m2) + (float)a.npad * xexp<TP>(-m2);
-    m_run = m2;
+
+  // ---- each row's two key halves: lanes l and l ^ 32, then the two key-group waves through LDS
+  __syncthreads();
+  float* xm = reinterpret_cast<float*>(&lds[0][0]);   // [256 rows][2 halves] max, then sum
+  float* xl = xm + 2 * kXWide;
+#pragma unroll
+  for (int rr = 0; rr < 2; ++rr) {
+    const int lr = rg * 64 + rr * 32 + l32;
+    const float lt = l_run[rr] + __shfl_xor(l_run[rr], 32, 64);
+    if (hi == 0) {
+      xm[lr * 2 + kg] = m_run[rr];
+      xl[lr * 2 + kg] = lt;
+    }
   }
-  if (!stats) {
-    m_run = 0.f;
-    lt = 1.f;
-  }
-  if (row_ok && hi == 0) {
-    a.m[(int64_t)h * a.Lrq + row] = m_run;
-    a.l[(int64_t)h * a.Lrq + row] = lt;
+  __syncthreads();
+  if (kg == 0 && hi == 0) {
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+      const int lr = rg * 64 + rr * 32 + l32, row = r0 + lr;
+      if (row >= a.Lrq) continue;
+      float m, lt;
+      if (stats) {
+        const float m0 = xm[lr * 2], m1 = xm[lr * 2 + 1];
+        m = fmaxf(m0, m1);
+        lt = m == -INFINITY ? 0.f : xl[lr * 2] * xexp<TP>(m0 - m) + xl[lr * 2 + 1] * xexp<TP>(m1 - m);
+        if (a.npad > 0) {
+          // the chunk padding's keys (zero rows of K) score 0
+          const float m2 = fmaxf(m, 0.f);
+          lt = lt * xexp<TP>(m - m2) + (float)a.npad * xexp<TP>(-m2);
+          m = m2;
+        }
+      } else {
+        m = 0.f;
+        lt = 1.f;
+      }
+      a.m[(int64_t)h * a.Lrq + row] = m;
+      a.l[(int64_t)h * a.Lrq + row] = lt;
+    }
   }
 }
 
@@ -686,20 +746,21 @@ extern "C" int fs_xattn(const fs_xattn_args* a, void* stream) {
     k.h0 = h0;
     k.hg = a->Hq - h0 < hg ? a->Hq - h0 : hg;
     const unsigned grid = (unsigned)(k.hg * ((g.Lrq + kXRows - 1) / kXRows));
+    const unsigned wgrid = (unsigned)(k.hg * ((g.Lrq + kXWide - 1) / kXWide));
     if (a->torch_path) {
       if (bf) {
-        xattn_scores_kernel<bf16_t, true><<<grid, kXThreads, 0, s>>>(k);
+        xattn_scores_wide_kernel<bf16_t, true><<<wgrid, kXWideThreads, 0, s>>>(k);
         xattn_sums_kernel<bf16_t, true><<<grid, kXThreads, 0, s>>>(k);
       } else {
-        xattn_scores_kernel<f16_t, true><<<grid, kXThreads, 0, s>>>(k);
+        xattn_scores_wide_kernel<f16_t, true><<<wgrid, kXWideThreads, 0, s>>>(k);
         xattn_sums_kernel<f16_t, true><<<grid, kXThreads, 0, s>>>(k);
       }
     } else {
       if (bf) {
-        xattn_scores_kernel<bf16_t, false><<<grid, kXThreads, 0, s>>>(k);
+        xattn_scores_wide_kernel<bf16_t, false><<<wgrid, kXWideThreads, 0, s>>>(k);
         xattn_sums_kernel<bf16_t, false><<<grid, kXThreads, 0, s>>>(k);
       } else {
-        xattn_scores_kernel<f16_t, false><<<grid, kXThreads, 0, s>>>(k);
+        xattn_scores_wide_kernel<f16_t, false><<<wgrid, kXWideThreads, 0, s>>>(k);
         xattn_sums_kernel<f16_t, false><<<grid, kXThreads, 0, s>>>(k);
       }
     }
