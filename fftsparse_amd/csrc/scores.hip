@@ -71,8 +71,18 @@ __global__ __launch_bounds__(kScoreThreads) void scores_kernel(fs_scores_args a,
   // LDS as the S half-tiles written after the MFMAs
   __shared__ __attribute__((aligned(16))) float sl[kScoreTile][kScoreTile / 2 + 1];
   __shared__ int taus[kMaxSamples];
+  __shared__ short rel[kMaxSamples];               // the sampled diagonals that cross this tile
+  __shared__ int nrel;
+  __shared__ float csum[4][kScoreTile];            // per-wave column partials
   uint16_t* kt = reinterpret_cast<uint16_t*>(&sl[0][0]);
-  const int h = blockIdx.x / ntiles, t = blockIdx.x - h * ntiles;
+  // Workgroup w runs on XCD w % 8.  XCD x takes the contiguous range of
+  // (head, tile) items [x per, (x + 1) per): a head's tiles (and the heads of
+  // one KV group) share one XCD, so the Q_b / K_b panels each tile re-reads
+  // are fetched into that XCD's L2 once instead of into all eight.
+  const int total = a.Hq * ntiles, per = (total + 7) / 8;
+  const int slot = (int)(blockIdx.x >> 3), item = (int)(blockIdx.x & 7) * per + slot;
+  if (slot >= per || item >= total) return;
+  const int h = item / ntiles, t = item - h * ntiles;
   int I, J;
   tile_ij(t, I, J);
   const int N = a.N, D = a.D;
@@ -117,6 +127,7 @@ __global__ __launch_bounds__(kScoreThreads) void scores_kernel(fs_scores_args a,
   if (tid < a.n_samples) tv = a.sample_taus[tid];
   for (int e = tid + kScoreThreads; e < a.n_samples; e += kScoreThreads) taus[e] = a.sample_taus[e];
   if (tid < a.n_samples) taus[tid] = tv;
+  if (tid == 0) nrel = 0;
 #pragma unroll
   for (int u = 0; u < kMaxChunks; ++u) {
     const int c = tid + u * kScoreThreads, r = c / cpr, cc = c - r * cpr;
@@ -134,12 +145,37 @@ __global__ __launch_bounds__(kScoreThreads) void scores_kernel(fs_scores_args a,
       acc[jt] = ScoreMma<T>::mma(av, bv, acc[jt]);
     }
   }
+  // the sampled diagonals tau = i - j that cross the tile, i - j in [i0 - j0 - 127, i0 - j0 + 127]
+  // (their order in rel is arbitrary: each one's elements go to fixed places)
+  for (int e = tid; e < a.n_samples; e += kScoreThreads) {
+    const int tau = taus[e];
+    if (tau >= 0 && tau < N && tau >= i0 - j0 - (kScoreTile - 1) && tau <= i0 - j0 + (kScoreTile - 1))
+      rel[atomicAdd(&nrel, 1)] = (short)e;
+  }
 
   // The S tile goes through LDS in two halves of 64 columns (a smaller LDS
   // footprint, so more workgroups per CU).  C layout: lane holds row
   // (r/4)*8 + hi*4 + r%4, column l32 of each 32x32 block.
   const int64_t tb = (int64_t)h * ntiles + t;
   const bool diag_tile = I == J;
+  // ---- column sums over rows i >= j, i <= N-2, from the accumulators: the
+  // lane's 16 rows, then the other lane half (rows hi * 4 ..), then the four
+  // waves in order (through LDS)
+  if (a.n_cols > 0) {
+    const int ie = min(kScoreTile - 1, N - 2 - i0);
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) {
+      const int jl = jt * 32 + l32;
+      float c = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int il = wave * 32 + (r >> 2) * 8 + hi * 4 + (r & 3);
+        if (il <= ie && (!diag_tile || il >= jl)) c += acc[jt][r];
+      }
+      c += __shfl_xor(c, 32, 64);
+      if (hi == 0) csum[wave][jl] = c;
+    }
+  }
   const int dl = tid - (kScoreTile - 1);           // this thread's local diagonal iloc - jloc
   const bool lag_on = a.keep_tau != nullptr && tid < 2 * kScoreTile - 1 && !(diag_tile && dl < 0);
   float lag = 0.f;
@@ -157,19 +193,10 @@ __global__ __launch_bounds__(kScoreThreads) void scores_kernel(fs_scores_args a,
 #pragma unroll 8
       for (int il = ib; il <= ie; ++il) lag += sl[il][il - dl - c0];
     }
-    // ---- column sums over rows i >= j, i <= N-2
-    if (a.n_cols > 0 && tid < kScoreTile / 2) {
-      const int jl = c0 + tid, j = j0 + jl;
-      const int ib = diag_tile ? jl : 0;
-      const int ie = min(kScoreTile - 1, N - 2 - i0);
-      float s = 0.f;
-#pragma unroll 8
-      for (int il = ib; il <= ie; ++il) s += sl[il][tid];
-      pcol[tb * kScoreTile + jl] = (j < N) ? s : 0.f;
-    }
-    // ---- sampled diagonals: S[j + tau][j] / sqrt(D) for j < N - tau - 1
-    for (int e = tid; e < a.n_samples * (kScoreTile / 2); e += kScoreThreads) {
-      const int s = e / (kScoreTile / 2), jh = e - s * (kScoreTile / 2);
+    // ---- sampled diagonals crossing the tile: S[j + tau][j] / sqrt(D) for j < N - tau - 1
+    const int nr = nrel;
+    for (int e = tid; e < nr * (kScoreTile / 2); e += kScoreThreads) {
+      const int s = rel[e / (kScoreTile / 2)], jh = e % (kScoreTile / 2);
       const int tau = taus[s];
       const int j = j0 + c0 + jh, i = j + tau;
       if (tau < 0 || tau >= N || j >= N - tau - 1) continue;
@@ -182,6 +209,8 @@ __global__ __launch_bounds__(kScoreThreads) void scores_kernel(fs_scores_args a,
       a.last_scores[(int64_t)h * N + j0 + c0 + tid] = Conv<T>::round(sl[N - 1 - i0][tid]);
   }
   if (a.keep_tau != nullptr && tid < 2 * kScoreTile - 1) pdiag[tb * kDiagSlots + tid] = lag;
+  if (a.n_cols > 0 && tid < kScoreTile)
+    pcol[tb * kScoreTile + tid] = (j0 + tid < N) ? ((csum[0][tid] + csum[1][tid]) + csum[2][tid]) + csum[3][tid] : 0.f;
 }
 
 __global__ __launch_bounds__(kFinalThreads) void scores_final_kernel(fs_scores_args a, int ntiles, float inv_sqrt_d,
@@ -317,7 +346,7 @@ static int launch_scores(const fs_scores_args& a, hipStream_t s) {
   float* pcol = reinterpret_cast<float*>(w + o_col);
   float* dvs = reinterpret_cast<float*>(w + o_dv);
   const float inv_sqrt_d = 1.0f / (float)sqrt((double)a.D);
-  scores_kernel<T><<<a.Hq * ntiles, kScoreThreads, 0, s>>>(a, ntiles, inv_sqrt_d, pdiag, pcol, dvs);
+  scores_kernel<T><<<(a.Hq * ntiles + 7) / 8 * 8, kScoreThreads, 0, s>>>(a, ntiles, inv_sqrt_d, pdiag, pcol, dvs);
   if (int rc = fs_host::launch_status("fs_scores (tiles)")) return rc;
   const size_t smem = (size_t)a.N * sizeof(float);
   if (int rc = fs_host::allow_dynamic_lds(scores_final_kernel, smem, "fs_scores")) return rc;
