@@ -239,6 +239,64 @@ __device__ __forceinline__ float group16_sum(float v) {
   return v;
 }
 
+// Bit position of the r-th (from 0) set bit of x; r < popcount(x).
+__device__ __forceinline__ int nth_set_bit(uint64_t x, int r) {
+  int p = 0;
+  for (int s = 32; s > 0; s >>= 1) {
+    const int c = __popcll(x & ((1ull << s) - 1));
+    if (r >= c) {
+      r -= c;
+      x >>= s;
+      p += s;
+    }
+  }
+  return p;
+}
+
+// Ascending block list of one row written in 16-byte chunks of 8 entries.
+// The row's membership words are held one per lane by a group of G lanes
+// (G a power of two): lane w of the group holds word w (entries 64 w + bit),
+// in m, and the number of entries in the group's lower words, in pos; T is the
+// row's entry count.  Every lane of the wave first puts its word and prefix in
+// its slot of the wave's LDS arrays wm[64] / wp[64] (lane gbase + w: the
+// group's first lane is gbase).  Chunk c (entries 8c .. 8c+7) is then formed by
+// lane c % G of the group: the word holding entry 8c is the last one whose
+// prefix is <= 8c, found by binary search over the prefixes, and the entries
+// follow from its set bits onwards.  Slots past T in the last chunk hold 0.
+// out must be 16-byte aligned with room for 8 ceil(T / 8) entries.  One store
+// per 8 entries, instead of one per entry, keeps the write within the memory
+// pipeline's address rate.
+__device__ __forceinline__ void write_list_chunks(uint16_t* out, uint64_t m, int pos, int T, int G, int w,
+                                                  int gbase, uint64_t* wm, int* wp) {
+  const int lane = (int)__lane_id();
+  wm[lane] = m;
+  wp[lane] = pos;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const int nch = (T + 7) >> 3;
+  for (int c = w; c < nch; c += G) {
+    const int e0 = 8 * c;
+    int ws = 0;                                    // the last word whose prefix is <= e0
+    for (int st = G >> 1; st > 0; st >>= 1)
+      if (ws + st < G && wp[gbase + ws + st] <= e0) ws += st;
+    uint64_t x = wm[gbase + ws];
+    x &= ~((1ull << nth_set_bit(x, e0 - wp[gbase + ws])) - 1);
+    uint32_t pk[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      uint32_t v = 0;
+      if (e0 + k < T) {
+        while (x == 0 && ws + 1 < G) x = wm[gbase + ++ws];
+        v = x ? (uint32_t)(64 * ws + __builtin_ctzll(x)) : 0u;
+        x &= x - 1;
+      }
+      pk[k >> 1] |= v << (16 * (k & 1));
+    }
+    *reinterpret_cast<uint4*>(out + e0) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+  }
+}
+
 }  // namespace fs
 
 // host side ----------------------------------------------------------------

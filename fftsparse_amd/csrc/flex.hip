@@ -986,12 +986,16 @@ __global__ __launch_bounds__(64) void flex_lists_kernel(FlexListK a) {
   if (w < NW) {
     // vertical columns v <= r
     m = vm[w];
-    // slash: column c = r - s for offset s; bit b of word w is c = 64 w + b, s = r - c
-    for (int b = 0; b < 64; ++b) {
-      const int c = 64 * w + b;
-      if (c > r) break;
-      const int s = r - c;
-      if ((sm[s >> 6] >> (s & 63)) & 1) m |= 1ull << b;
+    // slash: column c = r - s for offset s; bit b of word w is c = 64 w + b,
+    // s = t - b with t = r - 64 w, so the word is the offset mask's bits
+    // t - 63 .. t reversed (offsets below 0 read as 0: columns past r)
+    const int t = r - 64 * w;
+    if (t >= 0) {
+      const int lo = t - 63, q = lo >> 6, sh = lo & 63;   // q = floor(lo / 64)
+      const uint64_t w0 = q >= 0 ? sm[q] : 0ull;
+      const uint64_t w1 = q + 1 < kFWords ? sm[q + 1] : 0ull;
+      const uint64_t win = sh ? (w0 >> sh) | (w1 << (64 - sh)) : w0;   // bit k: offset lo + k
+      m |= __builtin_bitreverse64(win);
     }
     if (sparse) m |= a.cover[((int64_t)h * nb + r) * kFWords + w];
     const int b0 = 0, b1 = min(64, r + 1 - 64 * w);   // causal: columns <= r
@@ -1006,11 +1010,18 @@ __global__ __launch_bounds__(64) void flex_lists_kernel(FlexListK a) {
   }
   const int total = __shfl(incl, 63, 64);
   uint16_t* out = a.blk_idx + ((int64_t)h * nb + r) * nb;
-  int pos = incl - c;
-  while (m) {
-    const int b = __builtin_ctzll(m);
-    out[pos++] = (uint16_t)(64 * w + b);
-    m &= m - 1;
+  if ((nb & 7) == 0 && ((uintptr_t)a.blk_idx & 15) == 0) {
+    // rows aligned to 16 bytes: 16-byte stores of 8 entries
+    __shared__ uint64_t stw[64];
+    __shared__ int stp[64];
+    write_list_chunks(out, m, incl - c, total, 64, w, 0, stw, stp);
+  } else {
+    int pos = incl - c;
+    while (m) {
+      const int b = __builtin_ctzll(m);
+      out[pos++] = (uint16_t)(64 * w + b);
+      m &= m - 1;
+    }
   }
   if (lane == 0) a.blk_cnt[(int64_t)h * nb + r] = total;
 }

@@ -40,6 +40,9 @@ template <typename T, bool DIFF>
 __global__ __launch_bounds__(kSelThreads) void select_kernel(fs_select_args a, int rows_per_wave,
                                                              float inv_sqrt_d) {
   extern __shared__ float panel[];       // [RPW][N] scores (diffuse heads) then [RPW][D] q rows
+  // per-head flag bytes (per-row path); the word-parallel path stages each
+  // wave's list words and prefixes here instead (3 KiB)
+  __shared__ __attribute__((aligned(16))) uint8_t flags[kSelMaxN];
   const int RPW = rows_per_wave * kSelWaves;
   const int N = a.N, Nk = a.Nk, D = a.D;
   const int chunks = (N + RPW - 1) / RPW;
@@ -170,6 +173,10 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(fs_select_args a, i
       }
     }
     __syncthreads();
+    // rows aligned to 16 bytes: the lists go out in 16-byte chunks
+    const bool chunked = (Nk & 7) == 0 && ((uintptr_t)a.blk_idx & 15) == 0;
+    uint64_t* stw = reinterpret_cast<uint64_t*>(flags) + wave * 64;
+    int* stp = reinterpret_cast<int*>(flags + kSelWaves * 64 * sizeof(uint64_t)) + wave * 64;
     int lpr = 1;                                   // lanes per row (power of two >= NW)
     while (lpr < NW) lpr <<= 1;
     const int rpi = 64 / lpr;                      // rows per wave pass
@@ -203,7 +210,12 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(fs_select_args a, i
         if (w >= o) incl += v;
       }
       const int total = __shfl(incl, lpr - 1, lpr);
-      if (row_ok) {
+      if (chunked) {
+        // 16-byte stores of 8 entries (the whole wave takes part; rows past N write nothing)
+        uint16_t* out = a.blk_idx + ((int64_t)h * N + min(i, N - 1)) * Nk;
+        write_list_chunks(out, m, incl - c, row_ok ? total : 0, lpr, w, g * lpr, stw, stp);
+        if (row_ok && w == 0) a.blk_cnt[(int64_t)h * N + i] = total;
+      } else if (row_ok) {
         uint16_t* out = a.blk_idx + ((int64_t)h * N + i) * Nk;
         int pos = incl - c;
         while (m) {
@@ -217,7 +229,6 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(fs_select_args a, i
     return;
   }
   // ---- per-head lag / column / last-row flags, staged in LDS (bit 0 lag, 1 column, 2 last row)
-  __shared__ uint8_t flags[kSelMaxN];
   for (int j = tid; j < N; j += kSelThreads) {
     uint8_t f = 0;
     if (a.keep_tau && a.keep_tau[(int64_t)h * N + j]) f |= 1;
