@@ -839,14 +839,42 @@ __global__ __launch_bounds__(64) void union_kernel(const int32_t* __restrict__ c
   const int lane = threadIdx.x;
   for (int j = 0; j < kUnionMaxRows; ++j) bits[j][lane] = 0ull;
   __syncthreads();
+  // Each lane reads 8 consecutive entries of a row (one 16-byte load when the
+  // rows are 16-byte aligned) and ORs them into the row's bit words, one LDS
+  // atomic per word they touch (the lists ascend, so usually one or two).
+  const bool v16 = (Nk & 7) == 0 && ((uintptr_t)idx & 15) == 0;
   for (int j = 0; j < R; ++j) {
     const int row = grp * R + j;
     if (row >= Nq) break;
     const int n = min(max(cnt[(int64_t)h * Nq + row], 0), Nk);
     const uint16_t* li = idx + ((int64_t)h * Nq + row) * Nk;
-    for (int e = lane; e < n; e += 64) {
-      const int blk = li[e];
-      if (blk < Nk) atomicOr(&bits[j][blk >> 6], 1ull << (blk & 63));
+    for (int e0 = 8 * lane; e0 < n; e0 += 8 * 64) {
+      uint32_t ent[4];
+      if (v16 && e0 + 8 <= n) {
+        const uint4 q = *reinterpret_cast<const uint4*>(li + e0);
+        ent[0] = q.x; ent[1] = q.y; ent[2] = q.z; ent[3] = q.w;
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t lo = e0 + 2 * k < n ? li[e0 + 2 * k] : 0xffffu;
+          const uint32_t hi = e0 + 2 * k + 1 < n ? li[e0 + 2 * k + 1] : 0xffffu;
+          ent[k] = lo | (hi << 16);
+        }
+      }
+      unsigned long long acc = 0ull;
+      int cw = -1;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int blk = (int)((ent[k >> 1] >> (16 * (k & 1))) & 0xffffu);
+        if (e0 + k >= n || blk >= Nk) continue;
+        if ((blk >> 6) != cw) {
+          if (cw >= 0) atomicOr(&bits[j][cw], acc);
+          cw = blk >> 6;
+          acc = 0ull;
+        }
+        acc |= 1ull << (blk & 63);
+      }
+      if (cw >= 0) atomicOr(&bits[j][cw], acc);
     }
   }
   __syncthreads();
@@ -861,13 +889,24 @@ __global__ __launch_bounds__(64) void union_kernel(const int32_t* __restrict__ c
   }
   const int total = __shfl(incl, 63, 64);
   uint32_t* out = u_idx + ((int64_t)h * Ng + grp) * Nk;
-  int pos = incl - c;
-  while (any) {
-    const int b = __builtin_ctzll(any);
-    any &= any - 1;
+  // entry: block | (rows of the group that selected it) << 16
+  auto entry = [&](int wd, int b) -> uint32_t {
     uint32_t rows = 0;
-    for (int j = 0; j < R; ++j) rows |= (uint32_t)((bits[j][lane] >> b) & 1ull) << j;
-    out[pos++] = (uint32_t)(64 * lane + b) | (rows << 16);
+    for (int j = 0; j < R; ++j) rows |= (uint32_t)((bits[j][wd] >> b) & 1ull) << j;
+    return (uint32_t)(64 * wd + b) | (rows << 16);
+  };
+  if ((Nk & 3) == 0 && ((uintptr_t)u_idx & 15) == 0) {
+    // 16-byte stores of 4 entries
+    __shared__ uint64_t stw[64];
+    __shared__ int stp[64];
+    write_list_chunks(out, (uint64_t)any, incl - c, total, 64, lane, 0, stw, stp, entry);
+  } else {
+    int pos = incl - c;
+    while (any) {
+      const int b = __builtin_ctzll(any);
+      any &= any - 1;
+      out[pos++] = entry(lane, b);
+    }
   }
   if (lane == 0) u_cnt[(int64_t)h * Ng + grp] = total;
 }

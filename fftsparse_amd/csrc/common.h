@@ -253,30 +253,33 @@ __device__ __forceinline__ int nth_set_bit(uint64_t x, int r) {
   return p;
 }
 
-// Ascending block list of one row written in 16-byte chunks of 8 entries.
-// The row's membership words are held one per lane by a group of G lanes
-// (G a power of two): lane w of the group holds word w (entries 64 w + bit),
-// in m, and the number of entries in the group's lower words, in pos; T is the
-// row's entry count.  Every lane of the wave first puts its word and prefix in
-// its slot of the wave's LDS arrays wm[64] / wp[64] (lane gbase + w: the
-// group's first lane is gbase).  Chunk c (entries 8c .. 8c+7) is then formed by
-// lane c % G of the group: the word holding entry 8c is the last one whose
-// prefix is <= 8c, found by binary search over the prefixes, and the entries
-// follow from its set bits onwards.  Slots past T in the last chunk hold 0.
-// out must be 16-byte aligned with room for 8 ceil(T / 8) entries.  One store
-// per 8 entries, instead of one per entry, keeps the write within the memory
+// Ascending block list of one row written in 16-byte chunks.  The row's
+// membership words are held one per lane by a group of G lanes (G a power of
+// two): lane w of the group holds word w (blocks 64 w + bit), in m, and the
+// number of entries in the group's lower words, in pos; T is the row's entry
+// count.  Every lane of the wave first puts its word and prefix in its slot of
+// the wave's LDS arrays wm[64] / wp[64] (lane gbase + w: the group's first lane
+// is gbase).  Chunk c (entries PER c .. PER c + PER - 1, PER = 16 /
+// sizeof(E)) is then formed by lane c % G of the group: the word holding its
+// first entry is the last one whose prefix is <= PER c, found by binary search
+// over the prefixes, and the entries follow from that word's set bits onwards;
+// entry (word ws, bit b) is value(ws, b).  Slots past T in the last chunk hold
+// 0.  out must be 16-byte aligned with room for PER ceil(T / PER) entries.  One
+// store per chunk, instead of one per entry, keeps the write within the memory
 // pipeline's address rate.
-__device__ __forceinline__ void write_list_chunks(uint16_t* out, uint64_t m, int pos, int T, int G, int w,
-                                                  int gbase, uint64_t* wm, int* wp) {
+template <typename E, typename F>
+__device__ __forceinline__ void write_list_chunks(E* out, uint64_t m, int pos, int T, int G, int w, int gbase,
+                                                  uint64_t* wm, int* wp, F value) {
+  constexpr int PER = 16 / sizeof(E);
   const int lane = (int)__lane_id();
   wm[lane] = m;
   wp[lane] = pos;
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  const int nch = (T + 7) >> 3;
+  const int nch = (T + PER - 1) / PER;
   for (int c = w; c < nch; c += G) {
-    const int e0 = 8 * c;
+    const int e0 = PER * c;
     int ws = 0;                                    // the last word whose prefix is <= e0
     for (int st = G >> 1; st > 0; st >>= 1)
       if (ws + st < G && wp[gbase + ws + st] <= e0) ws += st;
@@ -284,17 +287,23 @@ __device__ __forceinline__ void write_list_chunks(uint16_t* out, uint64_t m, int
     x &= ~((1ull << nth_set_bit(x, e0 - wp[gbase + ws])) - 1);
     uint32_t pk[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
+    for (int k = 0; k < PER; ++k) {
       uint32_t v = 0;
       if (e0 + k < T) {
         while (x == 0 && ws + 1 < G) x = wm[gbase + ++ws];
-        v = x ? (uint32_t)(64 * ws + __builtin_ctzll(x)) : 0u;
+        v = x ? (uint32_t)value(ws, __builtin_ctzll(x)) : 0u;
         x &= x - 1;
       }
-      pk[k >> 1] |= v << (16 * (k & 1));
+      if constexpr (PER == 8) pk[k >> 1] |= v << (16 * (k & 1));
+      else pk[k] = v;
     }
     *reinterpret_cast<uint4*>(out + e0) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
   }
+}
+// The plain list: entry = block index 64 ws + b.
+__device__ __forceinline__ void write_list_chunks(uint16_t* out, uint64_t m, int pos, int T, int G, int w,
+                                                  int gbase, uint64_t* wm, int* wp) {
+  write_list_chunks(out, m, pos, T, G, w, gbase, wm, wp, [](int ws, int b) { return 64 * ws + b; });
 }
 
 }  // namespace fs
