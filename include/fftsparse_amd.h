@@ -202,7 +202,9 @@ FS_API int fs_scores_noalloc(const fs_scores_args* a, void* stream);
  *   column: col_mode 2, or col_mode 1 and stripe head: col_sel[h][j] && j <= i
  * with is_stripe[h] = mean_s(diag_var[h][s]) <= stripe_threshold (false when
  * stripe_all_diffuse or the mean is nan).  Output: blk_cnt[h][i] and the
- * selected j in ascending order at blk_idx[(h*N + i) * Nk ...].  N <= 8192
+ * selected j in ascending order at blk_idx[(h*N + i) * Nk ...]; the entries
+ * of a row past its count are unspecified (with Nk a multiple of 8 the list is
+ * written in 16-byte chunks, the last one padded with 0).  N <= 8192
  * (D <= 256 with dyn_mode 1). */
 typedef struct {
   const void* q_b; const void* k_b;
@@ -297,13 +299,14 @@ FS_API int fs_xattn(const fs_xattn_args* a, void* stream);
  * their block-level causal attention; the top pooled vertical columns (block 0
  * forced) in every row at or after them and the top pooled slash offsets
  * (offset 0 forced) as block diagonals (ties: lower index).  Outputs ascending
- * block lists blk_cnt [Hq][N], blk_idx [Hq][N][N] (N = ceil(L/bs)), optionally
+ * block lists blk_cnt [Hq][N], blk_idx [Hq][N][N] (N = ceil(L/bs); entries past
+ * a row's count unspecified, as for fs_select), optionally
  * head_info [Hq][4] (vertical budget, slash budget, sparse, 0), head_js [Hq]
  * and the per-token vertical / slash profiles [Hq][L] (fp32).
  * work: fs_flex_work_bytes(Hq, Hk, L, bs, tau) bytes, with the tau of the
  * call (tau <= 0, the reference's default, makes no head sparse and needs no
  * room for the block-level attention and covers).  bf16/f16, D = 128,
- * bs 32, 64 or 128, L > bs, N <= 4096. */
+ * bs 16, 32, 64 or 128, L > bs, N <= 4096. */
 typedef struct {
   const void* q; int64_t q_sh, q_sl;
   const void* k; int64_t k_sh, k_sl;
