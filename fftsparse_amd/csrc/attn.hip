@@ -827,17 +827,18 @@ __global__ __launch_bounds__(kOrderThreads) void order_kernel(const int32_t* __r
 
 // ---- union lists of groups of R consecutive list rows (union mode) -------
 // One wave per (head, group): the rows' block lists as bit rows in LDS, their
-// OR word by word (lane w: blocks 64 w .. 64 w + 63), a prefix of the popcounts
-// over the lanes, and each lane writes its blocks in ascending order as
-// block | (rows that selected it) << 16.  Nk <= 4096, R <= 8.
+// OR word by word (lane l: words l and l + 64, blocks 64 w .. 64 w + 63), a
+// prefix of the popcounts, and the union written in ascending order as
+// block | (rows that selected it) << 16.  Nk <= 8192, R <= 8.
 constexpr int kUnionMaxRows = 8;
 __global__ __launch_bounds__(64) void union_kernel(const int32_t* __restrict__ cnt, const uint16_t* __restrict__ idx,
                                                    int Nq, int Nk, int R, int Ng, int32_t* __restrict__ u_cnt,
                                                    uint32_t* __restrict__ u_idx) {
-  __shared__ unsigned long long bits[kUnionMaxRows][64];
+  constexpr int kW = 2 * 64;                       // words per row: Nk <= 8192
+  __shared__ unsigned long long bits[kUnionMaxRows][kW];
   const int h = blockIdx.x / Ng, grp = blockIdx.x - h * Ng;
   const int lane = threadIdx.x;
-  for (int j = 0; j < kUnionMaxRows; ++j) bits[j][lane] = 0ull;
+  for (int j = 0; j < kUnionMaxRows; ++j) bits[j][lane] = bits[j][lane + 64] = 0ull;
   __syncthreads();
   // Each lane reads 8 consecutive entries of a row (one 16-byte load when the
   // rows are 16-byte aligned) and ORs them into the row's bit words, one LDS
@@ -878,16 +879,23 @@ __global__ __launch_bounds__(64) void union_kernel(const int32_t* __restrict__ c
     }
   }
   __syncthreads();
-  unsigned long long any = 0ull;
-  for (int j = 0; j < R; ++j) any |= bits[j][lane];
-  const int c = __popcll(any);
-  int incl = c;
+  unsigned long long any0 = 0ull, any1 = 0ull;
+  for (int j = 0; j < R; ++j) {
+    any0 |= bits[j][lane];
+    any1 |= bits[j][lane + 64];
+  }
+  const int c0 = __popcll(any0), c1 = __popcll(any1);
+  int i0 = c0, i1 = c1;
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
-    const int v = __shfl_up(incl, o, 64);
-    if (lane >= o) incl += v;
+    const int v0 = __shfl_up(i0, o, 64), v1 = __shfl_up(i1, o, 64);
+    if (lane >= o) {
+      i0 += v0;
+      i1 += v1;
+    }
   }
-  const int total = __shfl(incl, 63, 64);
+  const int t0 = __shfl(i0, 63, 64);
+  const int total = t0 + __shfl(i1, 63, 64);
   uint32_t* out = u_idx + ((int64_t)h * Ng + grp) * Nk;
   // entry: block | (rows of the group that selected it) << 16
   auto entry = [&](int wd, int b) -> uint32_t {
@@ -897,16 +905,21 @@ __global__ __launch_bounds__(64) void union_kernel(const int32_t* __restrict__ c
   };
   if ((Nk & 3) == 0 && ((uintptr_t)u_idx & 15) == 0) {
     // 16-byte stores of 4 entries
-    __shared__ uint64_t stw[64];
-    __shared__ int stp[64];
-    write_list_chunks(out, (uint64_t)any, incl - c, total, 64, lane, 0, stw, stp, entry);
+    __shared__ uint64_t stw[kW];
+    __shared__ int stp[kW];
+    stw[lane] = any0;
+    stp[lane] = i0 - c0;
+    stw[lane + 64] = any1;
+    stp[lane + 64] = t0 + i1 - c1;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    list_chunks_from_lds(out, total, kW, lane, 64, stw, stp, entry);
   } else {
-    int pos = incl - c;
-    while (any) {
-      const int b = __builtin_ctzll(any);
-      any &= any - 1;
-      out[pos++] = entry(lane, b);
-    }
+    int pos = i0 - c0;
+    for (unsigned long long m = any0; m; m &= m - 1) out[pos++] = entry(lane, __builtin_ctzll(m));
+    pos = t0 + i1 - c1;
+    for (unsigned long long m = any1; m; m &= m - 1) out[pos++] = entry(lane + 64, __builtin_ctzll(m));
   }
   if (lane == 0) u_cnt[(int64_t)h * Ng + grp] = total;
 }
@@ -1037,8 +1050,8 @@ static int check_attn(const fs_attn_args* a, const char* fn) {
   FS_CHECK_SUPPORTED(a->bs == 16 || a->bs == 32 || a->bs == 64 || a->bs == 128, "%s: block size %d unsupported", fn,
                      a->bs);
   // union mode (16- and 32-token lists): block indices and their rows packed in 32-bit entries
-  FS_CHECK_SUPPORTED(!(a->blk_cnt && a->bs < 64) || (a->Lk + a->bs - 1) / a->bs <= 4096,
-                     "%s: %d-token lists over more than 4096 key blocks unsupported", fn, a->bs);
+  FS_CHECK_SUPPORTED(!(a->blk_cnt && a->bs < 64) || (a->Lk + a->bs - 1) / a->bs <= 8192,
+                     "%s: %d-token lists over more than 8192 key blocks unsupported", fn, a->bs);
   FS_CHECK_SUPPORTED(a->dtype == FS_DTYPE_BF16 || a->dtype == FS_DTYPE_F16,
                      "%s: dtype %d unsupported (bf16/f16)", fn, a->dtype);
   FS_CHECK_SUPPORTED(a->Hk <= 4096, "%s: %d KV heads > 4096", fn, a->Hk);

@@ -253,44 +253,36 @@ __device__ __forceinline__ int nth_set_bit(uint64_t x, int r) {
   return p;
 }
 
-// Ascending block list of one row written in 16-byte chunks.  The row's
-// membership words are held one per lane by a group of G lanes (G a power of
-// two): lane w of the group holds word w (blocks 64 w + bit), in m, and the
-// number of entries in the group's lower words, in pos; T is the row's entry
-// count.  Every lane of the wave first puts its word and prefix in its slot of
-// the wave's LDS arrays wm[64] / wp[64] (lane gbase + w: the group's first lane
-// is gbase).  Chunk c (entries PER c .. PER c + PER - 1, PER = 16 /
-// sizeof(E)) is then formed by lane c % G of the group: the word holding its
-// first entry is the last one whose prefix is <= PER c, found by binary search
-// over the prefixes, and the entries follow from that word's set bits onwards;
-// entry (word ws, bit b) is value(ws, b).  Slots past T in the last chunk hold
-// 0.  out must be 16-byte aligned with room for PER ceil(T / PER) entries.  One
-// store per chunk, instead of one per entry, keeps the write within the memory
-// pipeline's address rate.
+// Ascending block list of one row written in 16-byte chunks.  The row's G
+// membership words (G a power of two) are in LDS: word w (blocks 64 w + bit) at
+// wm[w], and the number of entries in the lower words at wp[w]; T is the row's
+// entry count.  Chunk c (entries PER c .. PER c + PER - 1, PER = 16 /
+// sizeof(E)) is formed by one lane: the word holding its first entry is the
+// last one whose prefix is <= PER c, found by binary search over the
+// prefixes, and the entries follow from that word's set bits onwards; entry
+// (word ws, bit b) is value(ws, b).  The calling lane writes chunks c0, c0 +
+// step, ...  Slots past T in the last chunk hold 0.  out must be 16-byte
+// aligned with room for PER ceil(T / PER) entries.  One store per chunk,
+// instead of one per entry, keeps the write within the memory pipeline's
+// address rate.
 template <typename E, typename F>
-__device__ __forceinline__ void write_list_chunks(E* out, uint64_t m, int pos, int T, int G, int w, int gbase,
-                                                  uint64_t* wm, int* wp, F value) {
+__device__ __forceinline__ void list_chunks_from_lds(E* out, int T, int G, int c0, int step, const uint64_t* wm,
+                                                     const int* wp, F value) {
   constexpr int PER = 16 / sizeof(E);
-  const int lane = (int)__lane_id();
-  wm[lane] = m;
-  wp[lane] = pos;
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   const int nch = (T + PER - 1) / PER;
-  for (int c = w; c < nch; c += G) {
+  for (int c = c0; c < nch; c += step) {
     const int e0 = PER * c;
     int ws = 0;                                    // the last word whose prefix is <= e0
     for (int st = G >> 1; st > 0; st >>= 1)
-      if (ws + st < G && wp[gbase + ws + st] <= e0) ws += st;
-    uint64_t x = wm[gbase + ws];
-    x &= ~((1ull << nth_set_bit(x, e0 - wp[gbase + ws])) - 1);
+      if (ws + st < G && wp[ws + st] <= e0) ws += st;
+    uint64_t x = wm[ws];
+    x &= ~((1ull << nth_set_bit(x, e0 - wp[ws])) - 1);
     uint32_t pk[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
       uint32_t v = 0;
       if (e0 + k < T) {
-        while (x == 0 && ws + 1 < G) x = wm[gbase + ++ws];
+        while (x == 0 && ws + 1 < G) x = wm[++ws];
         v = x ? (uint32_t)value(ws, __builtin_ctzll(x)) : 0u;
         x &= x - 1;
       }
@@ -299,6 +291,21 @@ __device__ __forceinline__ void write_list_chunks(E* out, uint64_t m, int pos, i
     }
     *reinterpret_cast<uint4*>(out + e0) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
   }
+}
+// Wave-level form: the row's words are held one per lane by a group of G lanes
+// (lane w of the group: word w in m, its prefix in pos; the group's first lane
+// is gbase); every lane of the wave puts them in its slot of the wave's LDS
+// arrays wm[64] / wp[64], then lane w of the group writes chunks w, w + G, ...
+template <typename E, typename F>
+__device__ __forceinline__ void write_list_chunks(E* out, uint64_t m, int pos, int T, int G, int w, int gbase,
+                                                  uint64_t* wm, int* wp, F value) {
+  const int lane = (int)__lane_id();
+  wm[lane] = m;
+  wp[lane] = pos;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  list_chunks_from_lds(out, T, G, w, G, wm + gbase, wp + gbase, value);
 }
 // The plain list: entry = block index 64 ws + b.
 __device__ __forceinline__ void write_list_chunks(uint16_t* out, uint64_t m, int pos, int T, int G, int w,

@@ -54,7 +54,7 @@ constexpr int kFThreads = 256;
 constexpr int kFTile = 128;                      // key columns per tile
 constexpr int kFChunk = 2048;                    // key columns per workgroup
 constexpr int kFHeadThreads = 1024;
-constexpr int kFMaxBlocks = 4096;
+constexpr int kFMaxBlocks = 8192;
 constexpr int kFWords = kFMaxBlocks / 64;
 
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
@@ -973,7 +973,8 @@ struct FlexListK {
   int Hq, nb;
 };
 
-// one wave per (head, block row): 64-bit membership words, popcount offsets
+// one wave per (head, block row): lane l forms the row's 64-bit membership
+// words l and l + 64, popcount offsets, the ascending list
 __global__ __launch_bounds__(64) void flex_lists_kernel(FlexListK a) {
   const int h = blockIdx.x / a.nb, r = blockIdx.x % a.nb;
   const int lane = threadIdx.x, nb = a.nb;
@@ -981,47 +982,54 @@ __global__ __launch_bounds__(64) void flex_lists_kernel(FlexListK a) {
   const uint64_t* vm = a.vmask + (int64_t)h * kFWords;
   const uint64_t* sm = a.smask + (int64_t)h * kFWords;
   const bool sparse = a.info[h * 4 + 2] != 0;
-  uint64_t m = 0;
-  const int w = lane;
-  if (w < NW) {
+  auto word = [&](int w) -> uint64_t {
+    if (w >= NW) return 0ull;
     // vertical columns v <= r
-    m = vm[w];
+    uint64_t m = vm[w];
     // slash: column c = r - s for offset s; bit b of word w is c = 64 w + b,
     // s = t - b with t = r - 64 w, so the word is the offset mask's bits
     // t - 63 .. t reversed (offsets below 0 read as 0: columns past r)
     const int t = r - 64 * w;
-    if (t >= 0) {
-      const int lo = t - 63, q = lo >> 6, sh = lo & 63;   // q = floor(lo / 64)
-      const uint64_t w0 = q >= 0 ? sm[q] : 0ull;
-      const uint64_t w1 = q + 1 < kFWords ? sm[q + 1] : 0ull;
-      const uint64_t win = sh ? (w0 >> sh) | (w1 << (64 - sh)) : w0;   // bit k: offset lo + k
-      m |= __builtin_bitreverse64(win);
-    }
+    if (t < 0) return 0ull;                        // every column of the word is past r
+    const int lo = t - 63, q = lo >> 6, sh = lo & 63;   // q = floor(lo / 64)
+    const uint64_t w0 = q >= 0 ? sm[q] : 0ull;
+    const uint64_t w1 = q + 1 < kFWords ? sm[q + 1] : 0ull;
+    const uint64_t win = sh ? (w0 >> sh) | (w1 << (64 - sh)) : w0;   // bit k: offset lo + k
+    m |= __builtin_bitreverse64(win);
     if (sparse) m |= a.cover[((int64_t)h * nb + r) * kFWords + w];
-    const int b0 = 0, b1 = min(64, r + 1 - 64 * w);   // causal: columns <= r
-    if (b1 <= b0) m = 0;
-    else if (b1 < 64) m &= (1ull << b1) - 1;
-  }
-  const int c = __popcll(m);
-  int incl = c;
+    if (t < 63) m &= (1ull << (t + 1)) - 1;        // causal: columns <= r
+    return m;
+  };
+  const uint64_t m0 = word(lane), m1 = word(lane + 64);
+  const int c0 = __popcll(m0), c1 = __popcll(m1);
+  int i0 = c0, i1 = c1;
   for (int o = 1; o < 64; o <<= 1) {
-    const int v = __shfl_up(incl, o, 64);
-    if (lane >= o) incl += v;
+    const int v0 = __shfl_up(i0, o, 64), v1 = __shfl_up(i1, o, 64);
+    if (lane >= o) {
+      i0 += v0;
+      i1 += v1;
+    }
   }
-  const int total = __shfl(incl, 63, 64);
+  const int t0 = __shfl(i0, 63, 64);
+  const int total = t0 + __shfl(i1, 63, 64);
   uint16_t* out = a.blk_idx + ((int64_t)h * nb + r) * nb;
   if ((nb & 7) == 0 && ((uintptr_t)a.blk_idx & 15) == 0) {
     // rows aligned to 16 bytes: 16-byte stores of 8 entries
-    __shared__ uint64_t stw[64];
-    __shared__ int stp[64];
-    write_list_chunks(out, m, incl - c, total, 64, w, 0, stw, stp);
+    __shared__ uint64_t stw[2 * 64];
+    __shared__ int stp[2 * 64];
+    stw[lane] = m0;
+    stp[lane] = i0 - c0;
+    stw[lane + 64] = m1;
+    stp[lane + 64] = t0 + i1 - c1;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    list_chunks_from_lds(out, total, 2 * 64, lane, 64, stw, stp, [](int ws, int b) { return 64 * ws + b; });
   } else {
-    int pos = incl - c;
-    while (m) {
-      const int b = __builtin_ctzll(m);
-      out[pos++] = (uint16_t)(64 * w + b);
-      m &= m - 1;
-    }
+    int pos = i0 - c0;
+    for (uint64_t m = m0; m; m &= m - 1) out[pos++] = (uint16_t)(64 * lane + __builtin_ctzll(m));
+    pos = t0 + i1 - c1;
+    for (uint64_t m = m1; m; m &= m - 1) out[pos++] = (uint16_t)(64 * (lane + 64) + __builtin_ctzll(m));
   }
   if (lane == 0) a.blk_cnt[(int64_t)h * nb + r] = total;
 }

@@ -101,8 +101,8 @@ def Flexprefill_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gamma
     """Flexprefill.py:1063-1098: q/k/v [B, L, H, D] -> [B, L, H, D].  Sequences
     of at most max(2 bs, ceil(min_budget / bs) bs) tokens take dense causal
     attention (:1084-1085), the others the FlexPrefill selection and the
-    block-sparse attention, at 16-, 32-, 64- or 128-token blocks (at most 4096
-    blocks: 65536 tokens at 16, 131072 at 32).  With ``gqa_interleave``
+    block-sparse attention, at 16-, 32-, 64- or 128-token blocks (at most 8192
+    blocks: 131072 tokens at 16, 262144 at 32).  With ``gqa_interleave``
     query head h reads KV head h % Hk in the selection and the sparse attention
     (the dense branch keeps flash_attn_func's grouped heads, as the reference)."""
     assert q.is_cuda, "input tensors must be on the GPU"

@@ -72,3 +72,43 @@ def test_random_lists_against_fp32(i):
             worst = max(worst, (o[t0:t1, h] - ref).abs().max().item())
     print(f"  max_abs {worst:.3e}", flush=True)
     assert worst <= 2e-2
+
+
+@pytest.mark.parametrize("bs,Lk", [(16, 131072), (32, 200000)])
+def test_union_lists_beyond_4096_key_blocks(bs, Lk):
+    """16- and 32-token lists over more than 4096 key blocks (8192 and 6250):
+    the union lists hold rows of 128 64-bit words.  Random lists at 3%, causal;
+    sampled query blocks (both ends and around block 4096) against fp32."""
+    Hk, g = 1, 2
+    Hq = Hk * g
+    print(f"[case] union-attn bs={bs} Lk={Lk} Hq={Hq}", flush=True)
+    N = -(-Lk // bs)
+    gen = torch.Generator().manual_seed(31 + bs)
+    q = torch.randn(1, Hq, Lk, 128, generator=gen).to(torch.bfloat16)
+    k = torch.randn(1, Hk, Lk, 128, generator=gen).to(torch.bfloat16)
+    v = torch.randn(1, Hk, Lk, 128, generator=gen).to(torch.bfloat16)
+    mask = torch.rand(Hq, N, N, generator=gen) < 0.03
+    mask |= torch.eye(N, dtype=torch.bool)[None]
+    mask &= torch.tril(torch.ones(N, N, dtype=torch.bool))[None]
+    cnt = mask.sum(-1).to(torch.int32)
+    # ascending lists: the selected indices first, in order (argsort of a key that puts them first)
+    key = torch.where(mask, torch.arange(N, dtype=torch.int32)[None, None, :], N + torch.arange(N, dtype=torch.int32))
+    idx = key.argsort(-1).to(torch.int32)
+    del key
+    out = block_sparse_attention(q.to(DEV), k.to(DEV), v.to(DEV), cnt.to(DEV), idx.to(torch.uint16).to(DEV),
+                                 block_size=bs, is_causal=True)
+    torch.cuda.synchronize()
+    o = out[0].float().cpu()
+    scale, worst = 128 ** -0.5, 0.0
+    for h in range(Hq):
+        kh, vh = k[0, h // g].float(), v[0, h // g].float()
+        for r in (0, 5, 4095, 4096, 4097, N - 2, N - 1):
+            t0, t1 = r * bs, min(Lk, (r + 1) * bs)
+            cols = idx[h, r, :int(cnt[h, r])].tolist()
+            kidx = torch.cat([torch.arange(j * bs, min(Lk, (j + 1) * bs)) for j in cols])
+            s = (q[0, h, t0:t1].float() @ kh[kidx].T) * scale
+            s = s.masked_fill(kidx[None, :] > torch.arange(t0, t1)[:, None], float("-inf"))
+            ref = torch.softmax(s, -1) @ vh[kidx]
+            worst = max(worst, (o[t0:t1, h] - ref).abs().max().item())
+    print(f"  max_abs {worst:.3e}", flush=True)
+    assert worst <= 2e-2

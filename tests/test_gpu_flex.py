@@ -160,6 +160,7 @@ def _check(q, k, *, bs, gamma, tau, min_budget=None, max_budget=None, gqa_interl
     (8192, 8, 8, 64, 0.99, torch.bfloat16, (None, 512)),        # MHA, max budget clamps
     (4100, 4, 2, 16, 0.9, torch.bfloat16, (None, None)),         # 16-token blocks, ragged
     (6000, 2, 1, 16, 0.95, torch.float16, (256, 1024)),          # 16-token blocks, token budgets
+    (70000, 2, 1, 16, 0.9, torch.bfloat16, (None, None)),        # 4375 blocks: rows of more than 64 words
 ])
 def test_flex_selection_parity(L, Hq, Hk, bs, gamma, dtype, budget):
     _case(L=L, Hq=Hq, Hk=Hk, bs=bs, gamma=gamma, dtype=dtype, budget=budget)
@@ -373,6 +374,63 @@ def test_flex_full_length_32_token_blocks():
     n_sparse = int(info[:, 2].sum())
     print(f"  density {density(a):.4f} sparse heads {n_sparse}")
     assert n_sparse > 0
+
+
+def test_flex_8192_blocks_16_token_prefill():
+    """131072 tokens at 16-token blocks: 8192 blocks, the maximum (rows of 128
+    64-bit words, sparse covers cut over 67M entries, union lists over 8192 key
+    blocks).  Lists ascending and causal with block 0 and the diagonal,
+    deterministic; some head sparse; Flexprefill_prefill's output on sampled
+    query blocks of every head within max-abs 2e-2 of fp32 attention under
+    the kernel's lists."""
+    L, Hq, Hk, bs = 131072, 4, 1, 16
+    _case(L=L, Hq=Hq, Hk=Hk, bs=bs, prefill=True)
+    q, k, v = make_qkv(L, Hq, Hk, dtype=torch.bfloat16, seed=52)
+    ql, kl, vl = (x.to(DEV) for x in _blhd(q, k, v))
+    # a tau between the heads' divergences (their largest gap), so that some heads are sparse
+    js = flex_select(ql, kl, gamma=0.9, tau=0.0, block_size=bs).js.double().sort().values.cpu()
+    i = int((js[1:] - js[:-1]).argmax())
+    tau = float(0.5 * (js[i] + js[i + 1]))
+    a = flex_select(ql, kl, gamma=0.9, tau=tau, block_size=bs)
+    b = flex_select(ql, kl, gamma=0.9, tau=tau, block_size=bs)
+    torch.cuda.synchronize()
+    H, N = a.blk_cnt.shape
+    assert N == 8192
+    assert torch.equal(a.blk_cnt, b.blk_cnt) and torch.equal(a.head_info, b.head_info)
+    cnt = a.blk_cnt.to(torch.int64)
+    idx = a.blk_idx.view(torch.int16).to(torch.int64) & 0xFFFF
+    pos = torch.arange(N, device=DEV)
+    for h in range(H):
+        ia = idx[h]
+        valid = pos[None, :] < cnt[h, :, None]
+        ib = b.blk_idx[h].view(torch.int16).to(torch.int64) & 0xFFFF
+        assert bool(((ia == ib) | ~valid).all())
+        assert bool(((ia <= pos[:, None]) | ~valid).all())
+        assert bool(((ia[:, 1:] > ia[:, :-1]) | ~valid[:, 1:]).all())
+        assert bool((ia[:, 0] == 0).all())
+        assert bool((ia.gather(1, (cnt[h] - 1).clamp(min=0)[:, None])[:, 0] == pos).all())
+        del ia, ib, valid
+    info = a.head_info.cpu()
+    n_sparse = int(info[:, 2].sum())
+    print(f"  density {density(a):.4f} sparse heads {n_sparse} max row {int(cnt.max())}", flush=True)
+    assert n_sparse > 0
+    out = Flexprefill_prefill(ql, kl, vl, gamma=0.9, tau=tau, block_size=bs)
+    torch.cuda.synchronize()
+    o = out[0].float().cpu()
+    rows = [0, 1, 4095, 4096, 6000, N - 2, N - 1]
+    scale, worst = 128 ** -0.5, 0.0
+    for h in range(H):
+        kh, vh = k[0, h * Hk // Hq].float(), v[0, h * Hk // Hq].float()
+        for r in rows:
+            cols = idx[h, r, :int(cnt[h, r])].cpu().tolist()
+            t0, t1 = r * bs, min(L, (r + 1) * bs)
+            kidx = torch.cat([torch.arange(j * bs, min(L, (j + 1) * bs)) for j in cols])
+            s_ = (q[0, h, t0:t1].float() @ kh[kidx].T) * scale
+            s_ = s_.masked_fill(kidx[None, :] > torch.arange(t0, t1)[:, None], float("-inf"))
+            ref = torch.softmax(s_, -1) @ vh[kidx]
+            worst = max(worst, (o[t0:t1, h] - ref).abs().max().item())
+    print(f"  sampled rows max_abs {worst:.3e}", flush=True)
+    assert worst <= 2e-2
 
 
 @pytest.mark.parametrize("L,bs", [(65, 32), (100, 32), (129, 64), (2049, 32), (2049, 128), (4097, 64), (33, 16),

@@ -68,7 +68,7 @@ def test_bad_shapes_rejected_without_gpu():
     assert lib.fs_flex(ctypes.byref(f), None) == -1
     f.Hk, f.q_sl = 1, 100                                        # 200-byte row stride
     assert lib.fs_flex(ctypes.byref(f), None) == -1
-    f.q_sl, f.L, f.bs = 128, 4096 * 16 + 1, 16                   # 4097 blocks
+    f.q_sl, f.L, f.bs = 128, 8192 * 16 + 1, 16                   # 8193 blocks
     assert lib.fs_flex(ctypes.byref(f), None) == -2
     assert lib.fs_flex_work_bytes(4, 1, 4096, 64, 0.1) > 4 * 4096 * 4 * 2
     # tau <= 0 (the reference's default) makes no head sparse: no room for the
@@ -79,6 +79,9 @@ def test_bad_shapes_rejected_without_gpu():
                       q_sl=128, k_sl=128, v_sl=128, o_sl=512, blk_cnt=18, blk_idx=16)
     assert lib.fs_bsattn(ctypes.byref(x), None) == -1             # the lists are read as 32-bit words
     assert b"4-byte aligned" in lib.fs_last_error()
+    x.blk_cnt, x.bs, x.Lq, x.Lk = 16, 16, 8193 * 16, 8193 * 16    # union lists of 8193 key blocks
+    assert lib.fs_bsattn(ctypes.byref(x), None) == -2
+    assert b"8192 key blocks" in lib.fs_last_error()
     a = _lib.AttnArgs(q=16, k=16, v=16, out=16, dtype=1, B=1, Hq=3, Hk=2, Lq=10, Lk=10, D=128, bs=128)
     assert lib.fs_bsattn(ctypes.byref(a), None) == -1
     a = _lib.AttnArgs(q=16, k=16, v=16, out=16, work=16, dtype=1, B=1, Hq=4, Hk=2, Lq=10, Lk=10, D=96, bs=128)
