@@ -741,33 +741,59 @@ __global__ __launch_bounds__(kFHeadThreads) void flex_head_kernel(FlexHeadK a) {
   nv = min(max(nv, a.min_b), a.max_b);
   ns = min(max(ns, a.min_b), a.max_b);
 
-  // pooled vertical / slash (block sums in order)
+  // pooled vertical / slash (block sums in order; the loads of 8 entries are
+  // issued before they are added; entries past L read as 0)
   for (int j = tid; j < nb; j += kFHeadThreads) {
     float sv = 0.f, ss = 0.f;
-    for (int c = j * bs; c < min(L, (j + 1) * bs); ++c) {
-      sv += vt[c];
-      ss += st[c];
+    for (int c0 = j * bs; c0 < (j + 1) * bs; c0 += 8) {
+      float xv[8], xs[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const bool in = c0 + u < L;
+        xv[u] = in ? vt[c0 + u] : 0.f;
+        xs[u] = in ? st[c0 + u] : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        sv += xv[u];
+        ss += xs[u];
+      }
     }
     pv[j] = sv;
     ps[j] = ss;
   }
-  // mean over the bs rows of the scaled last queries, in T
+  // mean over the bs rows of the scaled last queries, in T (8 loads issued at a time)
   if (tid < kFD) {
     const uint16_t* qh = a.q + (int64_t)h * a.q_sh;
     float s = 0.f;
-    for (int i = 0; i < bs; ++i) {
-      const float x = to_f32(T{qh[(int64_t)(L - bs + i) * a.q_sl + tid]}) / a.sqrt_d;
-      s += Conv<T>::round(x);
+    for (int i0 = 0; i0 < bs; i0 += 8) {
+      float x[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) x[u] = to_f32(T{qh[(int64_t)(L - bs + i0 + u) * a.q_sl + tid]}) / a.sqrt_d;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) s += Conv<T>::round(x[u]);
     }
     lqm[tid] = Conv<T>::round(s / (float)bs);
   }
   __syncthreads();
-  // avg_qk (T) and its softmax over the blocks
+  // avg_qk (T) and its softmax over the blocks (a K block mean in two halves of
+  // 8 loads of 8 dims)
   float mx = -INFINITY;
   for (int j = tid; j < nb; j += kFHeadThreads) {
-    const uint16_t* kr = a.avg_k + ((int64_t)kvh * nb + j) * kFD;
+    const uint4* kr = reinterpret_cast<const uint4*>(a.avg_k + ((int64_t)kvh * nb + j) * kFD);
     float s = 0.f;
-    for (int d = 0; d < kFD; ++d) s += lqm[d] * to_f32(T{kr[d]});
+#pragma unroll 1
+    for (int c0 = 0; c0 < kFD / 8; c0 += 8) {
+      uint4 kv[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) kv[c] = kr[c0 + c];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const uint32_t w[4] = {kv[c].x, kv[c].y, kv[c].z, kv[c].w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s += lqm[8 * (c0 + c) + e] * to_f32(T{(uint16_t)(w[e >> 1] >> (16 * (e & 1)))});
+      }
+    }
     pk[j] = Conv<T>::round(s);
     mx = fmaxf(mx, pk[j]);
   }
@@ -800,15 +826,20 @@ __global__ __launch_bounds__(kFHeadThreads) void flex_head_kernel(FlexHeadK a) {
   // slash: top ns pooled entries j -> offsets nb - 1 - j
   __shared__ uint64_t sb[kFWords];
   topk_bits(ps, nb, min(ns, nb), sb, &cs, scan);
-  for (int w = tid; w < kFWords; w += kFHeadThreads) a.smask[(int64_t)h * kFWords + w] = 0;
-  __syncthreads();
+  // word w of the offsets: bit b is offset 64 w + b = entry x - b, x = nb - 1 - 64 w,
+  // so the word is entries x - 63 .. x reversed (entries below 0 read as 0)
+  for (int w = tid; w < kFWords; w += kFHeadThreads) {
+    const int x = nb - 1 - 64 * w;
+    uint64_t word = 0;
+    if (x >= 0) {
+      const int lo = x - 63, q = lo >> 6, sh = lo & 63;   // q = floor(lo / 64)
+      const uint64_t w0 = q >= 0 ? sb[q] : 0ull;
+      const uint64_t w1 = q + 1 < kFWords ? sb[q + 1] : 0ull;
+      word = __builtin_bitreverse64(sh ? (w0 >> sh) | (w1 << (64 - sh)) : w0);
+    }
+    a.smask[(int64_t)h * kFWords + w] = word;
+  }
   if (tid == 0) {
-    uint64_t* out = a.smask + (int64_t)h * kFWords;
-    for (int j = 0; j < nb; ++j)
-      if ((sb[j >> 6] >> (j & 63)) & 1) {
-        const int off = nb - 1 - j;
-        out[off >> 6] |= 1ull << (off & 63);
-      }
     a.info[h * 4 + 0] = nv;
     a.info[h * 4 + 1] = ns;
     a.info[h * 4 + 2] = sparse ? 1 : 0;
@@ -828,61 +859,134 @@ struct FlexCoverK {
   float sqrt_d, gamma;
 };
 
-// block-level causal attention rows of a sparse head: one workgroup per (head, block row)
+// block-level causal attention rows of a sparse head: one workgroup per (head,
+// kCoverRows consecutive block rows).  The K block means are staged in LDS 256
+// rows at a time (row stride 260 bytes: thread t reads row t, bank (t + d / 2)
+// % 64, conflict-free) and each staged row serves all the workgroup's query
+// rows.  Per row, as one row per workgroup would: the score of key block j is
+// the fp32 sum over d in order, rounded to T; thread t takes the blocks j = t,
+// t + 256, ... (its exponential sums in that order), the maxima and sums are
+// reduced by the same tree, and the scores and their exponentials pass
+// through the row's place in attn.
+constexpr int kCoverRows = 8;
+constexpr int kCoverStride = kFD + 2;            // staged row: 130 bf16 = 260 bytes
 template <typename T>
 __global__ __launch_bounds__(kFThreads) void flex_cover_rows_kernel(FlexCoverK a) {
-  __shared__ float aq[kFD];
-  __shared__ float rowv[kFMaxBlocks];
+  __shared__ float aq[kCoverRows][kFD];
+  __shared__ __attribute__((aligned(16))) uint16_t kst[kFThreads * kCoverStride];
   __shared__ float red[kFThreads];
-  const int h = blockIdx.x / a.nb, i = blockIdx.x % a.nb;
+  // a head's workgroups in order of decreasing row (the longest rows start
+  // first); consecutive workgroups (one head's) fall on different XCDs
+  const int ngr = (a.nb + kCoverRows - 1) / kCoverRows;
+  const int h = blockIdx.x / ngr, i0 = (ngr - 1 - (int)(blockIdx.x % ngr)) * kCoverRows;
   if (a.info[h * 4 + 2] == 0) return;              // not a sparse head
   const int tid = threadIdx.x, bs = a.bs, nb = a.nb, L = a.L;
+  const int nr = min(kCoverRows, nb - i0);         // rows of this workgroup
   const int kvh = kv_head(h, a.Hq, a.Hk, a.gqa_interleave);
   const int pad = nb * bs - L;
-  if (tid < kFD) {
-    // block mean of q over bs rows (zero padded), in T; the last block rescaled
-    // as (mean * bs) / (bs - pad), each step rounded to T
+  // block means of q over bs rows (zero padded), in T; the last block rescaled
+  // as (mean * bs) / (bs - pad), each step rounded to T.  Thread t forms the
+  // means of dim t % 128 for rows t / 128, t / 128 + 2, ...; the loads of 8
+  // tokens of every such row are issued before they are added (in token order).
+  {
+    constexpr int kPer = kCoverRows * kFD / kFThreads;   // (row, dim) pairs per thread
     const uint16_t* qh = a.q + (int64_t)h * a.q_sh;
-    float s = 0.f;
-    for (int r = 0; r < bs; ++r) {
-      const int t = i * bs + r;
-      if (t < L) s += to_f32(T{qh[(int64_t)t * a.q_sl + tid]});
+    const int d = tid % kFD, rr0 = tid / kFD;
+    float sum[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) sum[u] = 0.f;
+    for (int r0 = 0; r0 < bs; r0 += 8) {
+      float x[kPer][8];
+#pragma unroll
+      for (int u = 0; u < kPer; ++u)
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+          const int i = i0 + rr0 + 2 * u, t = i * bs + r0 + r;
+          x[u][r] = (rr0 + 2 * u < nr && t < L) ? to_f32(T{qh[(int64_t)t * a.q_sl + d]}) : 0.f;
+        }
+#pragma unroll
+      for (int u = 0; u < kPer; ++u)
+#pragma unroll
+        for (int r = 0; r < 8; ++r) sum[u] += x[u][r];
     }
-    float m = Conv<T>::round(s / (float)bs);
-    if (pad && i == nb - 1) m = Conv<T>::round(Conv<T>::round(m * (float)bs) / (float)(bs - pad));
-    aq[tid] = Conv<T>::round(m / a.sqrt_d);
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int rr = rr0 + 2 * u, i = i0 + rr;
+      if (rr >= nr) continue;
+      float m = Conv<T>::round(sum[u] / (float)bs);
+      if (pad && i == nb - 1) m = Conv<T>::round(Conv<T>::round(m * (float)bs) / (float)(bs - pad));
+      aq[rr][d] = Conv<T>::round(m / a.sqrt_d);
+    }
   }
-  __syncthreads();
-  float mx = -INFINITY;
-  for (int j = tid; j <= i; j += kFThreads) {
-    const uint16_t* kr = a.avg_k + ((int64_t)kvh * nb + j) * kFD;
-    float s = 0.f;
-    for (int d = 0; d < kFD; ++d) s += aq[d] * to_f32(T{kr[d]});
-    rowv[j] = Conv<T>::round(s);
-    mx = fmaxf(mx, rowv[j]);
-  }
-  red[tid] = mx;
-  __syncthreads();
-  for (int s = kFThreads / 2; s > 0; s >>= 1) {
-    if (tid < s) red[tid] = fmaxf(red[tid], red[tid + s]);
+  const int last = i0 + nr - 1;                    // the workgroup's last row: keys 0 .. last
+  float mx[kCoverRows];
+#pragma unroll
+  for (int rr = 0; rr < kCoverRows; ++rr) mx[rr] = -INFINITY;
+  float* rows = a.attn + ((int64_t)h * nb + i0) * nb;
+  const uint16_t* kbase = a.avg_k + (int64_t)kvh * nb * kFD;
+  for (int j0 = 0; j0 <= last; j0 += kFThreads) {
+    __syncthreads();                               // aq written / the previous tile consumed
+    // stage rows j0 .. j0 + 255 (16-byte global loads, 4-byte LDS writes)
+    for (int c = tid; c < kFThreads * (kFD / 8); c += kFThreads) {
+      const int r = c / (kFD / 8), cc = c - r * (kFD / 8);
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (j0 + r <= last) v = *reinterpret_cast<const uint4*>(kbase + (int64_t)(j0 + r) * kFD + cc * 8);
+      uint32_t* dst = reinterpret_cast<uint32_t*>(kst + r * kCoverStride + cc * 8);
+      dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
+    }
     __syncthreads();
+    const int j = j0 + tid;
+    if (j <= last) {
+      float acc[kCoverRows];
+#pragma unroll
+      for (int rr = 0; rr < kCoverRows; ++rr) acc[rr] = 0.f;
+      const uint32_t* kr = reinterpret_cast<const uint32_t*>(kst + tid * kCoverStride);
+      for (int d2 = 0; d2 < kFD / 2; ++d2) {
+        const uint32_t w = kr[d2];
+        const float k0 = to_f32(T{(uint16_t)(w & 0xffffu)}), k1 = to_f32(T{(uint16_t)(w >> 16)});
+#pragma unroll
+        for (int rr = 0; rr < kCoverRows; ++rr) {
+          acc[rr] += aq[rr][2 * d2] * k0;
+          acc[rr] += aq[rr][2 * d2 + 1] * k1;
+        }
+      }
+#pragma unroll
+      for (int rr = 0; rr < kCoverRows; ++rr) {
+        if (rr < nr && j <= i0 + rr) {
+          const float v = Conv<T>::round(acc[rr]);
+          rows[(int64_t)rr * nb + j] = v;
+          mx[rr] = fmaxf(mx[rr], v);
+        }
+      }
+    }
   }
-  mx = red[0];
-  __syncthreads();
-  float se = 0.f;
-  for (int j = tid; j <= i; j += kFThreads) {
-    rowv[j] = expf(rowv[j] - mx);
-    se += rowv[j];
-  }
-  red[tid] = se;
-  __syncthreads();
-  for (int s = kFThreads / 2; s > 0; s >>= 1) {
-    if (tid < s) red[tid] += red[tid + s];
+  for (int rr = 0; rr < nr; ++rr) {
+    const int i = i0 + rr;
+    float* out = rows + (int64_t)rr * nb;
+    red[tid] = mx[rr];
     __syncthreads();
+    for (int s = kFThreads / 2; s > 0; s >>= 1) {
+      if (tid < s) red[tid] = fmaxf(red[tid], red[tid + s]);
+      __syncthreads();
+    }
+    const float m = red[0];
+    __syncthreads();
+    float se = 0.f;
+    for (int j = tid; j <= i; j += kFThreads) {
+      const float e = expf(out[j] - m);
+      out[j] = e;
+      se += e;
+    }
+    red[tid] = se;
+    __syncthreads();
+    for (int s = kFThreads / 2; s > 0; s >>= 1) {
+      if (tid < s) red[tid] += red[tid + s];
+      __syncthreads();
+    }
+    se = red[0];
+    __syncthreads();
+    for (int j = tid; j < nb; j += kFThreads) out[j] = j <= i ? out[j] / se : 0.f;
   }
-  se = red[0];
-  float* out = a.attn + ((int64_t)h * nb + i) * nb;
-  for (int j = tid; j < nb; j += kFThreads) out[j] = j <= i ? rowv[j] / se : 0.f;
 }
 
 // the cover of gamma * N over a sparse head's N x N probabilities
@@ -1155,7 +1259,7 @@ static int launch_flex(const fs_flex_args& a, hipStream_t s) {
   ck.cover = reinterpret_cast<uint64_t*>(w + lay.cover);
   ck.Hq = a.Hq; ck.Hk = a.Hk; ck.L = a.L; ck.bs = a.bs; ck.nb = nb; ck.gqa_interleave = a.gqa_interleave;
   ck.sqrt_d = k.sqrt_d; ck.gamma = a.gamma;
-  if (sparse) flex_cover_rows_kernel<T><<<(unsigned)(a.Hq * nb), kFThreads, 0, s>>>(ck);
+  if (sparse) flex_cover_rows_kernel<T><<<(unsigned)(a.Hq * ((nb + kCoverRows - 1) / kCoverRows)), kFThreads, 0, s>>>(ck);
   // the sparse heads' covers: mass cut at gamma N of N^2 entries (rows add to one,
   // total nb <= 2^12: masses x 2^(58 - ceil(log2 nb)))
   CutJobs cc{};
