@@ -86,6 +86,24 @@ template <> struct XMma<f16_t> {
   }
 };
 
+// Rounding to the input dtype by the hardware conversion (round to nearest
+// even, as the bit-level one in common.h for every finite value), without the
+// per-element NaN branch: the score epilogue rounds 128 values per lane per tile.
+template <typename T> struct XCvt;
+template <> struct XCvt<bf16_t> {
+  static __device__ __forceinline__ float round(float f) { return (float)(__bf16)f; }
+  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)lo) | ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)hi) << 16);
+  }
+};
+template <> struct XCvt<f16_t> {
+  static __device__ __forceinline__ float round(float f) { return (float)(_Float16)f; }
+  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)lo) |
+           ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)hi) << 16);
+  }
+};
+
 struct XScoreK {
   const uint16_t* q;
   const uint16_t* k;            // k, or the K' buffer (double / triple)
@@ -97,13 +115,14 @@ struct XScoreK {
   int real_rows, npad, softmax;
   float scale;                  // Triton path: log2(e) / sqrt(D) / S / norm
   float inv_sqrt, inv_S, inv_norm;   // torch path: float32 reciprocals of the divisors
-  float* m;                     // [Hq][Lrq] row max (exp2 domain on the Triton path)
-  float* l;                     // [Hq][Lrq] row sum
+  float* m;                     // [nck][Hq][Lrq] row max of each key chunk (exp2 domain on the Triton path)
+  float* l;                     // [nck][Hq][Lrq] row sum of each key chunk
   float* sums;                  // [Hq][Nb][Nb] block sums (values of T)
   float* pad_sum;               // [Hq][Nb] non-causal: the sum of every key block of the chunk padding
   uint16_t* scores;             // [hg][head_stride] the rounded scores of heads h0 .. h0+hg-1, row tiles
   int64_t head_stride;
   int h0, hg;                   // the heads of this launch
+  int kc, items;                // key tiles (of 256) per score workgroup; workgroups per head
 };
 
 __host__ __device__ inline int ximin(int a, int b) { return a < b ? a : b; }
@@ -113,6 +132,16 @@ __host__ __device__ inline int xnct(int rt, int Lrq, int Lrk, int causal, int kd
   int last_key = Lrk - 1;
   if (causal) last_key = ximin(last_key, last_row * kdb + kdb - 1);
   return last_key < 0 ? 1 : last_key / kXKeys + 1;
+}
+// 256-key tiles of the 256-row tile R of the score pass, and its key chunks of kc tiles
+__host__ __device__ inline int xnct_wide(int R, int Lrq, int Lrk, int causal, int kdb) {
+  const int last_row = ximin(Lrq, (R + 1) * 256) - 1;
+  int last_key = Lrk - 1;
+  if (causal) last_key = ximin(last_key, last_row * kdb + kdb - 1);
+  return last_key < 0 ? 1 : last_key / 256 + 1;
+}
+__host__ __device__ inline int xchunks(int R, int Lrq, int Lrk, int causal, int kdb, int kc) {
+  return (xnct_wide(R, Lrq, Lrk, causal, kdb) + kc - 1) / kc;
 }
 // first stored score of row tile rt (every earlier tile is whole)
 __host__ __device__ inline int64_t xoffset(int rt, int Lrq, int Lrk, int causal, int kdb) {
@@ -134,9 +163,9 @@ __device__ __forceinline__ bool xkey_ok(const XScoreK& a, int row, int key) {
 // the score in the softmax's domain from the fp32 accumulator (or a stored value)
 template <typename T, bool TP>
 __device__ __forceinline__ float xscaled(const XScoreK& a, float acc) {
-  const float r = Conv<T>::round(acc);
+  const float r = XCvt<T>::round(acc);
   if constexpr (!TP) return r * a.scale;
-  return Conv<T>::round(Conv<T>::round(Conv<T>::round(r * a.inv_sqrt) * a.inv_S) * a.inv_norm);
+  return XCvt<T>::round(XCvt<T>::round(XCvt<T>::round(r * a.inv_sqrt) * a.inv_S) * a.inv_norm);
 }
 template <bool TP>
 __device__ __forceinline__ float xexp(float x) {
@@ -156,15 +185,32 @@ __device__ __forceinline__ float xexp(float x) {
 // the end.
 constexpr int kXWide = 256;
 constexpr int kXWideThreads = 512;
+constexpr int kXChunkTiles = 8;   // 256-key tiles per score workgroup (2048 reshaped keys)
+constexpr int kXBlock = 32;       // consecutive work items per XCD turn (one per CU)
 constexpr int kXHalf = 64;
 template <typename T, bool TP>
 __global__ __launch_bounds__(kXWideThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void xattn_scores_wide_kernel(XScoreK a) {
   // [buffer][Q' rows 0..255, then K' rows 0..255][64 dims]: 2 x 64 KiB
   __shared__ __attribute__((aligned(1024))) uint16_t lds[2][2 * kXWide * kXHalf];
+  // Work items (head, 256-row tile R, chunk c of kc key tiles): a head's items
+  // run R from the last down and c up; consecutive items go in blocks of
+  // kXBlock to one XCD (workgroup w runs on XCD w % 8, blocks dealt in turn),
+  // so the XCD's CUs hold a few row tiles x several key chunks of one head at a
+  // time and share their Q' and K' stage copies in its L2.
   const int nrt = (a.Lrq + kXWide - 1) / kXWide;
-  const int R = nrt - 1 - (int)(blockIdx.x / a.hg);                  // longest rows first
-  const int h = a.h0 + (int)(blockIdx.x % a.hg);
+  const int xslot = (int)(blockIdx.x >> 3);
+  const int item = ((xslot / kXBlock) * 8 + (int)(blockIdx.x & 7)) * kXBlock + xslot % kXBlock;
+  if (item >= a.hg * a.items) return;
+  const int hidx = item / a.items;
+  int p = item - hidx * a.items, R = nrt - 1;
+  for (; R > 0; --R) {
+    const int nc = xchunks(R, a.Lrq, a.Lrk, a.causal, a.kdb, a.kc);
+    if (p < nc) break;
+    p -= nc;
+  }
+  const int chunk = p;
+  const int h = a.h0 + hidx;
   const int hk = h / (a.Hq / a.Hk);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l32 = lane & 31, hi = lane >> 5;
   const int rg = wave & 3, kg = wave >> 2;          // 64-row group, 128-key group
@@ -175,7 +221,9 @@ void xattn_scores_wide_kernel(XScoreK a) {
   const int last_row = min(a.Lrq, r0 + kXWide) - 1;
   int last_key = a.Lrk - 1;
   if (a.causal) last_key = min(last_key, last_row * a.kdb + a.kdb - 1);
-  const int nct = last_key / kXWide + 1;           // 256-key tiles
+  const int nct = last_key / kXWide + 1;           // 256-key tiles of the row tile
+  const int ct0 = chunk * a.kc, ct1 = min(nct, ct0 + a.kc);   // this workgroup's key tiles
+  if (ct0 >= nct) return;
   // this wave's rows lie in one 128-row tile of the stored layout
   const int rt = wr0 / kXRows;
   const int NK = xnct(rt, a.Lrq, a.Lrk, a.causal, a.kdb) * kXKeys;
@@ -196,7 +244,7 @@ void xattn_scores_wide_kernel(XScoreK a) {
   // stage s = (ct S + j) 2 + dh: key tile ct, token offset j, dims 64 dh .. +63, buffer s & 1.
   // 512 rows of 128 bytes = 64 regions of 1 KiB (8 rows); waves 0-3 copy Q', 4-7 K'
   auto issue = [&](int s) {
-    const int dh = s & 1, sj = s >> 1, ct = sj / S, j = sj - ct * S;
+    const int dh = s & 1, sj = s >> 1, ct = ct0 + sj / S, j = sj % S;
     const int oj = (int)((a.qorder >> (4 * j)) & 15);
     const uint32_t lb = lds0 + (uint32_t)((s & 1) * 2 * kXWide * kXHalf * 2);
 #pragma unroll
@@ -213,11 +261,32 @@ void xattn_scores_wide_kernel(XScoreK a) {
   };
   auto epilogue = [&](int ct) {
     const int n0 = ct * kXWide + kg * kXKeys;        // this wave's first key
+    // the lane's key offsets are formed here from an opaque copy of its half's
+    // offset, not hoisted out of the stage loop (64 loop-invariant registers
+    // would leave the MFMA loop none to read its operands ahead)
+    int h4 = hi * 4;
+    asm volatile("" : "+v"(h4));
 #pragma unroll
     for (int rr = 0; rr < 2; ++rr) {
       const int row = wr0 + rr * 32 + l32;
       const bool row_ok = row < a.Lrq;
-      auto valid = [&](int kk, int r) { return row_ok && xkey_ok<TP>(a, row, n0 + kk * 32 + (r >> 2) * 8 + hi * 4 + (r & 3)); };
+      // the row's visible keys are one range [klo, khi] (xkey_ok as bounds), so a
+      // key's test is two compares with no branch
+      int klo = 0, khi = a.Lrk - 1;
+      if (a.causal) {
+        if constexpr (TP) {
+          khi = min(khi, row * a.kdb + a.kdb - 1);
+          if (a.own_chunk) klo = (row * a.kdb / a.own_chunk) * a.own_chunk;
+        } else {
+          khi = min(khi, row);
+        }
+      }
+      if (!row_ok) khi = -1;
+      // all ones when the key lies outside [klo, khi] (sign bits; no lane masks held)
+      auto outside = [&](int kk, int r) -> uint32_t {
+        const int key = n0 + kk * 32 + (r >> 2) * 8 + h4 + (r & 3);
+        return (uint32_t)(((khi - key) | (key - klo)) >> 31);
+      };
       auto xval = [&](int kk, int r) { return xscaled<T, TP>(a, acc[kk][rr][r]); };
       if (row_ok && n0 < NK) {
         uint16_t* dst = dst_base + (int64_t)(row - rt * kXRows) * NK;
@@ -228,18 +297,25 @@ void xattn_scores_wide_kernel(XScoreK a) {
             uint32_t w[2];
 #pragma unroll
             for (int e = 0; e < 2; ++e)
-              w[e] = (uint32_t)__builtin_bit_cast(uint16_t, Conv<T>::store(acc[kk][rr][g * 4 + 2 * e])) |
-                     ((uint32_t)__builtin_bit_cast(uint16_t, Conv<T>::store(acc[kk][rr][g * 4 + 2 * e + 1])) << 16);
-            *reinterpret_cast<uint2*>(dst + n0 + kk * 32 + g * 8 + hi * 4) = make_uint2(w[0], w[1]);
+              w[e] = XCvt<T>::pack2(acc[kk][rr][g * 4 + 2 * e], acc[kk][rr][g * 4 + 2 * e + 1]);
+            *reinterpret_cast<uint2*>(dst + n0 + kk * 32 + g * 8 + h4) = make_uint2(w[0], w[1]);
           }
       }
       if (stats) {
+        // the accumulators (stored above) now hold the scaled scores, -inf for an
+        // invisible key: it adds nothing to the max, and its exponential is 0
+#pragma unroll
+        for (int kk = 0; kk < kXKK; ++kk)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const uint32_t o = outside(kk, r);
+            acc[kk][rr][r] = __uint_as_float((__float_as_uint(xval(kk, r)) & ~o) | (0xff800000u & o));
+          }
         float mx = -INFINITY;
 #pragma unroll
         for (int kk = 0; kk < kXKK; ++kk)
 #pragma unroll
-          for (int r = 0; r < 16; ++r)
-            if (valid(kk, r)) mx = fmaxf(mx, xval(kk, r));
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, acc[kk][rr][r]);
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));    // the row's other keys sit in lane ^ 32
         const float m_new = fmaxf(m_run[rr], mx);
         if (m_new > -INFINITY) {
@@ -247,8 +323,7 @@ void xattn_scores_wide_kernel(XScoreK a) {
 #pragma unroll
           for (int kk = 0; kk < kXKK; ++kk)
 #pragma unroll
-            for (int r = 0; r < 16; ++r)
-              if (valid(kk, r)) sm += xexp<TP>(xval(kk, r) - m_new);
+            for (int r = 0; r < 16; ++r) sm += xexp<TP>(acc[kk][rr][r] - m_new);
           l_run[rr] = l_run[rr] * xexp<TP>(m_run[rr] - m_new) + sm;
           m_run[rr] = m_new;
         }
@@ -260,10 +335,10 @@ void xattn_scores_wide_kernel(XScoreK a) {
     }
   };
 
-  const int nst = nct * S * 2;
+  const int nst = (ct1 - ct0) * S * 2;
   issue(0);
   for (int s = 0; s < nst; ++s) {
-    const int dh = s & 1, sj = s >> 1, ct = sj / S, j = sj - ct * S;
+    const int dh = s & 1, sj = s >> 1, ct = ct0 + sj / S, j = sj % S;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's copies of stage s
     __syncthreads();                               // every wave's copies landed; stage s-1 done
     if (s + 1 < nst) issue(s + 1);                 // into the buffer stage s-1 used
@@ -281,20 +356,40 @@ void xattn_scores_wide_kernel(XScoreK a) {
       }
       __syncthreads();
     }
-#pragma unroll
-    for (int st = 0; st < kXHalf / 16; ++st) {
-      uint4 bq[2];
+    // the operands of 16-dim step st + 1 are read while step st's MFMAs run
+    // (two register sets), so an MFMA waits only for reads issued a step earlier
+    uint4 bq[2][2], ak[2][kXKK];
+    auto load_ops = [&](int st, int b) {
 #pragma unroll
       for (int rr = 0; rr < 2; ++rr) {
         const int row = rg * 64 + rr * 32 + l32;
-        bq[rr] = *reinterpret_cast<const uint4*>(qb + row * kXHalf + (((2 * st + hi) ^ (row & 7)) << 3));
+        bq[b][rr] = *reinterpret_cast<const uint4*>(qb + row * kXHalf + (((2 * st + hi) ^ (row & 7)) << 3));
       }
 #pragma unroll
       for (int kk = 0; kk < kXKK; ++kk) {
         const int key = kg * kXKeys + kk * 32 + l32;
-        const uint4 ak = *reinterpret_cast<const uint4*>(kb + key * kXHalf + (((2 * st + hi) ^ (key & 7)) << 3));
+        ak[b][kk] = *reinterpret_cast<const uint4*>(kb + key * kXHalf + (((2 * st + hi) ^ (key & 7)) << 3));
+      }
+    };
+    load_ops(0, 0);
 #pragma unroll
-        for (int rr = 0; rr < 2; ++rr) acc[kk][rr] = XMma<T>::mma(ak, bq[rr], acc[kk][rr]);
+    for (int st = 0; st < kXHalf / 16; ++st) {
+      if (st + 1 < kXHalf / 16) load_ops(st + 1, (st + 1) & 1);
+#pragma unroll
+      for (int kk = 0; kk < kXKK; ++kk)
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) acc[kk][rr] = XMma<T>::mma(ak[st & 1][kk], bq[st & 1][rr], acc[kk][rr]);
+    }
+    {
+      // order: step 0's six reads, then each MFMA followed by one read of the
+      // next step until they are all issued (a step's reads go out during the
+      // previous step's first six MFMAs)
+      constexpr int NR = 2 + kXKK, NM = (kXHalf / 16) * kXKK * 2;
+      __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
+#pragma unroll
+      for (int i = 0; i < NM; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (i % (2 * kXKK) < NR && i < NM - 2 * kXKK) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
     }
     if (dh == 1 && j == S - 1) epilogue(ct);
@@ -319,23 +414,13 @@ void xattn_scores_wide_kernel(XScoreK a) {
     for (int rr = 0; rr < 2; ++rr) {
       const int lr = rg * 64 + rr * 32 + l32, row = r0 + lr;
       if (row >= a.Lrq) continue;
-      float m, lt;
-      if (stats) {
-        const float m0 = xm[lr * 2], m1 = xm[lr * 2 + 1];
-        m = fmaxf(m0, m1);
-        lt = m == -INFINITY ? 0.f : xl[lr * 2] * xexp<TP>(m0 - m) + xl[lr * 2 + 1] * xexp<TP>(m1 - m);
-        if (a.npad > 0) {
-          // the chunk padding's keys (zero rows of K) score 0
-          const float m2 = fmaxf(m, 0.f);
-          lt = lt * xexp<TP>(m - m2) + (float)a.npad * xexp<TP>(-m2);
-          m = m2;
-        }
-      } else {
-        m = 0.f;
-        lt = 1.f;
-      }
-      a.m[(int64_t)h * a.Lrq + row] = m;
-      a.l[(int64_t)h * a.Lrq + row] = lt;
+      // this key chunk's row max and sum (the block-sum pass merges the chunks)
+      const float m0 = xm[lr * 2], m1 = xm[lr * 2 + 1];
+      const float m = fmaxf(m0, m1);
+      const float lt = m == -INFINITY ? 0.f : xl[lr * 2] * xexp<TP>(m0 - m) + xl[lr * 2 + 1] * xexp<TP>(m1 - m);
+      const int64_t at = ((int64_t)chunk * a.Hq + h) * a.Lrq + row;
+      a.m[at] = m;
+      a.l[at] = lt;
     }
   }
 }
@@ -355,9 +440,28 @@ __global__ __launch_bounds__(kXThreads) void xattn_sums_kernel(XScoreK a) {
   if (tid < kXRows) {
     const int row = r0 + tid;
     const bool ok = row < a.Lrq && row < a.real_rows;   // padding rows add nothing
-    const float lv = ok ? a.l[(int64_t)h * a.Lrq + row] : 0.f;
+    float m = 0.f, lv = 0.f;
+    if (ok) {
+      if (!TP || a.softmax) {
+        // the row's key chunks: the max of their maxima, then their sums rescaled to it, in chunk order
+        const int nc = xchunks(row / kXWide, a.Lrq, a.Lrk, a.causal, a.kdb, a.kc);
+        const int64_t cs = (int64_t)a.Hq * a.Lrq, at = (int64_t)h * a.Lrq + row;
+        m = -INFINITY;
+        for (int c = 0; c < nc; ++c) m = fmaxf(m, a.m[c * cs + at]);
+        if (m != -INFINITY)
+          for (int c = 0; c < nc; ++c) lv += a.l[c * cs + at] * xexp<TP>(a.m[c * cs + at] - m);
+        if (a.npad > 0) {
+          // the chunk padding's keys (zero rows of K) score 0
+          const float m2 = fmaxf(m, 0.f);
+          lv = lv * xexp<TP>(m - m2) + (float)a.npad * xexp<TP>(-m2);
+          m = m2;
+        }
+      } else {
+        lv = 1.f;                                    // no softmax: p = exp(x)
+      }
+    }
     rok[tid] = ok && lv > 0.f;
-    rm[tid] = ok ? a.m[(int64_t)h * a.Lrq + row] : 0.f;
+    rm[tid] = m;
     rl[tid] = TP ? lv : (lv > 0.f ? 1.0f / lv : 0.f);   // torch path divides, Triton multiplies by 1 / l
   }
   __syncthreads();
@@ -620,10 +724,21 @@ static int xgeom(const fs_xattn_args* a, XGeom& g) {
   return 0;
 }
 
-// workspace: row max and sum [Hq][Lrq] each, pad sums [Hq][N], K' [Hk][Lp][D] (double / triple), the stored scores
+// workspace: row max and sum of each key chunk [nck][Hq][Lrq] each, pad sums [Hq][N], K' [Hk][Lp][D]
+// (double / triple), the stored scores
 static size_t xalign(size_t n) { return (n + 255) & ~(size_t)255; }
+// key chunks of the longest row tile (the most any row has)
+static int xattn_max_chunks(const XGeom& g) {
+  const int nrt = (g.Lrq + kXWide - 1) / kXWide;
+  int mx = 1;
+  for (int R = 0; R < nrt; ++R) {
+    const int c = xchunks(R, g.Lrq, g.Lrk, g.causal, g.kdb, kXChunkTiles);
+    mx = c > mx ? c : mx;
+  }
+  return mx;
+}
 static size_t xattn_stats_bytes(int Hq, const XGeom& g) {
-  return xalign((size_t)Hq * g.Lrq * 2 * sizeof(float) + (size_t)Hq * g.N * sizeof(float));
+  return xalign((size_t)xattn_max_chunks(g) * Hq * g.Lrq * 2 * sizeof(float) + (size_t)Hq * g.N * sizeof(float));
 }
 static size_t xattn_kaug_bytes(int Hk, const XGeom& g) { return g.aug ? xalign((size_t)Hk * g.Lp_blk * kXD * 2) : 0; }
 // heads whose scores the workspace holds at once (the passes run head group by head group)
@@ -713,9 +828,13 @@ extern "C" int fs_xattn(const fs_xattn_args* a, void* stream) {
   k.inv_S = 1.0f / (float)a->stride;
   k.inv_norm = 1.0f / a->norm;
   char* w = static_cast<char*>(a->work);
+  const int nck = xattn_max_chunks(g);
   k.m = reinterpret_cast<float*>(w);
-  k.l = k.m + (size_t)a->Hq * g.Lrq;
-  k.pad_sum = k.l + (size_t)a->Hq * g.Lrq;
+  k.l = k.m + (size_t)nck * a->Hq * g.Lrq;
+  k.pad_sum = k.l + (size_t)nck * a->Hq * g.Lrq;
+  k.kc = kXChunkTiles;
+  k.items = 0;
+  for (int R = 0; R < (g.Lrq + kXWide - 1) / kXWide; ++R) k.items += xchunks(R, g.Lrq, g.Lrk, g.causal, g.kdb, k.kc);
   k.sums = a->sums;
   uint16_t* kaug = reinterpret_cast<uint16_t*>(w + xattn_stats_bytes(a->Hq, g));
   k.scores = reinterpret_cast<uint16_t*>(w + xattn_stats_bytes(a->Hq, g) + xattn_kaug_bytes(a->Hk, g));
@@ -746,7 +865,8 @@ extern "C" int fs_xattn(const fs_xattn_args* a, void* stream) {
     k.h0 = h0;
     k.hg = a->Hq - h0 < hg ? a->Hq - h0 : hg;
     const unsigned grid = (unsigned)(k.hg * ((g.Lrq + kXRows - 1) / kXRows));
-    const unsigned wgrid = (unsigned)(k.hg * ((g.Lrq + kXWide - 1) / kXWide));
+    const int64_t nblk = ((int64_t)k.hg * k.items + kXBlock - 1) / kXBlock;   // blocks of work items
+    const unsigned wgrid = (unsigned)((nblk + 7) / 8 * 8 * kXBlock);
     if (a->torch_path) {
       if (bf) {
         xattn_scores_wide_kernel<bf16_t, true><<<wgrid, kXWideThreads, 0, s>>>(k);
