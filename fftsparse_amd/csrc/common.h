@@ -19,12 +19,13 @@ __device__ __forceinline__ float to_f32(f16_t x) {
   return (float)h;
 }
 
-// fp32 -> bf16, round to nearest even (nan kept quiet).
+// fp32 -> bf16, round to nearest even (nan kept quiet).  Written as a select
+// of the two results, so that unrolled code rounds without a branch per value.
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t rne = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  const uint32_t qnan = (u >> 16) | 0x40u;
+  return (uint16_t)((u & 0x7fffffffu) > 0x7f800000u ? qnan : rne);
 }
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
   _Float16 h = (_Float16)f;
