@@ -337,9 +337,12 @@ def main():
         from fftsparse_amd.flex import flex_select
         q_blhd, k_blhd = q.transpose(1, 2), k.transpose(1, 2)      # the reference's [B, L, H, D] views
 
+    host_sel = []
+
     def step(ev=None):
         if ev:
             ev[0].record()
+        th = time.perf_counter()
         if xattn:
             sel = xattn_select(q, k, stride=args.xattn_stride, threshold=args.threshold, block_size=bs)
         elif flex:
@@ -347,6 +350,7 @@ def main():
         else:
             sel = select_blocks(q, k, pipeline_groups=args.select_groups, **kw)
         if ev:
+            host_sel.append((time.perf_counter() - th) * 1e3)
             ev[1].record()
         call = AttentionCall(q, k, v, sel.blk_cnt, sel.blk_idx, block_size=bs)
         call.prepare()
@@ -484,6 +488,8 @@ def main():
         "select_ms": round(t_sel, 4),
         "attn_ms": round(t_att, 4),
         "select_ms_median": round(statistics.median(sel_ms), 4),
+        "select_ms_steps": [round(x, 4) for x in sel_ms],
+        "select_host_enqueue_ms": round(statistics.mean(host_sel), 4),
         "attn_ms_median": round(statistics.median(att_ms), 4),
         "attn_kernel_ms": round(t_run, 4),
         "host_wall_ms_per_step": round(wall, 4),

@@ -145,9 +145,26 @@ def select_blocks(query_states: torch.Tensor, key_states: torch.Tensor, *, block
     thr = f32(corr_threshold)
     corr_mode = 1 if correlation_selection_mode == "topk" else 0
     corr_q = f32(1.0 - correlation_topk_ratio)                  # torch.quantile's q in fp32 (:200-201)
-    sel = BlockSelection(params=p,
-                         blk_cnt=torch.empty(Hq, N, dtype=torch.int32, device=dev),
-                         blk_idx=torch.empty(Hq, N, Nk, dtype=torch.uint16, device=dev))
+    # Optional pipeline over groups of KV heads (each with its query heads):
+    # pooling of group g+1 (HBM bound) runs on the caller's stream while the
+    # latency-bound statistics and block-list kernels of group g run on a side
+    # stream.  Heads are independent, so the result does not depend on the
+    # grouping.  One group is the default: at config 2 the cross-stream waits
+    # cost more than the overlap saves (0.30 ms with 1 group, 0.41 ms with 4).
+    ngroups = max(1, min(pipeline_groups or 1, Hk)) if need_pool else 1
+    bounds = [Hk * g // ngroups for g in range(ngroups + 1)]
+    lib = _lib.load()
+
+    def pool(g):
+        k0, k1 = bounds[g], bounds[g + 1]
+        h0, h1 = k0 * G, k1 * G
+        qg, kg = q[:, h0:h1], k[:, k0:k1]
+        _lib.call("fs_pool", PoolArgs(q=qg.data_ptr(), q_sh=q.stride(1), q_sl=q.stride(2),
+                                      k=kg.data_ptr(), k_sh=k.stride(1), k_sl=k.stride(2),
+                                      dtype=dt, Hq=h1 - h0, Hk=k1 - k0, L=L_q, D=D, bs=block_size,
+                                      q_b=sel.q_b[h0:h1].data_ptr(), k_b=sel.k_b[k0:k1].data_ptr()))
+
+    sel = BlockSelection(params=p, blk_cnt=None, blk_idx=None)
     if pooled is not None:
         q_b, k_b = pooled
         if (tuple(q_b.shape) != (Hq, N, D) or tuple(k_b.shape) != (Hk, N, D) or q_b.dtype != q.dtype
@@ -157,6 +174,12 @@ def select_blocks(query_states: torch.Tensor, key_states: torch.Tensor, *, block
     elif need_pool:
         sel.q_b = torch.empty(Hq, N, D, dtype=q.dtype, device=dev)
         sel.k_b = torch.empty(Hk, N, D, dtype=q.dtype, device=dev)
+        # The first group's pooling (the longest kernel of the stage) goes out
+        # before the remaining buffers are allocated: a call on an idle GPU
+        # then waits only for this much host work.
+        pool(0)
+    sel.blk_cnt = torch.empty(Hq, N, dtype=torch.int32, device=dev)
+    sel.blk_idx = torch.empty(Hq, N, Nk, dtype=torch.uint16, device=dev)
     if p.corr_enabled:
         sel.corr = torch.empty(Hq, N, dtype=torch.float32, device=dev)
         sel.corr_sum = torch.empty(Hq, N, dtype=torch.float32, device=dev)
@@ -169,15 +192,6 @@ def select_blocks(query_states: torch.Tensor, key_states: torch.Tensor, *, block
     dyn_mode = 1 if p.corr_enabled else 0
     col_mode = (1 if n_cols else 0) if p.corr_enabled else (2 if n_cols else 0)
 
-    # Optional pipeline over groups of KV heads (each with its query heads):
-    # pooling of group g+1 (HBM bound) runs on the caller's stream while the
-    # latency-bound statistics and block-list kernels of group g run on a side
-    # stream.  Heads are independent, so the result does not depend on the
-    # grouping.  One group is the default: at config 2 the cross-stream waits
-    # cost more than the overlap saves (0.30 ms with 1 group, 0.41 ms with 4).
-    ngroups = max(1, min(pipeline_groups or 1, Hk)) if need_pool else 1
-    bounds = [Hk * g // ngroups for g in range(ngroups + 1)]
-    lib = _lib.load()
     works = []
     for g in range(ngroups):
         hq = (bounds[g + 1] - bounds[g]) * G
@@ -197,12 +211,8 @@ def select_blocks(query_states: torch.Tensor, key_states: torch.Tensor, *, block
         k0, k1 = bounds[g], bounds[g + 1]
         h0, h1 = k0 * G, k1 * G
         hq, hk = h1 - h0, k1 - k0
-        if need_pool and pooled is None:
-            qg, kg = q[:, h0:h1], k[:, k0:k1]
-            _lib.call("fs_pool", PoolArgs(q=qg.data_ptr(), q_sh=q.stride(1), q_sl=q.stride(2),
-                                          k=kg.data_ptr(), k_sh=k.stride(1), k_sl=k.stride(2),
-                                          dtype=dt, Hq=hq, Hk=hk, L=L_q, D=D, bs=block_size,
-                                          q_b=sel.q_b[h0:h1].data_ptr(), k_b=sel.k_b[k0:k1].data_ptr()))
+        if need_pool and pooled is None and g > 0:
+            pool(g)
         if side is not main:
             ev = torch.cuda.Event()
             ev.record(main)

@@ -7,7 +7,7 @@ reference does before it launches any device work
 """
 from __future__ import annotations
 
-from dataclasses import dataclass, field
+from dataclasses import dataclass, field, replace
 
 import numpy as np
 import torch
@@ -40,6 +40,9 @@ class PrefillParams:
     last_k: int = 0
 
 
+_derived: dict = {}
+
+
 def derive(L_q: int, L_k: int, block_size: int = 128, sink_ratio: float = 0.1,
            recent_ratio: float = 0.1, local_span_ratio: float = 0.1,
            enable_correlation_mask: bool = True, correlation_topk_ratio: float = 0.2,
@@ -47,6 +50,25 @@ def derive(L_q: int, L_k: int, block_size: int = 128, sink_ratio: float = 0.1,
            column_start_exclude_ratio: float = 0.1, column_end_exclude_ratio: float = 0.2,
            enable_last_block_mask: bool = True, diag_sample_ratio: float = 0.15,
            min_diag_samples: int = 5, max_diag_samples: int = 64) -> PrefillParams:
+    """The parameters of one call.  Memoised on the arguments (a prefill
+    repeats the same shapes layer after layer, and the sample positions take a
+    torch.linspace); each call returns its own copy."""
+    key = (L_q, L_k, block_size, sink_ratio, recent_ratio, local_span_ratio, enable_correlation_mask,
+           correlation_topk_ratio, enable_column_mask, column_topk_ratio, column_start_exclude_ratio,
+           column_end_exclude_ratio, enable_last_block_mask, diag_sample_ratio, min_diag_samples,
+           max_diag_samples)
+    p = _derived.get(key)
+    if p is None:
+        if len(_derived) >= 256:
+            _derived.clear()
+        p = _derived[key] = _derive(*key)
+    return replace(p, sample_taus=list(p.sample_taus))
+
+
+def _derive(L_q, L_k, block_size, sink_ratio, recent_ratio, local_span_ratio, enable_correlation_mask,
+            correlation_topk_ratio, enable_column_mask, column_topk_ratio, column_start_exclude_ratio,
+            column_end_exclude_ratio, enable_last_block_mask, diag_sample_ratio, min_diag_samples,
+            max_diag_samples) -> PrefillParams:
     bs = block_size
     N = (L_q + bs - 1) // bs
     Nk = (L_k + bs - 1) // bs

@@ -306,7 +306,7 @@ FS_API int fs_xattn(const fs_xattn_args* a, void* stream);
  * work: fs_flex_work_bytes(Hq, Hk, L, bs, tau) bytes, with the tau of the
  * call (tau <= 0, the reference's default, makes no head sparse and needs no
  * room for the block-level attention and covers).  bf16/f16, D = 128,
- * bs 16, 32, 64 or 128, L > bs, N <= 4096. */
+ * bs 16, 32, 64 or 128, L > bs, N <= 8192. */
 typedef struct {
   const void* q; int64_t q_sh, q_sl;
   const void* k; int64_t k_sh, k_sl;
@@ -332,7 +332,7 @@ FS_API int fs_flex(const fs_flex_args* a, void* stream);
  * causal limit (dense causal attention).  Supported: dtype bf16/f16, D == 128,
  * bs in {16, 32, 64, 128} (16 and 32: FlexPrefill's block sizes; their lists
  * are attended 128 queries at a time over the union of 128 / bs rows' lists,
- * up to 4096 key blocks).  All tensors are
+ * up to 8192 key blocks).  All tensors are
  * strided views with d contiguous.
  * work: fs_bsattn_work_bytes(a) bytes of device scratch (V is staged there
  * transposed, and the work items' longest-first order is computed there,
