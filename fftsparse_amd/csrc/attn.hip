@@ -4,7 +4,10 @@
 //
 // Pre-pass (vt_kernel): V [Lk][D] of every KV head is rewritten once per call
 // as V^T [D][Lp] (Lp = Nk * BS rounded up to 64, zero padded) with the keys of every group of
-// 16 stored in the order 0-3, 8-11, 4-7, 12-15.  That order is exactly the
+// 16 stored in the order 0-3, 8-11, 4-7, 12-15.  With 16- or 32-token block
+// lists (union mode) V^T is stored block by block instead, [Lp / bs][D][bs]:
+// the copy of one listed block is then one contiguous run of D * bs keys
+// rather than D pieces of bs keys (64 or 32 bytes) strided by Lp.  That order is exactly the
 // key order in which an S^T accumulator of v_mfma_f32_32x32x16 hands P to the
 // next MFMA (lane half hi owns keys hi*4..hi*4+3 and 8+hi*4..8+hi*4+3 of each
 // 16-key group), so every MFMA operand of the main kernel is one
@@ -108,9 +111,10 @@ __device__ __forceinline__ int vt_pos(int k) {
 }
 
 // ---- V -> V^T pre-pass: one workgroup per (b, hk, 64-key slab) -------------
+// lb = 0: rows of Lp keys; lb = 16 or 32: blocks of lb keys, [Lp / lb][kD][lb].
 __global__ __launch_bounds__(256) void vt_kernel(const uint16_t* __restrict__ v, int64_t v_sb, int64_t v_sh,
                                                  int64_t v_sl, uint16_t* __restrict__ vt, int Hk, int Lk,
-                                                 int Lp) {
+                                                 int Lp, int lb) {
   __shared__ uint16_t tile[64][kD + 2];
   const int slabs = Lp / 64;
   const int bh = blockIdx.x / slabs, slab = blockIdx.x - bh * slabs;
@@ -140,7 +144,9 @@ __global__ __launch_bounds__(256) void vt_kernel(const uint16_t* __restrict__ v,
       const int ka = vt_pos(p0 + 2 * e), kb = vt_pos(p0 + 2 * e + 1);
       w[e] = (uint32_t)tile[ka][d] | ((uint32_t)tile[kb][d] << 16);
     }
-    *reinterpret_cast<uint4*>(dst + (int64_t)d * Lp + k0 + p0) = make_uint4(w[0], w[1], w[2], w[3]);
+    const int k = k0 + p0;                       // 8 keys of one block (lb is a multiple of 8)
+    const int64_t o = lb ? ((int64_t)(k / lb) * kD + d) * lb + k % lb : (int64_t)d * Lp + k;
+    *reinterpret_cast<uint4*>(dst + o) = make_uint4(w[0], w[1], w[2], w[3]);
   }
 }
 
@@ -339,7 +345,7 @@ void bsattn_kernel(AttnKArgs a) {
       // K rows relative to this wave's 16 rows of the tile; V^T: the key
       // offset of the lane's 8 keys inside their union entry
       koff[i] = (uint32_t)((r - wave * 4 * NR) * a.k_sl + c * 8) * 2u;
-      voff[i] = (uint32_t)((2 * r + (c >> 3)) * a.Lp + (((c & 7) * 8) % LB)) * 2u;
+      voff[i] = (uint32_t)((2 * r + (c >> 3)) * LB + (((c & 7) * 8) % LB)) * 2u;   // V^T stored block by block
     } else {
       koff[i] = (uint32_t)(r * a.k_sl + c * 8) * 2u;
       voff[i] = (TK == 128 ? (uint32_t)(r * a.Lp + c * 8)                          // d = r
@@ -406,7 +412,7 @@ void bsattn_kernel(AttnKArgs a) {
 #pragma unroll
         for (int ie = 0; ie < EPT; ++ie) {
           const int blk = (int)(uent(key0 * EPT + ie) & 0xffffu);
-          ek[ie] = (uint32_t)(blk < a.Nk ? blk * LB : 0) * 2u;
+          ek[ie] = (uint32_t)(blk < a.Nk ? blk * kD * LB : 0) * 2u;
         }
 #pragma unroll
         for (int i = 0; i < NR; ++i) {
@@ -1082,7 +1088,7 @@ extern "C" int fs_bsattn_prepare(const fs_attn_args* a, void* stream) {
   const int Lp = vt_len(Nk, a->bs);
   vt_kernel<<<a->B * a->Hk * (Lp / 64), 256, 0, (hipStream_t)stream>>>(
       static_cast<const uint16_t*>(a->v), a->v_sb, a->v_sh, a->v_sl, static_cast<uint16_t*>(a->work), a->Hk, a->Lk,
-      Lp);
+      Lp, union_mode(*a) ? a->bs : 0);
   return fs_host::launch_status("fs_bsattn_prepare");
 }
 

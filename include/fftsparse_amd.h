@@ -354,10 +354,11 @@ FS_API size_t fs_bsattn_work_bytes(const fs_attn_args* a);
 /* The whole stage-2 call: fs_bsattn_prepare then fs_bsattn_run. */
 FS_API int fs_bsattn(const fs_attn_args* a, void* stream);
 /* The two halves of fs_bsattn, for callers that time or reuse them apart.
- * prepare: writes V^T of every KV head into work (depends on v only).
- * run: the longest-first order pass (block lists only) and the attention
- * kernel; reads V^T from work, so a prepare with the same v, Lk and work must
- * precede it on the stream.  Both replace the same reference call as
+ * prepare: writes V^T of every KV head into work (depends on v, and on bs
+ * and whether block lists are given: 16- and 32-token lists take V^T block
+ * by block).  run: the longest-first order pass (block lists only) and the
+ * attention kernel; reads V^T from work, so a prepare with the same v, Lk,
+ * bs, lists (present or not) and work must precede it on the stream.  Both replace the same reference call as
  * fs_bsattn (my_attn_v7.py:775-786). */
 FS_API int fs_bsattn_prepare(const fs_attn_args* a, void* stream);
 FS_API int fs_bsattn_run(const fs_attn_args* a, void* stream);
