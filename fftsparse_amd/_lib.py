@@ -169,11 +169,32 @@ def load() -> ctypes.CDLL:
     return lib
 
 
-def call(name: str, args) -> None:
-    """Invoke an entry point on torch's current stream; raise on a non-zero status."""
+def same_device(*tensors) -> torch.device:
+    """The one GPU that every given tensor (None entries skipped) lives on.
+    The kernels dereference the tensors' pointers on that GPU, so a host
+    tensor, or tensors on two GPUs, raise ValueError before any launch."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError(f"tensors must be on the GPU, got one on {t.device}")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
+    if dev is None:
+        raise ValueError("no tensor given")
+    return dev
+
+
+def call(name: str, args, device: torch.device | None = None) -> None:
+    """Invoke an entry point on torch's current stream of ``device`` (default:
+    the current device), with that device current; raise on a non-zero status."""
     lib = load()
-    stream = torch.cuda.current_stream().cuda_stream
-    rc = getattr(lib, name)(ctypes.byref(args), c_void_p(stream))
+    with torch.cuda.device(device if device is not None else torch.cuda.current_device()):
+        stream = torch.cuda.current_stream().cuda_stream
+        rc = getattr(lib, name)(ctypes.byref(args), c_void_p(stream))
     if rc != 0:
         msg = lib.fs_last_error().decode(errors="replace")
         if rc == -1:

@@ -111,6 +111,9 @@ def select_blocks(query_states: torch.Tensor, key_states: torch.Tensor, *, block
     Hk, L_k = k.shape[1], k.shape[2]
     if Hq % Hk:
         raise ValueError(f"query heads {Hq} must be a multiple of key heads {Hk}")
+    if k.shape[3] != D:
+        raise ValueError(f"query head_dim {D} and key head_dim {k.shape[3]} differ")
+    dev = _lib.same_device(q, k, *(pooled or ()))
     if L_q != L_k:
         raise ValueError(f"prefill expects L_q == L_k, got {L_q} and {L_k}")
     if q.dtype != k.dtype or q.dtype not in _lib.FS_DTYPE:
@@ -128,7 +131,6 @@ def select_blocks(query_states: torch.Tensor, key_states: torch.Tensor, *, block
         # my_attn_v7.py:190-191 returns a single tensor there and the six-way
         # unpacking at :568 raises.
         raise ValueError("not enough values to unpack (expected 6, got 1)")
-    dev = q.device
     dt = _lib.FS_DTYPE[q.dtype]
     N, Nk = p.N, p.Nk
     G = Hq // Hk
@@ -162,7 +164,7 @@ def select_blocks(query_states: torch.Tensor, key_states: torch.Tensor, *, block
         _lib.call("fs_pool", PoolArgs(q=qg.data_ptr(), q_sh=q.stride(1), q_sl=q.stride(2),
                                       k=kg.data_ptr(), k_sh=k.stride(1), k_sl=k.stride(2),
                                       dtype=dt, Hq=h1 - h0, Hk=k1 - k0, L=L_q, D=D, bs=block_size,
-                                      q_b=sel.q_b[h0:h1].data_ptr(), k_b=sel.k_b[k0:k1].data_ptr()))
+                                      q_b=sel.q_b[h0:h1].data_ptr(), k_b=sel.k_b[k0:k1].data_ptr()), dev)
 
     sel = BlockSelection(params=p, blk_cnt=None, blk_idx=None)
     if pooled is not None:
@@ -229,7 +231,7 @@ def select_blocks(query_states: torch.Tensor, key_states: torch.Tensor, *, block
                     col_start=p.col_start, col_end=p.col_end, n_cols=n_cols, last_k=last_k,
                     diag_var=ptr(sl(sel.diag_var, h0, h1)), col_mean=ptr(sl(sel.col_mean, h0, h1)),
                     col_sel=ptr(sl(sel.col_sel, h0, h1)), last_scores=ptr(sl(sel.last_scores, h0, h1)),
-                    last_sel=ptr(sl(sel.last_sel, h0, h1)), work=works[g].data_ptr()))
+                    last_sel=ptr(sl(sel.last_sel, h0, h1)), work=works[g].data_ptr()), dev)
             else:
                 if p.corr_enabled:
                     _lib.call("fs_corr", CorrArgs(
@@ -237,7 +239,7 @@ def select_blocks(query_states: torch.Tensor, key_states: torch.Tensor, *, block
                         local_window=p.local_window, keep_sink=p.keep_sink, remote_start=p.remote_start,
                         corr_threshold=thr, corr_mode=corr_mode, corr_quantile=corr_q,
                         work=works[g].data_ptr(), corr=ptr(sl(sel.corr, h0, h1)),
-                        corr_sum=ptr(sl(sel.corr_sum, h0, h1)), keep_tau=ptr(sl(sel.keep_tau, h0, h1))))
+                        corr_sum=ptr(sl(sel.corr_sum, h0, h1)), keep_tau=ptr(sl(sel.keep_tau, h0, h1))), dev)
                 if n_samples or n_cols or last_k:
                     _lib.call("fs_stats", StatsArgs(
                         q_b=ptr(q_b), k_b=ptr(k_b), dtype=dt, Hq=hq, Hk=hk, N=N, D=D,
@@ -245,7 +247,7 @@ def select_blocks(query_states: torch.Tensor, key_states: torch.Tensor, *, block
                         col_start=p.col_start, col_end=p.col_end, n_cols=n_cols, last_k=last_k,
                         diag_var=ptr(sl(sel.diag_var, h0, h1)), col_mean=ptr(sl(sel.col_mean, h0, h1)),
                         col_sel=ptr(sl(sel.col_sel, h0, h1)), last_scores=ptr(sl(sel.last_scores, h0, h1)),
-                        last_sel=ptr(sl(sel.last_sel, h0, h1))))
+                        last_sel=ptr(sl(sel.last_sel, h0, h1))), dev)
             _lib.call("fs_select", SelectArgs(
                 q_b=ptr(q_b), k_b=ptr(k_b), dtype=dt, Hq=hq, Hk=hk, N=N, Nk=Nk, D=D, mask_causal=1,
                 keep_sink=p.keep_sink, keep_recent=p.keep_recent, local_window=p.local_window,
@@ -255,7 +257,7 @@ def select_blocks(query_states: torch.Tensor, key_states: torch.Tensor, *, block
                 qk_topk_ratio=f32(qk_topk_ratio), col_mode=col_mode, col_sel=ptr(sl(sel.col_sel, h0, h1)),
                 last_sel=ptr(sl(sel.last_sel, h0, h1)), mean_var=ptr(sl(sel.mean_var, h0, h1)),
                 is_stripe=ptr(sl(sel.is_stripe, h0, h1)), blk_cnt=sel.blk_cnt[h0:h1].data_ptr(),
-                blk_idx=sel.blk_idx[h0:h1].data_ptr()))
+                blk_idx=sel.blk_idx[h0:h1].data_ptr()), dev)
     if side is not main:
         main.wait_stream(side)                    # every output is ready on the caller's stream
     if not keep_intermediates:
@@ -296,7 +298,7 @@ def rope_pool(query_states: torch.Tensor, key_states: torch.Tensor, cos: torch.T
     if cs[0].stride(0) != cs[1].stride(0):
         cs = [t.contiguous() for t in cs]
     N = (L + block_size - 1) // block_size
-    dev = q.device
+    dev = _lib.same_device(q, k, *cs)
     q_rot = torch.empty(1, L, Hq, D, dtype=q.dtype, device=dev).transpose(1, 2)
     k_rot = torch.empty(1, L, Hk, D, dtype=q.dtype, device=dev).transpose(1, 2)
     q_b = torch.empty(Hq, N, D, dtype=q.dtype, device=dev)
@@ -306,7 +308,8 @@ def rope_pool(query_states: torch.Tensor, key_states: torch.Tensor, cos: torch.T
         cos=cs[0].data_ptr(), sin=cs[1].data_ptr(), cs_sl=cs[0].stride(0),
         q_out=q_rot.data_ptr(), qo_sh=q_rot.stride(1), qo_sl=q_rot.stride(2),
         k_out=k_rot.data_ptr(), ko_sh=k_rot.stride(1), ko_sl=k_rot.stride(2),
-        dtype=_lib.FS_DTYPE[q.dtype], Hq=Hq, Hk=Hk, L=L, D=D, bs=block_size, q_b=q_b.data_ptr(), k_b=k_b.data_ptr()))
+        dtype=_lib.FS_DTYPE[q.dtype], Hq=Hq, Hk=Hk, L=L, D=D, bs=block_size, q_b=q_b.data_ptr(), k_b=k_b.data_ptr()),
+        dev)
     return q_rot, k_rot, q_b, k_b
 
 
@@ -364,8 +367,12 @@ class AttentionCall:
                     or not blk_idx.is_contiguous()):
                 raise ValueError(f"blk_idx must be a contiguous uint16 [{Hq}, {Nq}, {Nk}] tensor, got "
                                  f"{blk_idx.dtype} {tuple(blk_idx.shape)}")
-            if blk_cnt.device != q.device or blk_idx.device != q.device:
-                raise ValueError("block lists must be on the device of the queries")
+        if k.shape[3] != D or v.shape[3] != D:
+            raise ValueError(f"query, key and value head_dim differ: {D}, {k.shape[3]}, {v.shape[3]}")
+        if out is not None and (tuple(out.shape) != (B, Lq, Hq, D) or out.dtype != q.dtype):
+            raise ValueError(f"out must be a [{B}, {Lq}, {Hq}, {D}] {q.dtype} tensor, got {out.dtype} "
+                             f"{tuple(out.shape)}")
+        self.device = _lib.same_device(q, k, v, blk_cnt, blk_idx, out)
         if out is None:
             out = torch.empty(B, Lq, Hq, D, dtype=q.dtype, device=q.device)
         scale = 1.0 / math.sqrt(D) if softmax_scale is None else float(softmax_scale)
@@ -385,14 +392,14 @@ class AttentionCall:
         self._keep = (q, k, v, blk_cnt, blk_idx)      # the pointers in args stay valid
 
     def prepare(self) -> None:
-        _lib.call("fs_bsattn_prepare", self.args)
+        _lib.call("fs_bsattn_prepare", self.args, self.device)
 
     def run(self) -> torch.Tensor:
-        _lib.call("fs_bsattn_run", self.args)
+        _lib.call("fs_bsattn_run", self.args, self.device)
         return self.out
 
     def __call__(self) -> torch.Tensor:
-        _lib.call("fs_bsattn", self.args)
+        _lib.call("fs_bsattn", self.args, self.device)
         return self.out
 
 

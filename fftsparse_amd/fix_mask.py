@@ -32,7 +32,8 @@ def fixed_block_lists(L_q: int, L_k: int, H: int, device, *, block_size=128, sin
     _lib.call("fs_select", SelectArgs(dtype=0, Hq=H, Hk=1, N=N, Nk=Nk, D=0, mask_causal=0,
                                       keep_sink=keep_sink, keep_recent=keep_recent, local_window=lw,
                                       remote_start=lw + 1, dyn_mode=0, col_mode=0,
-                                      blk_cnt=sel.blk_cnt.data_ptr(), blk_idx=sel.blk_idx.data_ptr()))
+                                      blk_cnt=sel.blk_cnt.data_ptr(), blk_idx=sel.blk_idx.data_ptr()),
+              sel.blk_cnt.device)
     return sel
 
 

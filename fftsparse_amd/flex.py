@@ -66,6 +66,9 @@ def flex_select(q: torch.Tensor, k: torch.Tensor, *, gamma: float = 0.9, tau: fl
         raise ValueError(f"query heads {Hq} must be a multiple of key heads {Hk}")
     if q.dtype != k.dtype or q.dtype not in (torch.bfloat16, torch.float16):
         raise TypeError(f"unsupported dtypes {q.dtype}, {k.dtype} (bf16/f16)")
+    if k.shape[0] != B or k.shape[3] != D:
+        raise ValueError(f"query {tuple(q.shape)} and key {tuple(k.shape)} shapes do not match")
+    dev = _lib.same_device(q, k)
     qv = q.transpose(1, 2)                                            # [1, Hq, L, D] views
     kv = k.transpose(1, 2)
     if qv.stride(3) != 1 or qv.stride(2) % 8 or qv.stride(1) % 8 or qv.data_ptr() % 16:
@@ -74,7 +77,6 @@ def flex_select(q: torch.Tensor, k: torch.Tensor, *, gamma: float = 0.9, tau: fl
         kv = kv.contiguous()
     nb = -(-L // block_size)
     mnb, mxb = budgets(L, block_size, min_budget, max_budget)
-    dev = q.device
     sel = FlexSelection(blk_cnt=torch.empty(Hq, nb, dtype=torch.int32, device=dev),
                         blk_idx=torch.empty(Hq, nb, nb, dtype=torch.uint16, device=dev),
                         head_info=torch.empty(Hq, 4, dtype=torch.int32, device=dev),
@@ -90,7 +92,7 @@ def flex_select(q: torch.Tensor, k: torch.Tensor, *, gamma: float = 0.9, tau: fl
         gamma=float(gamma), tau=float(tau), min_blocks=mnb, max_blocks=mxb, gqa_interleave=int(bool(gqa_interleave)),
         blk_cnt=sel.blk_cnt.data_ptr(), blk_idx=sel.blk_idx.data_ptr(), head_info=sel.head_info.data_ptr(),
         head_js=sel.js.data_ptr(), vertical=sel.vertical.data_ptr(), slash=sel.slash.data_ptr(),
-        work=work.data_ptr()))
+        work=work.data_ptr()), dev)
     sel._keep = (qv, kv, work)
     return sel
 

@@ -124,7 +124,7 @@ def xattn_select(query_states: torch.Tensor, key_states: torch.Tensor, *, stride
             pm[:stride] = [int(x) for x in pv.tolist()]
     chunk = default_chunk_size(L) if chunk_size is None else int(chunk_size)
     N = -(-L // block_size)
-    dev = q.device
+    dev = _lib.same_device(q, k)
     thr = _thresholds(threshold, Hq, dev)
     sel = XSelection(blk_cnt=torch.empty(Hq, N, dtype=torch.int32, device=dev),
                      blk_idx=torch.empty(Hq, N, N, dtype=torch.uint16, device=dev),
@@ -149,7 +149,7 @@ def xattn_select(query_states: torch.Tensor, key_states: torch.Tensor, *, stride
     args.head_group = -(-Hq // groups)            # the same heads per group, as few groups as fit
     work = torch.empty(max(1, lib.fs_xattn_work_bytes(ctypes.byref(args))), dtype=torch.uint8, device=dev)
     args.work = work.data_ptr()
-    _lib.call("fs_xattn", args)
+    _lib.call("fs_xattn", args, dev)
     sel._keep = (thr, work)                          # alive until the stream has used them
     return sel
 

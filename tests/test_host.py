@@ -178,3 +178,30 @@ def test_selection_block_limits_without_gpu():
                        keep_tau=16, corr_threshold=0.9)
     assert lib.fs_corr(ctypes.byref(co), None) == -2
     assert b"N=4097" in lib.fs_last_error()
+
+
+def test_api_rejects_host_tensors_and_bad_shapes_before_any_launch():
+    """Every public entry point checks devices and shapes on the host: a host
+    tensor (its pointer would reach a kernel), a wrong-sized ``out`` (written
+    through its strides) or a key head_dim unlike the query's raise ValueError."""
+    from fftsparse_amd import AttentionCall, block_sparse_attention, select_blocks
+    from fftsparse_amd.flex import flex_select
+    from fftsparse_amd.xattn import xattn_select
+    q = torch.zeros(1, 4, 1280, 128, dtype=torch.bfloat16)
+    k = torch.zeros(1, 2, 1280, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="on the GPU"):
+        block_sparse_attention(q, k, k)
+    with pytest.raises(ValueError, match="out must be"):
+        AttentionCall(q, k, k, out=torch.zeros(1, 1280, 4, 64, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="head_dim"):
+        AttentionCall(q, k[..., :64], k[..., :64])
+    with pytest.raises(ValueError, match="on the GPU"):
+        select_blocks(q, k)
+    with pytest.raises(ValueError, match="head_dim"):
+        select_blocks(q, k[..., :64])
+    with pytest.raises(ValueError, match="do not match"):
+        flex_select(q.transpose(1, 2), k[..., :64].transpose(1, 2))
+    with pytest.raises(ValueError, match="on the GPU"):
+        flex_select(q.transpose(1, 2), k.transpose(1, 2))
+    with pytest.raises(ValueError, match="on the GPU"):
+        xattn_select(q, k)
