@@ -321,6 +321,19 @@ void bsattn_kernel(AttnKArgs a) {
     if (i >= nlisted) return 0xffffffffu;
     return ((cptr32)(uintptr_t)a.blk_idx)[lbase + i];
   };
+  // Union mode: the entries of tiles t, t+1 and t+2 are held in scalar
+  // registers (u0, u1, u2) and those of tile t+3 are loaded during iteration
+  // t, so neither a copy nor a mask waits on a list load.
+  struct TileEnt {
+    uint32_t e[EPT];
+  };
+  TileEnt u0{}, u1{}, u2{}, u3{};
+  auto load_tile = [&](int t) -> TileEnt {
+    TileEnt u;
+#pragma unroll
+    for (int ie = 0; ie < EPT; ++ie) u.e[ie] = uent(t * EPT + ie);
+    return u;
+  };
   auto key_of = [&](int t) -> int {
     if constexpr (UNION) {
       if (listed) return t;                        // union mode: copies and masks look the tile's entries up
@@ -354,12 +367,16 @@ void bsattn_kernel(AttnKArgs a) {
     }
   }
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)&lds[0][0][0]);
-  auto issue_k = [&](int key0, int buf) {
+  auto issue_k = [&](int key0, int buf, TileEnt ue) {
     const uint32_t lk = lds0 + (uint32_t)(buf * C::TILE * 2 + wave * NR * 1024);
     if constexpr (UNION) {
       if (listed) {
-        // key0 is the tile index: this wave's 16 rows belong to entry 16 wave / LB
-        const uint32_t e = uent(key0 * EPT + (16 * wave) / LB);
+        // key0 is the tile index, ue its entries: this wave's 16 rows belong to entry 16 wave / LB
+        const int wsel = (16 * wave) / LB;
+        uint32_t es = ue.e[0];
+#pragma unroll
+        for (int ie = 1; ie < EPT; ++ie) es = wsel == ie ? ue.e[ie] : es;
+        const uint32_t e = __builtin_amdgcn_readfirstlane(es);   // wave-uniform: the copy base is scalar
         const int blk = (int)(e & 0xffffu);
         key0 = blk < a.Nk ? blk * LB + (16 * wave) % LB : -1;
       }
@@ -403,7 +420,7 @@ void bsattn_kernel(AttnKArgs a) {
       }
     }
   };
-  auto issue_v = [&](int key0, int buf) {
+  auto issue_v = [&](int key0, int buf, TileEnt ue) {
     const uint32_t lv = lds0 + (uint32_t)((2 + buf) * C::TILE * 2 + wave * NR * 1024);
     if constexpr (UNION) {
       if (listed) {
@@ -411,7 +428,7 @@ void bsattn_kernel(AttnKArgs a) {
         uint32_t ek[EPT];
 #pragma unroll
         for (int ie = 0; ie < EPT; ++ie) {
-          const int blk = (int)(uent(key0 * EPT + ie) & 0xffffu);
+          const int blk = (int)(ue.e[ie] & 0xffffu);
           ek[ie] = (uint32_t)(blk < a.Nk ? blk * kD * LB : 0) * 2u;
         }
 #pragma unroll
@@ -484,7 +501,7 @@ void bsattn_kernel(AttnKArgs a) {
   // Masking (diagonal / partial / invisible half tiles only) of the tile kb
   // whose scores are in s; the running max is taken later, beside the
   // exponentials of that tile.
-  auto mask_only = [&](int key0, f32x16_t* s) {
+  auto mask_only = [&](int key0, f32x16_t* s, TileEnt ue) {
     if constexpr (UNION) {
       if (listed) {
         // key0 is the tile index.  Lane row jq of the group; a key of entry ie
@@ -498,7 +515,7 @@ void bsattn_kernel(AttnKArgs a) {
         bool full = true;
 #pragma unroll
         for (int ie = 0; ie < EPT; ++ie) {
-          ents[ie] = uent(key0 * EPT + ie);
+          ents[ie] = ue.e[ie];
           const int blk = (int)(ents[ie] & 0xffffu);
           if (blk >= a.Nk || ((ents[ie] >> 16) & wrows) != wrows || blk * LB + LB > a.Lk ||
               (a.is_causal && blk * LB + LB - 1 > qw0 + off))
@@ -612,9 +629,12 @@ void bsattn_kernel(AttnKArgs a) {
     __builtin_amdgcn_s_barrier();
     if (t + 2 < cnt) {
       kb2 = key_of(t + 2);
-      issue_k(kb2, t & 1);
+      issue_k(kb2, t & 1, u2);
     }
-    if (t < cnt) issue_v((UNION && listed) ? t : kb0, t & 1);
+    if (t < cnt) issue_v((UNION && listed) ? t : kb0, t & 1, u0);
+    if constexpr (UNION) {
+      if (listed) u3 = load_tile(t + 3);
+    }
     __builtin_amdgcn_s_setprio(2);
     // The row max of tile t, the raise of the running max and the
     // exponentials of tile t are VALU work independent of the MFMAs of S(t+1)
@@ -654,26 +674,38 @@ void bsattn_kernel(AttnKArgs a) {
       l_run = l_run * al + (r0 + r1);
       if (__builtin_amdgcn_ballot_w64(al != 1.0f) != 0) scale_o(al);   // O holds P V up to t-1 now
     }
-    if constexpr (decltype(hasS)::value) mask_only(kb1, s_next);
+    if constexpr (decltype(hasS)::value) mask_only(kb1, s_next, u1);
     kb0 = kb1;
     kb1 = kb2;
+    if constexpr (UNION) {
+      u0 = u1;
+      u1 = u2;
+      u2 = u3;
+    }
   };
   // The first two K tiles are requested before the Q loads are waited for,
   // so the two latencies overlap; one wait then retires both (the loop's own
   // waits then find no register load of Q outstanding).
+  if constexpr (UNION) {
+    if (listed) {
+      u0 = load_tile(0);
+      u1 = load_tile(1);
+      u2 = load_tile(2);
+    }
+  }
   if (cnt > 0) {
     kb0 = key_of(0);
-    issue_k(kb0, 0);
+    issue_k(kb0, 0, u0);
     if (cnt > 1) {
       kb1 = key_of(1);
-      issue_k(kb1, 1);
+      issue_k(kb1, 1, u1);
     }
   }
   __builtin_amdgcn_s_waitcnt(0);
   if (cnt > 0) {
     __builtin_amdgcn_s_barrier();
     compute_s(0, sa);
-    mask_only(kb0, sa);
+    mask_only(kb0, sa, u0);
     // t = 0: S(1) if it exists, exponentials of tile 0, no P V yet
     if (cnt > 1) iter(0, sb, sa, pb, pa, yes(), no(), yes());
     else iter(0, sb, sa, pb, pa, no(), no(), yes());
