@@ -31,7 +31,7 @@ def _case(i: int):
     return rng, bs, Hk, g, Lq, Lk, causal, dtype, dens, empty_rows
 
 
-@pytest.mark.parametrize("i", range(40))
+@pytest.mark.parametrize("i", range(100))
 def test_random_lists_against_fp32(i):
     rng, bs, Hk, g, Lq, Lk, causal, dtype, dens, empty_rows = _case(i)
     Hq = Hk * g

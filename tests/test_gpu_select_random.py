@@ -50,7 +50,7 @@ def _case(i: int):
     return bs, Hq, Hk, L, dtype, kw
 
 
-@pytest.mark.parametrize("i", range(24))
+@pytest.mark.parametrize("i", range(40))
 def test_random_parameters_against_oracle(i):
     bs, Hq, Hk, L, dtype, kw = _case(i)
     print(f"[case] random-select {i}: L={L} Hq={Hq} Hk={Hk} {dtype} {kw}", flush=True)
