@@ -452,9 +452,13 @@ def main():
                            "timed": "flex_select: last-block scores (2 passes), K block means, per-head budgets / "
                                     "JS test / top-k, sparse-head cover (2 launches), block lists"}
     else:
+        t_sel_med = statistics.median(sel_ms)
         roofline_select = {"bound": "hbm", "achieved": round(sel_bytes / (t_sel * 1e-3) / 1e9, 1),
                            "peak": PEAK_HBM_GBS, "unit": "GB/s",
                            "frac": round(sel_bytes / (t_sel * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                           # the same on the median step (the mean includes the first timed step,
+                           # which starts on an idle GPU)
+                           "frac_median": round(sel_bytes / (t_sel_med * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
                            "traffic": pmc_traffic("select", cfg.name),
                            "work": "Q and K read once (L*(Hq+Hkv)*D*2 bytes)",
                            "timed": "select_blocks: pool, block-score tiles + statistics (2 launches), block lists "
