@@ -202,6 +202,12 @@ struct AttnKArgs {
   int run;                      // query blocks per scheduling unit (block lists)
   float scale;
   int gqa_interleave;           // KV head h % Hk (else h / (Hq / Hk))
+  // dynamic assignment (block lists, null: the static one): ticket counters
+  // [8 XCDs + 1 shared pool], zeroed by the order pass; the first
+  // static_units units of the order are dealt to the XCDs round-robin, the
+  // last pool_units are taken by whichever XCD asks first
+  int32_t* ctr;
+  int static_units, pool_units;
 };
 
 // 16-byte LDS operand at byte offset off of base
@@ -239,10 +245,46 @@ void bsattn_kernel(AttnKArgs a) {
     // decreasing tile count, dealt round-robin to the XCDs; a unit's query
     // blocks take consecutive slots of one XCD, so they run side by side and
     // share the K/V tiles of their (shifted) lag diagonals and columns in its L2
-    const int unit_slot = slot / a.run, j = slot - unit_slot * a.run;
-    const int p = unit_slot * 8 + x;
-    if (p >= a.total) return;                     // total = Hq * ceil(Nq / run) units
-    const int unit = (int)((cptr32)(uintptr_t)a.order)[p];
+    int unit, j;
+    if (a.ctr != nullptr) {
+      // Dynamic assignment: the workgroup takes the next ticket of its XCD's
+      // share (the share's units in order, `run` consecutive tickets per unit,
+      // so a unit's query blocks still run side by side on one XCD); once the
+      // share is used up, the next ticket of the shared pool (the shortest
+      // units).  Measured per workgroup, the XCDs of one launch differ in
+      // time per tile by up to 10%, and a static deal left the faster ones
+      // idle for the last 5-10% of the kernel; the pool lets them take more.
+      // Every ticket is taken exactly once; workgroups past the last ticket
+      // return at once.
+      __shared__ int pick[2];
+      if (threadIdx.x == 0) {
+        int u = -1, jj = 0;
+        const int sx = a.static_units > x ? (a.static_units - x + 7) / 8 : 0;   // units x, x+8, .. of the share
+        const int i = atomicAdd(&a.ctr[x], 1);
+        if (i < sx * a.run) {
+          u = a.order[(i / a.run) * 8 + x];
+          jj = i % a.run;
+        } else {
+          const int t = atomicAdd(&a.ctr[8], 1);
+          if (t < a.pool_units * a.run) {
+            u = a.order[a.static_units + t / a.run];
+            jj = t % a.run;
+          }
+        }
+        pick[0] = u;
+        pick[1] = jj;
+      }
+      __syncthreads();
+      unit = __builtin_amdgcn_readfirstlane(pick[0]);
+      j = __builtin_amdgcn_readfirstlane(pick[1]);
+      if (unit < 0) return;
+    } else {
+      const int unit_slot = slot / a.run;
+      j = slot - unit_slot * a.run;
+      const int p = unit_slot * 8 + x;
+      if (p >= a.total) return;                   // total = Hq * ceil(Nq / run) units
+      unit = (int)((cptr32)(uintptr_t)a.order)[p];
+    }
     const int nc = (a.Nq + a.run - 1) / a.run;
     b = 0;
     h = unit / nc;
@@ -781,13 +823,17 @@ void bsattn_kernel(AttnKArgs a) {
 // while its query heads run, instead of every KV head's streaming at once.
 // Counting sort of key = hk * nbc + (nbc - 1 - (tile count >> shift)).
 constexpr int kOrderThreads = 1024;
+constexpr int kTicketCounters = 9;               // 8 XCD shares + the shared pool
+constexpr int kPoolPercent = 6;                  // share of the work units (the shortest) in the shared pool
 constexpr int kOrderMaxBins = 8192;
 constexpr int kOrderKeysPerThread = 8;           // keys kept in registers between the two passes
 // kvmajor = 0: one longest-first order over all units (the KV group left out of the key).
 __global__ __launch_bounds__(kOrderThreads) void order_kernel(const int32_t* __restrict__ cnt, int Hq, int Hk,
                                                               int gqa_interleave, int Nq, int run, int Nk, int shift,
-                                                              int32_t* __restrict__ order, int kvmajor) {
+                                                              int32_t* __restrict__ order, int kvmajor,
+                                                              int32_t* __restrict__ ctr) {
   __shared__ int hist[kOrderMaxBins];
+  if (ctr != nullptr && threadIdx.x < kTicketCounters) ctr[threadIdx.x] = 0;   // the attention kernel's tickets
   __shared__ int part[kOrderThreads];
   const int tid = threadIdx.x;
   const int nc = (Nq + run - 1) / run;
@@ -991,7 +1037,12 @@ static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 // workspace after V^T: the order [Hq * Nq] (+ union mode: u_cnt [Hq * Ng], u_idx [Hq * Ng * Nk])
 static size_t order_bytes(const fs_attn_args& a) {
   const int64_t Nq = (a.Lq + a.bs - 1) / a.bs;
-  return align256((size_t)a.Hq * Nq * sizeof(int32_t));
+  return align256((size_t)a.Hq * Nq * sizeof(int32_t)) + 256;   // + the ticket counters
+}
+static int32_t* ticket_counters(const fs_attn_args& a) {
+  const int64_t Nq = (a.Lq + a.bs - 1) / a.bs;
+  return reinterpret_cast<int32_t*>(static_cast<char*>(a.work) + vt_bytes(a) +
+                                    align256((size_t)a.Hq * Nq * sizeof(int32_t)));
 }
 static bool union_mode(const fs_attn_args& a) { return a.blk_cnt != nullptr && a.bs < 64; }
 static int union_groups(const fs_attn_args& a) {
@@ -1006,6 +1057,8 @@ static int launch_run(const fs_attn_args& a, int Nq, int Nk, hipStream_t s, int 
   if (Lp == 0) Lp = vt_len(Nk, BS);                // else: V^T laid out for another block size
   const uint16_t* vt = static_cast<const uint16_t*>(a.work);
   int32_t* order = nullptr;
+  int32_t* ctr = nullptr;
+  int static_units = 0, pool_units = 0;
   int total;
   unsigned grid;
   // Scheduling units of `run` consecutive query blocks: at C2 (Nq = 1024) a
@@ -1017,10 +1070,18 @@ static int launch_run(const fs_attn_args& a, int Nq, int Nk, hipStream_t s, int 
     while ((int64_t)a.Hk * (((run * Nk) >> shift) + 1) > kOrderMaxBins) ++shift;
     order = reinterpret_cast<int32_t*>(static_cast<char*>(a.work) + vt_bytes(a));
     total = a.Hq * ((Nq + run - 1) / run);
+    ctr = ticket_counters(a);
     order_kernel<<<1, kOrderThreads, 0, s>>>(a.blk_cnt, a.Hq, a.Hk, a.gqa_interleave ? 1 : 0, Nq, run, Nk, shift,
-                                             order, kv_major(a, Nq));
+                                             order, kv_major(a, Nq), ctr);
     if (int rc = fs_host::launch_status("fs_bsattn (order)")) return rc;
-    grid = (unsigned)((total + 7) / 8 * 8 * run);
+    // the last kPoolPercent% of the ordered units (the shortest) form the
+    // shared pool; XCD x's share is units x, x+8, .. of the rest.  Each XCD
+    // gets enough workgroups for its share and twice its even part of the
+    // pool; the ones that find no ticket left return at once.
+    pool_units = (int)((int64_t)total * kPoolPercent / 100);
+    static_units = total - pool_units;
+    const int64_t per_xcd = (int64_t)(static_units + 7) / 8 * run + 2 * (((int64_t)pool_units * run + 7) / 8);
+    grid = (unsigned)(8 * per_xcd);
   } else {
     total = a.B * Nq;
     grid = (unsigned)((total + 7) / 8 * a.Hq * 8);
@@ -1040,6 +1101,9 @@ static int launch_run(const fs_attn_args& a, int Nq, int Nk, hipStream_t s, int 
   k.run = run;
   k.scale = a.softmax_scale;
   k.gqa_interleave = a.gqa_interleave ? 1 : 0;
+  k.ctr = ctr;
+  k.static_units = static_units;
+  k.pool_units = pool_units;
   bsattn_kernel<BS, TK, T><<<grid, AttnCfg<BS, TK>::NT, 0, s>>>(k);
   return fs_host::launch_status("fs_bsattn");
 }
@@ -1063,7 +1127,7 @@ static int launch_run_union(const fs_attn_args& a, hipStream_t s) {
   while ((int64_t)a.Hk * (((run * NkL) >> shift) + 1) > kOrderMaxBins) ++shift;
   const int total = a.Hq * ((Ng + run - 1) / run);
   order_kernel<<<1, kOrderThreads, 0, s>>>(u_cnt, a.Hq, a.Hk, a.gqa_interleave ? 1 : 0, Ng, run, NkL, shift, order,
-                                           kv_major(a, Ng));
+                                           kv_major(a, Ng), nullptr);
   if (int rc = fs_host::launch_status("fs_bsattn (order)")) return rc;
   AttnKArgs k;
   k.q = static_cast<const uint16_t*>(a.q);
@@ -1079,6 +1143,8 @@ static int launch_run_union(const fs_attn_args& a, hipStream_t s) {
   k.Nq = Ng; k.Nk = NkL; k.Lp = vt_len(NkL, LB); k.total = total; k.is_causal = a.is_causal;
   k.run = run;
   k.scale = a.softmax_scale;
+  k.ctr = nullptr;                                 // static assignment
+  k.static_units = k.pool_units = 0;
   k.gqa_interleave = a.gqa_interleave ? 1 : 0;
   const unsigned grid = (unsigned)((total + 7) / 8 * 8 * run);
   bsattn_kernel<128, 64, T, LB><<<grid, AttnCfg<128, 64>::NT, 0, s>>>(k);
