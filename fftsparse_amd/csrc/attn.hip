@@ -1039,6 +1039,17 @@ static size_t order_bytes(const fs_attn_args& a) {
   const int64_t Nq = (a.Lq + a.bs - 1) / a.bs;
   return align256((size_t)a.Hq * Nq * sizeof(int32_t)) + 256;   // + the ticket counters
 }
+// Ticket assignment of `total` ordered work units of `run` workgroups: the
+// last kPoolPercent% of the units (the shortest) form the shared pool, XCD x's
+// share is units x, x+8, .. of the rest.  Each XCD gets enough workgroups for
+// its share and twice its even part of the pool; the ones that find no ticket
+// left return at once.  Returns the grid.
+static unsigned deal_units(int total, int run, int& static_units, int& pool_units) {
+  pool_units = (int)((int64_t)total * kPoolPercent / 100);
+  static_units = total - pool_units;
+  const int64_t per_xcd = (int64_t)(static_units + 7) / 8 * run + 2 * (((int64_t)pool_units * run + 7) / 8);
+  return (unsigned)(8 * per_xcd);
+}
 static int32_t* ticket_counters(const fs_attn_args& a) {
   const int64_t Nq = (a.Lq + a.bs - 1) / a.bs;
   return reinterpret_cast<int32_t*>(static_cast<char*>(a.work) + vt_bytes(a) +
@@ -1074,14 +1085,7 @@ static int launch_run(const fs_attn_args& a, int Nq, int Nk, hipStream_t s, int 
     order_kernel<<<1, kOrderThreads, 0, s>>>(a.blk_cnt, a.Hq, a.Hk, a.gqa_interleave ? 1 : 0, Nq, run, Nk, shift,
                                              order, kv_major(a, Nq), ctr);
     if (int rc = fs_host::launch_status("fs_bsattn (order)")) return rc;
-    // the last kPoolPercent% of the ordered units (the shortest) form the
-    // shared pool; XCD x's share is units x, x+8, .. of the rest.  Each XCD
-    // gets enough workgroups for its share and twice its even part of the
-    // pool; the ones that find no ticket left return at once.
-    pool_units = (int)((int64_t)total * kPoolPercent / 100);
-    static_units = total - pool_units;
-    const int64_t per_xcd = (int64_t)(static_units + 7) / 8 * run + 2 * (((int64_t)pool_units * run + 7) / 8);
-    grid = (unsigned)(8 * per_xcd);
+    grid = deal_units(total, run, static_units, pool_units);
   } else {
     total = a.B * Nq;
     grid = (unsigned)((total + 7) / 8 * a.Hq * 8);
@@ -1126,8 +1130,9 @@ static int launch_run_union(const fs_attn_args& a, hipStream_t s) {
   int shift = 0;
   while ((int64_t)a.Hk * (((run * NkL) >> shift) + 1) > kOrderMaxBins) ++shift;
   const int total = a.Hq * ((Ng + run - 1) / run);
+  int32_t* ctr = ticket_counters(a);              // after the order, inside order_bytes
   order_kernel<<<1, kOrderThreads, 0, s>>>(u_cnt, a.Hq, a.Hk, a.gqa_interleave ? 1 : 0, Ng, run, NkL, shift, order,
-                                           kv_major(a, Ng), nullptr);
+                                           kv_major(a, Ng), ctr);
   if (int rc = fs_host::launch_status("fs_bsattn (order)")) return rc;
   AttnKArgs k;
   k.q = static_cast<const uint16_t*>(a.q);
@@ -1143,10 +1148,9 @@ static int launch_run_union(const fs_attn_args& a, hipStream_t s) {
   k.Nq = Ng; k.Nk = NkL; k.Lp = vt_len(NkL, LB); k.total = total; k.is_causal = a.is_causal;
   k.run = run;
   k.scale = a.softmax_scale;
-  k.ctr = nullptr;                                 // static assignment
-  k.static_units = k.pool_units = 0;
+  k.ctr = ctr;
   k.gqa_interleave = a.gqa_interleave ? 1 : 0;
-  const unsigned grid = (unsigned)((total + 7) / 8 * 8 * run);
+  const unsigned grid = deal_units(total, run, k.static_units, k.pool_units);
   bsattn_kernel<128, 64, T, LB><<<grid, AttnCfg<128, 64>::NT, 0, s>>>(k);
   return fs_host::launch_status("fs_bsattn");
 }
