@@ -335,8 +335,11 @@ FS_API int fs_flex(const fs_flex_args* a, void* stream);
  * up to 8192 key blocks).  All tensors are
  * strided views with d contiguous.
  * work: fs_bsattn_work_bytes(a) bytes of device scratch (V is staged there
- * transposed, and the work items' longest-first order is computed there,
- * before the attention kernel runs). */
+ * transposed, and the work items' longest-first order and the counters from
+ * which the attention kernel's workgroups take their work items are formed
+ * there, before the attention kernel runs).  Calls that overlap on one
+ * workspace race; the lists' results do not depend on which workgroup takes
+ * which item. */
 typedef struct {
   const void* q; int64_t q_sb, q_sh, q_sl;
   const void* k; int64_t k_sb, k_sh, k_sl;
