@@ -824,7 +824,7 @@ void bsattn_kernel(AttnKArgs a) {
 // Counting sort of key = hk * nbc + (nbc - 1 - (tile count >> shift)).
 constexpr int kOrderThreads = 1024;
 constexpr int kTicketCounters = 9;               // 8 XCD shares + the shared pool
-constexpr int kPoolPercent = 6;                  // share of the work units (the shortest) in the shared pool
+constexpr int kPoolPercent = 10;                 // share of the work units (the shortest) in the shared pool
 constexpr int kOrderMaxBins = 8192;
 constexpr int kOrderKeysPerThread = 8;           // keys kept in registers between the two passes
 // kvmajor = 0: one longest-first order over all units (the KV group left out of the key).
