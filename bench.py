@@ -352,7 +352,7 @@ def main():
         if ev:
             host_sel.append((time.perf_counter() - th) * 1e3)
             ev[1].record()
-        call = AttentionCall(q, k, v, sel.blk_cnt, sel.blk_idx, block_size=bs)
+        call = AttentionCall(q, k, v, sel.blk_cnt, sel.blk_bits, block_size=bs)
         call.prepare()
         if ev:
             ev[2].record()
@@ -450,7 +450,7 @@ def main():
                            "work": ("K read 3x (2 score passes + block means: 3*L*Hkv*D*2 bytes), the sparse heads' Q "
                                     f"({n_sparse} heads), vertical/slash profiles written (2*Hq*L*4 bytes)"),
                            "timed": "flex_select: last-block scores (2 passes), K block means, per-head budgets / "
-                                    "JS test / top-k, sparse-head cover (2 launches), block lists"}
+                                    "JS test / top-k, sparse-head cover (2 launches), block mask"}
     else:
         t_sel_med = statistics.median(sel_ms)
         roofline_select = {"bound": "hbm", "achieved": round(sel_bytes / (t_sel * 1e-3) / 1e9, 1),

@@ -6,8 +6,8 @@ attn_src/fix_mask_attn/my_attn.py):
 
     myattn_prefill(q, k, v, layer_idx, ...)        v7 selection + sparse attention
     fix_mask.myattn_prefill(q, k, v, layer_idx, ...) fixed sink/recent/local mask
-    select_blocks(q, k, ...)                        stage 1 only (block lists)
-    block_sparse_attention(q, k, v, cnt, idx, ...)  stage 2 only
+    select_blocks(q, k, ...)                        stage 1 only (the block mask)
+    block_sparse_attention(q, k, v, cnt, bits, ...) stage 2 only (or block_mask=: base_blockmask)
     rope_pool(q, k, cos, sin, ...)                  the rotary embedding before the call, fused
                                                     with the block pooling (select_blocks(pooled=...))
 

@@ -19,7 +19,7 @@ import torch  # noqa: F401  (must precede the library load, see module docstring
 LIB_PATH = Path(os.environ.get("FFTSPARSE_AMD_LIB") or Path(__file__).resolve().with_name("libfftsparse_amd.so"))
 
 FS_DTYPE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 
 class PoolArgs(ctypes.Structure):
@@ -44,7 +44,7 @@ class XattnArgs(ctypes.Structure):
                 ("k", c_void_p), ("k_sh", c_int64), ("k_sl", c_int64),
                 ("dtype", c_int), ("Hq", c_int), ("Hk", c_int), ("L", c_int), ("D", c_int), ("stride", c_int),
                 ("bs", c_int), ("norm", c_float), ("threshold", c_void_p), ("keep_sink", c_int),
-                ("sums", c_void_p), ("blk_cnt", c_void_p), ("blk_idx", c_void_p), ("work", c_void_p),
+                ("sums", c_void_p), ("blk_cnt", c_void_p), ("blk_bits", c_void_p), ("work", c_void_p),
                 ("non_causal", c_int), ("torch_path", c_int), ("select_mode", c_int), ("perm", c_int * 16),
                 ("kdb", c_int), ("no_softmax", c_int), ("chunk", c_int), ("keep_recent", c_int),
                 ("head_group", c_int)]
@@ -55,7 +55,7 @@ class FlexArgs(ctypes.Structure):
                 ("k", c_void_p), ("k_sh", c_int64), ("k_sl", c_int64),
                 ("dtype", c_int), ("Hq", c_int), ("Hk", c_int), ("L", c_int), ("D", c_int), ("bs", c_int),
                 ("gamma", c_float), ("tau", c_float), ("min_blocks", c_int), ("max_blocks", c_int),
-                ("gqa_interleave", c_int), ("blk_cnt", c_void_p), ("blk_idx", c_void_p),
+                ("gqa_interleave", c_int), ("blk_cnt", c_void_p), ("blk_bits", c_void_p),
                 ("head_info", c_void_p), ("head_js", c_void_p), ("vertical", c_void_p), ("slash", c_void_p),
                 ("work", c_void_p)]
 
@@ -103,7 +103,7 @@ class SelectArgs(ctypes.Structure):
                 ("qk_topk_ratio", c_float),
                 ("col_mode", c_int), ("col_sel", c_void_p), ("last_sel", c_void_p),
                 ("mean_var", c_void_p), ("is_stripe", c_void_p),
-                ("blk_cnt", c_void_p), ("blk_idx", c_void_p)]
+                ("blk_cnt", c_void_p), ("blk_bits", c_void_p)]
 
 
 class AttnArgs(ctypes.Structure):
@@ -114,7 +114,7 @@ class AttnArgs(ctypes.Structure):
                 ("dtype", c_int), ("B", c_int), ("Hq", c_int), ("Hk", c_int), ("Lq", c_int), ("Lk", c_int),
                 ("D", c_int), ("bs", c_int),
                 ("is_causal", c_int), ("softmax_scale", c_float), ("gqa_interleave", c_int),
-                ("blk_cnt", c_void_p), ("blk_idx", c_void_p), ("work", c_void_p)]
+                ("blk_cnt", c_void_p), ("blk_bits", c_void_p), ("work", c_void_p)]
 
 
 STRUCTS = [PoolArgs, CorrArgs, StatsArgs, SelectArgs, AttnArgs, ScoresArgs, RopePoolArgs, XattnArgs, FlexArgs]

@@ -10,7 +10,7 @@ host synchronisation:
     fs_stats   diagonal statistics, column scores,
                last-row scores and their top-n       (:558-560, :581-596, :623-635)
     fs_select  stripe/diffuse decision, qk top-k,
-               mask composition -> per-row block lists (:600-641)
+               mask composition -> block mask, one bit per block (:600-641)
     fs_bsattn  block-sparse causal GQA attention     (:775-786)
 
 K/V may carry Hq heads (the reference's repeat_kv'd layout) or Hkv heads with
@@ -31,12 +31,46 @@ from .params import PrefillParams, derive, f32
 _MIN_BLOCKS = 10          # my_attn_v7.py:509
 
 
+def mask_words(nk: int) -> int:
+    """64-bit words per row of a block mask over ``nk`` key blocks."""
+    return (nk + 63) // 64
+
+
+def bits_from_mask(mask: torch.Tensor):
+    """Block mask bool [H, N, Nk] (or the reference's base_blockmask [1, H, N, Nk])
+    -> (blk_cnt int32 [H, N], blk_bits int64 [H, N, ceil(Nk/64)]): bit b of word w
+    of a row is key block 64 w + b."""
+    if mask.dim() == 4:
+        if mask.shape[0] != 1:
+            raise ValueError("a 4-d block mask must have batch size 1")
+        mask = mask[0]
+    if mask.dim() != 3 or mask.dtype != torch.bool:
+        raise ValueError(f"block mask must be a bool [H, N, Nk] tensor, got {mask.dtype} {tuple(mask.shape)}")
+    H, N, Nk = mask.shape
+    W = mask_words(Nk)
+    m = torch.zeros(H, N, W * 64, dtype=torch.int64, device=mask.device)
+    m[:, :, :Nk] = mask.to(torch.int64)
+    m = m.view(H, N, W, 2, 32)
+    sh = torch.arange(32, device=mask.device, dtype=torch.int64)
+    half = (m << sh).sum(-1)                              # [H, N, W, 2], each < 2^32
+    bits = half[..., 0] | (half[..., 1] << 32)
+    return mask.sum(-1, dtype=torch.int32).contiguous(), bits.contiguous()
+
+
+def mask_from_bits(blk_bits: torch.Tensor, nk: int) -> torch.Tensor:
+    """[H, N, W] block mask words -> bool [H, N, nk]."""
+    H, N, W = blk_bits.shape
+    sh = torch.arange(64, device=blk_bits.device, dtype=torch.int64)
+    m = ((blk_bits.to(torch.int64)[..., None] >> sh) & 1).bool().view(H, N, W * 64)
+    return m[:, :, :nk]
+
+
 @dataclass
 class BlockSelection:
     """Device-resident result of the mask selection stage."""
     params: PrefillParams
-    blk_cnt: torch.Tensor            # int32 [Hq, N]
-    blk_idx: torch.Tensor            # uint16 [Hq, N, Nk] (first blk_cnt entries of each row valid)
+    blk_cnt: torch.Tensor            # int32 [Hq, N], selected blocks per row
+    blk_bits: torch.Tensor           # int64 [Hq, N, ceil(Nk/64)], the block mask (bit j % 64 of word j / 64)
     q_b: torch.Tensor | None = None  # [Hq, N, D]
     k_b: torch.Tensor | None = None  # [Hk, N, D]
     corr: torch.Tensor | None = None
@@ -51,14 +85,8 @@ class BlockSelection:
     is_stripe: torch.Tensor | None = None
 
     def dense_mask(self) -> torch.Tensor:
-        """[Hq, N, Nk] bool mask rebuilt from the block lists (for checks)."""
-        H, N = self.blk_cnt.shape
-        Nk = self.blk_idx.shape[2]
-        idx = self.blk_idx.view(torch.int16).to(torch.int64) & 0xFFFF
-        valid = torch.arange(Nk, device=idx.device)[None, None, :] < self.blk_cnt[:, :, None].to(torch.int64)
-        m = torch.zeros(H, N, Nk + 1, dtype=torch.bool, device=idx.device)
-        m.scatter_(2, torch.where(valid, idx, torch.full_like(idx, Nk)), True)
-        return m[:, :, :Nk]
+        """[Hq, N, Nk] bool block mask."""
+        return mask_from_bits(self.blk_bits, self.params.Nk)
 
     def nnz(self) -> int:
         return int(self.blk_cnt.sum().item())
@@ -99,7 +127,7 @@ def select_blocks(query_states: torch.Tensor, key_states: torch.Tensor, *, block
                   enable_last_block_mask=True, diag_sample_ratio=0.15, min_diag_samples=5,
                   max_diag_samples=64, stripe_threshold=0.3, qk_topk_ratio=0.2,
                   keep_intermediates=False, pipeline_groups=None, pooled=None) -> BlockSelection:
-    """Stage 1 of my_attn_v7.myattn_prefill (:533-641): block lists for every
+    """Stage 1 of my_attn_v7.myattn_prefill (:533-641): the block mask of every
     (query head, query block).  q [1,Hq,L,D], k [1,Hk,L,D].  ``pooled``: the
     block means (q_b [Hq,N,D], k_b [Hk,N,D]) already formed by ``rope_pool``,
     which then replace the pooling pass."""
@@ -166,7 +194,7 @@ def select_blocks(query_states: torch.Tensor, key_states: torch.Tensor, *, block
                                       dtype=dt, Hq=h1 - h0, Hk=k1 - k0, L=L_q, D=D, bs=block_size,
                                       q_b=sel.q_b[h0:h1].data_ptr(), k_b=sel.k_b[k0:k1].data_ptr()), dev)
 
-    sel = BlockSelection(params=p, blk_cnt=None, blk_idx=None)
+    sel = BlockSelection(params=p, blk_cnt=None, blk_bits=None)
     if pooled is not None:
         q_b, k_b = pooled
         if (tuple(q_b.shape) != (Hq, N, D) or tuple(k_b.shape) != (Hk, N, D) or q_b.dtype != q.dtype
@@ -181,7 +209,7 @@ def select_blocks(query_states: torch.Tensor, key_states: torch.Tensor, *, block
         # then waits only for this much host work.
         pool(0)
     sel.blk_cnt = torch.empty(Hq, N, dtype=torch.int32, device=dev)
-    sel.blk_idx = torch.empty(Hq, N, Nk, dtype=torch.uint16, device=dev)
+    sel.blk_bits = torch.empty(Hq, N, mask_words(Nk), dtype=torch.int64, device=dev)
     if p.corr_enabled:
         sel.corr = torch.empty(Hq, N, dtype=torch.float32, device=dev)
         sel.corr_sum = torch.empty(Hq, N, dtype=torch.float32, device=dev)
@@ -257,7 +285,7 @@ def select_blocks(query_states: torch.Tensor, key_states: torch.Tensor, *, block
                 qk_topk_ratio=f32(qk_topk_ratio), col_mode=col_mode, col_sel=ptr(sl(sel.col_sel, h0, h1)),
                 last_sel=ptr(sl(sel.last_sel, h0, h1)), mean_var=ptr(sl(sel.mean_var, h0, h1)),
                 is_stripe=ptr(sl(sel.is_stripe, h0, h1)), blk_cnt=sel.blk_cnt[h0:h1].data_ptr(),
-                blk_idx=sel.blk_idx[h0:h1].data_ptr()), dev)
+                blk_bits=sel.blk_bits[h0:h1].data_ptr()), dev)
     if side is not main:
         main.wait_stream(side)                    # every output is ready on the caller's stream
     if not keep_intermediates:
@@ -343,7 +371,7 @@ class AttentionCall:
     ``__call__`` does both in one C call (fs_bsattn).  Every launch goes on
     torch's current stream."""
 
-    def __init__(self, query_states, key_states, value_states, blk_cnt=None, blk_idx=None, *,
+    def __init__(self, query_states, key_states, value_states, blk_cnt=None, blk_bits=None, *,
                  block_size=128, is_causal=True, softmax_scale=None, out=None, gqa_interleave=False):
         q = _check_layout(query_states)
         k = _check_layout(key_states)
@@ -356,23 +384,23 @@ class AttentionCall:
             # flash-attention kernels accept fp16/bf16 only, as does the reference's
             # block_sparse_attn_func.
             raise RuntimeError("FlashAttention only supports fp16 and bf16 data type")
-        if (blk_cnt is None) != (blk_idx is None):
-            raise ValueError("blk_cnt and blk_idx go together")
+        if (blk_cnt is None) != (blk_bits is None):
+            raise ValueError("blk_cnt and blk_bits go together")
         if blk_cnt is not None:
             Nq, Nk = -(-Lq // block_size), -(-Lk // block_size)
             if blk_cnt.dtype != torch.int32 or tuple(blk_cnt.shape) != (Hq, Nq) or not blk_cnt.is_contiguous():
                 raise ValueError(f"blk_cnt must be a contiguous int32 [{Hq}, {Nq}] tensor, got "
                                  f"{blk_cnt.dtype} {tuple(blk_cnt.shape)}")
-            if (blk_idx.dtype not in (torch.uint16, torch.int16) or tuple(blk_idx.shape) != (Hq, Nq, Nk)
-                    or not blk_idx.is_contiguous()):
-                raise ValueError(f"blk_idx must be a contiguous uint16 [{Hq}, {Nq}, {Nk}] tensor, got "
-                                 f"{blk_idx.dtype} {tuple(blk_idx.shape)}")
+            W = mask_words(Nk)
+            if blk_bits.dtype != torch.int64 or tuple(blk_bits.shape) != (Hq, Nq, W) or not blk_bits.is_contiguous():
+                raise ValueError(f"blk_bits must be a contiguous int64 [{Hq}, {Nq}, {W}] tensor, got "
+                                 f"{blk_bits.dtype} {tuple(blk_bits.shape)}")
         if k.shape[3] != D or v.shape[3] != D:
             raise ValueError(f"query, key and value head_dim differ: {D}, {k.shape[3]}, {v.shape[3]}")
         if out is not None and (tuple(out.shape) != (B, Lq, Hq, D) or out.dtype != q.dtype):
             raise ValueError(f"out must be a [{B}, {Lq}, {Hq}, {D}] {q.dtype} tensor, got {out.dtype} "
                              f"{tuple(out.shape)}")
-        self.device = _lib.same_device(q, k, v, blk_cnt, blk_idx, out)
+        self.device = _lib.same_device(q, k, v, blk_cnt, blk_bits, out)
         if out is None:
             out = torch.empty(B, Lq, Hq, D, dtype=q.dtype, device=q.device)
         scale = 1.0 / math.sqrt(D) if softmax_scale is None else float(softmax_scale)
@@ -383,13 +411,13 @@ class AttentionCall:
             out=out.data_ptr(), o_sb=out.stride(0), o_sh=out.stride(2), o_sl=out.stride(1),
             dtype=_lib.FS_DTYPE[q.dtype], B=B, Hq=Hq, Hk=Hk, Lq=Lq, Lk=Lk, D=D, bs=block_size,
             is_causal=int(bool(is_causal)), softmax_scale=scale, gqa_interleave=int(bool(gqa_interleave)),
-            blk_cnt=ptr(blk_cnt), blk_idx=ptr(blk_idx))
+            blk_cnt=ptr(blk_cnt), blk_bits=ptr(blk_bits))
         self.work = torch.empty(_lib.load().fs_bsattn_work_bytes(ctypes.byref(args)), dtype=torch.uint8,
                                 device=q.device)
         args.work = self.work.data_ptr()
         self.args = args
         self.out = out
-        self._keep = (q, k, v, blk_cnt, blk_idx)      # the pointers in args stay valid
+        self._keep = (q, k, v, blk_cnt, blk_bits)     # the pointers in args stay valid
 
     def prepare(self) -> None:
         _lib.call("fs_bsattn_prepare", self.args, self.device)
@@ -403,14 +431,21 @@ class AttentionCall:
         return self.out
 
 
-def block_sparse_attention(query_states, key_states, value_states, blk_cnt=None, blk_idx=None, *,
-                           block_size=128, is_causal=True, softmax_scale=None, out=None,
+def block_sparse_attention(query_states, key_states, value_states, blk_cnt=None, blk_bits=None, *,
+                           block_mask=None, block_size=128, is_causal=True, softmax_scale=None, out=None,
                            gqa_interleave=False) -> torch.Tensor:
-    """Block-sparse (or, with no block lists, dense causal) attention.
+    """Block-sparse (or, with no block mask, dense causal) attention.
 
     q [B,Hq,Lq,D], k/v [B,Hk,Lk,D] -> out [B, Lq, Hq, D] in the input dtype.
+    The mask is either (blk_cnt, blk_bits), as the selectors return it, or
+    ``block_mask``: a bool [Hq, Nq, Nk] or [1, Hq, Nq, Nk] tensor, the
+    reference's base_blockmask (my_attn_v7.py:780).
     Query head h reads KV head h // (Hq / Hk), or h % Hk with ``gqa_interleave``."""
-    return AttentionCall(query_states, key_states, value_states, blk_cnt, blk_idx, block_size=block_size,
+    if block_mask is not None:
+        if blk_cnt is not None or blk_bits is not None:
+            raise ValueError("give either block_mask or (blk_cnt, blk_bits)")
+        blk_cnt, blk_bits = bits_from_mask(block_mask)
+    return AttentionCall(query_states, key_states, value_states, blk_cnt, blk_bits, block_size=block_size,
                          is_causal=is_causal, softmax_scale=softmax_scale, out=out,
                          gqa_interleave=gqa_interleave)()
 
@@ -487,6 +522,6 @@ def v7_prefill(query_states, key_states, value_states, *, block_size=128, is_cau
     if query_states.dtype not in (torch.bfloat16, torch.float16):
         raise RuntimeError("FlashAttention only supports fp16 and bf16 data type")
     sel = select_blocks(query_states, key_states, block_size=block_size, **select_kw)
-    out = block_sparse_attention(query_states, key_states, value_states, sel.blk_cnt, sel.blk_idx,
+    out = block_sparse_attention(query_states, key_states, value_states, sel.blk_cnt, sel.blk_bits,
                                  block_size=block_size, is_causal=is_causal, softmax_scale=softmax_scale)
     return (out, sel) if return_selection else out

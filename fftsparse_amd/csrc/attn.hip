@@ -193,12 +193,13 @@ struct AttnKArgs {
   const uint16_t* k;
   const uint16_t* vt;
   uint16_t* out;
-  const int32_t* blk_cnt;
-  const uint16_t* blk_idx;
+  const int32_t* blk_cnt;       // work order only (non-null: block masks given)
+  const uint64_t* blk_bits;     // [Hq][Nq][NWk] block mask rows (64-token and longer blocks)
+  const uint32_t* u_idx;        // union mode: [Hq][Nq][Nk] union entries (block | rows << 16)
   const int32_t* order;
   int64_t q_sb, q_sh, k_sb, k_sh, o_sb, o_sh;
   int q_sl, k_sl, o_sl;
-  int Hq, Hk, Lq, Lk, Nq, Nk, Lp, total, is_causal;
+  int Hq, Hk, Lq, Lk, Nq, Nk, NWk, Lp, total, is_causal;
   int run;                      // query blocks per scheduling unit (block lists)
   float scale;
   int gqa_interleave;           // KV head h % Hk (else h / (Hq / Hk))
@@ -325,18 +326,26 @@ void bsattn_kernel(AttnKArgs a) {
     qf[st] = __builtin_bit_cast(V8, raw);
   }
 
-  // Block lists are read through the scalar unit (constant address space):
-  // their completion is tracked by lgkmcnt, so reading the next index never
+  // Block masks are read through the scalar unit (constant address space):
+  // their completion is tracked by lgkmcnt, so reading the next word never
   // waits on the tile copies in flight (vmcnt).
+  typedef const __attribute__((address_space(4))) uint64_t* cptr64;
   const bool listed = a.blk_cnt != nullptr;
   int64_t lbase = 0;
-  auto block_at = [&](int i) -> int {              // i-th listed key block
-    const int64_t gi = lbase + i;
-    const uint32_t w = ((cptr32)(uintptr_t)a.blk_idx)[gi >> 1];
-    return (int)((gi & 1) ? (w >> 16) : (w & 0xffffu));
-  };
   int cnt;                                         // key tiles of this query block
-  int nb_listed = 0;                               // listed key blocks after the causal trim
+  int nb_listed = 0;                               // union entries
+  // Row mask walk (64- and 128-token blocks): the set bits of the row in
+  // ascending order; it_cur holds the unread bits of word it_w.
+  int64_t rbase = 0;
+  int it_w = -1, it_blk = 0;
+  uint64_t it_cur = 0;
+  auto next_block = [&]() -> int {
+    while (it_cur == 0 && it_w + 1 < a.NWk) it_cur = ((cptr64)(uintptr_t)a.blk_bits)[rbase + ++it_w];
+    if (it_cur == 0) return a.Nk;                  // past the row (not reached: cnt counts the bits)
+    const int b = __builtin_ctzll(it_cur);
+    it_cur &= it_cur - 1;
+    return 64 * it_w + b;
+  };
   if (UNION && listed) {
     // the group's union list: 32-bit entries (block | rows << 16), no trim
     const int nb = min(max((int)((cptr32)(uintptr_t)a.blk_cnt)[(int64_t)h * a.Nq + qb], 0), a.Nk);
@@ -344,24 +353,29 @@ void bsattn_kernel(AttnKArgs a) {
     cnt = (nb + EPT - 1) / EPT;
     nb_listed = nb;
   } else if (listed) {
-    // a count past the row's Nk entries (or negative) is clamped to the row
-    int nb = min(max((int)((cptr32)(uintptr_t)a.blk_cnt)[(int64_t)h * a.Nq + qb], 0), a.Nk);
-    lbase = ((int64_t)h * a.Nq + qb) * a.Nk;
-    // drop trailing blocks entirely above the diagonal (lists are ascending)
-    if (a.is_causal) {
-      while (nb > 0 && block_at(nb - 1) * BS > q0 + BS - 1 + off) --nb;
+    // the selected blocks up to the causal limit (blocks kb with kb * BS <=
+    // the last visible key) and below Nk: the row's words counted lane-parallel
+    rbase = ((int64_t)h * a.Nq + qb) * a.NWk;
+    const int last_key = q0 + BS - 1 + off;
+    const int kb_lim = !a.is_causal ? a.Nk : (last_key < 0 ? 0 : min(a.Nk, last_key / BS + 1));
+    const int nwl = (kb_lim + 63) >> 6;
+    int c = 0;
+    for (int w = lane; w < nwl; w += 64) {
+      uint64_t x = a.blk_bits[rbase + w];
+      if (w == nwl - 1 && (kb_lim & 63)) x &= (1ull << (kb_lim & 63)) - 1;
+      c += __popcll(x);
     }
+    const int nb = __builtin_amdgcn_readfirstlane(wave_sum_i(c));
     cnt = nb * C::TPB;
-    nb_listed = nb;
   } else {
     const int last_key = a.is_causal ? min(a.Lk - 1, q0 + BS - 1 + off) : a.Lk - 1;
     cnt = last_key < 0 ? 0 : last_key / TK + 1;
   }
-  // first key of tile t (-1: an out-of-range list entry, skipped)
+  // first key of tile t (-1: an out-of-range entry, skipped)
   const int nlisted = nb_listed;
   auto uent = [&](int i) -> uint32_t {            // union entry i, all ones past the end
     if (i >= nlisted) return 0xffffffffu;
-    return ((cptr32)(uintptr_t)a.blk_idx)[lbase + i];
+    return ((cptr32)(uintptr_t)a.u_idx)[lbase + i];
   };
   // Union mode: the entries of tiles t, t+1 and t+2 are held in scalar
   // registers (u0, u1, u2) and those of tile t+3 are loaded during iteration
@@ -381,8 +395,9 @@ void bsattn_kernel(AttnKArgs a) {
       if (listed) return t;                        // union mode: copies and masks look the tile's entries up
     }
     if (!listed) return t * TK;
-    const int kb = block_at(t / C::TPB);
-    return kb < a.Nk ? kb * BS + (t % C::TPB) * TK : -1;
+    // called for t = 0, 1, 2, ... in order: a new block every TPB tiles
+    if (t % C::TPB == 0) it_blk = next_block();
+    return it_blk < a.Nk ? it_blk * BS + (t % C::TPB) * TK : -1;
   };
 
   // ---- tile DMA: wave w copies 1 KiB regions w*NR .. w*NR+NR-1 of the K tile
@@ -910,57 +925,30 @@ __global__ __launch_bounds__(kOrderThreads) void order_kernel(const int32_t* __r
   }
 }
 
-// ---- union lists of groups of R consecutive list rows (union mode) -------
-// One wave per (head, group): the rows' block lists as bit rows in LDS, their
-// OR word by word (lane l: words l and l + 64, blocks 64 w .. 64 w + 63), a
-// prefix of the popcounts, and the union written in ascending order as
+// ---- union lists of groups of R consecutive mask rows (union mode) -------
+// One wave per (head, group): the rows' mask words in LDS (lane l: words l and
+// l + 64, blocks 64 w .. 64 w + 63), their OR word by word, a prefix of the
+// popcounts, and the union written in ascending order as
 // block | (rows that selected it) << 16.  Nk <= 8192, R <= 8.
 constexpr int kUnionMaxRows = 8;
-__global__ __launch_bounds__(64) void union_kernel(const int32_t* __restrict__ cnt, const uint16_t* __restrict__ idx,
-                                                   int Nq, int Nk, int R, int Ng, int32_t* __restrict__ u_cnt,
-                                                   uint32_t* __restrict__ u_idx) {
+__global__ __launch_bounds__(64) void union_kernel(const uint64_t* __restrict__ mask, int Nq, int Nk, int R, int Ng,
+                                                   int32_t* __restrict__ u_cnt, uint32_t* __restrict__ u_idx) {
   constexpr int kW = 2 * 64;                       // words per row: Nk <= 8192
   __shared__ unsigned long long bits[kUnionMaxRows][kW];
   const int h = blockIdx.x / Ng, grp = blockIdx.x - h * Ng;
   const int lane = threadIdx.x;
-  for (int j = 0; j < kUnionMaxRows; ++j) bits[j][lane] = bits[j][lane + 64] = 0ull;
-  __syncthreads();
-  // Each lane reads 8 consecutive entries of a row (one 16-byte load when the
-  // rows are 16-byte aligned) and ORs them into the row's bit words, one LDS
-  // atomic per word they touch (the lists ascend, so usually one or two).
-  const bool v16 = (Nk & 7) == 0 && ((uintptr_t)idx & 15) == 0;
-  for (int j = 0; j < R; ++j) {
+  const int NW = (Nk + 63) >> 6;
+  // words past Nk's last word, and rows past Nq, are empty
+  for (int j = 0; j < kUnionMaxRows; ++j) {
     const int row = grp * R + j;
-    if (row >= Nq) break;
-    const int n = min(max(cnt[(int64_t)h * Nq + row], 0), Nk);
-    const uint16_t* li = idx + ((int64_t)h * Nq + row) * Nk;
-    for (int e0 = 8 * lane; e0 < n; e0 += 8 * 64) {
-      uint32_t ent[4];
-      if (v16 && e0 + 8 <= n) {
-        const uint4 q = *reinterpret_cast<const uint4*>(li + e0);
-        ent[0] = q.x; ent[1] = q.y; ent[2] = q.z; ent[3] = q.w;
-      } else {
+    const uint64_t* mr = mask + ((int64_t)h * Nq + row) * NW;
+    const bool ok = j < R && row < Nq;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const uint32_t lo = e0 + 2 * k < n ? li[e0 + 2 * k] : 0xffffu;
-          const uint32_t hi = e0 + 2 * k + 1 < n ? li[e0 + 2 * k + 1] : 0xffffu;
-          ent[k] = lo | (hi << 16);
-        }
-      }
-      unsigned long long acc = 0ull;
-      int cw = -1;
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const int blk = (int)((ent[k >> 1] >> (16 * (k & 1))) & 0xffffu);
-        if (e0 + k >= n || blk >= Nk) continue;
-        if ((blk >> 6) != cw) {
-          if (cw >= 0) atomicOr(&bits[j][cw], acc);
-          cw = blk >> 6;
-          acc = 0ull;
-        }
-        acc |= 1ull << (blk & 63);
-      }
-      if (cw >= 0) atomicOr(&bits[j][cw], acc);
+    for (int k = 0; k < 2; ++k) {
+      const int w = lane + 64 * k;
+      uint64_t x = (ok && w < NW) ? mr[w] : 0ull;
+      if (w == NW - 1 && (Nk & 63)) x &= (1ull << (Nk & 63)) - 1;
+      bits[j][w] = x;
     }
   }
   __syncthreads();
@@ -1096,12 +1084,13 @@ static int launch_run(const fs_attn_args& a, int Nq, int Nk, hipStream_t s, int 
   k.vt = vt;
   k.out = static_cast<uint16_t*>(a.out);
   k.blk_cnt = a.blk_cnt;
-  k.blk_idx = a.blk_idx;
+  k.blk_bits = a.blk_bits;
+  k.u_idx = nullptr;
   k.order = order;
   k.q_sb = a.q_sb; k.q_sh = a.q_sh; k.k_sb = a.k_sb; k.k_sh = a.k_sh; k.o_sb = a.o_sb; k.o_sh = a.o_sh;
   k.q_sl = (int)a.q_sl; k.k_sl = (int)a.k_sl; k.o_sl = (int)a.o_sl;
   k.Hq = a.Hq; k.Hk = a.Hk; k.Lq = a.Lq; k.Lk = a.Lk;
-  k.Nq = Nq; k.Nk = Nk; k.Lp = Lp; k.total = total; k.is_causal = a.is_causal;
+  k.Nq = Nq; k.Nk = Nk; k.NWk = (Nk + 63) / 64; k.Lp = Lp; k.total = total; k.is_causal = a.is_causal;
   k.run = run;
   k.scale = a.softmax_scale;
   k.gqa_interleave = a.gqa_interleave ? 1 : 0;
@@ -1124,7 +1113,7 @@ static int launch_run_union(const fs_attn_args& a, hipStream_t s) {
   int32_t* u_cnt = reinterpret_cast<int32_t*>(w + vt_bytes(a) + order_bytes(a));
   uint32_t* u_idx = reinterpret_cast<uint32_t*>(w + vt_bytes(a) + order_bytes(a) +
                                                 align256((size_t)a.Hq * Ng * sizeof(int32_t)));
-  union_kernel<<<(unsigned)(a.Hq * Ng), 64, 0, s>>>(a.blk_cnt, a.blk_idx, NqL, NkL, R, Ng, u_cnt, u_idx);
+  union_kernel<<<(unsigned)(a.Hq * Ng), 64, 0, s>>>(a.blk_bits, NqL, NkL, R, Ng, u_cnt, u_idx);
   if (int rc = fs_host::launch_status("fs_bsattn (union lists)")) return rc;
   const int run = min(16, max(1, Ng / 64));
   int shift = 0;
@@ -1140,12 +1129,13 @@ static int launch_run_union(const fs_attn_args& a, hipStream_t s) {
   k.vt = static_cast<const uint16_t*>(a.work);
   k.out = static_cast<uint16_t*>(a.out);
   k.blk_cnt = u_cnt;
-  k.blk_idx = reinterpret_cast<const uint16_t*>(u_idx);   // read as 32-bit entries
+  k.blk_bits = nullptr;
+  k.u_idx = u_idx;
   k.order = order;
   k.q_sb = a.q_sb; k.q_sh = a.q_sh; k.k_sb = a.k_sb; k.k_sh = a.k_sh; k.o_sb = a.o_sb; k.o_sh = a.o_sh;
   k.q_sl = (int)a.q_sl; k.k_sl = (int)a.k_sl; k.o_sl = (int)a.o_sl;
   k.Hq = a.Hq; k.Hk = a.Hk; k.Lq = a.Lq; k.Lk = a.Lk;
-  k.Nq = Ng; k.Nk = NkL; k.Lp = vt_len(NkL, LB); k.total = total; k.is_causal = a.is_causal;
+  k.Nq = Ng; k.Nk = NkL; k.NWk = 0; k.Lp = vt_len(NkL, LB); k.total = total; k.is_causal = a.is_causal;
   k.run = run;
   k.scale = a.softmax_scale;
   k.ctr = ctr;
@@ -1185,17 +1175,16 @@ static int check_attn(const fs_attn_args* a, const char* fn) {
   FS_CHECK_SUPPORTED(a->dtype == FS_DTYPE_BF16 || a->dtype == FS_DTYPE_F16,
                      "%s: dtype %d unsupported (bf16/f16)", fn, a->dtype);
   FS_CHECK_SUPPORTED(a->Hk <= 4096, "%s: %d KV heads > 4096", fn, a->Hk);
-  FS_CHECK_ARG(a->blk_cnt == nullptr || (a->blk_idx != nullptr && a->B == 1),
-               "%s: block lists need blk_idx and B == 1", fn);
+  FS_CHECK_ARG(a->blk_cnt == nullptr || (a->blk_bits != nullptr && a->B == 1),
+               "%s: block masks need blk_bits and B == 1", fn);
   const int64_t strides[] = {a->q_sb, a->q_sh, a->q_sl, a->k_sb, a->k_sh, a->k_sl,
                              a->v_sb, a->v_sh, a->v_sl, a->o_sb, a->o_sh, a->o_sl};
   for (int64_t st : strides) FS_CHECK_ARG(st % 8 == 0, "%s: strides must be multiples of 8 elements", fn);
   const uintptr_t ptrs[] = {(uintptr_t)a->q, (uintptr_t)a->k, (uintptr_t)a->v, (uintptr_t)a->out,
                             (uintptr_t)a->work};
   for (uintptr_t p : ptrs) FS_CHECK_ARG(p % 16 == 0, "%s: tensors must be 16-byte aligned", fn);
-  // the kernel reads the lists as 32-bit words
-  FS_CHECK_ARG((uintptr_t)a->blk_cnt % 4 == 0 && (uintptr_t)a->blk_idx % 4 == 0,
-               "%s: blk_cnt / blk_idx must be 4-byte aligned", fn);
+  FS_CHECK_ARG((uintptr_t)a->blk_cnt % 4 == 0 && (uintptr_t)a->blk_bits % 8 == 0,
+               "%s: blk_cnt / blk_bits must be 4- / 8-byte aligned", fn);
   const int64_t Nq = (a->Lq + a->bs - 1) / a->bs;
   const int64_t Nk = (a->Lk + a->bs - 1) / a->bs;
   FS_CHECK_SUPPORTED((int64_t)a->B * a->Hq * Nq < (1ll << 30) && (int64_t)a->B * a->Hk * Nk * a->bs / 64 < (1ll << 31),

@@ -27,7 +27,7 @@ int launch_status(const char* what) {
 }  // namespace fs_host
 
 extern "C" const char* fs_last_error(void) { return fs_host::g_err; }
-extern "C" int fs_abi_version(void) { return 11; }
+extern "C" int fs_abi_version(void) { return 12; }
 
 extern "C" size_t fs_sizeof_args(int which) {
   switch (which) {

@@ -1073,12 +1073,12 @@ struct FlexListK {
   const uint64_t* cover;        // [Hq][nb][kFWords] (rows of sparse heads)
   const int32_t* info;
   int32_t* blk_cnt;
-  uint16_t* blk_idx;
+  uint64_t* blk_bits;           // [Hq][nb][ceil(nb / 64)]
   int Hq, nb;
 };
 
 // one wave per (head, block row): lane l forms the row's 64-bit membership
-// words l and l + 64, popcount offsets, the ascending list
+// words l and l + 64 and stores them; the row's count is their popcount sum
 __global__ __launch_bounds__(64) void flex_lists_kernel(FlexListK a) {
   const int h = blockIdx.x / a.nb, r = blockIdx.x % a.nb;
   const int lane = threadIdx.x, nb = a.nb;
@@ -1105,36 +1105,10 @@ __global__ __launch_bounds__(64) void flex_lists_kernel(FlexListK a) {
     return m;
   };
   const uint64_t m0 = word(lane), m1 = word(lane + 64);
-  const int c0 = __popcll(m0), c1 = __popcll(m1);
-  int i0 = c0, i1 = c1;
-  for (int o = 1; o < 64; o <<= 1) {
-    const int v0 = __shfl_up(i0, o, 64), v1 = __shfl_up(i1, o, 64);
-    if (lane >= o) {
-      i0 += v0;
-      i1 += v1;
-    }
-  }
-  const int t0 = __shfl(i0, 63, 64);
-  const int total = t0 + __shfl(i1, 63, 64);
-  uint16_t* out = a.blk_idx + ((int64_t)h * nb + r) * nb;
-  if ((nb & 7) == 0 && ((uintptr_t)a.blk_idx & 15) == 0) {
-    // rows aligned to 16 bytes: 16-byte stores of 8 entries
-    __shared__ uint64_t stw[2 * 64];
-    __shared__ int stp[2 * 64];
-    stw[lane] = m0;
-    stp[lane] = i0 - c0;
-    stw[lane + 64] = m1;
-    stp[lane + 64] = t0 + i1 - c1;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    list_chunks_from_lds(out, total, 2 * 64, lane, 64, stw, stp, [](int ws, int b) { return 64 * ws + b; });
-  } else {
-    int pos = i0 - c0;
-    for (uint64_t m = m0; m; m &= m - 1) out[pos++] = (uint16_t)(64 * lane + __builtin_ctzll(m));
-    pos = t0 + i1 - c1;
-    for (uint64_t m = m1; m; m &= m - 1) out[pos++] = (uint16_t)(64 * (lane + 64) + __builtin_ctzll(m));
-  }
+  uint64_t* out = a.blk_bits + ((int64_t)h * nb + r) * NW;
+  if (lane < NW) out[lane] = m0;
+  if (lane + 64 < NW) out[lane + 64] = m1;
+  const int total = wave_sum_i(__popcll(m0) + __popcll(m1));
   if (lane == 0) a.blk_cnt[(int64_t)h * nb + r] = total;
 }
 
@@ -1285,7 +1259,7 @@ static int launch_flex(const fs_flex_args& a, hipStream_t s) {
   if (int rc = fs_host::launch_status("fs_flex (heads)")) return rc;
   FlexListK lk{};
   lk.vmask = hk.vmask; lk.smask = hk.smask; lk.cover = ck.cover; lk.info = hk.info;
-  lk.blk_cnt = a.blk_cnt; lk.blk_idx = a.blk_idx; lk.Hq = a.Hq; lk.nb = nb;
+  lk.blk_cnt = a.blk_cnt; lk.blk_bits = a.blk_bits; lk.Hq = a.Hq; lk.nb = nb;
   flex_lists_kernel<<<(unsigned)(a.Hq * nb), 64, 0, s>>>(lk);
   return fs_host::launch_status("fs_flex (lists)");
 }
@@ -1301,7 +1275,8 @@ extern "C" size_t fs_flex_work_bytes(int Hq, int Hk, int L, int bs, float tau) {
 
 extern "C" int fs_flex(const fs_flex_args* a, void* stream) {
   FS_CHECK_ARG(a != nullptr, "fs_flex: null args");
-  FS_CHECK_ARG(a->q && a->k && a->blk_cnt && a->blk_idx && a->work, "fs_flex: null pointer");
+  FS_CHECK_ARG(a->q && a->k && a->blk_cnt && a->blk_bits && a->work, "fs_flex: null pointer");
+  FS_CHECK_ARG(((uintptr_t)a->blk_bits & 7) == 0, "fs_flex: blk_bits must be 8-byte aligned");
   FS_CHECK_ARG(a->Hq > 0 && a->Hk > 0 && a->Hq % a->Hk == 0, "fs_flex: Hq=%d must be a multiple of Hk=%d", a->Hq,
                a->Hk);
   FS_CHECK_SUPPORTED(a->dtype == FS_DTYPE_BF16 || a->dtype == FS_DTYPE_F16, "fs_flex: dtype %d unsupported (bf16/f16)",

@@ -1,4 +1,4 @@
-// Block-mask composition and per-row block lists
+// Block-mask composition into the row bitmask (FS_MASK_WORDS words per row)
 // (reference: attn_src/fft_attn/my_attn_v7.py:542-550 prior, :558-560 last
 // row, :588-612 stripe/diffuse dynamic mask, :256-294 qk top-k, :623-641
 // columns; attn_src/fix_mask_attn/my_attn.py:39-79 for the fixed mask).
@@ -9,13 +9,13 @@
 // score panel.  N <= 8192.  Stripe / fixed rows (Nk <= 4096) are built word-parallel: a
 // lane forms the 64-bit membership mask of 64 key blocks (range masks for
 // the prior, columns and causal limit; a funnel-shifted window of the
-// bit-reversed lag mask for the lag diagonals), and writes its set bits at
-// the prefix sum of the lower words' popcounts.  A diffuse head first computes its score panel S[rows][0..last row] into LDS
+// bit-reversed lag mask for the lag diagonals) and stores it as word w of
+// the row.  A diffuse head first computes its score panel S[rows][0..last row] into LDS
 // (fp32 dot products, fixed order).  Each wave then walks one row at a time:
 // for a diffuse row it finds the k_i-th largest score by a 32-step bisection
 // on the ordered float key with wave-wide counts, and in a single ascending
 // pass over the key blocks it evaluates the membership rule 64 blocks at a
-// time, compacting the selected block indices with a ballot + mbcnt prefix.
+// time, the ballot of each pass being the row's next word.
 #include "common.h"
 
 namespace fs {
@@ -40,8 +40,7 @@ template <typename T, bool DIFF>
 __global__ __launch_bounds__(kSelThreads) void select_kernel(fs_select_args a, int rows_per_wave,
                                                              float inv_sqrt_d) {
   extern __shared__ float panel[];       // [RPW][N] scores (diffuse heads) then [RPW][D] q rows
-  // per-head flag bytes (per-row path); the word-parallel path stages each
-  // wave's list words and prefixes here instead (3 KiB)
+  // per-head flag bytes (per-row path)
   __shared__ __attribute__((aligned(16))) uint8_t flags[kSelMaxN];
   const int RPW = rows_per_wave * kSelWaves;
   const int N = a.N, Nk = a.Nk, D = a.D;
@@ -141,8 +140,8 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(fs_select_args a, i
   if (words) {
     // ---- word-parallel rows: lane (row g, word w) builds the membership of
     // blocks 64w .. 64w+63 of its row as a 64-bit mask from per-head masks
-    // staged in LDS, then writes its set bits at the offset given by the
-    // popcounts of the lower words.
+    // staged in LDS and stores it as word w of the row; the row's count is
+    // the sum of its words' popcounts.
     __shared__ uint64_t rkw[2 * kMaxWords + 2];  // bit x: keep_tau[N-1-x] (x < N), 0 beyond
     __shared__ uint64_t colw[kMaxWords], lastw[kMaxWords];
     __shared__ uint32_t fk[4096 / 4], fc[4096 / 4], fl[4096 / 4];   // the staged flag bytes
@@ -173,10 +172,6 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(fs_select_args a, i
       }
     }
     __syncthreads();
-    // rows aligned to 16 bytes: the lists go out in 16-byte chunks
-    const bool chunked = (Nk & 7) == 0 && ((uintptr_t)a.blk_idx & 15) == 0;
-    uint64_t* stw = reinterpret_cast<uint64_t*>(flags) + wave * 64;
-    int* stp = reinterpret_cast<int*>(flags + kSelWaves * 64 * sizeof(uint64_t)) + wave * 64;
     int lpr = 1;                                   // lanes per row (power of two >= NW)
     while (lpr < NW) lpr <<= 1;
     const int rpi = 64 / lpr;                      // rows per wave pass
@@ -203,27 +198,11 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(fs_select_args a, i
         if (use_cols) m |= colw[w] & range_bits(w, 0, i + 1);
         m &= range_bits(w, 0, jlim);
       }
-      const int c = __popcll(m);
-      int incl = c;
-      for (int o = 1; o < lpr; o <<= 1) {
-        const int v = __shfl_up(incl, o, lpr);
-        if (w >= o) incl += v;
-      }
-      const int total = __shfl(incl, lpr - 1, lpr);
-      if (chunked) {
-        // 16-byte stores of 8 entries (the whole wave takes part; rows past N write nothing)
-        uint16_t* out = a.blk_idx + ((int64_t)h * N + min(i, N - 1)) * Nk;
-        write_list_chunks(out, m, incl - c, row_ok ? total : 0, lpr, w, g * lpr, stw, stp);
-        if (row_ok && w == 0) a.blk_cnt[(int64_t)h * N + i] = total;
-      } else if (row_ok) {
-        uint16_t* out = a.blk_idx + ((int64_t)h * N + i) * Nk;
-        int pos = incl - c;
-        while (m) {
-          const int b = __builtin_ctzll(m);
-          out[pos++] = (uint16_t)(64 * w + b);
-          m &= m - 1;
-        }
-        if (w == 0) a.blk_cnt[(int64_t)h * N + i] = total;
+      int c = __popcll(m);
+      for (int o = lpr >> 1; o > 0; o >>= 1) c += __shfl_xor(c, o, lpr);
+      if (row_ok) {
+        if (w < NW) a.blk_bits[((int64_t)h * N + i) * NW + w] = m;
+        if (w == 0) a.blk_cnt[(int64_t)h * N + i] = c;
       }
     }
     return;
@@ -265,8 +244,8 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(fs_select_args a, i
       thr = prefix;
       need = k - gt;
     }
-    // ---- membership + compaction in ascending block order
-    uint16_t* out = a.blk_idx + ((int64_t)h * N + i) * Nk;
+    // ---- membership in ascending block order, one word per 64 blocks
+    uint64_t* out = a.blk_bits + ((int64_t)h * N + i) * NW;
     int cnt = 0, eq_seen = 0;
     for (int j0 = 0; j0 < jlim; j0 += 64) {
       const int j = j0 + lane;
@@ -295,9 +274,10 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(fs_select_args a, i
         eq_seen += __popcll(me);
       }
       const uint64_t m = __ballot(in);
-      if (in) out[cnt + rank_below(m)] = (uint16_t)j;
+      if (lane == 0) out[j0 >> 6] = m;
       cnt += __popcll(m);
     }
+    for (int w = ((jlim + 63) >> 6) + lane; w < NW; w += 64) out[w] = 0ull;   // words past the causal limit
     if (lane == 0) a.blk_cnt[(int64_t)h * N + i] = cnt;
   }
 }
@@ -321,7 +301,8 @@ using namespace fs;
 
 extern "C" int fs_select(const fs_select_args* a, void* stream) {
   FS_CHECK_ARG(a != nullptr, "fs_select: null args");
-  FS_CHECK_ARG(a->blk_cnt && a->blk_idx, "fs_select: null output");
+  FS_CHECK_ARG(a->blk_cnt && a->blk_bits, "fs_select: null output");
+  FS_CHECK_ARG(((uintptr_t)a->blk_bits & 7) == 0, "fs_select: blk_bits must be 8-byte aligned");
   FS_CHECK_ARG(a->Hq > 0 && a->Hk > 0 && a->Hq % a->Hk == 0, "fs_select: bad head counts");
   FS_CHECK_ARG(a->N >= 1 && a->Nk >= 1 && a->Nk <= 65535, "fs_select: bad block counts");
   FS_CHECK_ARG(a->dyn_mode == 0 || a->dyn_mode == 1, "fs_select: bad dyn_mode");

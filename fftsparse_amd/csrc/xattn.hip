@@ -566,7 +566,7 @@ struct XSelK {
   const float* pad_sum;         // [Hq][Nb] (non-causal)
   const double* thr;            // [Hq]
   int32_t* blk_cnt;             // [Hq][N]
-  uint16_t* blk_idx;            // [Hq][N][Nk]
+  uint64_t* blk_bits;           // [Hq][N][ceil(Nk / 64)]
   int Hq, Nb, N, Nk, Nbp, causal, keep_sink, keep_recent;
 };
 
@@ -653,20 +653,21 @@ __global__ __launch_bounds__(kXSelThreads) void xattn_select_kernel(XSelK a) {
   }
   __syncthreads();
 
-  // ascending list of the real blocks: the chosen ones, the forced ones (causal),
+  // the row's mask words over the real blocks: the chosen ones, the forced ones (causal),
   // block 0 (non-causal: the reference's unselected positions scatter to it),
   // row 0 whole with keep_sink, the diagonal with keep_recent
   if (wave == 0) {
     const int limit = (I == 0 && a.keep_sink) || !a.causal ? a.Nk : n;
-    uint16_t* out = a.blk_idx + ((int64_t)h * a.N + I) * a.Nk;
+    const int NW = (a.Nk + 63) >> 6;
+    uint64_t* out = a.blk_bits + ((int64_t)h * a.N + I) * NW;
     int cnt = 0;
-    for (int J0 = 0; J0 < limit; J0 += 64) {
+    for (int J0 = 0; J0 < NW * 64; J0 += 64) {
       const int J = J0 + lane;
       bool in = false;
       if (J < limit)
         in = (I == 0 && a.keep_sink) || J == 0 || sel[J] || (a.causal && J == I) || (a.keep_recent && J == I);
       const uint64_t m = __ballot(in);
-      if (in) out[cnt + rank_below(m)] = (uint16_t)J;
+      if (lane == 0) out[J0 >> 6] = m;
       cnt += __popcll(m);
     }
     if (lane == 0) a.blk_cnt[(int64_t)h * a.N + I] = cnt;
@@ -757,8 +758,9 @@ using namespace fs;
 static int xattn_check(const fs_xattn_args* a, bool need_buffers) {
   FS_CHECK_ARG(a != nullptr, "fs_xattn: null args");
   if (need_buffers)
-    FS_CHECK_ARG(a->q && a->k && a->threshold && a->sums && a->blk_cnt && a->blk_idx && a->work,
+    FS_CHECK_ARG(a->q && a->k && a->threshold && a->sums && a->blk_cnt && a->blk_bits && a->work,
                  "fs_xattn: null pointer");
+  FS_CHECK_ARG(((uintptr_t)a->blk_bits & 7) == 0, "fs_xattn: blk_bits must be 8-byte aligned");
   FS_CHECK_ARG(a->Hq > 0 && a->Hk > 0 && a->Hq % a->Hk == 0, "fs_xattn: Hq=%d must be a multiple of Hk=%d", a->Hq,
                a->Hk);
   FS_CHECK_ARG(a->L > 0, "fs_xattn: empty sequence");
@@ -891,7 +893,7 @@ extern "C" int fs_xattn(const fs_xattn_args* a, void* stream) {
   sk.pad_sum = k.pad_sum;
   sk.thr = a->threshold;
   sk.blk_cnt = a->blk_cnt;
-  sk.blk_idx = a->blk_idx;
+  sk.blk_bits = a->blk_bits;
   sk.Hq = a->Hq; sk.Nb = g.N; sk.N = g.N; sk.Nk = g.N; sk.Nbp = g.causal ? g.N : g.Nbp;
   sk.causal = g.causal; sk.keep_sink = a->keep_sink; sk.keep_recent = a->keep_recent;
   xattn_select_kernel<<<(unsigned)(a->Hq * g.N), kXSelThreads, 0, s>>>(sk);

@@ -5,7 +5,7 @@ Mirrors attn_src/Flexprefill.py: ``get_active_blocks`` (:946-1061) and
 ``Flexprefill_prefill`` (:1063-1098).  One C call (fs_flex) forms the
 last-block attention profile, the budgets, the JS-divergence test, the
 vertical / slash choice and the sparse heads' block cover, and emits per-row
-block lists.  Inputs use the reference's layout, [B, L, H, D].
+block masks.  Inputs use the reference's layout, [B, L, H, D].
 """
 from __future__ import annotations
 
@@ -16,14 +16,14 @@ import torch
 
 from . import _lib
 from ._lib import FlexArgs
-from .attn import block_sparse_attention
+from .attn import block_sparse_attention, mask_from_bits, mask_words
 
 
 @dataclass
 class FlexSelection:
     """Device-resident result of the FlexPrefill selection."""
     blk_cnt: torch.Tensor       # int32 [Hq, N]
-    blk_idx: torch.Tensor       # uint16 [Hq, N, N] (first blk_cnt entries of each row valid, ascending)
+    blk_bits: torch.Tensor      # int64 [Hq, N, ceil(N/64)]: the block mask (bit j % 64 of word j / 64)
     head_info: torch.Tensor     # int32 [Hq, 4]: vertical budget, slash budget, sparse head, 0
     js: torch.Tensor            # float32 [Hq]
     vertical: torch.Tensor      # float32 [Hq, L]: mean last-block attention per key
@@ -31,12 +31,8 @@ class FlexSelection:
     block_size: int
 
     def dense_mask(self) -> torch.Tensor:
-        H, N = self.blk_cnt.shape
-        idx = self.blk_idx.view(torch.int16).to(torch.int64) & 0xFFFF
-        valid = torch.arange(N, device=idx.device)[None, None, :] < self.blk_cnt[:, :, None].to(torch.int64)
-        m = torch.zeros(H, N, N + 1, dtype=torch.bool, device=idx.device)
-        m.scatter_(2, torch.where(valid, idx, torch.full_like(idx, N)), True)
-        return m[:, :, :N]
+        """[Hq, N, N] bool block mask."""
+        return mask_from_bits(self.blk_bits, self.blk_cnt.shape[1])
 
     def nnz(self) -> int:
         return int(self.blk_cnt.sum().item())
@@ -53,7 +49,7 @@ def budgets(L: int, block_size: int, min_budget=None, max_budget=None):
 
 def flex_select(q: torch.Tensor, k: torch.Tensor, *, gamma: float = 0.9, tau: float = 0.0, min_budget=None,
                 max_budget=None, gqa_interleave: bool = False, block_size: int = 32) -> FlexSelection:
-    """get_active_blocks (Flexprefill.py:946-1061) as block lists.  q [1, L, Hq, D],
+    """get_active_blocks (Flexprefill.py:946-1061) as a block mask.  q [1, L, Hq, D],
     k [1, L, Hk, D] on the GPU (bf16/f16, D = 128), the reference's layout."""
     assert q.shape[1] == k.shape[1]                                   # Flexprefill.py:1077
     B, L, Hq, D = q.shape
@@ -78,7 +74,7 @@ def flex_select(q: torch.Tensor, k: torch.Tensor, *, gamma: float = 0.9, tau: fl
     nb = -(-L // block_size)
     mnb, mxb = budgets(L, block_size, min_budget, max_budget)
     sel = FlexSelection(blk_cnt=torch.empty(Hq, nb, dtype=torch.int32, device=dev),
-                        blk_idx=torch.empty(Hq, nb, nb, dtype=torch.uint16, device=dev),
+                        blk_bits=torch.empty(Hq, nb, mask_words(nb), dtype=torch.int64, device=dev),
                         head_info=torch.empty(Hq, 4, dtype=torch.int32, device=dev),
                         js=torch.empty(Hq, dtype=torch.float32, device=dev),
                         vertical=torch.empty(Hq, L, dtype=torch.float32, device=dev),
@@ -90,7 +86,7 @@ def flex_select(q: torch.Tensor, k: torch.Tensor, *, gamma: float = 0.9, tau: fl
         q=qv.data_ptr(), q_sh=qv.stride(1), q_sl=qv.stride(2), k=kv.data_ptr(), k_sh=kv.stride(1),
         k_sl=kv.stride(2), dtype=_lib.FS_DTYPE[q.dtype], Hq=Hq, Hk=Hk, L=L, D=D, bs=block_size,
         gamma=float(gamma), tau=float(tau), min_blocks=mnb, max_blocks=mxb, gqa_interleave=int(bool(gqa_interleave)),
-        blk_cnt=sel.blk_cnt.data_ptr(), blk_idx=sel.blk_idx.data_ptr(), head_info=sel.head_info.data_ptr(),
+        blk_cnt=sel.blk_cnt.data_ptr(), blk_bits=sel.blk_bits.data_ptr(), head_info=sel.head_info.data_ptr(),
         head_js=sel.js.data_ptr(), vertical=sel.vertical.data_ptr(), slash=sel.slash.data_ptr(),
         work=work.data_ptr()), dev)
     sel._keep = (qv, kv, work)
@@ -118,7 +114,7 @@ def Flexprefill_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gamma
         return block_sparse_attention(qv, kv, vv, block_size=128, is_causal=True, softmax_scale=softmax_scale)
     sel = flex_select(q, k, gamma=gamma, tau=tau, min_budget=min_budget, max_budget=max_budget,
                       gqa_interleave=gqa_interleave, block_size=block_size)
-    return block_sparse_attention(qv, kv, vv, sel.blk_cnt, sel.blk_idx, block_size=block_size, is_causal=True,
+    return block_sparse_attention(qv, kv, vv, sel.blk_cnt, sel.blk_bits, block_size=block_size, is_causal=True,
                                   softmax_scale=softmax_scale, gqa_interleave=gqa_interleave)
 
 

@@ -10,7 +10,7 @@ block row (attn_src/xattn/src/utils.py:44-200).  use_triton=False selects the
 reference's torch path (Xattention.py:72-135, 170-258): the "inverse" (with
 kdb), "slash", "random", "double" and "triple" reshapings, its dtype
 roundings, and softmax=False.  One C call (fs_xattn) runs all of it and emits
-the per-row block lists fs_bsattn reads.
+the block mask fs_bsattn reads.
 
 K/V may carry Hq heads (the reference asserts that: its callers pass
 repeat_kv'd K/V) or Hkv heads with Hq % Hkv == 0 (native GQA, read as they are).
@@ -24,26 +24,21 @@ import torch
 
 from . import _lib
 from ._lib import XattnArgs
-from .attn import _check_layout, block_sparse_attention
+from .attn import _check_layout, block_sparse_attention, mask_from_bits, mask_words
 
 
 @dataclass
 class XSelection:
     """Device-resident result of the XAttention selection."""
     blk_cnt: torch.Tensor       # int32 [Hq, N]
-    blk_idx: torch.Tensor       # uint16 [Hq, N, N] (first blk_cnt entries of each row valid, ascending)
+    blk_bits: torch.Tensor      # int64 [Hq, N, ceil(N/64)]: the block mask (bit j % 64 of word j / 64)
     sums: torch.Tensor          # float32 [Hq, N, N]: block sums (values of the input dtype), causal part
     stride: int
     block_size: int
 
     def dense_mask(self) -> torch.Tensor:
-        """[Hq, N, N] bool mask rebuilt from the block lists."""
-        H, N = self.blk_cnt.shape
-        idx = self.blk_idx.view(torch.int16).to(torch.int64) & 0xFFFF
-        valid = torch.arange(N, device=idx.device)[None, None, :] < self.blk_cnt[:, :, None].to(torch.int64)
-        m = torch.zeros(H, N, N + 1, dtype=torch.bool, device=idx.device)
-        m.scatter_(2, torch.where(valid, idx, torch.full_like(idx, N)), True)
-        return m[:, :, :N]
+        """[Hq, N, N] bool block mask."""
+        return mask_from_bits(self.blk_bits, self.blk_cnt.shape[1])
 
     def nnz(self) -> int:
         return int(self.blk_cnt.sum().item())
@@ -127,14 +122,14 @@ def xattn_select(query_states: torch.Tensor, key_states: torch.Tensor, *, stride
     dev = _lib.same_device(q, k)
     thr = _thresholds(threshold, Hq, dev)
     sel = XSelection(blk_cnt=torch.empty(Hq, N, dtype=torch.int32, device=dev),
-                     blk_idx=torch.empty(Hq, N, N, dtype=torch.uint16, device=dev),
+                     blk_bits=torch.empty(Hq, N, mask_words(N), dtype=torch.int64, device=dev),
                      sums=torch.zeros(Hq, N, N, dtype=torch.float32, device=dev),
                      stride=stride, block_size=block_size)
     args = XattnArgs(
         q=q.data_ptr(), q_sh=q.stride(1), q_sl=q.stride(2), k=k.data_ptr(), k_sh=k.stride(1), k_sl=k.stride(2),
         dtype=_lib.FS_DTYPE[q.dtype], Hq=Hq, Hk=Hk, L=L, D=D, stride=stride, bs=block_size, norm=float(norm),
         threshold=thr.data_ptr(), keep_sink=int(bool(keep_sink)), sums=sel.sums.data_ptr(),
-        blk_cnt=sel.blk_cnt.data_ptr(), blk_idx=sel.blk_idx.data_ptr(),
+        blk_cnt=sel.blk_cnt.data_ptr(), blk_bits=sel.blk_bits.data_ptr(),
         non_causal=int(not causal), torch_path=int(not use_triton), select_mode=mode, kdb=int(kdb),
         no_softmax=int(not use_triton and not softmax), chunk=chunk, keep_recent=int(bool(keep_recent)))
     args.perm[:] = pm
@@ -179,7 +174,7 @@ def Xattention_prefill(query_states: torch.Tensor, key_states: torch.Tensor, val
     sel = xattn_select(query_states, key_states, stride=stride, threshold=threshold, norm=norm,
                        block_size=block_size, keep_sink=keep_sink, keep_recent=keep_recent, causal=causal,
                        use_triton=use_triton, kdb=kdb, chunk_size=chunk_size)
-    out = block_sparse_attention(query_states, key_states, value_states, sel.blk_cnt, sel.blk_idx,
+    out = block_sparse_attention(query_states, key_states, value_states, sel.blk_cnt, sel.blk_bits,
                                  block_size=block_size, is_causal=causal)
     return out.transpose(1, 2)
 

@@ -22,8 +22,8 @@
  *                create_qk_topk_block_mask    my_attn_v7.py:256-294 (diffuse heads)
  *                create_deterministic_block_mask attn_src/fix_mask_attn/my_attn.py:39-79 (fixed role)
  *                The dense [1,H,N,N] bool mask the reference hands to the
- *                kernel (my_attn_v7.py:710,780) is replaced by per-row lists
- *                of selected key blocks.
+ *                kernel (my_attn_v7.py:710,780) is kept as a row bitmask (see
+ *                "Block masks" below): the same mask, one bit per block.
  *   fs_xattn     XAttention's selector        attn_src/xattn/src/Xattention.py:14-303 (xattn_estimate),
  *                                            utils.py:44-200 (find_blocks_chunked); the mask its
  *                                            Xattention_prefill (:306-406) hands to block_sparse_attn_func
@@ -56,6 +56,19 @@ enum {
   FS_ERR_UNSUPPORTED = -2,  /* valid but not implemented (dtype, head dim, size) */
   FS_ERR_LAUNCH = -3        /* the HIP runtime rejected a launch */
 };
+
+/* ---- Block masks ---------------------------------------------------------
+ * Every selector writes, and fs_bsattn reads, the block mask as a row
+ * bitmask plus a count per row:
+ *   blk_bits[(h * N + i) * NW + w], NW = ceil(Nk / 64), 64-bit words: bit b of
+ *     word w is set iff query-block row i of head h selects key block 64 w + b
+ *     (bits at 64 w + b >= Nk are 0);
+ *   blk_cnt[h * N + i] = the number of set bits of the row.
+ * It is the reference's base_blockmask bool [1, H, N, N] (my_attn_v7.py:710,
+ * 780) with one bit per block: N * NW * 8 bytes per head (4 MiB for 32 heads at
+ * N = 1024, 256 MiB at N = 8192), whatever the number of selected blocks, and
+ * rows are written independently (no prefix sum over rows, no host sync). */
+#define FS_MASK_WORDS(Nk) (((Nk) + 63) / 64)
 
 /* ---- block pooling (my_attn_v7.py:105-114) ------------------------------
  * q: [Hq, L, D] view with element strides (q_sh, q_sl), d contiguous.
@@ -192,7 +205,7 @@ FS_API int fs_scores(const fs_scores_args* a, void* stream);
 #define FS_SCORES_STATIC_BYTES ((size_t)32 << 20)
 FS_API int fs_scores_noalloc(const fs_scores_args* a, void* stream);
 
-/* ---- mask composition -> per-row block lists ----------------------------
+/* ---- mask composition -> block mask --------------------------------------
  * Row i of head h selects key block j (0 <= j < Nk, and j <= i if mask_causal) iff
  *   prior:  j < keep_sink || j >= Nk - keep_recent || (local_window > 0 && |i-j| <= local_window)
  *   last:   last_sel && i == N-1 && last_sel[h][j]
@@ -201,11 +214,9 @@ FS_API int fs_scores_noalloc(const fs_scores_args* a, void* stream);
  *                             k_i = max(1, trunc(float(i+1) * qk_topk_ratio)), ties -> lower j
  *   column: col_mode 2, or col_mode 1 and stripe head: col_sel[h][j] && j <= i
  * with is_stripe[h] = mean_s(diag_var[h][s]) <= stripe_threshold (false when
- * stripe_all_diffuse or the mean is nan).  Output: blk_cnt[h][i] and the
- * selected j in ascending order at blk_idx[(h*N + i) * Nk ...]; the entries
- * of a row past its count are unspecified (with Nk a multiple of 8 the list is
- * written in 16-byte chunks, the last one padded with 0).  N <= 8192
- * (D <= 256 with dyn_mode 1). */
+ * stripe_all_diffuse or the mean is nan).  Output: the block mask blk_bits
+ * [Hq][N][FS_MASK_WORDS(Nk)] and blk_cnt [Hq][N] (every word of every row is
+ * written).  N <= 8192 (D <= 256 with dyn_mode 1). */
 typedef struct {
   const void* q_b; const void* k_b;
   int dtype, Hq, Hk, N, Nk, D;
@@ -222,7 +233,7 @@ typedef struct {
   float* mean_var;              /* [Hq] out (may be NULL) */
   uint8_t* is_stripe;           /* [Hq] out (may be NULL) */
   int32_t* blk_cnt;             /* [Hq][N] */
-  uint16_t* blk_idx;            /* [Hq][N][Nk] */
+  uint64_t* blk_bits;           /* [Hq][N][FS_MASK_WORDS(Nk)] */
 } fs_select_args;
 FS_API int fs_select(const fs_select_args* a, void* stream);
 
@@ -250,8 +261,8 @@ FS_API int fs_select(const fs_select_args* a, void* stream);
  * + (mass of the larger others) < row total * threshold[h]; non_causal: every
  * block of the chunk-padded row in decreasing order while the mass before it
  * < row total * threshold[h], and block 0 (ties: lower index first).  Outputs
- * the ascending block lists blk_cnt [Hq][N], blk_idx [Hq][N][N] of the
- * N = ceil(L/bs) real blocks (causal: the tril; keep_sink: row 0 lists every
+ * the block mask blk_bits [Hq][N][FS_MASK_WORDS(N)], blk_cnt [Hq][N] of the
+ * N = ceil(L/bs) real blocks (causal: the tril; keep_sink: row 0 selects every
  * block; keep_recent: the diagonal) and sums [Hq][N][N] (causal: its lower
  * triangle).  threshold: device array of Hq float64 values.  work:
  * fs_xattn_work_bytes(a) bytes of device scratch: the row statistics, K' for
@@ -269,7 +280,7 @@ typedef struct {
   int keep_sink;
   float* sums;
   int32_t* blk_cnt;
-  uint16_t* blk_idx;
+  uint64_t* blk_bits;
   void* work;
   int non_causal;       /* causal=False */
   int torch_path;       /* use_triton=False */
@@ -298,9 +309,8 @@ FS_API int fs_xattn(const fs_xattn_args* a, void* stream);
  * is below tau take min_blocks and, in addition, the cover of gamma * N of
  * their block-level causal attention; the top pooled vertical columns (block 0
  * forced) in every row at or after them and the top pooled slash offsets
- * (offset 0 forced) as block diagonals (ties: lower index).  Outputs ascending
- * block lists blk_cnt [Hq][N], blk_idx [Hq][N][N] (N = ceil(L/bs); entries past
- * a row's count unspecified, as for fs_select), optionally
+ * (offset 0 forced) as block diagonals (ties: lower index).  Outputs the block
+ * mask blk_bits [Hq][N][FS_MASK_WORDS(N)], blk_cnt [Hq][N] (N = ceil(L/bs)), optionally
  * head_info [Hq][4] (vertical budget, slash budget, sparse, 0), head_js [Hq]
  * and the per-token vertical / slash profiles [Hq][L] (fp32).
  * work: fs_flex_work_bytes(Hq, Hk, L, bs, tau) bytes, with the tau of the
@@ -315,7 +325,7 @@ typedef struct {
   int min_blocks, max_blocks;
   int gqa_interleave;
   int32_t* blk_cnt;
-  uint16_t* blk_idx;
+  uint64_t* blk_bits;
   int32_t* head_info;
   float* head_js;
   float* vertical;
@@ -328,17 +338,21 @@ FS_API int fs_flex(const fs_flex_args* a, void* stream);
 /* ---- block-sparse attention prefill --------------------------------------
  * out[b][t][h] = softmax(q[b][h][t] . k[b][hk][s] * scale) v[b][hk][s] over the
  * key tokens s of the selected key blocks of query block t / bs (and s <= t +
- * Lk - Lq when is_causal).  blk_cnt == NULL selects every key block up to the
+ * Lk - Lq when is_causal).  The selected key blocks of query block r of head
+ * h are the set bits of row (h, r) of the block mask blk_bits [Hq][Nq][NW]
+ * (NW = FS_MASK_WORDS(Nk); bits past the causal limit are ignored); blk_cnt
+ * [Hq][Nq] (the rows' bit counts) only orders the work, largest first.
+ * blk_cnt == NULL selects every key block up to the
  * causal limit (dense causal attention).  Supported: dtype bf16/f16, D == 128,
- * bs in {16, 32, 64, 128} (16 and 32: FlexPrefill's block sizes; their lists
- * are attended 128 queries at a time over the union of 128 / bs rows' lists,
+ * bs in {16, 32, 64, 128} (16 and 32: FlexPrefill's block sizes; their masks
+ * are attended 128 queries at a time over the union of 128 / bs rows,
  * up to 8192 key blocks).  All tensors are
  * strided views with d contiguous.
  * work: fs_bsattn_work_bytes(a) bytes of device scratch (V is staged there
  * transposed, and the work items' longest-first order and the counters from
  * which the attention kernel's workgroups take their work items are formed
  * there, before the attention kernel runs).  Calls that overlap on one
- * workspace race; the lists' results do not depend on which workgroup takes
+ * workspace race; the results do not depend on which workgroup takes
  * which item. */
 typedef struct {
   const void* q; int64_t q_sb, q_sh, q_sl;
@@ -350,7 +364,7 @@ typedef struct {
   float softmax_scale;
   int gqa_interleave;           /* query head h reads KV head h % Hk (else h / (Hq / Hk)) */
   const int32_t* blk_cnt;       /* [Hq][Nq] or NULL (B must be 1 when non-NULL) */
-  const uint16_t* blk_idx;      /* [Hq][Nq][Nk] */
+  const uint64_t* blk_bits;     /* [Hq][Nq][FS_MASK_WORDS(Nk)] */
   void* work;
 } fs_attn_args;
 FS_API size_t fs_bsattn_work_bytes(const fs_attn_args* a);

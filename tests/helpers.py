@@ -30,13 +30,36 @@ def block_match(gpu_mask: torch.Tensor, ref_mask: torch.Tensor, excusable: torch
     return (total - unexc) / total, exact / total, unexc
 
 
-def lists_from_mask(mask: torch.Tensor, device):
-    """Dense [H,N,Nk] bool mask -> (blk_cnt int32 [H,N], blk_idx uint16 [H,N,Nk])."""
-    H, N, Nk = mask.shape
-    cnt = mask.sum(-1).to(torch.int32)
-    order = torch.argsort((~mask).to(torch.int8), dim=-1, stable=True)
-    idx = order.to(torch.int16).view(torch.uint16).contiguous()
-    return cnt.to(device), idx.to(device)
+def mask_bits(mask: torch.Tensor, device):
+    """Dense [H,N,Nk] bool mask -> (blk_cnt int32 [H,N], blk_bits int64 [H,N,ceil(Nk/64)]) on device."""
+    from fftsparse_amd.attn import bits_from_mask
+    cnt, bits = bits_from_mask(mask)
+    return cnt.to(device), bits.to(device)
+
+
+def check_mask_rows(mask: torch.Tensor, rows):
+    """Rows i of a [H, N, Nk] bool block mask are causal (no block past i) and
+    hold block 0 and the diagonal block i."""
+    for i in rows:
+        r = mask[:, i]
+        assert not r[:, i + 1:].any(), f"row {i}: blocks past the diagonal"
+        assert r[:, 0].all() and r[:, i].all(), f"row {i}: sink or diagonal block missing"
+
+
+def check_mask_words(blk_bits: torch.Tensor, blk_cnt: torch.Tensor, nk: int):
+    """Every row of a block mask (words [H, N, W], on any device): its count
+    is its popcount, it is causal, and it holds block 0 and the diagonal block.
+    One head at a time ([N, Nk] bools)."""
+    from fftsparse_amd.attn import mask_from_bits
+    H, N, _ = blk_bits.shape
+    pos = torch.arange(N, device=blk_bits.device)
+    above = torch.arange(nk, device=blk_bits.device)[None, :] > pos[:, None]
+    for h in range(H):
+        m = mask_from_bits(blk_bits[h:h + 1], nk)[0]
+        assert torch.equal(m.sum(-1, dtype=torch.int32), blk_cnt[h]), f"head {h}: counts"
+        assert not bool((m & above).any()), f"head {h}: blocks past the diagonal"
+        assert bool(m[:, 0].all()) and bool(m[pos, pos.clamp(max=nk - 1)].all()), f"head {h}: sink / diagonal"
+        del m
 
 
 def rope_tables(L, D, theta, dtype):

@@ -27,7 +27,7 @@ import torch
 from fftsparse_amd import block_sparse_attention, myattn_prefill, select_blocks
 from fftsparse_amd.synth import CONFIGS, make_config
 from oracle import v7
-from tests.helpers import BAND, MATCH_MIN, PROD, block_match, lists_from_mask
+from tests.helpers import BAND, MATCH_MIN, PROD, block_match, mask_bits
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -81,12 +81,12 @@ def test_baseline_workload_parity(name, thr):
 
     # stage 2 under the oracle's mask
     qblocks = _sample_blocks(N)
-    cnt, idx = lists_from_mask(ref.mask, DEV)
-    out = block_sparse_attention(qg, kg, vg, cnt, idx, block_size=bs)
+    cnt, bits = mask_bits(ref.mask, DEV)
+    out = block_sparse_attention(qg, kg, vg, cnt, bits, block_size=bs)
     torch.cuda.synchronize()
     want = v7.block_sparse_attention(q, k, v, ref.mask, bs, qblocks=qblocks)
     _attn_rows_check(out[0], want, qblocks, bs, L, "attention under the oracle mask")
-    del out, cnt, idx
+    del out, cnt, bits
 
     # end to end: the layer's output under the lists it selected
     o = myattn_prefill(qg, kg, vg, layer_idx=0, **kw)

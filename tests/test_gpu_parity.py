@@ -15,7 +15,7 @@ import torch
 from fftsparse_amd import _lib, block_sparse_attention, fix_mask, myattn_prefill, rope_pool, select_blocks
 from fftsparse_amd.synth import make_qkv, make_config
 from oracle import v7
-from tests.helpers import BAND, MATCH_MIN, PROD, block_match, lists_from_mask, rope_tables
+from tests.helpers import BAND, MATCH_MIN, PROD, block_match, check_mask_rows, mask_bits, rope_tables
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -244,29 +244,26 @@ def test_topk_lag_keep_matches_quantile_of_own_corr(dtype, ratio):
     assert (keep.sum(-1) >= 1).all()
 
 
-def test_block_lists_are_ascending_and_deterministic():
+def test_block_mask_is_causal_and_deterministic():
+    """The block mask of two identical calls is the same word for word (every
+    word written), each row's count is its popcount, and the sampled rows are
+    causal with the sink block and the diagonal."""
     q, k, _ = make_qkv(32768, 8, 2, seed=5)
     qg, kg = _gpu(q, k)
     a = select_blocks(qg, kg, **PROD)
     b = select_blocks(qg, kg, **PROD)
     assert torch.equal(a.blk_cnt, b.blk_cnt)
-    N, Nk = a.params.N, a.params.Nk
-    used = torch.arange(Nk, device=DEV)[None, None, :] < a.blk_cnt[:, :, None]
-    ia = a.blk_idx.view(torch.int16).masked_fill(~used, 0)
-    ib = b.blk_idx.view(torch.int16).masked_fill(~used, 0)
-    assert torch.equal(ia, ib)
-    cnt = a.blk_cnt.cpu()
-    idx = a.blk_idx.view(torch.int16).cpu().to(torch.int64)
-    for h in range(cnt.shape[0]):
-        for i in range(0, N, 17):
-            row = idx[h, i, : cnt[h, i]]
-            assert bool((row[1:] > row[:-1]).all()) and int(row[-1]) == i and int(row[0]) == 0
+    assert torch.equal(a.blk_bits, b.blk_bits)
+    N = a.params.N
+    m = a.dense_mask().cpu()
+    assert torch.equal(m.sum(-1, dtype=torch.int32), a.blk_cnt.cpu())
+    check_mask_rows(m, range(0, N, 17))
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_pipeline_grouping_does_not_change_lists(dtype):
+def test_pipeline_grouping_does_not_change_the_mask(dtype):
     """The head-group pipeline (pooling of one group overlapping the statistics
-    of the previous one on a side stream) gives bit-identical block lists and
+    of the previous one on a side stream) gives a bit-identical block mask and
     statistics for every grouping."""
     q, k, _ = make_qkv(32768, 8, 4, dtype=dtype, seed=9)
     qg, kg = _gpu(q, k)
@@ -302,8 +299,8 @@ def test_attention_parity_reference_mask(L, Hq, Hk, bs, dtype):
     _print_case("attention", L=L, Hq=Hq, Hk=Hk, bs=bs, dtype=dtype)
     q, k, v = make_qkv(L, Hq, Hk, dtype=dtype, seed=6)
     ref_sel = v7.select_mask(q, k, **{**PROD, "block_size": bs})
-    cnt, idx = lists_from_mask(ref_sel.mask, DEV)
-    out = block_sparse_attention(*_gpu(q, k, v), cnt, idx, block_size=bs)
+    cnt, bits = mask_bits(ref_sel.mask, DEV)
+    out = block_sparse_attention(*_gpu(q, k, v), cnt, bits, block_size=bs)
     torch.cuda.synchronize()
     ref = v7.block_sparse_attention(q, k, v, ref_sel.mask, bs)
     _attn_check(out[0], ref)
@@ -314,8 +311,8 @@ def test_attention_noncausal_and_dense():
     N = 16
     mask = torch.rand(4, N, N, generator=torch.Generator().manual_seed(0)) < 0.3
     mask |= torch.eye(N, dtype=torch.bool)
-    cnt, idx = lists_from_mask(mask, DEV)
-    out = block_sparse_attention(*_gpu(q, k, v), cnt, idx, block_size=128, is_causal=False)
+    cnt, bits = mask_bits(mask, DEV)
+    out = block_sparse_attention(*_gpu(q, k, v), cnt, bits, block_size=128, is_causal=False)
     ref = v7.block_sparse_attention(q, k, v, mask, 128, is_causal=False)
     _attn_check(out[0], ref)
     out = block_sparse_attention(*_gpu(q, k, v), block_size=128, is_causal=True)
@@ -346,8 +343,8 @@ def test_attention_running_max_raises(growth):
     for bs in (128, 64, 32, 16):
         N = L // bs
         mask = torch.tril(torch.ones(2, N, N, dtype=torch.bool))
-        cnt, idx = lists_from_mask(mask, DEV)
-        out = block_sparse_attention(*_gpu(q, k, v), cnt, idx, block_size=bs)
+        cnt, bits = mask_bits(mask, DEV)
+        out = block_sparse_attention(*_gpu(q, k, v), cnt, bits, block_size=bs)
         _attn_check(out[0], ref)
 
 
@@ -375,8 +372,8 @@ def test_attention_short_blocks(bs, L, Hq, Hk, dtype, density, causal):
     mask[0, 5] = False                          # a row holding only ...
     mask[0, 5, 5] = True                        # ... its diagonal block
     mask[-1, 9] = False                         # a row with no block at all (output 0)
-    cnt, idx = lists_from_mask(mask, DEV)
-    out = block_sparse_attention(*_gpu(q, k, v), cnt, idx, block_size=bs, is_causal=causal)
+    cnt, bits = mask_bits(mask, DEV)
+    out = block_sparse_attention(*_gpu(q, k, v), cnt, bits, block_size=bs, is_causal=causal)
     torch.cuda.synchronize()
     ref = v7.block_sparse_attention(q, k, v, mask, bs, is_causal=causal)
     _attn_check(out[0], ref)
@@ -393,10 +390,10 @@ def test_attention_prepare_run_equals_single_call():
     N = (3000 + 127) // 128
     mask = torch.rand(4, N, N, generator=torch.Generator().manual_seed(1)) < 0.4
     mask = (mask | torch.eye(N, dtype=torch.bool)) & torch.ones(N, N, dtype=torch.bool).tril()
-    cnt, idx = lists_from_mask(mask, DEV)
+    cnt, bits = mask_bits(mask, DEV)
     qg, kg, vg = _gpu(q, k, v)
-    whole = block_sparse_attention(qg, kg, vg, cnt, idx).clone()
-    call = AttentionCall(qg, kg, vg, cnt, idx)
+    whole = block_sparse_attention(qg, kg, vg, cnt, bits).clone()
+    call = AttentionCall(qg, kg, vg, cnt, bits)
     call.prepare()
     first = call.run().clone()
     second = call.run()
@@ -469,17 +466,16 @@ def test_full_length_c2_properties():
     assert not ((sel.keep_tau.cpu().bool() != keep_ref) & ~near).any()
     cnt = sel.blk_cnt.cpu()
     assert int(cnt.min()) >= 1 and bool((cnt <= torch.arange(1, p.N + 1)[None, :]).all())
-    idx = sel.blk_idx.view(torch.int16).cpu().to(torch.int64)
-    for h in (0, 13, 31):
-        for i in (0, 511, 1023):
-            row = idx[h, i, : cnt[h, i]]
-            assert int(row[0]) == 0 and int(row[-1]) == i and bool((row[1:] > row[:-1]).all())
+    m = sel.dense_mask().cpu()
+    assert torch.equal(m.sum(-1, dtype=torch.int32), cnt)
+    check_mask_rows(m[[0, 13, 31]], (0, 511, 1023))
 
 
 def test_maximum_block_count_properties():
     """The largest supported selection, N = 8192 blocks (L = 1048576 at block
-    128): every row's list ascending, causal, with the sink block and the
-    diagonal; selection deterministic; attention output finite."""
+    128): rows causal, with the sink block and the diagonal, counts equal to
+    the rows' popcounts; selection deterministic; attention output finite.
+    The mask takes N * N / 8 bytes per head (8 MiB)."""
     _print_case("max-blocks", L=8192 * 128, Hq=2, Hk=1)
     g = torch.Generator(device=DEV).manual_seed(12)
     L, Hq, Hk = 8192 * 128, 2, 1
@@ -494,13 +490,13 @@ def test_maximum_block_count_properties():
     assert torch.equal(sel.blk_cnt, sel2.blk_cnt)
     cnt = sel.blk_cnt.cpu()
     assert bool((cnt >= 1).all()) and bool((cnt <= torch.arange(1, 8193)[None, :]).all())
-    idx = sel.blk_idx.view(torch.int16).cpu().to(torch.int64) & 0xFFFF
-    for h in range(Hq):
-        for i in (0, 1, 4095, 4096, 8190, 8191):
-            row = idx[h, i, : cnt[h, i]]
-            assert int(row[0]) == 0 and int(row[-1]) == i and bool((row[1:] > row[:-1]).all())
-    assert torch.equal(sel.dense_mask(), sel2.dense_mask())
-    out = block_sparse_attention(q, k, v, sel.blk_cnt, sel.blk_idx)
+    assert sel.blk_bits.numel() * 8 == Hq * 8192 * 8192 // 8
+    assert torch.equal(sel.blk_bits, sel2.blk_bits)
+    m = sel.dense_mask().cpu()
+    assert torch.equal(m.sum(-1, dtype=torch.int32), cnt)
+    check_mask_rows(m, (0, 1, 4095, 4096, 8190, 8191))
+    del m
+    out = block_sparse_attention(q, k, v, sel.blk_cnt, sel.blk_bits)
     torch.cuda.synchronize()
     assert bool(torch.isfinite(out.float()).all())
 

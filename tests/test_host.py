@@ -50,7 +50,7 @@ def test_bad_shapes_rejected_without_gpu():
     assert b"D=96" in lib.fs_last_error()
     r.D, r.q_sl = 128, 100                                       # 200-byte row stride
     assert lib.fs_rope_pool(ctypes.byref(r), None) == -1
-    x = _lib.XattnArgs(q=16, k=16, threshold=16, sums=16, blk_cnt=16, blk_idx=16, work=16, dtype=1, Hq=4, Hk=1,
+    x = _lib.XattnArgs(q=16, k=16, threshold=16, sums=16, blk_cnt=16, blk_bits=16, work=16, dtype=1, Hq=4, Hk=1,
                        L=4096, D=128, stride=8, bs=64, norm=1.0)
     assert lib.fs_xattn(ctypes.byref(x), None) == -2              # the reference asserts block_size == 128
     assert b"block size" in lib.fs_last_error()
@@ -58,7 +58,7 @@ def test_bad_shapes_rejected_without_gpu():
     assert lib.fs_xattn(ctypes.byref(x), None) == -2
     x.stride, x.Hk = 8, 3
     assert lib.fs_xattn(ctypes.byref(x), None) == -1
-    f = _lib.FlexArgs(q=16, k=16, blk_cnt=16, blk_idx=16, work=16, dtype=1, Hq=4, Hk=1, L=4096, D=128, bs=8,
+    f = _lib.FlexArgs(q=16, k=16, blk_cnt=16, blk_bits=16, work=16, dtype=1, Hq=4, Hk=1, L=4096, D=128, bs=8,
                       gamma=0.9, tau=0.1, min_blocks=1, max_blocks=64, q_sl=128, k_sl=128, q_sh=128, k_sh=128)
     assert lib.fs_flex(ctypes.byref(f), None) == -2              # the reference asserts 16, 32, 64 or 128
     assert b"block size" in lib.fs_last_error()
@@ -76,9 +76,13 @@ def test_bad_shapes_rejected_without_gpu():
     nb = 4096 // 64
     assert lib.fs_flex_work_bytes(4, 1, 4096, 64, 0.1) - lib.fs_flex_work_bytes(4, 1, 4096, 64, 0.0) >= 4 * nb * nb * 4
     x = _lib.AttnArgs(q=16, k=16, v=16, out=16, work=16, dtype=1, B=1, Hq=4, Hk=2, Lq=1280, Lk=1280, D=128, bs=128,
-                      q_sl=128, k_sl=128, v_sl=128, o_sl=512, blk_cnt=18, blk_idx=16)
-    assert lib.fs_bsattn(ctypes.byref(x), None) == -1             # the lists are read as 32-bit words
-    assert b"4-byte aligned" in lib.fs_last_error()
+                      q_sl=128, k_sl=128, v_sl=128, o_sl=512, blk_cnt=18, blk_bits=16)
+    assert lib.fs_bsattn(ctypes.byref(x), None) == -1             # counts are read as 32-bit words
+    assert b"4- / 8-byte aligned" in lib.fs_last_error()
+    x.blk_cnt, x.blk_bits = 16, 20                                # mask words are 64-bit
+    assert lib.fs_bsattn(ctypes.byref(x), None) == -1
+    assert b"4- / 8-byte aligned" in lib.fs_last_error()
+    x.blk_bits = 16
     x.blk_cnt, x.bs, x.Lq, x.Lk = 16, 16, 8193 * 16, 8193 * 16    # union lists of 8193 key blocks
     assert lib.fs_bsattn(ctypes.byref(x), None) == -2
     assert b"8192 key blocks" in lib.fs_last_error()
@@ -136,17 +140,38 @@ def test_synthetic_inputs_are_pinned():
     assert CONFIGS["c2"].period == 512 and CONFIGS["c3a"].theta == 1000000.0
 
 
-def test_block_lists_checked_before_any_launch():
-    """Lists of the wrong dtype, shape or layout raise ValueError on the host."""
+def test_block_masks_checked_before_any_launch():
+    """Masks of the wrong dtype, shape or layout raise ValueError on the host."""
     q = torch.zeros(1, 4, 1280, 128, dtype=torch.bfloat16)
     k = torch.zeros(1, 2, 1280, 128, dtype=torch.bfloat16)
     cnt = torch.ones(4, 10, dtype=torch.int32)
-    idx = torch.zeros(4, 10, 10, dtype=torch.uint16)
-    bad = [(cnt.to(torch.int64), idx), (cnt[:, :9], idx), (cnt, idx[:, :, :9]), (cnt, idx.to(torch.int32)),
-           (cnt, idx.transpose(1, 2)), (cnt, None)]
-    for c, i in bad:
+    bits = torch.zeros(4, 10, 1, dtype=torch.int64)
+    wide = torch.zeros(4, 10, 2, dtype=torch.int64)
+    bad = [(cnt.to(torch.int64), bits), (cnt[:, :9], bits), (cnt, bits[:3]), (cnt, bits.to(torch.int32)),
+           (cnt, wide), (cnt, wide[:, :, ::2]), (cnt, None), (None, bits)]
+    for c, b in bad:
         with pytest.raises(ValueError):
-            fftsparse_amd.AttentionCall(q, k, k, c, i)
+            fftsparse_amd.AttentionCall(q, k, k, c, b)
+    with pytest.raises(ValueError):                               # a block mask of the wrong size
+        fftsparse_amd.block_sparse_attention(q, k, k, block_mask=torch.ones(4, 10, 9, dtype=torch.bool))
+    with pytest.raises(ValueError):                               # mask and words together
+        fftsparse_amd.block_sparse_attention(q, k, k, cnt, bits, block_mask=torch.ones(4, 10, 10, dtype=torch.bool))
+
+
+def test_mask_bits_round_trip():
+    """bits_from_mask / mask_from_bits: bit b of word w is key block 64 w + b,
+    counts are the rows' popcounts, for row lengths around word boundaries."""
+    from fftsparse_amd.attn import bits_from_mask, mask_from_bits
+    g = torch.Generator().manual_seed(3)
+    for nk in (1, 63, 64, 65, 128, 130, 1000):
+        m = torch.rand(3, 5, nk, generator=g) < 0.4
+        m[0, 0] = True                                           # a full row: every word all ones
+        cnt, bits = bits_from_mask(m)
+        assert bits.shape == (3, 5, (nk + 63) // 64) and bits.dtype == torch.int64
+        assert torch.equal(mask_from_bits(bits, nk), m) and torch.equal(cnt, m.sum(-1, dtype=torch.int32))
+        w = int(bits[1, 2, 0]) & (2 ** 64 - 1)
+        assert all(((w >> b) & 1) == int(m[1, 2, b]) for b in range(min(64, nk)))
+    assert int(bits_from_mask(torch.ones(1, 1, 64, dtype=torch.bool))[1][0, 0, 0]) == -1   # all 64 bits set
 
 
 def test_noalloc_scores_rejects_sizes_past_its_static_buffer_without_gpu():
@@ -171,7 +196,7 @@ def test_selection_block_limits_without_gpu():
     sc = _lib.ScoresArgs(q_b=16, k_b=16, work=16, dtype=1, Hq=1, Hk=1, N=8193, D=128, n_cols=0, last_k=0)
     assert lib.fs_scores(ctypes.byref(sc), None) == -2
     assert b"N=8193 > 8192" in lib.fs_last_error()
-    se = _lib.SelectArgs(q_b=16, k_b=16, dtype=1, Hq=1, Hk=1, N=8193, Nk=8193, D=128, blk_cnt=16, blk_idx=16)
+    se = _lib.SelectArgs(q_b=16, k_b=16, dtype=1, Hq=1, Hk=1, N=8193, Nk=8193, D=128, blk_cnt=16, blk_bits=16)
     assert lib.fs_select(ctypes.byref(se), None) == -2
     assert b"N=8193 > 8192" in lib.fs_last_error()
     co = _lib.CorrArgs(q_b=16, k_b=16, dtype=0, Hq=1, Hk=1, N=4097, D=128, work=16, corr=16, corr_sum=16,
