@@ -525,6 +525,12 @@ void bsattn_kernel(AttnKArgs a) {
   // by more than 2^8, so p = 2^(s*sc - m) <= 256 and most tiles skip the rescale.
   const float sc = a.scale * 1.44269504088896340736f;
   constexpr float kSlack = 8.0f;
+  // Split tiles (block 64, two key groups of 16 MFMAs per wave) take their
+  // exponentials against the running max with no row max: a tile whose row
+  // sum exceeds 2^64 (or is inf / nan, as on a row's first tile) is redone
+  // with the raised max.  Against the row max: C3a -4.6%; at block 128 (32
+  // MFMAs per wave) the row max is kept, the other form measured 3.5% slower.
+  constexpr bool kRowMax = C::KG == 1;
   float m_run = -INFINITY, l_run = 0.f;
   f32x16_t o[kD / 32];
 #pragma unroll
@@ -701,35 +707,64 @@ void bsattn_kernel(AttnKArgs a) {
     if constexpr (decltype(hasS)::value) compute_s((t + 1) & 1, s_next);
     if constexpr (decltype(hasPV)::value) pv_mma((t - 1) & 1, p_prev);
     if constexpr (decltype(hasE)::value) {
-      float mx = row_max(s_cur), m0, m1;
-      halves(mx, m0, m1);
-      mx = fmaxf(m0, m1) * sc;
-      // a row raises its running max only when a score exceeds it by more than the slack
-      const bool up = mx > m_run + kSlack;
-      al = up ? __builtin_amdgcn_exp2f(m_run - mx) : 1.0f;
-      m_run = up ? mx : m_run;
-      rs = exp_part(s_cur, p_cur, m_run == -INFINITY ? 0.f : m_run);
+      if constexpr (kRowMax) {
+        float mx = row_max(s_cur), m0, m1;
+        halves(mx, m0, m1);
+        mx = fmaxf(m0, m1) * sc;
+        // a row raises its running max only when a score exceeds it by more than the slack
+        const bool up = mx > m_run + kSlack;
+        al = up ? __builtin_amdgcn_exp2f(m_run - mx) : 1.0f;
+        m_run = up ? mx : m_run;
+        rs = exp_part(s_cur, p_cur, m_run == -INFINITY ? 0.f : m_run);
+      } else {
+        // exponentials against the running max with no row max; a row whose
+        // sum overflows (or the first tile, m_run = -inf: inf / nan) is redone below
+        rs = exp_part(s_cur, p_cur, m_run);
+      }
     }
     if constexpr (decltype(hasS)::value && decltype(hasPV)::value && decltype(hasE)::value) {
-      // Steady state: the scheduler interleaves one MFMA with two VALU
+      // Steady state: the scheduler interleaves one MFMA with three VALU
       // instructions (a wave issues in order, so MFMAs issued back to back
       // would hold its exponentials until the last one), the LDS operand
-      // reads running six MFMAs ahead (measured best of 2 .. 8).
+      // reads running six MFMAs ahead (measured best of 2 .. 8; three VALU
+      // per MFMA against two: C2 -2.4%, C3a -4.6%, C3b -1.5%).
       constexpr int NM = C::KT * (kD / 16) + (C::KH / 16) * (kD / 32);
       constexpr int LA = 6;
+      constexpr int VPM = 3;
       __builtin_amdgcn_sched_group_barrier(0x100, LA, 0);        // DS reads
 #pragma unroll
       for (int i = 0; i < NM; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // MFMA
         if (i + LA < NM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);       // VALU
+        __builtin_amdgcn_sched_group_barrier(0x002, VPM, 0);     // VALU
       }
     }
     if constexpr (decltype(hasE)::value) {
       float r0, r1;
       halves(rs, r0, r1);
-      l_run = l_run * al + (r0 + r1);
-      if (__builtin_amdgcn_ballot_w64(al != 1.0f) != 0) scale_o(al);   // O holds P V up to t-1 now
+      if constexpr (kRowMax) {
+        l_run = l_run * al + (r0 + r1);
+        if (__builtin_amdgcn_ballot_w64(al != 1.0f) != 0) scale_o(al);   // O holds P V up to t-1 now
+      } else {
+        float tot = r0 + r1;
+        const bool bad = !(tot <= 0x1p64f);            // p above 2^64 somewhere, inf or nan
+        if (__builtin_amdgcn_ballot_w64(bad) != 0) {   // rare: the row's max, raised running max, exps again
+          // the first pass's P stays defined before the branch (else its packing sinks out of the MFMA block)
+#pragma unroll
+          for (int kk = 0; kk < C::KH / 16; ++kk) asm volatile("" : "+v"(p_cur[kk]));
+          float mx = row_max(s_cur), m0, m1;
+          halves(mx, m0, m1);
+          mx = fmaxf(m0, m1) * sc;
+          const float mnew = bad ? fmaxf(m_run, mx) : m_run;
+          al = (!bad || m_run == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(m_run - mnew);
+          m_run = mnew;
+          rs = exp_part(s_cur, p_cur, m_run == -INFINITY ? 0.f : m_run);
+          halves(rs, r0, r1);
+          tot = r0 + r1;
+          scale_o(al);                                 // O holds P V up to t-1 now
+        }
+        l_run = l_run * al + tot;
+      }
     }
     if constexpr (decltype(hasS)::value) mask_only(kb1, s_next, u1);
     kb0 = kb1;
