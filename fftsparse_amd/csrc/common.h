@@ -57,6 +57,10 @@ __device__ __forceinline__ uint32_t order_key(float f) {
 // ---- wave helpers (wave64) --------------------------------------------------
 __device__ __forceinline__ int lane_id() { return (int)__lane_id(); }
 
+// Number of lanes of the wave for which p holds (wave-uniform: a ballot and a
+// scalar popcount, no cross-lane data movement).  Call in uniform control flow.
+__device__ __forceinline__ int wave_count(bool p) { return (int)__popcll(__ballot(p)); }
+
 __device__ __forceinline__ float wave_sum(float v) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;

@@ -3,19 +3,22 @@
 // row, :588-612 stripe/diffuse dynamic mask, :256-294 qk top-k, :623-641
 // columns; attn_src/fix_mask_attn/my_attn.py:39-79 for the fixed mask).
 //
-// One workgroup (4 waves) owns RPW consecutive query-block rows of one head.
-// Stripe heads (and the fixed mask) and diffuse heads are served by two
-// launches of the kernel, so only the diffuse launch reserves LDS for the
-// score panel.  N <= 8192.  Stripe / fixed rows (Nk <= 4096) are built word-parallel: a
-// lane forms the 64-bit membership mask of 64 key blocks (range masks for
-// the prior, columns and causal limit; a funnel-shifted window of the
-// bit-reversed lag mask for the lag diagonals) and stores it as word w of
-// the row.  A diffuse head first computes its score panel S[rows][0..last row] into LDS
-// (fp32 dot products, fixed order).  Each wave then walks one row at a time:
-// for a diffuse row it finds the k_i-th largest score by a 32-step bisection
-// on the ordered float key with wave-wide counts, and in a single ascending
-// pass over the key blocks it evaluates the membership rule 64 blocks at a
-// time, the ballot of each pass being the row's next word.
+// One launch serves every head.  One workgroup (4 waves) owns RPW consecutive
+// query-block rows of one head and decides from diag_var whether the head is
+// a stripe or a diffuse head.  N <= 8192.  Stripe / fixed rows (Nk <= 4096)
+// are built word-parallel: a lane forms the 64-bit membership mask of 64 key
+// blocks (range masks for the prior, columns and causal limit; a
+// funnel-shifted window of the bit-reversed lag mask for the lag diagonals)
+// and stores it as word w of the row.  A diffuse head computes its score
+// panel S[rows][0..last row] into LDS (fp32 dot products, fixed order) in
+// passes of a few rows, so the LDS the launch reserves for the panel stays
+// small enough for four workgroups per CU.  Each wave then walks one row at a
+// time: for a diffuse row it finds the k_i-th largest score by a 32-step
+// bisection on the ordered float key with wave-wide counts, and in a single
+// ascending pass over the key blocks it evaluates the membership rule 64
+// blocks at a time, the ballot of each pass being the row's next word.
+#include <algorithm>
+
 #include "common.h"
 
 namespace fs {
@@ -23,7 +26,16 @@ namespace fs {
 constexpr int kSelThreads = 256;
 constexpr int kSelWaves = kSelThreads / 64;
 constexpr int kMaxWords = 64;                       // word-parallel path: Nk <= 4096
-constexpr int kSelMaxN = 8192;                      // per-row path (a diffuse head's 4-row score panel fits LDS)
+constexpr int kSelMaxN = 8192;                      // per-row path: flag bytes + a one-row score panel fit the LDS budget
+constexpr int kMaxPanelRows = 16;                   // rows of a diffuse head's score panel per pass
+constexpr size_t kSelLdsBudget = 52 * 1024;         // flag bytes + score panel + q rows (three workgroups per CU)
+
+// LDS of the word-parallel path (the start of the launch's dynamic LDS)
+struct WordRowsLds {
+  uint64_t rkw[2 * kMaxWords + 2];                  // bit x: keep_tau[N-1-x] (x < N), 0 beyond
+  uint64_t colw[kMaxWords], lastw[kMaxWords];
+  uint32_t fk[4096 / 4], fc[4096 / 4], fl[4096 / 4];   // the staged flag bytes
+};
 
 // bits of word w (blocks 64w .. 64w+63) that lie in [lo, hi)
 __device__ __forceinline__ uint64_t range_bits(int w, int lo, int hi) {
@@ -33,15 +45,14 @@ __device__ __forceinline__ uint64_t range_bits(int w, int lo, int hi) {
   return upto & ~((1ull << b0) - 1);
 }
 
-// DIFF selects the head kind a launch serves: false = stripe heads and the
-// fixed (dyn_mode 0) mask, no score panel and no dynamic LDS; true = diffuse
-// heads, with the panel.  Each launch returns at once for heads of the other kind.
-template <typename T, bool DIFF>
-__global__ __launch_bounds__(kSelThreads) void select_kernel(fs_select_args a, int rows_per_wave,
+// panel_rows: rows of a diffuse head's score panel per pass (0 without the
+// dynamic mask).  Dynamic LDS: WordRowsLds (word-parallel rows) or, for the
+// per-row path, the head's flag bytes [N], then the panel [panel_rows][N] and
+// the pass's q rows [panel_rows][D].
+template <typename T>
+__global__ __launch_bounds__(kSelThreads) void select_kernel(fs_select_args a, int rows_per_wave, int panel_rows,
                                                              float inv_sqrt_d) {
-  extern __shared__ float panel[];       // [RPW][N] scores (diffuse heads) then [RPW][D] q rows
-  // per-head flag bytes (per-row path)
-  __shared__ __attribute__((aligned(16))) uint8_t flags[kSelMaxN];
+  extern __shared__ __attribute__((aligned(16))) unsigned char sel_lds[];
   const int RPW = rows_per_wave * kSelWaves;
   const int N = a.N, Nk = a.Nk, D = a.D;
   const int chunks = (N + RPW - 1) / RPW;
@@ -50,7 +61,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(fs_select_args a, i
   const int hk = h / (a.Hq / a.Hk);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int NW = (Nk + 63) >> 6;                   // 64-block words per row
-  const bool words = !DIFF && NW <= kMaxWords;     // word-parallel rows (below)
+  const bool word_rows = NW <= kMaxWords;          // stripe / fixed rows are built word-parallel (below)
 
   // The word-parallel path stages the head's lag / column / last-row flags.
   // Their loads are issued here, before the decision's, so that one wait
@@ -58,7 +69,7 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(fs_select_args a, i
   constexpr int kFlagWords = 4096 / 4 / kSelThreads;
   uint32_t fkr[kFlagWords], fcr[kFlagWords], flr[kFlagWords];
   const int nw4 = (N + 3) >> 2;
-  if (words) {
+  if (word_rows) {                                 // (loaded for a diffuse head too: the decision comes later)
     const int64_t hb = (int64_t)h * N;
     const bool v4 = (N & 3) == 0;                  // row starts 4-byte aligned (buffers are)
 #pragma unroll
@@ -95,45 +106,16 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(fs_select_args a, i
       mv = s / (float)a.n_samples;
       stripe = mv <= a.stripe_threshold;        // false for nan
     }
-    if (!DIFF && r0 == 0 && tid == 0) {
+    if (r0 == 0 && tid == 0) {
       if (a.mean_var) a.mean_var[h] = mv;
       if (a.is_stripe) a.is_stripe[h] = stripe ? 1 : 0;
     }
   }
   const bool diffuse = a.dyn_mode == 1 && !stripe;
-  if (diffuse != DIFF) return;                     // the other launch serves this head
+  const bool words = word_rows && !diffuse;
   const bool use_lags = a.dyn_mode == 1 && stripe;
   const bool use_cols = a.col_mode == 2 || (a.col_mode == 1 && stripe);
   const int rend = min(N, r0 + RPW);
-
-  if (DIFF) {
-    // ---- score panel S[i][j] = (q_b[i] . k_b[j]) * (1/sqrt(D)), j <= i (:234-249)
-    const T* qb = static_cast<const T*>(a.q_b) + (int64_t)h * N * D;
-    const T* kb = static_cast<const T*>(a.k_b) + (int64_t)hk * N * D;
-    float* qrows = panel + (size_t)RPW * N;
-    for (int e = tid; e < RPW * D; e += kSelThreads) {
-      const int rr = e / D, d = e - rr * D;
-      qrows[e] = (r0 + rr < N) ? to_f32(qb[(int64_t)(r0 + rr) * D + d]) : 0.f;
-    }
-    __syncthreads();
-    const int jmax = rend;                                   // columns 0 .. rend-1
-    for (int j = tid; j < jmax; j += kSelThreads) {
-      float acc[16];
-#pragma unroll
-      for (int rr = 0; rr < 16; ++rr) acc[rr] = 0.f;
-      const T* kr = kb + (int64_t)j * D;
-      for (int d = 0; d < D; ++d) {
-        const float kv = to_f32(kr[d]);
-#pragma unroll
-        for (int rr = 0; rr < 16; ++rr)
-          if (rr < RPW) acc[rr] += qrows[rr * D + d] * kv;
-      }
-#pragma unroll
-      for (int rr = 0; rr < 16; ++rr)
-        if (rr < RPW) panel[(size_t)rr * N + j] = acc[rr] * inv_sqrt_d;
-    }
-    __syncthreads();
-  }
 
   const int lw = a.local_window;
   const bool has_last = a.last_sel != nullptr;
@@ -142,9 +124,13 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(fs_select_args a, i
     // blocks 64w .. 64w+63 of its row as a 64-bit mask from per-head masks
     // staged in LDS and stores it as word w of the row; the row's count is
     // the sum of its words' popcounts.
-    __shared__ uint64_t rkw[2 * kMaxWords + 2];  // bit x: keep_tau[N-1-x] (x < N), 0 beyond
-    __shared__ uint64_t colw[kMaxWords], lastw[kMaxWords];
-    __shared__ uint32_t fk[4096 / 4], fc[4096 / 4], fl[4096 / 4];   // the staged flag bytes
+    WordRowsLds& wl = *reinterpret_cast<WordRowsLds*>(sel_lds);
+    uint64_t* rkw = wl.rkw;
+    uint64_t* colw = wl.colw;
+    uint64_t* lastw = wl.lastw;
+    uint32_t* fk = wl.fk;
+    uint32_t* fc = wl.fc;
+    uint32_t* fl = wl.fl;
 #pragma unroll
     for (int u = 0; u < kFlagWords; ++u) {
       const int w4 = tid + u * kSelThreads;
@@ -208,6 +194,9 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(fs_select_args a, i
     return;
   }
   // ---- per-head lag / column / last-row flags, staged in LDS (bit 0 lag, 1 column, 2 last row)
+  uint8_t* flags = sel_lds;
+  float* panel = reinterpret_cast<float*>(sel_lds + ((N + 15) & ~15));   // [panel_rows][N]
+  float* qrows = panel + (size_t)panel_rows * N;                           // [panel_rows][D]
   for (int j = tid; j < N; j += kSelThreads) {
     uint8_t f = 0;
     if (a.keep_tau && a.keep_tau[(int64_t)h * N + j]) f |= 1;
@@ -217,81 +206,108 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(fs_select_args a, i
   }
   __syncthreads();
 
-  for (int rr = wave; rr < RPW; rr += kSelWaves) {
-    const int i = r0 + rr;
-    if (i >= N) break;
-    const int jlim = a.mask_causal ? min(i + 1, Nk) : Nk;
-    const float* srow = panel + (size_t)rr * N;
-    // ---- diffuse row: k_i-th largest of S[i][0..i] (:271-276)
-    uint32_t thr = 0;
-    int need = 0;
-    if (DIFF) {
-      int k = (int)((float)(i + 1) * a.qk_topk_ratio);
-      if (k < 1) k = 1;
-      const int n = i + 1;
-      if (k > n) k = n;
-      uint32_t prefix = 0;
-      for (int b = 31; b >= 0; --b) {
-        const uint32_t cand = prefix | (1u << b);
-        int c = 0;
-        for (int j = lane; j < n; j += 64) c += order_key(srow[j]) >= cand;
-        c = wave_sum_i(c);
-        if (c >= k) prefix = cand;
+  // rows r0 + p0 .. r0 + pend - 1 per pass: a diffuse head's panel holds
+  // panel_rows rows; other heads take all their rows in one pass
+  const int P = diffuse ? panel_rows : RPW;
+  const int nrows = min(RPW, N - r0);
+  for (int p0 = 0; p0 < nrows; p0 += P) {
+    const int pend = min(nrows, p0 + P);
+    if (diffuse) {
+      // ---- score panel S[i][j] = (q_b[i] . k_b[j]) * (1/sqrt(D)), j <= last row of the pass (:234-249)
+      const T* qb = static_cast<const T*>(a.q_b) + (int64_t)h * N * D;
+      const T* kb = static_cast<const T*>(a.k_b) + (int64_t)hk * N * D;
+      __syncthreads();                             // the previous pass is done with the panel
+      for (int e = tid; e < P * D; e += kSelThreads) {
+        const int rr = e / D, d = e - rr * D;
+        qrows[e] = (p0 + rr < pend) ? to_f32(qb[(int64_t)(r0 + p0 + rr) * D + d]) : 0.f;
       }
-      int gt = 0;
-      for (int j = lane; j < n; j += 64) gt += order_key(srow[j]) > prefix;
-      gt = wave_sum_i(gt);
-      thr = prefix;
-      need = k - gt;
-    }
-    // ---- membership in ascending block order, one word per 64 blocks
-    uint64_t* out = a.blk_bits + ((int64_t)h * N + i) * NW;
-    int cnt = 0, eq_seen = 0;
-    for (int j0 = 0; j0 < jlim; j0 += 64) {
-      const int j = j0 + lane;
-      const bool valid = j < jlim;
-      bool in = false;
-      bool eq = false;
-      if (valid) {
-        // prior (:83-95): sink | recent | local window
-        in = j < a.keep_sink || j >= Nk - a.keep_recent || (lw > 0 && abs(i - j) <= lw);
-        const uint8_t fj = j < N ? flags[j] : 0;
-        if (has_last && i == N - 1 && (fj & 4)) in = true;
-        if (use_lags) {
-          const int t = i - j;
-          if (t >= a.remote_start && j >= a.keep_sink && (flags[t] & 1)) in = true;
+      __syncthreads();
+      const int jmax = r0 + pend;                  // columns 0 .. the pass's last row
+      for (int j = tid; j < jmax; j += kSelThreads) {
+        float acc[kMaxPanelRows];
+#pragma unroll
+        for (int rr = 0; rr < kMaxPanelRows; ++rr) acc[rr] = 0.f;
+        const T* kr = kb + (int64_t)j * D;
+        for (int d = 0; d < D; ++d) {
+          const float kv = to_f32(kr[d]);
+#pragma unroll
+          for (int rr = 0; rr < kMaxPanelRows; ++rr)
+            if (rr < P) acc[rr] += qrows[rr * D + d] * kv;
         }
-        if (DIFF && j <= i) {
-          const uint32_t key = order_key(srow[j]);
-          if (key > thr) in = true;
-          eq = key == thr;
-        }
-        if (use_cols && j <= i && (fj & 2)) in = true;
+#pragma unroll
+        for (int rr = 0; rr < kMaxPanelRows; ++rr)
+          if (rr < P) panel[(size_t)rr * N + j] = acc[rr] * inv_sqrt_d;
       }
-      if (DIFF) {
-        const uint64_t me = __ballot(eq);
-        if (eq && eq_seen + rank_below(me) < need) in = true;
-        eq_seen += __popcll(me);
-      }
-      const uint64_t m = __ballot(in);
-      if (lane == 0) out[j0 >> 6] = m;
-      cnt += __popcll(m);
+      __syncthreads();
     }
-    for (int w = ((jlim + 63) >> 6) + lane; w < NW; w += 64) out[w] = 0ull;   // words past the causal limit
-    if (lane == 0) a.blk_cnt[(int64_t)h * N + i] = cnt;
+    for (int rr = p0 + wave; rr < pend; rr += kSelWaves) {
+      const int i = r0 + rr;
+      const int jlim = a.mask_causal ? min(i + 1, Nk) : Nk;
+      const float* srow = panel + (size_t)(rr - p0) * N;
+      // ---- diffuse row: k_i-th largest of S[i][0..i] (:271-276)
+      uint32_t thr = 0;
+      int need = 0;
+      if (diffuse) {
+        int k = (int)((float)(i + 1) * a.qk_topk_ratio);
+        if (k < 1) k = 1;
+        const int n = i + 1;
+        if (k > n) k = n;
+        uint32_t prefix = 0;
+        for (int b = 31; b >= 0; --b) {
+          const uint32_t cand = prefix | (1u << b);
+          int c = 0;
+          for (int j0 = 0; j0 < n; j0 += 64) c += wave_count(j0 + lane < n && order_key(srow[j0 + lane]) >= cand);
+          if (c >= k) prefix = cand;
+        }
+        int gt = 0;
+        for (int j0 = 0; j0 < n; j0 += 64) gt += wave_count(j0 + lane < n && order_key(srow[j0 + lane]) > prefix);
+        thr = prefix;
+        need = k - gt;
+      }
+      // ---- membership in ascending block order, one word per 64 blocks
+      uint64_t* out = a.blk_bits + ((int64_t)h * N + i) * NW;
+      int cnt = 0, eq_seen = 0;
+      for (int j0 = 0; j0 < jlim; j0 += 64) {
+        const int j = j0 + lane;
+        const bool valid = j < jlim;
+        bool in = false;
+        bool eq = false;
+        if (valid) {
+          // prior (:83-95): sink | recent | local window
+          in = j < a.keep_sink || j >= Nk - a.keep_recent || (lw > 0 && abs(i - j) <= lw);
+          const uint8_t fj = j < N ? flags[j] : 0;
+          if (has_last && i == N - 1 && (fj & 4)) in = true;
+          if (use_lags) {
+            const int t = i - j;
+            if (t >= a.remote_start && j >= a.keep_sink && (flags[t] & 1)) in = true;
+          }
+          if (diffuse && j <= i) {
+            const uint32_t key = order_key(srow[j]);
+            if (key > thr) in = true;
+            eq = key == thr;
+          }
+          if (use_cols && j <= i && (fj & 2)) in = true;
+        }
+        if (diffuse) {
+          const uint64_t me = __ballot(eq);
+          if (eq && eq_seen + rank_below(me) < need) in = true;
+          eq_seen += __popcll(me);
+        }
+        const uint64_t m = __ballot(in);
+        if (lane == 0) out[j0 >> 6] = m;
+        cnt += __popcll(m);
+      }
+      for (int w = ((jlim + 63) >> 6) + lane; w < NW; w += 64) out[w] = 0ull;   // words past the causal limit
+      if (lane == 0) a.blk_cnt[(int64_t)h * N + i] = cnt;
+    }
   }
 }
 
 template <typename T>
-static int launch_select(const fs_select_args& a, unsigned grid, size_t smem, int rows_per_wave,
+static int launch_select(const fs_select_args& a, unsigned grid, size_t smem, int rows_per_wave, int panel_rows,
                          float inv_sqrt_d, hipStream_t s) {
-  // stripe heads and the fixed mask: no panel
-  select_kernel<T, false><<<grid, kSelThreads, 0, s>>>(a, rows_per_wave, inv_sqrt_d);
-  if (a.dyn_mode == 1) {
-    // diffuse heads (possible only with the dynamic mask)
-    if (int rc = fs_host::allow_dynamic_lds(select_kernel<T, true>, smem, "fs_select")) return rc;
-    select_kernel<T, true><<<grid, kSelThreads, smem, s>>>(a, rows_per_wave, inv_sqrt_d);
-  }
+  if (int rc = fs_host::allow_dynamic_lds(select_kernel<T>, smem, "fs_select")) return rc;
+  select_kernel<T><<<grid, kSelThreads, smem, s>>>(a, rows_per_wave, panel_rows, inv_sqrt_d);
   return 0;
 }
 
@@ -316,19 +332,33 @@ extern "C" int fs_select(const fs_select_args* a, void* stream) {
                "fs_select: dynamic, column and last-row masks need N == Nk");
   FS_CHECK_SUPPORTED(a->N <= kSelMaxN && (a->dyn_mode == 0 || a->D <= 256), "fs_select: N=%d > %d or D=%d > 256",
                      a->N, kSelMaxN, a->D);
-  const int rows_per_wave = a->N <= 1024 ? 4 : (a->N <= 2048 ? 2 : 1);
+  // rows per wave: 16 word-parallel rows of <= 1024 blocks (four rows per
+  // pass of 16 lanes each), fewer for longer rows; one on the per-row path
+  const int NW = (a->Nk + 63) / 64;
+  const int rows_per_wave = NW <= 16 ? 16 : (NW <= 32 ? 8 : (NW <= kMaxWords ? 4 : 1));
   const int RPW = rows_per_wave * kSelWaves;
   const int chunks = (a->N + RPW - 1) / RPW;
   const float inv_sqrt_d = a->D > 0 ? 1.0f / (float)sqrt((double)a->D) : 1.0f;
-  const size_t smem = a->dyn_mode == 1 ? (size_t)RPW * (a->N + a->D) * sizeof(float) : 0;
+  // dynamic LDS: the word-parallel path's, or flag bytes + a diffuse head's
+  // panel of panel_rows rows (a multiple of 4 rows when 4 fit) + its q rows
+  const size_t flag_bytes = ((size_t)a->N + 15) & ~(size_t)15;
+  int panel_rows = 0;
+  if (a->dyn_mode == 1) {
+    const size_t per_row = (size_t)(a->N + a->D) * sizeof(float);
+    panel_rows = (int)std::min<size_t>((kSelLdsBudget - flag_bytes) / per_row, (size_t)std::min(RPW, kMaxPanelRows));
+    if (panel_rows >= 4) panel_rows &= ~3;
+    panel_rows = std::max(panel_rows, 1);
+  }
+  size_t smem = flag_bytes + (size_t)panel_rows * (a->N + a->D) * sizeof(float);
+  if (NW <= kMaxWords) smem = std::max(smem, sizeof(WordRowsLds));
   hipStream_t s = (hipStream_t)stream;
   const unsigned grid = (unsigned)(a->Hq * chunks);
   const int dt = a->dyn_mode == 1 ? a->dtype : FS_DTYPE_F32;
   int rc = 0;
   switch (dt) {
-    case FS_DTYPE_F32: rc = launch_select<float>(*a, grid, smem, rows_per_wave, inv_sqrt_d, s); break;
-    case FS_DTYPE_BF16: rc = launch_select<bf16_t>(*a, grid, smem, rows_per_wave, inv_sqrt_d, s); break;
-    case FS_DTYPE_F16: rc = launch_select<f16_t>(*a, grid, smem, rows_per_wave, inv_sqrt_d, s); break;
+    case FS_DTYPE_F32: rc = launch_select<float>(*a, grid, smem, rows_per_wave, panel_rows, inv_sqrt_d, s); break;
+    case FS_DTYPE_BF16: rc = launch_select<bf16_t>(*a, grid, smem, rows_per_wave, panel_rows, inv_sqrt_d, s); break;
+    case FS_DTYPE_F16: rc = launch_select<f16_t>(*a, grid, smem, rows_per_wave, panel_rows, inv_sqrt_d, s); break;
     default: fs_host::set_error("fs_select: dtype %d unsupported", a->dtype); return FS_ERR_UNSUPPORTED;
   }
   if (rc) return rc;
