@@ -84,6 +84,16 @@ __device__ __forceinline__ f32x2_t rope_pair(f32x2_t x, f32x2_t rot, f32x2_t c, 
   return Round2<T>::go(f32x2_t{a[0] + b[0], a[1] + b[1]}, bits);
 }
 
+// Block means are stored non-temporally: interleaved with the read stream,
+// plain write-back stores of the 256-byte results cost the pass 9% of its
+// time (209 against 191 us for 1.34 GB with the stores dropped); streaming
+// stores bring that to 203 us.
+__device__ __forceinline__ void store_mean(float* p, float v) { __builtin_nontemporal_store(v, p); }
+template <typename T>
+__device__ __forceinline__ void store_mean(T* p, float v) {
+  __builtin_nontemporal_store(Conv<T>::store(v).u, reinterpret_cast<uint16_t*>(p));
+}
+
 template <typename T, bool ROPE>
 __global__ __launch_bounds__(kPoolThreads) void pool_kernel(PoolK a, int N) {
   constexpr int VEC = 16 / sizeof(T);
@@ -217,7 +227,7 @@ __global__ __launch_bounds__(kPoolThreads) void pool_kernel(PoolK a, int N) {
   for (int d = tid; d < D; d += kPoolThreads) {
     float s = 0.f;
     for (int r = 0; r < rpp; ++r) s += red[r * D + d];
-    dst[d] = Conv<T>::store(s * inv);
+    store_mean(&dst[d], s * inv);
   }
 }
 

@@ -12,7 +12,8 @@
 //
 // scores_kernel: one workgroup (4 waves) per (head, 128 x 128 tile I >= J of
 // the lower triangle).  Wave w computes rows 32w .. 32w+31 of the tile with
-// v_mfma_f32_32x32x16 (K tile staged in LDS), the tile is written to LDS in
+// v_mfma_f32_32x32x16 (K tile copied to LDS with global_load_lds_dwordx4, no
+// register staging, so four workgroups fit a CU), the tile is written to LDS in
 // two halves of 64 columns, and fixed-order per-tile partials
 // are written to the work buffer: the 255 diagonal sums, the 128 column sums
 // over rows i >= j, i <= N-2, the elements of every sampled diagonal that
@@ -213,6 +214,7 @@ __global__ __launch_bounds__(kScoreThreads) void scores_kernel(fs_scores_args a,
     pcol[tb * kScoreTile + tid] = (j0 + tid < N) ? ((csum[0][tid] + csum[1][tid]) + csum[2][tid]) + csum[3][tid] : 0.f;
 }
 
+
 __global__ __launch_bounds__(kFinalThreads) void scores_final_kernel(fs_scores_args a, int ntiles, float inv_sqrt_d,
                                                                      const float* __restrict__ pdiag,
                                                                      const float* __restrict__ pcol,
@@ -275,26 +277,57 @@ __global__ __launch_bounds__(kFinalThreads) void scores_final_kernel(fs_scores_a
     }
   }
 
-  // ---- diagonal statistics, one wave per sample, jobs 4 .. 4+kDiagJobs-1 (:342-349)
+  // ---- diagonal statistics, one wave per sample, jobs 4 .. 4+kDiagJobs-1 (:342-349):
+  // var(diff(d)) / max(mean|d|, 1e-6) over d = S[j + tau][j] / sqrt(D), j < N - tau - 1.
+  // Diagonals of up to 1024 elements are read into registers in one round of
+  // loads; the sums run over j = lane, lane + 64, .. in order either way.
   for (int s = (job - 4) * (kFinalThreads / 64) + wave; job >= 4 && s < a.n_samples;
        s += kDiagJobs * (kFinalThreads / 64)) {
     const int tau = a.sample_taus[s];
     const int nd = (tau >= 0 && tau < N) ? N - tau - 1 : 0;
     const float* dv = dvs + ((int64_t)h * a.n_samples + s) * N;
-    float sabs = 0.f, se = 0.f;
-#pragma unroll 4
-    for (int j = lane; j < nd; j += 64) {
-      sabs += fabsf(dv[j]);
-      if (j + 1 < nd) se += dv[j + 1] - dv[j];
-    }
-    const float mean_abs = wave_sum(sabs) / (float)nd;
     const int ne = nd - 1;
-    const float mean_e = wave_sum(se) / (float)ne;
-    float sq = 0.f;
+    float sabs = 0.f, se = 0.f, sq = 0.f, mean_abs, mean_e;
+    constexpr int kReg = 16;
+    if (nd <= 64 * kReg) {
+      float x[kReg], y[kReg];
+#pragma unroll
+      for (int k = 0; k < kReg; ++k) {             // every load issued (indices clamped), then the sums
+        const int j = lane + 64 * k;
+        x[k] = dv[max(min(j, nd - 1), 0)];
+        y[k] = dv[max(min(j + 1, nd - 1), 0)];
+      }
+#pragma unroll
+      for (int k = 0; k < kReg; ++k) {
+        const int j = lane + 64 * k;
+        if (j < nd) {
+          sabs += fabsf(x[k]);
+          if (j + 1 < nd) se += y[k] - x[k];
+        }
+      }
+      mean_abs = wave_sum(sabs) / (float)nd;
+      mean_e = wave_sum(se) / (float)ne;
+#pragma unroll
+      for (int k = 0; k < kReg; ++k) {
+        const int j = lane + 64 * k;
+        if (j < ne) {
+          const float e = (y[k] - x[k]) - mean_e;
+          sq += e * e;
+        }
+      }
+    } else {
 #pragma unroll 4
-    for (int j = lane; j < ne; j += 64) {
-      const float e = (dv[j + 1] - dv[j]) - mean_e;
-      sq += e * e;
+      for (int j = lane; j < nd; j += 64) {
+        sabs += fabsf(dv[j]);
+        if (j + 1 < nd) se += dv[j + 1] - dv[j];
+      }
+      mean_abs = wave_sum(sabs) / (float)nd;
+      mean_e = wave_sum(se) / (float)ne;
+#pragma unroll 4
+      for (int j = lane; j < ne; j += 64) {
+        const float e = (dv[j + 1] - dv[j]) - mean_e;
+        sq += e * e;
+      }
     }
     const float var = wave_sum(sq) / (float)(ne - 1);
     if (lane == 0) a.diag_var[(int64_t)h * a.n_samples + s] = var / clamp_min_nan(mean_abs, 1e-6f);
