@@ -72,6 +72,10 @@ def parse():
     ap.add_argument("--gemm-ceiling", action="store_true",
                     help="only time a bf16 8192^3 torch.matmul (hipBLASLt) 3 + 60 times, the practical MFMA ceiling "
                          "the attention kernel is compared with in the profiles, then exit")
+    ap.add_argument("--traffic-rows", nargs=4, default=None,
+                    metavar=("FETCH_CSV", "WRITE_CSV", "CAL_FETCH_CSV", "CAL_WRITE_CSV"),
+                    help="only print the profiles/traffic.txt rows of --config from rocprofv3 --pmc FETCH_SIZE / "
+                         "WRITE_SIZE collections of this bench and of --copy-calib 1024, then exit (no GPU)")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (5 times) to calibrate "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE, then exit")
@@ -197,19 +201,80 @@ def cpu_baseline_xattn(q, k, v, args, bs, nnz_total, sel):
     }, parity
 
 
+# The sources each traffic row depends on (fftsparse_amd/csrc, plus the C-ABI header).
+TRAFFIC_SOURCES = {"bsattn": ("attn.hip", "common.h"),
+                   "select": ("pool.hip", "scores.hip", "select.hip", "common.h")}
+# rocprofv3 kernel names summed into each row
+TRAFFIC_KERNELS = {"bsattn": ("bsattn_kernel",),
+                   "select": ("pool_kernel", "scores_kernel", "scores_final_kernel", "select_kernel")}
+
+
+def src_hash(kernel):
+    """First 16 hex digits of the sha256 of the sources a traffic row was
+    measured with (TRAFFIC_SOURCES, then include/fftsparse_amd.h)."""
+    import hashlib
+    h = hashlib.sha256()
+    paths = [os.path.join(ROOT, "fftsparse_amd", "csrc", n) for n in TRAFFIC_SOURCES[kernel]]
+    for path in paths + [os.path.join(ROOT, "include", "fftsparse_amd.h")]:
+        with open(path, "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
 def pmc_traffic(kernel, config):
     """HBM bytes per launch of a kernel from the committed rocprofv3 --pmc
-    summary (FETCH_SIZE and WRITE_SIZE, calibrated against a plain copy), or
-    None when that kernel/config was not profiled."""
+    summary profiles/traffic.txt (FETCH_SIZE and WRITE_SIZE, calibrated
+    against a plain copy), or None when that kernel/config was not profiled
+    or was profiled with other sources than these (the row's source hash
+    differs from src_hash)."""
     path = os.path.join(ROOT, "profiles", "traffic.txt")
     try:
+        cur = src_hash(kernel)
         for line in open(path):
             f = line.split()
-            if len(f) >= 4 and not line.startswith("#") and f[0] == kernel and f[1] == config:
-                return int(float(f[2]) + float(f[3]))
+            if len(f) >= 5 and not line.startswith("#") and f[0] == kernel and f[1] == config:
+                return int(float(f[2]) + float(f[3])) if f[4] == cur else None
     except OSError:
         pass
     return None
+
+
+def traffic_rows(config, fetch_csv, write_csv, cal_fetch_csv, cal_write_csv):
+    """Rows of profiles/traffic.txt from four rocprofv3 --pmc counter
+    collections (run_counter_collection.csv): FETCH_SIZE and WRITE_SIZE of
+    `bench.py --no-cpu --no-dense --steps 1 --warmup 1` on the config, and of
+    `bench.py --copy-calib 1024` (a plain 1 GiB copy, which fixes the scale of
+    each counter).  Each row is the per-launch average summed over the row's
+    kernels, scaled to bytes, with the source hash of the build measured."""
+    import csv
+
+    def load(path):
+        acc = {}
+        for row in csv.DictReader(open(path)):
+            acc.setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
+        return acc
+
+    def copy_kib(acc):
+        vals = [v for name, vs in acc.items() if "copyBuffer" in name for v in vs]
+        if not vals:
+            raise SystemExit("no copy kernel in the calibration collection")
+        return sum(vals) / len(vals)
+
+    copy_kib_true = 1024 * 1024                      # 1 GiB read and written, in KiB
+    f_scale = copy_kib_true / copy_kib(load(cal_fetch_csv)) * 1024
+    w_scale = copy_kib_true / copy_kib(load(cal_write_csv)) * 1024
+    fetch, write = load(fetch_csv), load(write_csv)
+    rows = []
+    for kernel, names in TRAFFIC_KERNELS.items():
+        fb = wb = 0.0
+        for name, vs in fetch.items():
+            if any(n in name for n in names):
+                fb += sum(vs) / len(vs) * f_scale
+        for name, vs in write.items():
+            if any(n in name for n in names):
+                wb += sum(vs) / len(vs) * w_scale
+        rows.append(f"{kernel} {config} {fb:.0f} {wb:.0f} {src_hash(kernel)}")
+    return rows
 
 
 def _cpu_model():
@@ -276,6 +341,9 @@ def main():
                                    "(one KV head and its query heads per GPU, no exchange), which is not a "
                                    "code path here", "n_gpus": args.gpus}))
         sys.exit(2)
+    if args.traffic_rows:
+        print("\n".join(traffic_rows(args.config, *args.traffic_rows)))
+        return
     import torch
     if args.gemm_ceiling:
         n = 8192

@@ -42,6 +42,7 @@
 // and the same columns, which then hit that XCD's L2).
 // The dense path gives XCD x every 8th query-block row (last rows first) of
 // every head.
+#include <atomic>
 #include <climits>
 #include <type_traits>
 
@@ -1040,16 +1041,18 @@ __global__ __launch_bounds__(64) void union_kernel(const uint64_t* __restrict__ 
 // per group, attention 2.03 -> 1.90 ms; configs 2 and 3 have 7 to 14 and
 // keep the grouped order, 2.2% and 0.8% faster with it).
 static int kv_major(const fs_attn_args& a, int Nq) {
-  static int cus[64];                              // CU count per device, read once
+  // CU count per device, read once; host threads may race to fill an entry,
+  // so it is atomic (they store the same value)
+  static std::atomic<int> cus[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 1;
-  if (cus[dev] == 0) {
-    int n = 0;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 1;
-    cus[dev] = n;
+    cus[dev].store(n, std::memory_order_relaxed);
   }
   const int64_t per_group = (int64_t)(a.Hq / a.Hk) * Nq;   // workgroups of one KV group
-  return per_group >= 4 * 2 * (int64_t)cus[dev] ? 1 : 0;
+  return per_group >= 4 * 2 * (int64_t)n ? 1 : 0;
 }
 
 static size_t vt_bytes(const fs_attn_args& a) {
