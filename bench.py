@@ -529,8 +529,8 @@ def main():
                            "frac_median": round(sel_bytes / (t_sel_med * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
                            "traffic": pmc_traffic("select", cfg.name),
                            "work": "Q and K read once (L*(Hq+Hkv)*D*2 bytes)",
-                           "timed": "select_blocks: pool, block-score tiles + statistics (2 launches), block lists "
-                                    "(2 launches)"}
+                           "timed": "select_blocks: pool, block-score tiles + statistics (2 launches), block masks "
+                                    "(1 launch)"}
     sel_desc = (f"XAttention selection (stride {args.xattn_stride}, threshold {args.threshold})" if xattn
                 else f"FlexPrefill selection and attention at {bs}-token blocks (gamma {args.flex_gamma}, tau "
                      f"{args.flex_tau}; the reference benchmark's call uses the default block size, 32)" if flex
@@ -585,7 +585,7 @@ def main():
 
 def run_selection_only(args, cfg, q, k, kw):
     """The v7 block selection alone (select_blocks: pool, lag correlation and
-    statistics, block lists) on the config's inputs in their dtype, HIP events
+    statistics, block masks) on the config's inputs in their dtype, HIP events
     on torch's current stream; one JSON line with its time and HBM roofline."""
     import torch
     from fftsparse_amd import select_blocks
