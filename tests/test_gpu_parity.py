@@ -212,6 +212,8 @@ def test_selection_parity_c0(name, over):
     (24000, 7, 1, 64, torch.bfloat16, dict(correlation_selection_mode="topk", correlation_topk_ratio=0.3)),
     (300000, 4, 1, 64, torch.bfloat16, {}),                      # N = 4688 > 4096 blocks
     (300000, 2, 1, 64, torch.bfloat16, dict(stripe_threshold=0.0)),   # diffuse heads' score panel at N = 4688
+    (131072, 2, 1, 16, torch.bfloat16, {}),                      # N = 8192, the selection kernels' maximum
+    (131072, 1, 1, 16, torch.bfloat16, dict(stripe_threshold=0.0)),   # a diffuse head's panel at N = 8192
 ])
 def test_selection_parity_bf16(L, Hq, Hk, bs, dtype, over):
     _print_case("selection", L=L, Hq=Hq, Hk=Hk, bs=bs, dtype=dtype, over=over)
