@@ -476,8 +476,9 @@ def test_full_length_c2_properties():
 def test_maximum_block_count_properties():
     """The largest supported selection, N = 8192 blocks (L = 1048576 at block
     128): rows causal, with the sink block and the diagonal, counts equal to
-    the rows' popcounts; selection deterministic; attention output finite.
-    The mask takes N * N / 8 bytes per head (8 MiB)."""
+    the rows' popcounts; selection deterministic; attention output finite,
+    and on sampled query blocks within the bars of fp32 attention under the
+    same lists.  The mask takes N * N / 8 bytes per head (8 MiB)."""
     _print_case("max-blocks", L=8192 * 128, Hq=2, Hk=1)
     g = torch.Generator(device=DEV).manual_seed(12)
     L, Hq, Hk = 8192 * 128, 2, 1
@@ -496,11 +497,17 @@ def test_maximum_block_count_properties():
     assert torch.equal(sel.blk_bits, sel2.blk_bits)
     m = sel.dense_mask().cpu()
     assert torch.equal(m.sum(-1, dtype=torch.int32), cnt)
-    check_mask_rows(m, (0, 1, 4095, 4096, 8190, 8191))
-    del m
+    rows = (0, 1, 4095, 4096, 8190, 8191)
+    check_mask_rows(m, rows)
     out = block_sparse_attention(q, k, v, sel.blk_cnt, sel.blk_bits)
     torch.cuda.synchronize()
     assert bool(torch.isfinite(out.float()).all())
+    # sampled query blocks against fp32 attention under the same lists
+    want = v7.block_sparse_attention(q.cpu(), k.cpu(), v.cpu(), m, 128, qblocks=rows)
+    t = torch.cat([torch.arange(i * 128, (i + 1) * 128) for i in rows])
+    err = (out[0].float().cpu()[t] - want[t]).abs()                  # [L, Hq, D] rows
+    print(f"  attention max_abs={err.max().item():.3e} mean_abs={err.mean().item():.3e}", flush=True)
+    assert err.max().item() <= 2e-2 and err.mean().item() <= 1e-3
 
 
 def test_block_count_above_the_limit_is_rejected():
