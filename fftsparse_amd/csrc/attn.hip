@@ -112,20 +112,22 @@ __device__ __forceinline__ int vt_pos(int k) {
 }
 
 // ---- V -> V^T pre-pass: one workgroup per (b, hk, 64-key slab) -------------
-// lb = 0: rows of Lp keys; lb = 16 or 32: blocks of lb keys, [Lp / lb][kD][lb].
+// lb = 0: rows of Lp keys; lb = 16 or 32: blocks of lb keys, [Lp / lb][D][lb].
+template <int D>
 __global__ __launch_bounds__(256) void vt_kernel(const uint16_t* __restrict__ v, int64_t v_sb, int64_t v_sh,
                                                  int64_t v_sl, uint16_t* __restrict__ vt, int Hk, int Lk,
                                                  int Lp, int lb) {
-  __shared__ uint16_t tile[64][kD + 2];
+  constexpr int CPR = D / 8;                     // 16-byte chunks per key row
+  __shared__ uint16_t tile[64][D + 2];
   const int slabs = Lp / 64;
   const int bh = blockIdx.x / slabs, slab = blockIdx.x - bh * slabs;
   const int b = bh / Hk, hk = bh - b * Hk;
   const uint16_t* src = v + b * v_sb + hk * v_sh;
-  uint16_t* dst = vt + (int64_t)bh * kD * Lp;
+  uint16_t* dst = vt + (int64_t)bh * D * Lp;
   const int k0 = slab * 64;
   const int tid = threadIdx.x;
-  for (int c = tid; c < 64 * 16; c += 256) {
-    const int r = c >> 4, cc = (c & 15) * 8;
+  for (int c = tid; c < 64 * CPR; c += 256) {
+    const int r = c / CPR, cc = (c % CPR) * 8;
     uint4 val = make_uint4(0, 0, 0, 0);
     if (k0 + r < Lk) val = *reinterpret_cast<const uint4*>(src + (int64_t)(k0 + r) * v_sl + cc);
     const uint32_t w[4] = {val.x, val.y, val.z, val.w};
@@ -136,8 +138,8 @@ __global__ __launch_bounds__(256) void vt_kernel(const uint16_t* __restrict__ v,
     }
   }
   __syncthreads();
-  // write 128 rows (d) x 64 keys: each thread emits 8 keys (16 bytes)
-  for (int c = tid; c < kD * 8; c += 256) {
+  // write D rows (d) x 64 keys: each thread emits 8 keys (16 bytes)
+  for (int c = tid; c < D * 8; c += 256) {
     const int d = c >> 3, p0 = (c & 7) * 8;     // 8 stored positions p0 .. p0+7
     uint32_t w[4];
 #pragma unroll
@@ -146,7 +148,7 @@ __global__ __launch_bounds__(256) void vt_kernel(const uint16_t* __restrict__ v,
       w[e] = (uint32_t)tile[ka][d] | ((uint32_t)tile[kb][d] << 16);
     }
     const int k = k0 + p0;                       // 8 keys of one block (lb is a multiple of 8)
-    const int64_t o = lb ? ((int64_t)(k / lb) * kD + d) * lb + k % lb : (int64_t)d * Lp + k;
+    const int64_t o = lb ? ((int64_t)(k / lb) * D + d) * lb + k % lb : (int64_t)d * Lp + k;
     *reinterpret_cast<uint4*>(dst + o) = make_uint4(w[0], w[1], w[2], w[3]);
   }
 }
@@ -154,7 +156,7 @@ __global__ __launch_bounds__(256) void vt_kernel(const uint16_t* __restrict__ v,
 // ---- main kernel -------------------------------------------------------------
 // BS: query / key block size of the block lists; TK: keys per LDS tile
 // (BS, or BS / 2 for two tiles per key block).
-template <int BS, int TK>
+template <int BS, int TK, int D = kD>
 struct AttnCfg {
   static constexpr int QW = BS / 32;          // query waves (32 queries each)
   // key groups: waves sharing the keys of a tile (2 or 1)
@@ -164,7 +166,7 @@ struct AttnCfg {
   static constexpr int KH = TK / KG;          // keys per wave per tile
   static constexpr int KT = KH / 32;          // 32-key sub-tiles per wave
   static constexpr int TPB = BS >= TK ? BS / TK : 1;   // tiles per key block
-  static constexpr int TILE = TK * kD;        // elements of one K (or V^T) tile
+  static constexpr int TILE = TK * D;         // elements of one K (or V^T) tile
   static constexpr int REGIONS = TILE * 2 / 1024;   // 1 KiB DMA regions per tile
   static constexpr int DMA_PER_WAVE = 2 * REGIONS / NW;
   static_assert(KG == 1 || KG == 2, "tile is a block or half a block");
@@ -173,8 +175,6 @@ struct AttnCfg {
 // V^T row length: the key blocks, zero padded to whole 64-key slabs
 __host__ __device__ inline int vt_len(int Nk, int bs) { return (Nk * bs + 63) / 64 * 64; }
 
-// element offset of 16-byte chunk c of 256-byte row r, swizzled
-__device__ __forceinline__ int swz(int r, int c) { return r * kD + ((c ^ (r & 15)) << 3); }
 
 // One 1 KiB global -> LDS copy per wave: lane l's 16 bytes land at lds_base + 16 l.
 __device__ __forceinline__ void dma16(uint32_t lds_base, const void* gptr) {
@@ -224,10 +224,14 @@ __device__ __forceinline__ uint4 lds16(const char* base, uint32_t off) {
 // block its row did not select are masked.  A tile of TK keys holds TK / LB
 // union entries, so every K / V^T tile copy serves 128 queries and every wave
 // does 32 x TK per barrier, as with 128-token blocks.
-template <int BS, int TK, typename T, int LB = BS>
-__global__ __launch_bounds__((AttnCfg<BS, TK>::NT)) __attribute__((amdgpu_waves_per_eu(2, 2)))
+template <int BS, int TK, typename T, int LB = BS, int D = kD>
+__global__ __launch_bounds__((AttnCfg<BS, TK, D>::NT)) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void bsattn_kernel(AttnKArgs a) {
-  using C = AttnCfg<BS, TK>;
+  using C = AttnCfg<BS, TK, D>;
+  static_assert(D == 64 || D == 128, "head dim 64 or 128");
+  // K tiles: rows of D * 2 bytes, CPR 16-byte chunks each, chunk c of row r
+  // stored at c ^ (r & SWM); a 1 KiB copy region holds RPR rows
+  constexpr int ROWB = D * 2, CPR = D / 8, SWM = CPR - 1, RPR = 1024 / ROWB, LCPR = D == 128 ? 4 : 3;
   constexpr bool UNION = LB < BS;
   constexpr int EPT = UNION ? TK / LB : 1;         // union entries per tile
   static_assert(!UNION || (BS == 128 && TK == 64 && (LB == 16 || LB == 32)), "union mode: 16- or 32-token lists");
@@ -312,16 +316,16 @@ void bsattn_kernel(AttnKArgs a) {
   const int kbase = kh * C::KH;
   const uint16_t* qp = a.q + b * a.q_sb + h * a.q_sh;
   const uint16_t* kp = a.k + b * a.k_sb + hk * a.k_sh;
-  const uint16_t* vtp = a.vt + (int64_t)(b * a.Hk + hk) * kD * a.Lp;
+  const uint16_t* vtp = a.vt + (int64_t)(b * a.Hk + hk) * D * a.Lp;
   const int q0 = qb * BS;
   const int off = a.Lk - a.Lq;
   const int qw0 = q0 + qq * 32;                 // first query of this wave
   const int qrow = qw0 + l32;                   // this lane's query
 
   // Q^T fragments (B operand of S^T = K Q^T): dims st*16 + hi*8 .. +7
-  V8 qf[kD / 16];
+  V8 qf[D / 16];
 #pragma unroll
-  for (int st = 0; st < kD / 16; ++st) {
+  for (int st = 0; st < D / 16; ++st) {
     uint4 raw = make_uint4(0, 0, 0, 0);
     if (qrow < a.Lq) raw = *reinterpret_cast<const uint4*>(qp + (int64_t)qrow * a.q_sl + st * 16 + hi * 8);
     qf[st] = __builtin_bit_cast(V8, raw);
@@ -409,16 +413,21 @@ void bsattn_kernel(AttnKArgs a) {
   uint32_t koff[NR], voff[NR];
 #pragma unroll
   for (int i = 0; i < NR; ++i) {
-    const int R = wave * NR + i;                   // region: LDS rows 4R .. 4R+3
-    const int r = 4 * R + (lane >> 4);
+    const int R = wave * NR + i;                   // region R of the K tile and of the V^T tile
+    const int r = 4 * R + (lane >> 4);             // V^T: 256-byte LDS rows 4R .. 4R+3
     const int c = (lane & 15) ^ (r & 15);
+    int rk = r, ck = c;                            // K: rows RPR R .. RPR R + RPR - 1
+    if constexpr (D != 128) {
+      rk = RPR * R + (lane >> LCPR);
+      ck = (lane & SWM) ^ (rk & SWM);
+    }
     if constexpr (UNION) {
       // K rows relative to this wave's 16 rows of the tile; V^T: the key
       // offset of the lane's 8 keys inside their union entry
-      koff[i] = (uint32_t)((r - wave * 4 * NR) * a.k_sl + c * 8) * 2u;
+      koff[i] = (uint32_t)((rk - wave * RPR * NR) * a.k_sl + ck * 8) * 2u;
       voff[i] = (uint32_t)((2 * r + (c >> 3)) * LB + (((c & 7) * 8) % LB)) * 2u;   // V^T stored block by block
     } else {
-      koff[i] = (uint32_t)(r * a.k_sl + c * 8) * 2u;
+      koff[i] = (uint32_t)(rk * a.k_sl + ck * 8) * 2u;
       voff[i] = (TK == 128 ? (uint32_t)(r * a.Lp + c * 8)                          // d = r
                            : (uint32_t)((2 * r + (c >> 3)) * a.Lp + (c & 7) * 8))  // two d rows per LDS row
                 * 2u;
@@ -443,7 +452,7 @@ void bsattn_kernel(AttnKArgs a) {
       // this wave's 16 rows of the tile from key0
       const int kc = min(max(key0, 0), a.Lk - 1);
       const uint16_t* base = kp + (int64_t)kc * a.k_sl;
-      if (key0 >= 0 && key0 + 4 * NR <= a.Lk) {
+      if (key0 >= 0 && key0 + RPR * NR <= a.Lk) {
 #pragma unroll
         for (int i = 0; i < NR; ++i) dma16s(lk + i * 1024, base, koff[i]);
       } else {
@@ -452,8 +461,8 @@ void bsattn_kernel(AttnKArgs a) {
         asm volatile("" : "+v"(ln));
 #pragma unroll
         for (int i = 0; i < NR; ++i) {
-          const int rr = 4 * i + (ln >> 4);          // row within this wave's block
-          const int c = (ln & 15) ^ ((4 * (wave * NR + i) + (ln >> 4)) & 15);
+          const int rr = RPR * i + (ln >> LCPR);     // row within this wave's block
+          const int c = (ln & SWM) ^ ((RPR * (wave * NR + i) + (ln >> LCPR)) & SWM);
           dma16s(lk + i * 1024, base, (uint32_t)(min(rr, a.Lk - 1 - kc) * a.k_sl + c * 8) * 2u);
         }
       }
@@ -472,8 +481,8 @@ void bsattn_kernel(AttnKArgs a) {
       asm volatile("" : "+v"(ln));                 // keep this rare path's offsets out of the loop preheader
 #pragma unroll
       for (int i = 0; i < NR; ++i) {
-        const int r = 4 * (wave * NR + i) + (ln >> 4);
-        const int c = (ln & 15) ^ (r & 15);
+        const int r = RPR * (wave * NR + i) + (ln >> LCPR);
+        const int c = (ln & SWM) ^ (r & SWM);
         dma16s(lk + i * 1024, base, (uint32_t)(min(r, a.Lk - 1 - kc) * a.k_sl + c * 8) * 2u);
       }
     }
@@ -487,7 +496,7 @@ void bsattn_kernel(AttnKArgs a) {
 #pragma unroll
         for (int ie = 0; ie < EPT; ++ie) {
           const int blk = (int)(ue.e[ie] & 0xffffu);
-          ek[ie] = (uint32_t)(blk < a.Nk ? blk * kD * LB : 0) * 2u;
+          ek[ie] = (uint32_t)(blk < a.Nk ? blk * D * LB : 0) * 2u;
         }
 #pragma unroll
         for (int i = 0; i < NR; ++i) {
@@ -515,9 +524,10 @@ void bsattn_kernel(AttnKArgs a) {
   // For V^T tiles of 64 keys an LDS row holds two d rows (d = 2 r + (chunk >> 3)):
   // the lane's d row dt * 32 + l32 sits in LDS row dt * 16 + (l32 >> 1), chunk
   // (l32 & 1) * 8 + C0 + hi.
-  const uint32_t lane_off = (uint32_t)(l32 * 256 + ((hi ^ (l32 & 15)) << 4));
+  const uint32_t lane_off = (uint32_t)(l32 * ROWB + ((hi ^ (l32 & SWM)) << 4));   // K tile rows
+  const uint32_t lane_off_vr = (uint32_t)(l32 * 256 + ((hi ^ (l32 & 15)) << 4));   // 256-byte V^T rows
   const uint32_t lane_off_v =
-      TK == 128 ? lane_off
+      TK == 128 ? lane_off_vr
                 : (uint32_t)((l32 >> 1) * 256 + (((((l32 & 1) << 3) | hi) ^ (l32 >> 1)) << 4));
   constexpr int VROW = TK == 128 ? 32 * 256 : 16 * 256;   // bytes per 32 d rows of V^T
 
@@ -533,25 +543,25 @@ void bsattn_kernel(AttnKArgs a) {
   // MFMAs per wave) the row max is kept, the other form measured 3.5% slower.
   constexpr bool kRowMax = C::KG == 1;
   float m_run = -INFINITY, l_run = 0.f;
-  f32x16_t o[kD / 32];
+  f32x16_t o[D / 32];
 #pragma unroll
-  for (int dt = 0; dt < kD / 32; ++dt)
+  for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[dt][r] = 0.f;
 
   // S^T = K Q^T for this wave's keys of the K tile in buffer kbuf
   auto compute_s = [&](int kbuf, f32x16_t* s) {
-    const char* kt_base = reinterpret_cast<const char*>(lds[0][kbuf]) + kbase * 256;
+    const char* kt_base = reinterpret_cast<const char*>(lds[0][kbuf]) + kbase * ROWB;
 #pragma unroll
     for (int kt = 0; kt < C::KT; ++kt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[kt][r] = 0.f;
 #pragma unroll
-    for (int st = 0; st < kD / 16; ++st) {
+    for (int st = 0; st < D / 16; ++st) {
       const uint32_t lo = lane_off ^ (uint32_t)(st << 5);
 #pragma unroll
       for (int kt = 0; kt < C::KT; ++kt) {
-        const V8 ka = __builtin_bit_cast(V8, lds16(kt_base + kt * 32 * 256, lo));
+        const V8 ka = __builtin_bit_cast(V8, lds16(kt_base + kt * 32 * ROWB, lo));
         s[kt] = Ops::mma(ka, qf[st], s[kt]);
       }
     }
@@ -658,7 +668,7 @@ void bsattn_kernel(AttnKArgs a) {
     for (int kk = 0; kk < C::KH / 16; ++kk) {
       const uint32_t lo = lane_off_v ^ (uint32_t)(((kbase >> 3) + 2 * kk) << 4);
 #pragma unroll
-      for (int dt = 0; dt < kD / 32; ++dt) {
+      for (int dt = 0; dt < D / 32; ++dt) {
         const V8 va = __builtin_bit_cast(V8, lds16(vt_base + dt * VROW, lo));
         o[dt] = Ops::mma(va, pb[kk], o[dt]);
       }
@@ -667,7 +677,7 @@ void bsattn_kernel(AttnKArgs a) {
   auto scale_o = [&](float alpha) {
     if (alpha != 1.0f) {                             // per query row (lane); rare
 #pragma unroll
-      for (int dt = 0; dt < kD / 32; ++dt)
+      for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
     }
@@ -729,7 +739,7 @@ void bsattn_kernel(AttnKArgs a) {
       // would hold its exponentials until the last one), the LDS operand
       // reads running six MFMAs ahead (measured best of 2 .. 8; three VALU
       // per MFMA against two: C2 -2.4%, C3a -4.6%, C3b -1.5%).
-      constexpr int NM = C::KT * (kD / 16) + (C::KH / 16) * (kD / 32);
+      constexpr int NM = C::KT * (D / 16) + (C::KH / 16) * (D / 32);
       constexpr int LA = 6;
       constexpr int VPM = 3;
       __builtin_amdgcn_sched_group_barrier(0x100, LA, 0);        // DS reads
@@ -822,14 +832,14 @@ void bsattn_kernel(AttnKArgs a) {
   }
   // ---- merge the two key halves through LDS (split tiles), normalise, store
   float f0 = 1.0f, f1 = 0.0f, l = l_run;
-  constexpr int PER = (kD / 32) * 16 + 2;
+  constexpr int PER = (D / 32) * 16 + 2;
   const float* src = reinterpret_cast<const float*>(&lds[0][0][0]) + (size_t)qq * PER * 64;   // [QW][PER][64]
   if constexpr (C::KG == 2) {
     __syncthreads();
     if (kh == 1) {
       float* dst = reinterpret_cast<float*>(&lds[0][0][0]) + (size_t)qq * PER * 64;
 #pragma unroll
-      for (int dt = 0; dt < kD / 32; ++dt)
+      for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) dst[(dt * 16 + r) * 64 + lane] = o[dt][r];
       dst[(PER - 2) * 64 + lane] = m_run;
@@ -849,7 +859,7 @@ void bsattn_kernel(AttnKArgs a) {
   const float inv = l > 0.f ? 1.0f / l : 0.f;
   uint16_t* op = a.out + b * a.o_sb + h * a.o_sh + (int64_t)qrow * a.o_sl;
 #pragma unroll
-  for (int dt = 0; dt < kD / 32; ++dt)
+  for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
     for (int g4 = 0; g4 < 4; ++g4) {
       float v4[4];
@@ -1089,7 +1099,7 @@ static int union_groups(const fs_attn_args& a) {
 }
 
 // order pass (block lists only) and the main kernel, reading V^T from the workspace
-template <int BS, int TK, typename T>
+template <int BS, int TK, typename T, int D>
 static int launch_run(const fs_attn_args& a, int Nq, int Nk, hipStream_t s, int Lp = 0) {
   if (Lp == 0) Lp = vt_len(Nk, BS);                // else: V^T laid out for another block size
   const uint16_t* vt = static_cast<const uint16_t*>(a.work);
@@ -1135,13 +1145,13 @@ static int launch_run(const fs_attn_args& a, int Nq, int Nk, hipStream_t s, int 
   k.ctr = ctr;
   k.static_units = static_units;
   k.pool_units = pool_units;
-  bsattn_kernel<BS, TK, T><<<grid, AttnCfg<BS, TK>::NT, 0, s>>>(k);
+  bsattn_kernel<BS, TK, T, BS, D><<<grid, AttnCfg<BS, TK, D>::NT, 0, s>>>(k);
   return fs_host::launch_status("fs_bsattn");
 }
 
 // union mode (16- and 32-token lists): union lists, order pass over the
 // groups, the 128-query kernel over the unions
-template <int LB, typename T>
+template <int LB, typename T, int D>
 static int launch_run_union(const fs_attn_args& a, hipStream_t s) {
   constexpr int R = 128 / LB;
   const int NqL = (a.Lq + LB - 1) / LB, NkL = (a.Lk + LB - 1) / LB;
@@ -1179,7 +1189,7 @@ static int launch_run_union(const fs_attn_args& a, hipStream_t s) {
   k.ctr = ctr;
   k.gqa_interleave = a.gqa_interleave ? 1 : 0;
   const unsigned grid = deal_units(total, run, k.static_units, k.pool_units);
-  bsattn_kernel<128, 64, T, LB><<<grid, AttnCfg<128, 64>::NT, 0, s>>>(k);
+  bsattn_kernel<128, 64, T, LB, D><<<grid, AttnCfg<128, 64, D>::NT, 0, s>>>(k);
   return fs_host::launch_status("fs_bsattn");
 }
 
@@ -1204,7 +1214,7 @@ static int check_attn(const fs_attn_args* a, const char* fn) {
   FS_CHECK_ARG(a->B >= 1 && a->Hq >= 1 && a->Hk >= 1 && a->Hq % a->Hk == 0,
                "%s: Hq=%d must be a multiple of Hk=%d", fn, a->Hq, a->Hk);
   FS_CHECK_ARG(a->Lq >= 1 && a->Lk >= 1, "%s: empty sequence", fn);
-  FS_CHECK_SUPPORTED(a->D == kD, "%s: head_dim %d unsupported (128 only)", fn, a->D);
+  FS_CHECK_SUPPORTED(a->D == 128 || a->D == 64, "%s: head_dim %d unsupported (64 or 128)", fn, a->D);
   FS_CHECK_SUPPORTED(a->bs == 16 || a->bs == 32 || a->bs == 64 || a->bs == 128, "%s: block size %d unsupported", fn,
                      a->bs);
   // union mode (16- and 32-token lists): block indices and their rows packed in 32-bit entries
@@ -1237,10 +1247,28 @@ extern "C" int fs_bsattn_prepare(const fs_attn_args* a, void* stream) {
   if (int rc = check_attn(a, "fs_bsattn_prepare")) return rc;
   const int Nk = (a->Lk + a->bs - 1) / a->bs;
   const int Lp = vt_len(Nk, a->bs);
-  vt_kernel<<<a->B * a->Hk * (Lp / 64), 256, 0, (hipStream_t)stream>>>(
+  auto vt = a->D == 64 ? vt_kernel<64> : vt_kernel<128>;
+  vt<<<a->B * a->Hk * (Lp / 64), 256, 0, (hipStream_t)stream>>>(
       static_cast<const uint16_t*>(a->v), a->v_sb, a->v_sh, a->v_sl, static_cast<uint16_t*>(a->work), a->Hk, a->Lk,
       Lp, union_mode(*a) ? a->bs : 0);
   return fs_host::launch_status("fs_bsattn_prepare");
+}
+
+// head dim D, element type T: the kernels of one call
+template <typename T, int D>
+static int run_typed(const fs_attn_args* a, int Nq, int Nk, hipStream_t s) {
+  if (a->bs == 128) return launch_run<128, 64, T, D>(*a, Nq, Nk, s);
+  if (a->bs < 64) {
+    if (a->blk_cnt) {
+      // 16- and 32-token lists: unions over groups of 128 queries
+      return a->bs == 32 ? launch_run_union<32, T, D>(*a, s) : launch_run_union<16, T, D>(*a, s);
+    }
+    // dense causal attention does not depend on the block size: the 128-token
+    // kernel, reading V^T as it was laid out for this block size
+    const int Nq128 = (a->Lq + 127) / 128, Nk128 = (a->Lk + 127) / 128;
+    return launch_run<128, 64, T, D>(*a, Nq128, Nk128, s, vt_len(Nk, a->bs));
+  }
+  return launch_run<64, 64, T, D>(*a, Nq, Nk, s);
 }
 
 extern "C" int fs_bsattn_run(const fs_attn_args* a, void* stream) {
@@ -1248,24 +1276,9 @@ extern "C" int fs_bsattn_run(const fs_attn_args* a, void* stream) {
   const int Nq = (a->Lq + a->bs - 1) / a->bs;
   const int Nk = (a->Lk + a->bs - 1) / a->bs;
   hipStream_t s = (hipStream_t)stream;
-  if (a->bs == 128) {
-    return a->dtype == FS_DTYPE_BF16 ? launch_run<128, 64, bf16_t>(*a, Nq, Nk, s)
-                                     : launch_run<128, 64, f16_t>(*a, Nq, Nk, s);
-  }
-  if (a->bs < 64) {
-    if (a->blk_cnt) {
-      // 16- and 32-token lists: unions over groups of 128 queries
-      if (a->bs == 32)
-        return a->dtype == FS_DTYPE_BF16 ? launch_run_union<32, bf16_t>(*a, s) : launch_run_union<32, f16_t>(*a, s);
-      return a->dtype == FS_DTYPE_BF16 ? launch_run_union<16, bf16_t>(*a, s) : launch_run_union<16, f16_t>(*a, s);
-    }
-    // dense causal attention does not depend on the block size: the 128-token
-    // kernel, reading V^T as it was laid out for this block size
-    const int Nq128 = (a->Lq + 127) / 128, Nk128 = (a->Lk + 127) / 128;
-    return a->dtype == FS_DTYPE_BF16 ? launch_run<128, 64, bf16_t>(*a, Nq128, Nk128, s, vt_len(Nk, a->bs))
-                                     : launch_run<128, 64, f16_t>(*a, Nq128, Nk128, s, vt_len(Nk, a->bs));
-  }
-  return a->dtype == FS_DTYPE_BF16 ? launch_run<64, 64, bf16_t>(*a, Nq, Nk, s) : launch_run<64, 64, f16_t>(*a, Nq, Nk, s);
+  if (a->D == 64)
+    return a->dtype == FS_DTYPE_BF16 ? run_typed<bf16_t, 64>(a, Nq, Nk, s) : run_typed<f16_t, 64>(a, Nq, Nk, s);
+  return a->dtype == FS_DTYPE_BF16 ? run_typed<bf16_t, 128>(a, Nq, Nk, s) : run_typed<f16_t, 128>(a, Nq, Nk, s);
 }
 
 extern "C" int fs_bsattn(const fs_attn_args* a, void* stream) {

@@ -343,7 +343,7 @@ FS_API int fs_flex(const fs_flex_args* a, void* stream);
  * (NW = FS_MASK_WORDS(Nk); bits past the causal limit are ignored); blk_cnt
  * [Hq][Nq] (the rows' bit counts) only orders the work, largest first.
  * blk_cnt == NULL selects every key block up to the
- * causal limit (dense causal attention).  Supported: dtype bf16/f16, D == 128,
+ * causal limit (dense causal attention).  Supported: dtype bf16/f16, D in {64, 128},
  * bs in {16, 32, 64, 128} (16 and 32: FlexPrefill's block sizes; their masks
  * are attended 128 queries at a time over the union of 128 / bs rows,
  * up to 8192 key blocks).  All tensors are

@@ -2,8 +2,9 @@
 cases against fp32 attention under the same block mask: block sizes 16, 32,
 64 and 128 (16 and 32 in union mode), ragged lengths, GQA group sizes 1, 2,
 4 and 7, causal and not, fewer queries than keys (bottom-right aligned), bf16
-and fp16, densities from 5% to every block, and empty rows.  Bar: max-abs
-2e-2 on six sampled query blocks of every head (rows with no visible key: 0)."""
+and fp16, head dims 128 and 64, densities from 5% to every block, and empty
+rows.  Bar: max-abs 2e-2 on six sampled query blocks of every head (rows with
+no visible key: 0)."""
 from __future__ import annotations
 
 import random
@@ -33,17 +34,16 @@ def _case(i: int):
     return rng, bs, Hk, g, Lq, Lk, causal, dtype, dens, empty_rows
 
 
-@pytest.mark.parametrize("i", range(100))
-def test_random_lists_against_fp32(i):
+def _random_case(i: int, D: int):
     rng, bs, Hk, g, Lq, Lk, causal, dtype, dens, empty_rows = _case(i)
     Hq = Hk * g
-    print(f"[case] random-attn {i}: bs={bs} Hq={Hq} Hk={Hk} Lq={Lq} Lk={Lk} causal={causal} {dtype} "
+    print(f"[case] random-attn {i}: D={D} bs={bs} Hq={Hq} Hk={Hk} Lq={Lq} Lk={Lk} causal={causal} {dtype} "
           f"density={dens} empty_rows={empty_rows}", flush=True)
     Nq, Nk = -(-Lq // bs), -(-Lk // bs)
     gen = torch.Generator().manual_seed(1000 + i)
-    q = torch.randn(1, Hq, Lq, 128, generator=gen).to(dtype)
-    k = torch.randn(1, Hk, Lk, 128, generator=gen).to(dtype)
-    v = torch.randn(1, Hk, Lk, 128, generator=gen).to(dtype)
+    q = torch.randn(1, Hq, Lq, D, generator=gen).to(dtype)
+    k = torch.randn(1, Hk, Lk, D, generator=gen).to(dtype)
+    v = torch.randn(1, Hk, Lk, D, generator=gen).to(dtype)
     mask = torch.rand(Hq, Nq, Nk, generator=gen) < dens
     if empty_rows:
         mask[:, ::3] = False
@@ -52,14 +52,14 @@ def test_random_lists_against_fp32(i):
                                  block_size=bs, is_causal=causal)
     torch.cuda.synchronize()
     o = out[0].float().cpu()
-    off, scale = Lk - Lq, 128 ** -0.5
+    off, scale = Lk - Lq, D ** -0.5
     worst = 0.0
     for h in range(Hq):
         kh, vh = k[0, h // g].float(), v[0, h // g].float()
         for r in rng.sample(range(Nq), min(Nq, 6)):
             t0, t1 = r * bs, min(Lq, (r + 1) * bs)
             cols = torch.nonzero(mask[h, r]).flatten().tolist()
-            ref = torch.zeros(t1 - t0, 128)
+            ref = torch.zeros(t1 - t0, D)
             if cols:
                 kidx = torch.cat([torch.arange(j * bs, min(Lk, (j + 1) * bs)) for j in cols])
                 s = (q[0, h, t0:t1].float() @ kh[kidx].T) * scale
@@ -69,6 +69,18 @@ def test_random_lists_against_fp32(i):
             worst = max(worst, (o[t0:t1, h] - ref).abs().max().item())
     print(f"  max_abs {worst:.3e}", flush=True)
     assert worst <= 2e-2
+
+
+@pytest.mark.parametrize("i", range(100))
+def test_random_lists_against_fp32(i):
+    _random_case(i, 128)
+
+
+@pytest.mark.parametrize("i", range(100, 132))
+def test_random_lists_against_fp32_head_dim_64(i):
+    """Head dim 64 (block_sparse_attn's other supported size): K tiles of
+    128-byte rows, the same V^T layout."""
+    _random_case(i, 64)
 
 
 @pytest.mark.parametrize("bs,Lk", [(16, 131072), (32, 200000)])

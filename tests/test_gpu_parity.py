@@ -423,6 +423,30 @@ def test_myattn_prefill_end_to_end_c1_shape():
     _attn_check(out.view(q.shape[2], q.shape[1], q.shape[3]), ref, rows)
 
 
+@pytest.mark.parametrize("bs", [128, 64])
+def test_myattn_prefill_head_dim_64(bs):
+    """Head dim 64: the selection against the oracle's, and myattn_prefill's
+    output against fp32 attention under its own lists on sampled query blocks
+    of every head."""
+    _print_case("myattn_prefill", D=64, bs=bs)
+    q, k, v = make_qkv(32768, 8, 2, D=64, dtype=torch.bfloat16, seed=9)
+    qg, kg, vg = _gpu(q, k, v)
+    kw = {**PROD, "block_size": bs}
+    out = myattn_prefill(qg, kg, vg, layer_idx=0, **kw)
+    sel = select_blocks(qg, kg, **kw)
+    torch.cuda.synchronize()
+    assert out.shape == (1, q.shape[2], q.shape[1] * 64) and out.dtype == q.dtype
+    ref_sel = v7.select_mask(q, k, **kw)
+    frac, exact, unexc = block_match(sel.dense_mask(), ref_sel.mask, ref_sel.excusable)
+    print(f"  match={frac:.6f} exact={exact:.6f}")
+    assert frac >= MATCH_MIN
+    N = sel.params.N
+    qblocks = [0, 1, N // 3, N // 2, N - 2, N - 1]
+    ref = v7.block_sparse_attention(q, k, v, sel.dense_mask().cpu(), bs, qblocks=qblocks)
+    rows = torch.cat([torch.arange(i * bs, (i + 1) * bs) for i in qblocks])
+    _attn_check(out.view(q.shape[2], q.shape[1], 64), ref, rows)
+
+
 def test_short_sequence_fallback_is_dense_causal():
     q, k, v = make_qkv(1000, 4, 2, seed=8)                      # L < 10 * bs
     out = myattn_prefill(*_gpu(q, k, v), layer_idx=0, **PROD)
