@@ -10,14 +10,16 @@
 //                   reference forms the suffix sums of q_b first, which is the same sum)
 //   last row        S[N-1][j] rounded to the input dtype    (:54-72)
 //
-// scores_kernel: one workgroup (4 waves) per (head, 128 x 128 tile I >= J of
-// the lower triangle).  Wave w computes rows 32w .. 32w+31 of the tile with
-// v_mfma_f32_32x32x16 (K tile copied to LDS with global_load_lds_dwordx4, no
-// register staging, so four workgroups fit a CU), the tile is written to LDS in
-// two halves of 64 columns, and fixed-order per-tile partials
-// are written to the work buffer: the 255 diagonal sums, the 128 column sums
-// over rows i >= j, i <= N-2, the elements of every sampled diagonal that
-// crosses the tile, and the last row.
+// scores_kernel: one workgroup (4 waves) per (head, 128 x 64 column half of a
+// 128 x 128 tile I >= J of the lower triangle).  Wave w computes rows
+// 32w .. 32w+31 of the half with v_mfma_f32_32x32x16 (the half's 64 K rows
+// staged in LDS), the half goes through LDS in two quarters of 32 columns
+// (20 KiB of LDS and 80 registers per lane, so six workgroups fit a CU), and
+// fixed-order partials are written to the work buffer: the 255 diagonal sums
+// of each half, the column sums over rows i >= j, i <= N-2, the elements of
+// every sampled diagonal that crosses the half, and the last row.  (Whole
+// tiles per workgroup, three to a CU: 31.3 against 28.7 us at N = 1024 with
+// 32 heads, the 1152 tiles in two rounds of workgroups either way.)
 // scores_final_kernel: grid (head, job): job 0 adds the lag partials and
 // selects the lags, 2 the column scores and their top-n, 3 the last-row
 // top-k, 4 .. 7 the diagonal statistics (one wave per sample; job 1 is
@@ -29,6 +31,8 @@
 namespace fs {
 
 constexpr int kScoreTile = 128;
+constexpr int kHalf = kScoreTile / 2;           // columns per score workgroup
+constexpr int kQuarter = kScoreTile / 4;        // columns per S pass through LDS
 constexpr int kScoreThreads = 256;
 constexpr int kFinalThreads = 1024;
 constexpr int kDiagSlots = 256;                 // 255 local diagonals per tile (+1 pad)
@@ -65,25 +69,25 @@ __device__ __forceinline__ void tile_ij(int t, int& I, int& J) {
 __device__ __forceinline__ int tile_id(int I, int J) { return I * (I + 1) / 2 + J; }
 
 template <typename T>
-__global__ __launch_bounds__(kScoreThreads) void scores_kernel(fs_scores_args a, int ntiles, float inv_sqrt_d,
-                                                               float* __restrict__ pdiag, float* __restrict__ pcol,
-                                                               float* __restrict__ dvs) {
-  // the K tile (bf16/f16 [128][D], D <= 128: 32 KiB) is staged in the same
-  // LDS as the S half-tiles written after the MFMAs
-  __shared__ __attribute__((aligned(16))) float sl[kScoreTile][kScoreTile / 2 + 1];
-  __shared__ int taus[kMaxSamples];
-  __shared__ short rel[kMaxSamples];               // the sampled diagonals that cross this tile
+__global__ __launch_bounds__(kScoreThreads) __attribute__((amdgpu_waves_per_eu(5))) void scores_kernel(
+    fs_scores_args a, int ntiles, float inv_sqrt_d, float* __restrict__ pdiag, float* __restrict__ pcol,
+    float* __restrict__ dvs) {
+  // The half's K rows (bf16/f16 [64][D], D <= 128: 16 KiB) are staged in the
+  // same LDS as the S quarters written after the MFMAs.
+  __shared__ __attribute__((aligned(16))) float sl[kScoreTile][kQuarter + 1];
+  __shared__ short rel[kMaxSamples];               // the sampled diagonals that cross this half
   __shared__ int nrel;
-  __shared__ float csum[4][kScoreTile];            // per-wave column partials
+  __shared__ float csum[4][kHalf];                 // per-wave column partials
   uint16_t* kt = reinterpret_cast<uint16_t*>(&sl[0][0]);
   // Workgroup w runs on XCD w % 8.  XCD x takes the contiguous range of
-  // (head, tile) items [x per, (x + 1) per): a head's tiles (and the heads of
-  // one KV group) share one XCD, so the Q_b / K_b panels each tile re-reads
-  // are fetched into that XCD's L2 once instead of into all eight.
-  const int total = a.Hq * ntiles, per = (total + 7) / 8;
+  // (head, tile, half) items [x per, (x + 1) per): a head's tiles (and the
+  // heads of one KV group) share one XCD, so the Q_b / K_b panels each tile
+  // re-reads are fetched into that XCD's L2 once instead of into all eight.
+  const int total = a.Hq * ntiles * 2, per = (total + 7) / 8;
   const int slot = (int)(blockIdx.x >> 3), item = (int)(blockIdx.x & 7) * per + slot;
   if (slot >= per || item >= total) return;
-  const int h = item / ntiles, t = item - h * ntiles;
+  const int ht = item >> 1, hf = item & 1;
+  const int h = ht / ntiles, t = ht - h * ntiles;
   int I, J;
   tile_ij(t, I, J);
   const int N = a.N, D = a.D;
@@ -92,17 +96,19 @@ __global__ __launch_bounds__(kScoreThreads) void scores_kernel(fs_scores_args a,
   const int l32 = lane & 31, hi = lane >> 5;
   const uint16_t* qb = static_cast<const uint16_t*>(a.q_b) + (int64_t)h * N * D;
   const uint16_t* kb = static_cast<const uint16_t*>(a.k_b) + (int64_t)hk * N * D;
-  const int i0 = I * kScoreTile, j0 = J * kScoreTile;
+  const int i0 = I * kScoreTile, jt0 = J * kScoreTile;     // first row and column of the tile
+  const int c0 = hf * kHalf;                               // first tile column of this half
+  const int j0 = jt0 + c0;                                 // first column of this half
 
-  // ---- S tile: A = q rows (row i), B = k rows as columns (col j), K = d
-  f32x16_t acc[4];
+  // ---- S half: A = q rows (row i), B = k rows as columns (col j), K = d
+  f32x16_t acc[2];
 #pragma unroll
-  for (int jt = 0; jt < 4; ++jt)
+  for (int jt = 0; jt < 2; ++jt)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[jt][r] = 0.f;
-  // Every global load of the tile is issued before the first wait: this
-  // wave's Q operands (all D/16 steps, in registers), the K tile (to LDS,
-  // rows past N zero) and the sampled lags.
+  // Every global load of the half is issued before the first wait: this
+  // wave's Q operands (all D/16 steps, in registers) and the K rows (to LDS,
+  // rows past N zero).
   constexpr int kMaxSteps = 128 / 16;              // D <= 128
   const int qi = i0 + wave * 32 + l32;
   const uint16_t* qrow = qb + (int64_t)min(qi, N - 1) * D + hi * 8;
@@ -116,23 +122,19 @@ __global__ __launch_bounds__(kScoreThreads) void scores_kernel(fs_scores_args a,
   // lanes of an MFMA operand read take one row each, and without the swizzle
   // every row's chunk would sit in the same banks
   const int sw = (cpr & (cpr - 1)) == 0 ? cpr - 1 : 0;
-  constexpr int kMaxChunks = kScoreTile * (128 / 8) / kScoreThreads;   // per thread, D <= 128
+  constexpr int kMaxChunks = kHalf * (128 / 8) / kScoreThreads;   // per thread, D <= 128
   uint4 kv[kMaxChunks];
 #pragma unroll
   for (int u = 0; u < kMaxChunks; ++u) {
     const int c = tid + u * kScoreThreads, r = c / cpr, cc = c - r * cpr;
-    kv[u] = (c < kScoreTile * cpr && j0 + r < N) ? *reinterpret_cast<const uint4*>(kb + (int64_t)(j0 + r) * D + cc * 8)
-                                                : make_uint4(0, 0, 0, 0);
+    kv[u] = (c < kHalf * cpr && j0 + r < N) ? *reinterpret_cast<const uint4*>(kb + (int64_t)(j0 + r) * D + cc * 8)
+                                            : make_uint4(0, 0, 0, 0);
   }
-  int tv = 0;
-  if (tid < a.n_samples) tv = a.sample_taus[tid];
-  for (int e = tid + kScoreThreads; e < a.n_samples; e += kScoreThreads) taus[e] = a.sample_taus[e];
-  if (tid < a.n_samples) taus[tid] = tv;
   if (tid == 0) nrel = 0;
 #pragma unroll
   for (int u = 0; u < kMaxChunks; ++u) {
     const int c = tid + u * kScoreThreads, r = c / cpr, cc = c - r * cpr;
-    if (c < kScoreTile * cpr) *reinterpret_cast<uint4*>(kt + r * D + ((cc ^ (r & sw)) * 8)) = kv[u];
+    if (c < kHalf * cpr) *reinterpret_cast<uint4*>(kt + r * D + ((cc ^ (r & sw)) * 8)) = kv[u];
   }
   __syncthreads();
 #pragma unroll
@@ -140,21 +142,22 @@ __global__ __launch_bounds__(kScoreThreads) void scores_kernel(fs_scores_args a,
     if (st >= D / 16) break;
     const uint4 av = qv[st];
 #pragma unroll
-    for (int jt = 0; jt < 4; ++jt) {
+    for (int jt = 0; jt < 2; ++jt) {
       const int kr = jt * 32 + l32;
       const uint4 bv = *reinterpret_cast<const uint4*>(kt + kr * D + (((2 * st + hi) ^ (kr & sw)) * 8));
       acc[jt] = ScoreMma<T>::mma(av, bv, acc[jt]);
     }
   }
-  // the sampled diagonals tau = i - j that cross the tile, i - j in [i0 - j0 - 127, i0 - j0 + 127]
-  // (their order in rel is arbitrary: each one's elements go to fixed places)
+  // the sampled diagonals tau = i - j that cross the half, i - j in
+  // [i0 - j0 - 63, i0 - j0 + 127] (their order in rel is arbitrary: each
+  // one's elements go to fixed places)
   for (int e = tid; e < a.n_samples; e += kScoreThreads) {
-    const int tau = taus[e];
-    if (tau >= 0 && tau < N && tau >= i0 - j0 - (kScoreTile - 1) && tau <= i0 - j0 + (kScoreTile - 1))
+    const int tau = a.sample_taus[e];
+    if (tau >= 0 && tau < N && tau >= i0 - j0 - (kHalf - 1) && tau <= i0 - j0 + (kScoreTile - 1))
       rel[atomicAdd(&nrel, 1)] = (short)e;
   }
 
-  // The S tile goes through LDS in two halves of 64 columns (a smaller LDS
+  // The S half goes through LDS in two quarters of 32 columns (a smaller LDS
   // footprint, so more workgroups per CU).  C layout: lane holds row
   // (r/4)*8 + hi*4 + r%4, column l32 of each 32x32 block.
   const int64_t tb = (int64_t)h * ntiles + t;
@@ -165,8 +168,8 @@ __global__ __launch_bounds__(kScoreThreads) void scores_kernel(fs_scores_args a,
   if (a.n_cols > 0) {
     const int ie = min(kScoreTile - 1, N - 2 - i0);
 #pragma unroll
-    for (int jt = 0; jt < 4; ++jt) {
-      const int jl = jt * 32 + l32;
+    for (int jt = 0; jt < 2; ++jt) {
+      const int jl = c0 + jt * 32 + l32;             // tile column
       float c = 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -174,44 +177,44 @@ __global__ __launch_bounds__(kScoreThreads) void scores_kernel(fs_scores_args a,
         if (il <= ie && (!diag_tile || il >= jl)) c += acc[jt][r];
       }
       c += __shfl_xor(c, 32, 64);
-      if (hi == 0) csum[wave][jl] = c;
+      if (hi == 0) csum[wave][jt * 32 + l32] = c;
     }
   }
   const int dl = tid - (kScoreTile - 1);           // this thread's local diagonal iloc - jloc
   const bool lag_on = a.keep_tau != nullptr && tid < 2 * kScoreTile - 1 && !(diag_tile && dl < 0);
   float lag = 0.f;
-  for (int hf = 0; hf < 2; ++hf) {
-    const int c0 = hf * (kScoreTile / 2);          // first tile column of this half
-    __syncthreads();                               // K tile / previous half consumed
 #pragma unroll
-    for (int jj = 0; jj < 2; ++jj)
+  for (int qt = 0; qt < 2; ++qt) {
+    const int cq = c0 + qt * kQuarter;             // first tile column of this quarter
+    __syncthreads();                               // K rows / previous quarter consumed
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sl[wave * 32 + (r >> 2) * 8 + hi * 4 + (r & 3)][jj * 32 + l32] = acc[2 * hf + jj][r];
+    for (int r = 0; r < 16; ++r) sl[wave * 32 + (r >> 2) * 8 + hi * 4 + (r & 3)][l32] = acc[qt][r];
     __syncthreads();
-    // ---- lag sums along the local diagonal, rows ascending (this half's columns)
+    // ---- lag sums along the local diagonal, rows ascending (this quarter's columns)
     if (lag_on) {
-      const int ib = max(0, dl + c0), ie = min(kScoreTile - 1, dl + c0 + kScoreTile / 2 - 1);
+      const int ib = max(0, dl + cq), ie = min(kScoreTile - 1, dl + cq + kQuarter - 1);
 #pragma unroll 8
-      for (int il = ib; il <= ie; ++il) lag += sl[il][il - dl - c0];
+      for (int il = ib; il <= ie; ++il) lag += sl[il][il - dl - cq];
     }
-    // ---- sampled diagonals crossing the tile: S[j + tau][j] / sqrt(D) for j < N - tau - 1
+    // ---- sampled diagonals crossing the quarter: S[j + tau][j] / sqrt(D) for j < N - tau - 1
     const int nr = nrel;
-    for (int e = tid; e < nr * (kScoreTile / 2); e += kScoreThreads) {
-      const int s = rel[e / (kScoreTile / 2)], jh = e % (kScoreTile / 2);
-      const int tau = taus[s];
-      const int j = j0 + c0 + jh, i = j + tau;
+    for (int e = tid; e < nr * kQuarter; e += kScoreThreads) {
+      const int s = rel[e / kQuarter], jq = e % kQuarter;
+      const int tau = a.sample_taus[s];
+      const int j = jt0 + cq + jq, i = j + tau;
       if (tau < 0 || tau >= N || j >= N - tau - 1) continue;
       const int il = i - i0;
       if (il < 0 || il >= kScoreTile) continue;
-      dvs[((int64_t)h * a.n_samples + s) * N + j] = sl[il][jh] * inv_sqrt_d;
+      dvs[((int64_t)h * a.n_samples + s) * N + j] = sl[il][jq] * inv_sqrt_d;
     }
     // ---- last row, rounded to the input dtype
-    if (a.last_k > 0 && i0 <= N - 1 && N - 1 < i0 + kScoreTile && tid < kScoreTile / 2 && j0 + c0 + tid < N)
-      a.last_scores[(int64_t)h * N + j0 + c0 + tid] = Conv<T>::round(sl[N - 1 - i0][tid]);
+    if (a.last_k > 0 && i0 <= N - 1 && N - 1 < i0 + kScoreTile && tid < kQuarter && jt0 + cq + tid < N)
+      a.last_scores[(int64_t)h * N + jt0 + cq + tid] = Conv<T>::round(sl[N - 1 - i0][tid]);
   }
-  if (a.keep_tau != nullptr && tid < 2 * kScoreTile - 1) pdiag[tb * kDiagSlots + tid] = lag;
-  if (a.n_cols > 0 && tid < kScoreTile)
-    pcol[tb * kScoreTile + tid] = (j0 + tid < N) ? ((csum[0][tid] + csum[1][tid]) + csum[2][tid]) + csum[3][tid] : 0.f;
+  if (a.keep_tau != nullptr && tid < 2 * kScoreTile - 1) pdiag[(tb * 2 + hf) * kDiagSlots + tid] = lag;
+  if (a.n_cols > 0 && tid < kHalf)
+    pcol[tb * kScoreTile + c0 + tid] =
+        (j0 + tid < N) ? ((csum[0][tid] + csum[1][tid]) + csum[2][tid]) + csum[3][tid] : 0.f;
 }
 
 
@@ -244,7 +247,11 @@ __global__ __launch_bounds__(kFinalThreads) void scores_final_kernel(fs_scores_a
         const int dl = t - dd * kScoreTile;                  // local diagonal
         if (dl < -(kScoreTile - 1) || dl > kScoreTile - 1) continue;
 #pragma unroll 8
-        for (int J = 0; J + dd < NT; ++J) cs += pdiag[(hb + tile_id(J + dd, J)) * kDiagSlots + dl + kScoreTile - 1];
+        for (int J = 0; J + dd < NT; ++J) {
+          const float* pd = pdiag + (hb + tile_id(J + dd, J)) * 2 * kDiagSlots + dl + kScoreTile - 1;
+          cs += pd[0];
+          cs += pd[kDiagSlots];
+        }
       }
       if (a.corr_sum) a.corr_sum[(int64_t)h * N + t] = cs;
       float v = cs / (float)max(N - t, 1);
@@ -360,7 +367,7 @@ __global__ __launch_bounds__(kFinalThreads) void scores_final_kernel(fs_scores_a
 static size_t part_offsets(int Hq, int N, int n_samples, size_t* o_col, size_t* o_dv) {
   const int NT = (N + kScoreTile - 1) / kScoreTile;
   const size_t ntiles = (size_t)NT * (NT + 1) / 2;
-  const size_t diag = (size_t)Hq * ntiles * kDiagSlots * sizeof(float);
+  const size_t diag = (size_t)Hq * ntiles * 2 * kDiagSlots * sizeof(float);
   const size_t col = (size_t)Hq * ntiles * kScoreTile * sizeof(float);
   const size_t dv = (size_t)Hq * n_samples * N * sizeof(float);
   if (o_col) *o_col = diag;
@@ -379,7 +386,7 @@ static int launch_scores(const fs_scores_args& a, hipStream_t s) {
   float* pcol = reinterpret_cast<float*>(w + o_col);
   float* dvs = reinterpret_cast<float*>(w + o_dv);
   const float inv_sqrt_d = 1.0f / (float)sqrt((double)a.D);
-  scores_kernel<T><<<(a.Hq * ntiles + 7) / 8 * 8, kScoreThreads, 0, s>>>(a, ntiles, inv_sqrt_d, pdiag, pcol, dvs);
+  scores_kernel<T><<<(a.Hq * ntiles * 2 + 7) / 8 * 8, kScoreThreads, 0, s>>>(a, ntiles, inv_sqrt_d, pdiag, pcol, dvs);
   if (int rc = fs_host::launch_status("fs_scores (tiles)")) return rc;
   const size_t smem = (size_t)a.N * sizeof(float);
   if (int rc = fs_host::allow_dynamic_lds(scores_final_kernel, smem, "fs_scores")) return rc;
