@@ -198,7 +198,7 @@ FS_API int fs_scores(const fs_scores_args* a, void* stream);
  * until the process ends; a->work is ignored (may be NULL).  Same outputs as
  * fs_scores, bit for bit.  A call whose fs_scores_work_bytes(Hq, N, n_samples)
  * exceeds the array is rejected with FS_ERR_UNSUPPORTED before any launch
- * (BASELINE shapes need <= 10 MiB: Hq = 32, N = 1024, 64 samples).  Calls
+ * (BASELINE shapes need <= 11 MiB: Hq = 32, N = 1024, 64 samples).  Calls
  * on one GPU share its array: calls that overlap on one GPU (several streams
  * or threads) race; order them on one stream.  The first call on a device
  * looks the array's device address up (no allocation). */
