@@ -60,6 +60,9 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--select-groups", type=int, default=None,
                     help="KV-head groups of the selection pipeline (default: the library's choice)")
+    ap.add_argument("--tp-share", type=int, default=1, metavar="G",
+                    help="run one GPU's share of G-way sharding by KV-head group: the first Hkv / G KV heads "
+                         "and their query heads of the config's inputs, at the config's length")
     ap.add_argument("--cpu-heads", type=int, default=2,
                     help="query heads (all their query blocks) timed for the CPU attention sample")
     ap.add_argument("--c4-len", type=int, default=131072, help="config c4: prefill length")
@@ -382,6 +385,11 @@ def main():
     flex = args.selector == "flex"
     t_gen = time.perf_counter()
     q, k, v = make_config(cfg, seed=args.seed)
+    if args.tp_share > 1:
+        G = args.tp_share
+        if k.shape[1] % G:
+            raise SystemExit(f"--tp-share {G} must divide the config's {k.shape[1]} KV heads")
+        q, k, v = (x[:, :x.shape[1] // G].contiguous() for x in (q, k, v))
     if args.dtype:
         q, k, v = (x.to(getattr(torch, args.dtype)) for x in (q, k, v))
     q, k, v = q.to(dev), k.to(dev), v.to(dev)
@@ -553,7 +561,9 @@ def main():
                    "seq_len": L, "global_batch": 1, "block_size": bs,
                    **({"flex_gamma": args.flex_gamma, "flex_tau": args.flex_tau} if flex else
                       {("xattn_threshold" if xattn else "corr_threshold"): args.threshold}),
-                   "parallelism": "none (1 GPU)"},
+                   "parallelism": ("none (1 GPU)" if args.tp_share == 1 else
+                                   f"one GPU's share of {args.tp_share}-way sharding by KV-head group "
+                                   f"(the first {Hk} KV heads and their {Hq} query heads)")},
         "speedup_vs_dense": round(dense_ms / ms, 3) if dense_ms == dense_ms else None,
         "dense_ms": round(dense_ms, 3) if dense_ms == dense_ms else None,
         "dense": {k2: (round(v2, 3) if isinstance(v2, float) else v2) for k2, v2 in dense.items()},
