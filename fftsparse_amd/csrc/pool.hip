@@ -234,8 +234,12 @@ __global__ __launch_bounds__(kPoolThreads) void pool_kernel(PoolK a, int N) {
 // The plain pass reserves LDS it does not use so that at most five
 // workgroups share a CU: fewer concurrent streams of 32 KiB reads keep the
 // DRAM accesses more local (C2 pooling 198-200 -> 196 us, A/B over two
-// boxes; three per CU measured 207 us, six or eight 198-200 us).
+// boxes; three per CU measured 207 us, six or eight 198-200 us).  Blocks of
+// fewer than 128 tokens read half as much per workgroup or less, and six
+// workgroups per CU keep more bytes in flight (64-token blocks, 65536 tokens
+// of 28 + 4 heads: 99.3 -> 82.2-83.2 us; eight per CU 84.6-85.2).
 constexpr size_t kPoolLdsReserve = 24 * 1024;     // + the kernel's 8 KiB
+constexpr size_t kPoolLdsReserveSmall = 16 * 1024;
 
 template <bool ROPE>
 static int launch_pool(const PoolK& k, int dtype, hipStream_t s, const char* what) {
@@ -243,7 +247,7 @@ static int launch_pool(const PoolK& k, int dtype, hipStream_t s, const char* wha
   const int H = k.Hq + k.Hk;
   const int64_t blocks = ROPE ? (int64_t)((N + 7) / 8) * 8 * H : (int64_t)N * H;
   FS_CHECK_SUPPORTED(blocks < (1ll << 31), "%s: grid too large", what);
-  const size_t lds = ROPE ? 0 : kPoolLdsReserve;
+  const size_t lds = ROPE ? 0 : (k.bs >= 128 ? kPoolLdsReserve : kPoolLdsReserveSmall);
   switch (dtype) {
     case FS_DTYPE_F32: pool_kernel<float, ROPE><<<(unsigned)blocks, kPoolThreads, lds, s>>>(k, N); break;
     case FS_DTYPE_BF16: pool_kernel<bf16_t, ROPE><<<(unsigned)blocks, kPoolThreads, lds, s>>>(k, N); break;
