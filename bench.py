@@ -463,6 +463,9 @@ def main():
     esz = q.element_size()
     sel_bytes = L * Hq * D * esz + L * Hk * D * esz
     t_sel = statistics.mean(sel_ms)
+    # the traffic rows were measured on the config's default workload: threshold
+    # 0.9, its own dtype, every head
+    traffic_key = cfg.name if (args.threshold == 0.9 and not args.dtype and args.tp_share == 1) else None
     stripe = (int(sel.is_stripe.sum().item()) if not (xattn or flex) and sel.is_stripe is not None else None)
 
     dense = {}
@@ -535,7 +538,7 @@ def main():
                            # the same on the median step (the mean includes the first timed step,
                            # which starts on an idle GPU)
                            "frac_median": round(sel_bytes / (t_sel_med * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-                           "traffic": pmc_traffic("select", cfg.name),
+                           "traffic": pmc_traffic("select", traffic_key),
                            "work": "Q and K read once (L*(Hq+Hkv)*D*2 bytes)",
                            "timed": "select_blocks: pool, block-score tiles + statistics (2 launches), block masks "
                                     "(1 launch)"}
@@ -580,7 +583,7 @@ def main():
         "stripe_heads": stripe,
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": None if (xattn or flex) else pmc_traffic("bsattn", cfg.name),
+                     "traffic": None if (xattn or flex) else pmc_traffic("bsattn", traffic_key),
                      "kernel": (f"fs::bsattn_kernel<128, 64, {'bf16' if q.dtype == torch.bfloat16 else 'f16'}, {bs}>"
                                 + (" (union of 128 / bs rows' lists per workgroup)" if bs < 64 else "")),
                      "work": f"4*D*bs^2 flop per selected (query block, key block) tile x {nnz} tiles",
