@@ -35,9 +35,10 @@ class _Stop(Exception):
     """Ends a forward pass once the layer under test has been captured."""
 
 
-def _tiny(L, seed=0):
-    cfg = LlamaConfig(hidden_size=1024, intermediate_size=2048, num_hidden_layers=2, num_attention_heads=8,
-                      num_key_value_heads=2, head_dim=128, vocab_size=1000, max_position_embeddings=max(L, 8192))
+def _tiny(L, seed=0, head_dim=128):
+    cfg = LlamaConfig(hidden_size=8 * head_dim, intermediate_size=2048, num_hidden_layers=2, num_attention_heads=8,
+                      num_key_value_heads=2, head_dim=head_dim, vocab_size=1000,
+                      max_position_embeddings=max(L, 8192))
     torch.manual_seed(seed)
     return LlamaForCausalLM(cfg).to(DEV, torch.bfloat16).eval()
 
@@ -84,11 +85,12 @@ def _check_against_oracle(q, k, v, out, label, qblocks=None):
         assert err.mean().item() <= 1e-3
 
 
-def test_registered_prefill_matches_oracle():
-    """A 2-layer Llama prefill of 4096 tokens (8 query / 2 KV heads): the
-    registered attention of each layer against the oracle."""
-    print("[case] hf registered prefill vs oracle L=4096", flush=True)
-    m = _tiny(4096)
+@pytest.mark.parametrize("head_dim", [128, 64])
+def test_registered_prefill_matches_oracle(head_dim):
+    """A 2-layer Llama prefill of 4096 tokens (8 query / 2 KV heads, head dim
+    128 or 64): the registered attention of each layer against the oracle."""
+    print(f"[case] hf registered prefill vs oracle L=4096 head_dim={head_dim}", flush=True)
+    m = _tiny(4096, head_dim=head_dim)
     fh.patch_model(m)
     ids = torch.randint(0, 1000, (1, 4096), generator=torch.Generator().manual_seed(7)).to(DEV)
     try:
@@ -98,19 +100,20 @@ def test_registered_prefill_matches_oracle():
                 m(input_ids=ids, use_cache=False)
             q, k, v = got["q"], got["k"], got["v"]
             # the layout transformers passes: the projection's [1, L, H, D] storage seen as [1, H, L, D]
-            assert q.stride(1) == 128 and q.stride(2) == 8 * 128 and k.shape[1] == 2
-            assert got["scaling"] == 128 ** -0.5
+            assert q.stride(1) == head_dim and q.stride(2) == 8 * head_dim and k.shape[1] == 2
+            assert got["scaling"] == head_dim ** -0.5
             _check_against_oracle(q, k, v, got["out"], f"layer {layer}")
     finally:
         fh.register()
 
 
-def test_fused_rope_prefill_matches_oracle(monkeypatch):
+@pytest.mark.parametrize("head_dim", [128, 64])
+def test_fused_rope_prefill_matches_oracle(monkeypatch, head_dim):
     """patch_model(fused_rope=True): the pre-RoPE states go through rope_pool;
     the reference rotation is transformers' apply_rotary_pos_emb of the same
     states, and the layer output is checked against the oracle on it."""
-    print("[case] hf fused-rope prefill vs oracle L=4096", flush=True)
-    m = _tiny(4096, seed=1)
+    print(f"[case] hf fused-rope prefill vs oracle L=4096 head_dim={head_dim}", flush=True)
+    m = _tiny(4096, seed=1, head_dim=head_dim)
     fh.patch_model(m, fused_rope=True)
     ids = torch.randint(0, 1000, (1, 4096), generator=torch.Generator().manual_seed(8)).to(DEV)
     seen = {}
