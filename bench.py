@@ -75,6 +75,10 @@ def parse():
     ap.add_argument("--gemm-ceiling", action="store_true",
                     help="only time a bf16 8192^3 torch.matmul (hipBLASLt) 3 + 60 times, the practical MFMA ceiling "
                          "the attention kernel is compared with in the profiles, then exit")
+    ap.add_argument("--power-sample", action="store_true",
+                    help="only sample board power and the shader clock (amdsmi, every 50 ms) while the config's "
+                         "attention runs back to back on its lists, then on the full causal set, then a bf16 "
+                         "8192^3 torch.matmul and a 1 GiB device copy, about 4 s each; one JSON line, then exit")
     ap.add_argument("--traffic-rows", nargs=4, default=None,
                     metavar=("FETCH_CSV", "WRITE_CSV", "CAL_FETCH_CSV", "CAL_WRITE_CSV"),
                     help="only print the profiles/traffic.txt rows of --config from rocprofv3 --pmc FETCH_SIZE / "
@@ -402,6 +406,8 @@ def main():
 
     if args.selection_only:
         return run_selection_only(args, cfg, q, k, kw)
+    if args.power_sample:
+        return run_power_sample(args, cfg, q, k, v, kw)
 
     # One step = selection (pool, corr, stats, select) + attention (V^T
     # pre-pass, then order + attention kernel), all on torch's current stream,
@@ -594,6 +600,69 @@ def main():
         "input_gen_s": round(t_gen, 1),
     }
     print(json.dumps(line), flush=True)
+
+
+def run_power_sample(args, cfg, q, k, v, kw, secs=4.0):
+    """Board power and shader clock while one kernel runs back to back: a
+    thread samples amdsmi every 50 ms; the first second of each run (the
+    clock's ramp) is dropped.  The attention runs on the config's own lists
+    (one selection first), then on the full causal block set; the references
+    are a bf16 8192^3 torch.matmul (hipBLASLt) and a 1 GiB device copy."""
+    import threading
+    import amdsmi
+    import torch
+    from fftsparse_amd import AttentionCall, select_blocks
+    amdsmi.amdsmi_init()
+    handle = amdsmi.amdsmi_get_processor_handles()[0]
+
+    def sample(stop, out):
+        while not stop.is_set():
+            p = amdsmi.amdsmi_get_power_info(handle)
+            c = amdsmi.amdsmi_get_clock_info(handle, amdsmi.AmdSmiClkType.GFX)
+            out.append((time.perf_counter(), p.get("current_socket_power"), c.get("clk"), p.get("power_limit")))
+            time.sleep(0.05)
+
+    def run(fn):
+        fn()
+        torch.cuda.synchronize()
+        out, stop = [], threading.Event()
+        th = threading.Thread(target=sample, args=(stop, out))
+        th.start()
+        t0 = time.perf_counter()
+        n = 0
+        while time.perf_counter() - t0 < secs:
+            for _ in range(4):
+                fn()
+            torch.cuda.synchronize()
+            n += 4
+        t1 = time.perf_counter()
+        stop.set()
+        th.join()
+        rows = [r for r in out if r[0] - t0 > 1.0 and isinstance(r[1], (int, float)) and isinstance(r[2], (int, float))]
+        return {"launches": n, "ms_per_launch": round((t1 - t0) * 1e3 / n, 4), "samples": len(rows),
+                "power_w_median": statistics.median(r[1] for r in rows) if rows else None,
+                "power_w_range": [min(r[1] for r in rows), max(r[1] for r in rows)] if rows else None,
+                "gfx_mhz_median": statistics.median(r[2] for r in rows) if rows else None,
+                "gfx_mhz_range": [min(r[2] for r in rows), max(r[2] for r in rows)] if rows else None,
+                "power_limit_w": (out[0][3] / 1e6 if out and isinstance(out[0][3], (int, float)) else None)}
+
+    sel = select_blocks(q, k, **kw)
+    lists = AttentionCall(q, k, v, sel.blk_cnt, sel.blk_bits, block_size=cfg.block_size)
+    lists.prepare()
+    res = {"attention_lists": run(lists.run)}
+    dense = AttentionCall(q, k, v, block_size=cfg.block_size)
+    dense.prepare()
+    res["attention_dense"] = run(dense.run)
+    del dense, lists
+    n = 8192
+    a = torch.randn(n, n, device=q.device, dtype=torch.bfloat16)
+    b = torch.randn(n, n, device=q.device, dtype=torch.bfloat16)
+    res["gemm_8192"] = run(lambda: a @ b)
+    del a, b
+    x = torch.ones(1 << 30, dtype=torch.uint8, device=q.device)
+    y = torch.empty_like(x)
+    res["copy_1gib"] = run(lambda: y.copy_(x))
+    print(json.dumps({"power_sample": cfg.name, "secs_each": secs, **res}), flush=True)
 
 
 def run_selection_only(args, cfg, q, k, kw):
